@@ -1,0 +1,143 @@
+/*
+ * mitok.h — C ABI of the MI355X token loop for the rustCrates transformer.
+ *
+ * The reference crate (src/neural_networks/..., Rust, CPU-only) has no
+ * foreign-function boundary on this path except the OpenBLAS `zgemm_` it
+ * calls (utils/matrix.rs:13-15).  This header is the boundary a Rust FFI crate
+ * binds instead: each entry point names the Rust item it replaces.  The Rust
+ * binding and the drop-in wiring are in INTEGRATION.md.
+ *
+ * Conventions
+ *  - Complex<f64> (num-complex 0.4.6, #[repr(C)] {re, im}) crosses the ABI as
+ *    two interleaved doubles; a [rows][cols] complex matrix is rows*cols*2
+ *    doubles, row-major, exactly Vec<Vec<Complex<f64>>> flattened.
+ *  - Weight layouts are the reference's: Linear/Dense weights [in][out]
+ *    (linear_layer.rs:38, layer.rs:268), attention heads [heads][dim][head_dim]
+ *    (masked_attention_head.rs:64-75), bias_pos [heads][max_ctx][max_ctx].
+ *  - A NULL tensor leaves the device tensor zeroed (fill it with
+ *    mitok_init_seeded); NULL gamma/beta/biases take the reference's initial
+ *    values (gamma 1, beta 0: norm_layer.rs:45-50; biases 1+0i: layer.rs:269,
+ *    linear_layer.rs:39).
+ *  - Every call returns 0 or a MITOK_ERR_* code and never aborts; the message
+ *    is in mitok_last_error() (thread-local).  Where the reference panics
+ *    (NaN in GELU, non-finite FFN output, unknown token id, NaN logits), the
+ *    call returns MITOK_ERR_NAN / MITOK_ERR_ARG instead.
+ *  - A network is used by one thread at a time (the reference takes
+ *    &mut NeuralNetwork); calls are synchronous on return.
+ */
+#ifndef MITOK_H
+#define MITOK_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MITOK_OK 0
+#define MITOK_ERR_ARG 1
+#define MITOK_ERR_HIP 2
+#define MITOK_ERR_STATE 3
+#define MITOK_ERR_NAN 4
+#define MITOK_ERR_NOMEM 5
+
+/* OperationMode (network_types/neural_network_generic.rs:17-20) */
+#define MITOK_TRAINING 0
+#define MITOK_PRODUCTION 1
+
+/* kernel classes for mitok_timing_enable */
+#define MITOK_TIME_VOCAB 1       /* the vocab Linear (the Linear before Softmax) */
+#define MITOK_TIME_LAYER_GEMM 2  /* Q/K/V and FFN projections */
+#define MITOK_TIME_ATTENTION 3   /* attention kernels */
+#define MITOK_TIME_STEP 4        /* one whole decode step (one token for every sequence) */
+
+typedef struct mitok_network mitok_network; /* NeuralNetwork (neural_network_generic.rs:23-31) */
+
+int mitok_version(void);
+const char* mitok_last_error(void);
+int mitok_device_count(int* count);
+
+/* create(...) (neural_network_generic.rs:76-88): an empty layer list on `device`. */
+int mitok_network_create(int device, mitok_network** out);
+void mitok_network_destroy(mitok_network* net);
+int mitok_num_layers(const mitok_network* net);
+
+/* ---- LayerEnum variants, appended in order (network_components/layer.rs:75-88) ---- */
+/* EmbeddingLayer (embedding_layer.rs:24-36, forward :158-211); table [vocab][dim] */
+int mitok_add_embedding(mitok_network* net, uint32_t vocab, uint32_t dim, const double* table);
+/* PositionalEncodingLayer (positional_encoding_layer.rs:15-32, forward :35-99) */
+int mitok_add_positional_encoding(mitok_network* net, uint32_t dim, double base);
+/* NormalNormLayer (norm_layer.rs:17-62, forward :84-130) */
+int mitok_add_norm(mitok_network* net, uint32_t dim, double eps, const double* gamma, const double* beta);
+/* SelfAttentionLayer of `heads` MaskedAttentionHeads plus its NormalNormLayer
+ * (self_attention_layer.rs:29-50, forward :55-133; masked_attention_head.rs:64-106,
+ * forward :122-220).  max_ctx sizes bias_pos (the reference fixes it at 512,
+ * transformer_network.rs:32) and the KV cache. */
+int mitok_add_self_attention(mitok_network* net, uint32_t heads, uint32_t dim, uint32_t max_ctx, double eps,
+                             const double* wq, const double* wk, const double* wv, const double* bias_pos,
+                             const double* gamma, const double* beta);
+/* FeedForwardLayer = Dense(GELU) -> Linear (feedforward_layer.rs:30-48, forward :56-138) */
+int mitok_add_feed_forward(mitok_network* net, uint32_t dim, uint32_t hidden, const double* w1, const double* b1,
+                           const double* w2, const double* b2);
+/* LinearLayer (linear_layer.rs:37-54, forward :55-75); w [in][out] */
+int mitok_add_linear(mitok_network* net, uint32_t in, uint32_t out, const double* w, const double* b);
+/* SoftmaxLayer (softmax_output_layer.rs:30-65) */
+int mitok_add_softmax(mitok_network* net, int operation_mode);
+
+/* Seeded Xavier-uniform weights (initialize_weights_complex, utils/weights_initializer.rs:73-89),
+ * computed on the device from a counter generator: the CPU checker holds the same values. */
+int mitok_init_seeded(mitok_network* net, uint64_t seed);
+/* Reads a weight tensor back (slots as in oracle/oracle.h; slot 3 = Re(bias_pos), n doubles). */
+int mitok_get_tensor(mitok_network* net, uint32_t layer, uint32_t slot, double* out, uint64_t n);
+/* Drops every KV cache (k_cache = v_cache = None, masked_attention_head.rs:54-57). */
+int mitok_reset(mitok_network* net);
+
+/* predict (transformer_network.rs:315-504).  ids [batch][seq], right-padded:
+ * entries at or beyond lens[b] become PAD=1 (embedding_layer.rs:112-155).
+ * time_steps [batch] or NULL: RoPE position when forward_only && > 0.
+ * forward_only: KV-cache semantics (masked_attention_head.rs:135-178) and
+ *   out = Re(logits) (convert_c_to_f64_3d); otherwise stateless and out = the
+ *   SoftmaxLayer output for its OperationMode.
+ * last_row_only: out is [batch][vocab] from row lens[b]-1, else [batch][seq][vocab].
+ * out_padding_mask [batch][seq] or NULL. */
+int mitok_predict(mitok_network* net, const uint32_t* ids, const uint32_t* lens, uint32_t batch, uint32_t seq,
+                  const uint32_t* time_steps, int forward_only, int last_row_only, double* out,
+                  uint32_t* out_padding_mask);
+
+/* Layers [first, last) on hidden states: in [batch][seq][dim_in] complex,
+ * out [batch][seq][dim_out] complex; padding_mask [batch][seq] or NULL (all 1).
+ * This is each layer's forward(&LayerInput) -> LayerOutput chained. */
+int mitok_forward_layers(mitok_network* net, uint32_t first, uint32_t last, const double* in,
+                         const uint32_t* padding_mask, uint32_t batch, uint32_t seq, const uint32_t* time_steps,
+                         int forward_only, double* out);
+
+/* Greedy token loop on ids (predict_token_by_token, transformer_network.rs:165-313,
+ * without the text tokenizer): resets the caches, runs the prompt, then feeds
+ * each greedy id back for n_new tokens in total.  Sequence b of a batch is an
+ * independent batch-1 run.  Only token ids cross PCIe per step.
+ * out_ids [batch][n_new]; out_logits [n_new][batch][vocab] or NULL. */
+int mitok_generate(mitok_network* net, const uint32_t* prompt, const uint32_t* lens, uint32_t batch, uint32_t seq,
+                   uint32_t n_new, uint32_t* out_ids, double* out_logits);
+
+/* greedy_decoding (src/utils/sampling_methods.rs:5-18) on the device for host
+ * logits [rows][vocab]: last index among equal maxima; NaN -> MITOK_ERR_NAN. */
+int mitok_greedy_decoding(mitok_network* net, const double* logits, uint32_t rows, uint32_t vocab, uint32_t* out_ids);
+
+/* ---- measurement (no reference counterpart: the reference prints wall
+ * clock only, transformer_network.rs:307-310) ---- */
+/* Wall time of the last mitok_generate on the device stream, in ms:
+ * t[0] prefill (prompt forward + first id), t[1] all decode steps, t[2] 1 if
+ * the decode steps ran as a replayed HIP graph. */
+int mitok_last_timings(mitok_network* net, double* t3);
+/* HIP-event timing of one kernel class during the following calls (0 disables;
+ * decode steps then run without graph replay so each launch is bracketed). */
+int mitok_timing_enable(mitok_network* net, int kernel_class);
+/* Accumulated since enable: total ms, launches, algorithmic HBM bytes of those launches. */
+int mitok_timing_read(mitok_network* net, double* total_ms, uint64_t* launches, double* alg_bytes);
+/* 0 = replay decode steps as HIP graphs (default), 1 = launch kernels directly. */
+int mitok_set_graph_mode(mitok_network* net, int direct_launch);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,294 @@
+"""ctypes wrapper of the CPU oracle (oracle/liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py as the checker.  The product (rustcrates_amd/)
+never imports it.
+
+The oracle restates the reference's forward path line by line; see oracle.c for
+the per-function citations.  Functions with no independent check are listed
+as "parity unpinned" in the module docstring of tests/test_oracle_pins.py.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+TRAINING, PRODUCTION = 0, 1
+
+
+class OracleError(RuntimeError):
+    pass
+
+
+class _C64(C.Structure):
+    _fields_ = [("re", C.c_double), ("im", C.c_double)]
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def _load():
+    if not os.path.exists(LIB_PATH):
+        build()
+    lib = C.CDLL(LIB_PATH)
+    P = C.c_void_p
+    u32, u64, i32, f64 = C.c_uint32, C.c_uint64, C.c_int, C.c_double
+    sig = {
+        "orc_last_error": (C.c_char_p, []),
+        "orc_cmul": (_C64, [_C64, _C64]),
+        "orc_cdiv": (_C64, [_C64, _C64]),
+        "orc_csqrt": (_C64, [_C64]),
+        "orc_ctanh": (_C64, [_C64]),
+        "orc_gelu": (_C64, [_C64, P]),
+        "orc_zgemm": (None, [u32, u32, u32, P, P, P]),
+        "orc_layernorm_row": (None, [P, u32, f64, P, P, P]),
+        "orc_softmax_row_real": (None, [P, u32, P]),
+        "orc_greedy_row": (C.c_int64, [P, u32]),
+        "orc_rope_row": (None, [P, u32, f64, u64, P]),
+        "orc_draw": (u64, [u64, u64, u64]),
+        "orc_uniform": (f64, [u64, u64, u64, f64]),
+        "orc_gen_prompts": (None, [u64, u32, u32, P, u32, P]),
+        "orc_gen_normal": (None, [u64, u64, P]),
+        "orc_net_create": (P, []),
+        "orc_net_destroy": (None, [P]),
+        "orc_num_layers": (i32, [P]),
+        "orc_add_embedding": (i32, [P, u32, u32, P]),
+        "orc_add_positional_encoding": (i32, [P, u32, f64]),
+        "orc_add_norm": (i32, [P, u32, f64, P, P]),
+        "orc_add_self_attention": (i32, [P, u32, u32, u32, f64, P, P, P, P, P, P]),
+        "orc_add_feed_forward": (i32, [P, u32, u32, P, P, P, P]),
+        "orc_add_linear": (i32, [P, u32, u32, P, P]),
+        "orc_add_softmax": (i32, [P, i32]),
+        "orc_init_seeded": (i32, [P, u64]),
+        "orc_get_tensor": (i32, [P, u32, u32, P, u64]),
+        "orc_reset": (i32, [P]),
+        "orc_set_threads": (None, [i32]),
+        "orc_predict": (i32, [P, P, P, u32, u32, P, i32, i32, P, P]),
+        "orc_forward_layers": (i32, [P, u32, u32, P, P, u32, u32, P, i32, P]),
+        "orc_generate": (i32, [P, P, P, u32, u32, u32, P, P]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        _lib = _load()
+    return _lib
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+def _c128(a):
+    return None if a is None else np.ascontiguousarray(a, dtype=np.complex128)
+
+
+def _check(rc):
+    if rc != 0:
+        raise OracleError(f"oracle error {rc}: {lib().orc_last_error().decode()}")
+
+
+def set_threads(n: int) -> None:
+    lib().orc_set_threads(int(n))
+
+
+# ---- scalar / row helpers (for pinning tests) ----
+def cmul(a: complex, b: complex) -> complex:
+    r = lib().orc_cmul(_C64(a.real, a.imag), _C64(b.real, b.imag))
+    return complex(r.re, r.im)
+
+
+def cdiv(a: complex, b: complex) -> complex:
+    r = lib().orc_cdiv(_C64(a.real, a.imag), _C64(b.real, b.imag))
+    return complex(r.re, r.im)
+
+
+def csqrt(z: complex) -> complex:
+    r = lib().orc_csqrt(_C64(z.real, z.imag))
+    return complex(r.re, r.im)
+
+
+def ctanh(z: complex) -> complex:
+    r = lib().orc_ctanh(_C64(z.real, z.imag))
+    return complex(r.re, r.im)
+
+
+def gelu(z: complex) -> tuple[complex, bool]:
+    flag = C.c_int(0)
+    r = lib().orc_gelu(_C64(z.real, z.imag), C.byref(flag))
+    return complex(r.re, r.im), bool(flag.value)
+
+
+def zgemm(A: np.ndarray, B: np.ndarray) -> np.ndarray:
+    A, B = _c128(A), _c128(B)
+    m, k = A.shape
+    k2, n = B.shape
+    assert k == k2
+    Cm = np.empty((m, n), np.complex128)
+    lib().orc_zgemm(m, n, k, _ptr(A), _ptr(B), _ptr(Cm))
+    return Cm
+
+
+def layernorm_row(x, eps, gamma=None, beta=None):
+    x = _c128(x)
+    d = x.shape[0]
+    g = _c128(np.ones(d) if gamma is None else gamma)
+    b = _c128(np.zeros(d) if beta is None else beta)
+    out = np.empty(d, np.complex128)
+    lib().orc_layernorm_row(_ptr(x), d, float(eps), _ptr(g), _ptr(b), _ptr(out))
+    return out
+
+
+def softmax_row_real(x):
+    x = _c128(x)
+    out = np.empty(x.shape[0], np.float64)
+    lib().orc_softmax_row_real(_ptr(x), x.shape[0], _ptr(out))
+    return out
+
+
+def greedy_row(row) -> int:
+    row = np.ascontiguousarray(row, dtype=np.float64)
+    r = lib().orc_greedy_row(_ptr(row), row.shape[0])
+    if r < 0:
+        raise OracleError("greedy_decoding: NaN in logits")
+    return int(r)
+
+
+def rope_row(x, base, position):
+    x = _c128(x)
+    out = np.empty_like(x)
+    lib().orc_rope_row(_ptr(x), x.shape[0], float(base), int(position), _ptr(out))
+    return out
+
+
+def draw(seed, stream, index) -> int:
+    return int(lib().orc_draw(seed, stream, index))
+
+
+def uniform(seed, stream, index, lim) -> float:
+    return float(lib().orc_uniform(seed, stream, index, lim))
+
+
+def gen_prompts(seed: int, lens, vocab: int, max_len: int | None = None) -> np.ndarray:
+    lens = np.ascontiguousarray(lens, dtype=np.uint32)
+    B = lens.shape[0]
+    S = int(max_len if max_len is not None else lens.max())
+    ids = np.empty((B, S), np.uint32)
+    lib().orc_gen_prompts(seed, B, S, _ptr(lens), vocab, _ptr(ids))
+    return ids
+
+
+def gen_normal(seed: int, shape) -> np.ndarray:
+    n = int(np.prod(shape))
+    out = np.empty(n, np.complex128)
+    lib().orc_gen_normal(seed, n, _ptr(out))
+    return out.reshape(shape)
+
+
+class Network:
+    """NeuralNetwork of the oracle: layers are appended in LayerEnum order."""
+
+    def __init__(self):
+        self._h = lib().orc_net_create()
+        if not self._h:
+            raise OracleError("orc_net_create failed")
+        self.vocab = None
+
+    def close(self):
+        if self._h:
+            lib().orc_net_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def num_layers(self) -> int:
+        return lib().orc_num_layers(self._h)
+
+    def add_embedding(self, vocab, dim, table=None):
+        _check(lib().orc_add_embedding(self._h, vocab, dim, _ptr(_c128(table))))
+
+    def add_positional_encoding(self, dim, base=1250.0):
+        _check(lib().orc_add_positional_encoding(self._h, dim, base))
+
+    def add_norm(self, dim, eps, gamma=None, beta=None):
+        _check(lib().orc_add_norm(self._h, dim, eps, _ptr(_c128(gamma)), _ptr(_c128(beta))))
+
+    def add_self_attention(self, heads, dim, max_ctx, eps=1e-12, wq=None, wk=None, wv=None, bias_pos=None,
+                           gamma=None, beta=None):
+        _check(lib().orc_add_self_attention(self._h, heads, dim, max_ctx, eps, _ptr(_c128(wq)), _ptr(_c128(wk)),
+                                            _ptr(_c128(wv)), _ptr(_c128(bias_pos)), _ptr(_c128(gamma)),
+                                            _ptr(_c128(beta))))
+
+    def add_feed_forward(self, dim, hidden, w1=None, b1=None, w2=None, b2=None):
+        _check(lib().orc_add_feed_forward(self._h, dim, hidden, _ptr(_c128(w1)), _ptr(_c128(b1)),
+                                          _ptr(_c128(w2)), _ptr(_c128(b2))))
+
+    def add_linear(self, d_in, d_out, w=None, b=None):
+        self.vocab = d_out
+        _check(lib().orc_add_linear(self._h, d_in, d_out, _ptr(_c128(w)), _ptr(_c128(b))))
+
+    def add_softmax(self, mode=PRODUCTION):
+        _check(lib().orc_add_softmax(self._h, mode))
+
+    def init_seeded(self, seed):
+        _check(lib().orc_init_seeded(self._h, seed))
+
+    def get_tensor(self, layer, slot, n):
+        out = np.empty(n, np.complex128)
+        _check(lib().orc_get_tensor(self._h, layer, slot, _ptr(out), n))
+        return out
+
+    def reset(self):
+        _check(lib().orc_reset(self._h))
+
+    def predict(self, ids, lens=None, time_steps=None, forward_only=True, last_row_only=False):
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        B, S = ids.shape
+        lens = np.full(B, S, np.uint32) if lens is None else np.ascontiguousarray(lens, dtype=np.uint32)
+        ts = None if time_steps is None else np.ascontiguousarray(time_steps, dtype=np.uint32)
+        V = self.vocab
+        out = np.empty((B, V) if last_row_only else (B, S, V), np.float64)
+        mask = np.empty((B, S), np.uint32)
+        _check(lib().orc_predict(self._h, _ptr(ids), _ptr(lens), B, S, _ptr(ts), int(forward_only),
+                                 int(last_row_only), _ptr(out), _ptr(mask)))
+        return out, mask
+
+    def forward_layers(self, first, last, x, mask=None, time_steps=None, forward_only=True, d_out=None):
+        x = _c128(x)
+        B, S, _ = x.shape
+        m = None if mask is None else np.ascontiguousarray(mask, dtype=np.uint32)
+        ts = None if time_steps is None else np.ascontiguousarray(time_steps, dtype=np.uint32)
+        out = np.empty((B, S, d_out if d_out else x.shape[2]), np.complex128)
+        _check(lib().orc_forward_layers(self._h, first, last, _ptr(x), _ptr(m), B, S, _ptr(ts), int(forward_only),
+                                        _ptr(out)))
+        return out
+
+    def generate(self, prompt, lens=None, n_new=1, want_logits=False):
+        prompt = np.ascontiguousarray(prompt, dtype=np.uint32)
+        B, S = prompt.shape
+        lens = np.full(B, S, np.uint32) if lens is None else np.ascontiguousarray(lens, dtype=np.uint32)
+        ids = np.empty((B, n_new), np.uint32)
+        logits = np.empty((n_new, B, self.vocab), np.float64) if want_logits else None
+        _check(lib().orc_generate(self._h, _ptr(prompt), _ptr(lens), B, S, n_new, _ptr(ids), _ptr(logits)))
+        return (ids, logits) if want_logits else ids

@@ -1,0 +1,950 @@
+/*
+ * oracle.c — CPU restatement of the rustCrates transformer token loop.
+ *
+ * TEST INFRASTRUCTURE ONLY (see oracle.h).  Never linked into the product.
+ *
+ * Build: oracle/Makefile (gcc -O3 -ffp-contract=off -fopenmp, glibc libm).
+ *
+ * Citations are to the reference crate, relative to src/neural_networks/.
+ * Batch semantics: at batch 1 this is the reference exactly.  At batch > 1 the
+ * reference's cached decode only extends sequence 0 (masked_attention_head.rs:
+ * 141-172), so the oracle defines batched decode as independent per-sequence
+ * runs: sequence b caches its own lens[b] keys and decodes on its own length.
+ */
+#define _GNU_SOURCE
+#include "oracle.h"
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+static __thread char g_err[512];
+
+static int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+const char* orc_last_error(void) { return g_err; }
+
+void orc_set_threads(int n) {
+#ifdef _OPENMP
+  if (n > 0) omp_set_num_threads(n);
+#else
+  (void)n;
+#endif
+}
+
+/* ------------------------------------------------------------------------ */
+/* num-complex 0.4.6 arithmetic                                             */
+/* ------------------------------------------------------------------------ */
+
+static inline oc64 c_add(oc64 a, oc64 b) { return (oc64){a.re + b.re, a.im + b.im}; }
+static inline oc64 c_sub(oc64 a, oc64 b) { return (oc64){a.re - b.re, a.im - b.im}; }
+/* impl Mul for Complex: re = a.re*b.re - a.im*b.im, im = a.re*b.im + a.im*b.re */
+static inline oc64 c_mul(oc64 a, oc64 b) { return (oc64){a.re * b.re - a.im * b.im, a.re * b.im + a.im * b.re}; }
+/* Complex * f64 and f64 * Complex scale both parts */
+static inline oc64 c_scale(oc64 a, double t) { return (oc64){a.re * t, a.im * t}; }
+/* Complex / f64 (unscale) */
+static inline oc64 c_unscale(oc64 a, double t) { return (oc64){a.re / t, a.im / t}; }
+/* impl Div for Complex: multiply by the conjugate over norm_sqr */
+static inline oc64 c_div(oc64 a, oc64 b) {
+  double n = b.re * b.re + b.im * b.im;
+  double re = a.re * b.re + a.im * b.im;
+  double im = a.im * b.re - a.re * b.im;
+  return (oc64){re / n, im / n};
+}
+
+/* Complex::sqrt: positive-real and imaginary-axis shortcuts, else polar form
+ * from_polar(sqrt(hypot), atan2/2). */
+static oc64 c_sqrt(oc64 z) {
+  if (z.im == 0.0) {
+    if (!signbit(z.re)) return (oc64){sqrt(z.re), z.im};
+    double im = sqrt(-z.re);
+    return signbit(z.im) ? (oc64){0.0, -im} : (oc64){0.0, im};
+  }
+  if (z.re == 0.0) {
+    double x = sqrt(fabs(z.im) / 2.0);
+    return signbit(z.im) ? (oc64){x, -x} : (oc64){x, x};
+  }
+  double r = hypot(z.re, z.im);
+  double theta = atan2(z.im, z.re);
+  double rs = sqrt(r), th = theta / 2.0;
+  return (oc64){rs * cos(th), rs * sin(th)};
+}
+
+/* Complex::tanh: (sinh 2a + i sin 2b) / (cosh 2a + cos 2b) */
+static oc64 c_tanh(oc64 z) {
+  double two_re = z.re + z.re, two_im = z.im + z.im;
+  double den = cosh(two_re) + cos(two_im);
+  return c_unscale((oc64){sinh(two_re), sin(two_im)}, den);
+}
+
+oc64 orc_cmul(oc64 a, oc64 b) { return c_mul(a, b); }
+oc64 orc_cdiv(oc64 a, oc64 b) { return c_div(a, b); }
+oc64 orc_csqrt(oc64 z) { return c_sqrt(z); }
+oc64 orc_ctanh(oc64 z) { return c_tanh(z); }
+
+/* gelu_complex (utils/activation.rs:195-212).  powi(3) is num-traits binary
+ * exponentiation: z * (z * z). */
+static oc64 gelu_c(oc64 z, int* nan_flag) {
+  const double sqrt_2_over_pi = sqrt(2.0 / M_PI);
+  oc64 z3 = c_mul(z, c_mul(z, z));
+  oc64 f = c_scale(c_add(z, c_mul((oc64){0.044715, 0.0}, z3)), sqrt_2_over_pi);
+  /* f64::max / f64::min return the non-NaN operand, like fmax / fmin */
+  oc64 cl = {fmin(fmax(f.re, -30.0), 30.0), fmin(fmax(f.im, -30.0), 30.0)};
+  oc64 t = c_tanh(cl);
+  if (isnan(t.re) || isnan(t.im)) *nan_flag = 1; /* reference panics here */
+  return c_mul(c_scale(z, 0.5), c_add((oc64){1.0, 0.0}, t));
+}
+
+oc64 orc_gelu(oc64 z, int* nan_flag) {
+  int f = 0;
+  oc64 r = gelu_c(z, &f);
+  if (nan_flag) *nan_flag = f;
+  return r;
+}
+
+/* ------------------------------------------------------------------------ */
+/* L1 kernels                                                               */
+/* ------------------------------------------------------------------------ */
+
+/* One output row of multiply_complex: acc[j] = sum_k a[k] * B[k][j], each sum a
+ * sequential complex fold from 0 in k order (zgemm_ alpha=1, beta=0;
+ * utils/matrix.rs:16-65). */
+static void zgemm_row(uint32_t n, uint32_t k, const oc64* a, const oc64* B, oc64* c) {
+  for (uint32_t j = 0; j < n; ++j) c[j] = (oc64){0.0, 0.0};
+  for (uint32_t kk = 0; kk < k; ++kk) {
+    const oc64 av = a[kk];
+    const oc64* b = B + (size_t)kk * n;
+    for (uint32_t j = 0; j < n; ++j) c[j] = c_add(c[j], c_mul(av, b[j]));
+  }
+}
+
+static void zgemm_serial(uint32_t m, uint32_t n, uint32_t k, const oc64* A, const oc64* B, oc64* C) {
+  for (uint32_t i = 0; i < m; ++i) zgemm_row(n, k, A + (size_t)i * k, B, C + (size_t)i * n);
+}
+
+void orc_zgemm(uint32_t m, uint32_t n, uint32_t k, const oc64* A, const oc64* B, oc64* C) {
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < (int64_t)m; ++i) zgemm_row(n, k, A + (size_t)i * k, B, C + (size_t)i * n);
+}
+
+/* NormalNormLayer::normalize (norm_layer.rs:64-82) */
+void orc_layernorm_row(const oc64* x, uint32_t d, double eps, const oc64* gamma, const oc64* beta, oc64* out) {
+  const double len = (double)d;
+  oc64 sum = {0.0, 0.0};
+  for (uint32_t i = 0; i < d; ++i) sum = c_add(sum, x[i]);
+  const oc64 mean = c_unscale(sum, len);
+  oc64 vs = {0.0, 0.0};
+  for (uint32_t i = 0; i < d; ++i) {
+    oc64 t = c_sub(x[i], mean);
+    vs = c_add(vs, c_mul(t, t)); /* powu(2) = t * t */
+  }
+  const oc64 var = c_unscale(vs, len);
+  const oc64 stddev = c_sqrt(c_add(var, (oc64){eps, 0.0}));
+  for (uint32_t i = 0; i < d; ++i) {
+    oc64 v = c_add(c_mul(c_div(c_sub(x[i], mean), stddev), gamma[i]), beta[i]);
+    out[i] = (oc64){v.re, 0.0};
+  }
+}
+
+/* softmax_row_real (utils/activation.rs:431-439) */
+void orc_softmax_row_real(const oc64* x, uint32_t n, double* out) {
+  double mx = -INFINITY;
+  for (uint32_t i = 0; i < n; ++i) mx = fmax(mx, x[i].re);
+  double sum = 0.0;
+  for (uint32_t i = 0; i < n; ++i) {
+    out[i] = exp(x[i].re - mx);
+    sum += out[i];
+  }
+  for (uint32_t i = 0; i < n; ++i) out[i] = out[i] / sum;
+}
+
+/* greedy_decoding (src/utils/sampling_methods.rs:5-18): Iterator::max_by with
+ * partial_cmp keeps the LAST of equal maxima; a NaN makes unwrap() panic. */
+int64_t orc_greedy_row(const double* row, uint32_t n) {
+  if (n == 0) return 0;
+  uint32_t best = 0;
+  if (isnan(row[0])) return -1;
+  for (uint32_t i = 1; i < n; ++i) {
+    if (isnan(row[i])) return -1;
+    if (row[i] >= row[best]) best = i;
+  }
+  return best;
+}
+
+/* apply_rotary_positional_encoding (positional_encoding_layer.rs:181-209) */
+void orc_rope_row(const oc64* x, uint32_t d, double base, uint64_t position, oc64* out) {
+  const uint32_t half = d / 2;
+  for (uint32_t i = 0; i < half; ++i) {
+    double theta = (double)position / pow(base * 1.0, 2.0 * (double)i / (double)d);
+    if (theta < -1.0) theta = -1.0; /* f64::clamp */
+    if (theta > 1.0) theta = 1.0;
+    double s = sin(theta), c = cos(theta);
+    oc64 e = x[2 * i], o = x[2 * i + 1];
+    out[2 * i] = (oc64){e.re * c - o.re * s, e.im * c - o.im * s};
+    out[2 * i + 1] = (oc64){e.re * s + o.re * c, e.im * s + o.im * c};
+  }
+}
+
+/* ------------------------------------------------------------------------ */
+/* counter generator (shared definition with the HIP path)                  */
+/* ------------------------------------------------------------------------ */
+
+static inline uint64_t mix64(uint64_t z) {
+  z += 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+uint64_t orc_draw(uint64_t seed, uint64_t stream, uint64_t index) {
+  return mix64(mix64(mix64(seed) ^ stream) ^ index);
+}
+
+/* uniform on [-lim, lim): (2u - 1) is exact, one rounding in the product */
+double orc_uniform(uint64_t seed, uint64_t stream, uint64_t index, double lim) {
+  double u = (double)(orc_draw(seed, stream, index) >> 11) * 0x1.0p-53;
+  return (2.0 * u - 1.0) * lim;
+}
+
+#define STREAM_PROMPT 0x7F00000000ull
+#define STREAM_NORMAL 0x7E00000000ull
+
+void orc_gen_prompts(uint64_t seed, uint32_t batch, uint32_t max_len, const uint32_t* lens, uint32_t vocab,
+                     uint32_t* ids) {
+  for (uint32_t b = 0; b < batch; ++b)
+    for (uint32_t s = 0; s < max_len; ++s) {
+      uint32_t id = 1; /* PAD */
+      if (!lens || s < lens[b])
+        id = (uint32_t)(((unsigned __int128)orc_draw(seed, STREAM_PROMPT + b, s) * vocab) >> 64);
+      ids[(size_t)b * max_len + s] = id;
+    }
+}
+
+/* Box-Muller; re and im of element p are the pair drawn from (2p, 2p+1) */
+void orc_gen_normal(uint64_t seed, uint64_t n, oc64* out) {
+  for (uint64_t p = 0; p < n; ++p) {
+    double u1 = (double)((orc_draw(seed, STREAM_NORMAL, 2 * p) >> 11) + 1) * 0x1.0p-53;
+    double u2 = (double)(orc_draw(seed, STREAM_NORMAL, 2 * p + 1) >> 11) * 0x1.0p-53;
+    double r = sqrt(-2.0 * log(u1));
+    out[p] = (oc64){r * cos(2.0 * M_PI * u2), r * sin(2.0 * M_PI * u2)};
+  }
+}
+
+/* ------------------------------------------------------------------------ */
+/* network                                                                  */
+/* ------------------------------------------------------------------------ */
+
+typedef struct {
+  int kind;
+  uint32_t d_in, d_out;
+  uint32_t vocab;
+  oc64* table;
+  double base;
+  double eps;
+  oc64 *gamma, *beta;
+  uint32_t heads, dh, max_ctx;
+  oc64 *wq, *wk, *wv, *bias_pos; /* [h][d][dh] x3, [h][max_ctx][max_ctx] */
+  oc64 *kc, *vc;                 /* [h][cache_B][max_ctx][dh] */
+  uint32_t* clen;                /* [cache_B] */
+  uint32_t cache_B;
+  int cache_valid;
+  uint32_t hidden;
+  oc64 *w1, *b1, *w2, *b2; /* Linear uses w1/b1 */
+  int mode;
+} orc_layer;
+
+struct orc_net {
+  orc_layer* layers;
+  int n, cap;
+};
+
+orc_net* orc_net_create(void) { return (orc_net*)calloc(1, sizeof(orc_net)); }
+
+static void free_cache(orc_layer* L) {
+  free(L->kc);
+  free(L->vc);
+  free(L->clen);
+  L->kc = L->vc = NULL;
+  L->clen = NULL;
+  L->cache_valid = 0;
+  L->cache_B = 0;
+}
+
+void orc_net_destroy(orc_net* net) {
+  if (!net) return;
+  for (int i = 0; i < net->n; ++i) {
+    orc_layer* L = &net->layers[i];
+    free(L->table);
+    free(L->gamma);
+    free(L->beta);
+    free(L->wq);
+    free(L->wk);
+    free(L->wv);
+    free(L->bias_pos);
+    free(L->w1);
+    free(L->b1);
+    free(L->w2);
+    free(L->b2);
+    free_cache(L);
+  }
+  free(net->layers);
+  free(net);
+}
+
+int orc_num_layers(const orc_net* net) { return net ? net->n : 0; }
+
+static orc_layer* push_layer(orc_net* net, int kind) {
+  if (net->n == net->cap) {
+    int cap = net->cap ? net->cap * 2 : 16;
+    orc_layer* l = (orc_layer*)realloc(net->layers, sizeof(orc_layer) * cap);
+    if (!l) return NULL;
+    net->layers = l;
+    net->cap = cap;
+  }
+  orc_layer* L = &net->layers[net->n++];
+  memset(L, 0, sizeof *L);
+  L->kind = kind;
+  return L;
+}
+
+static oc64* dup_or_zero(const oc64* src, size_t n) {
+  oc64* p = (oc64*)malloc(n * sizeof(oc64));
+  if (!p) return NULL;
+  if (src) memcpy(p, src, n * sizeof(oc64));
+  else memset(p, 0, n * sizeof(oc64));
+  return p;
+}
+
+static oc64* fill_const(const oc64* src, size_t n, oc64 v) {
+  oc64* p = (oc64*)malloc(n * sizeof(oc64));
+  if (!p) return NULL;
+  for (size_t i = 0; i < n; ++i) p[i] = src ? src[i] : v;
+  return p;
+}
+
+int orc_add_embedding(orc_net* net, uint32_t vocab, uint32_t dim, const oc64* table) {
+  if (!net || !vocab || !dim) return fail(ORC_ERR_ARG, "embedding: bad dims");
+  orc_layer* L = push_layer(net, ORC_EMBEDDING);
+  L->vocab = vocab;
+  L->d_in = L->d_out = dim;
+  L->table = dup_or_zero(table, (size_t)vocab * dim);
+  return L->table ? ORC_OK : fail(ORC_ERR_NOMEM, "embedding: out of memory");
+}
+
+int orc_add_positional_encoding(orc_net* net, uint32_t dim, double base) {
+  if (!net || !dim || (dim % 2)) return fail(ORC_ERR_ARG, "positional encoding: dim must be even");
+  orc_layer* L = push_layer(net, ORC_POSITIONAL_ENCODING);
+  L->d_in = L->d_out = dim;
+  L->base = base;
+  return ORC_OK;
+}
+
+int orc_add_norm(orc_net* net, uint32_t dim, double eps, const oc64* gamma, const oc64* beta) {
+  if (!net || !dim) return fail(ORC_ERR_ARG, "norm: bad dims");
+  orc_layer* L = push_layer(net, ORC_NORM);
+  L->d_in = L->d_out = dim;
+  L->eps = eps;
+  L->gamma = fill_const(gamma, dim, (oc64){1.0, 0.0});
+  L->beta = fill_const(beta, dim, (oc64){0.0, 0.0});
+  return (L->gamma && L->beta) ? ORC_OK : fail(ORC_ERR_NOMEM, "norm: out of memory");
+}
+
+int orc_add_self_attention(orc_net* net, uint32_t heads, uint32_t dim, uint32_t max_ctx, double eps,
+                           const oc64* wq, const oc64* wk, const oc64* wv, const oc64* bias_pos,
+                           const oc64* gamma, const oc64* beta) {
+  if (!net || !heads || !dim || dim % heads || !max_ctx) return fail(ORC_ERR_ARG, "self-attention: bad dims");
+  orc_layer* L = push_layer(net, ORC_SELF_ATTENTION);
+  L->heads = heads;
+  L->d_in = L->d_out = dim;
+  L->dh = dim / heads;
+  L->max_ctx = max_ctx;
+  L->eps = eps;
+  size_t wn = (size_t)heads * dim * L->dh;
+  L->wq = dup_or_zero(wq, wn);
+  L->wk = dup_or_zero(wk, wn);
+  L->wv = dup_or_zero(wv, wn);
+  L->bias_pos = dup_or_zero(bias_pos, (size_t)heads * max_ctx * max_ctx);
+  L->gamma = fill_const(gamma, dim, (oc64){1.0, 0.0});
+  L->beta = fill_const(beta, dim, (oc64){0.0, 0.0});
+  if (!L->wq || !L->wk || !L->wv || !L->bias_pos || !L->gamma || !L->beta)
+    return fail(ORC_ERR_NOMEM, "self-attention: out of memory");
+  return ORC_OK;
+}
+
+int orc_add_feed_forward(orc_net* net, uint32_t dim, uint32_t hidden, const oc64* w1, const oc64* b1,
+                         const oc64* w2, const oc64* b2) {
+  if (!net || !dim || !hidden) return fail(ORC_ERR_ARG, "feed-forward: bad dims");
+  orc_layer* L = push_layer(net, ORC_FEED_FORWARD);
+  L->d_in = L->d_out = dim;
+  L->hidden = hidden;
+  L->w1 = dup_or_zero(w1, (size_t)dim * hidden);
+  L->w2 = dup_or_zero(w2, (size_t)hidden * dim);
+  L->b1 = fill_const(b1, hidden, (oc64){1.0, 0.0});
+  L->b2 = fill_const(b2, dim, (oc64){1.0, 0.0});
+  if (!L->w1 || !L->w2 || !L->b1 || !L->b2) return fail(ORC_ERR_NOMEM, "feed-forward: out of memory");
+  return ORC_OK;
+}
+
+int orc_add_linear(orc_net* net, uint32_t in, uint32_t out, const oc64* w, const oc64* b) {
+  if (!net || !in || !out) return fail(ORC_ERR_ARG, "linear: bad dims");
+  orc_layer* L = push_layer(net, ORC_LINEAR);
+  L->d_in = in;
+  L->d_out = out;
+  L->w1 = dup_or_zero(w, (size_t)in * out);
+  L->b1 = fill_const(b, out, (oc64){1.0, 0.0});
+  if (!L->w1 || !L->b1) return fail(ORC_ERR_NOMEM, "linear: out of memory");
+  return ORC_OK;
+}
+
+int orc_add_softmax(orc_net* net, int operation_mode) {
+  if (!net) return fail(ORC_ERR_ARG, "softmax: null net");
+  orc_layer* L = push_layer(net, ORC_SOFTMAX);
+  L->mode = operation_mode;
+  return ORC_OK;
+}
+
+/* Xavier-uniform (utils/weights_initializer.rs:73-89) from the counter
+ * generator: re from draw 2e, im from draw 2e+1, limit sqrt(6/(rows+cols)). */
+static void xavier_fill(oc64* w, uint32_t rows, uint32_t cols, uint64_t seed, uint64_t stream) {
+  const double lim = sqrt(6.0 / (double)((uint64_t)rows + cols));
+  const int64_t n = (int64_t)rows * cols;
+#pragma omp parallel for schedule(static)
+  for (int64_t e = 0; e < n; ++e)
+    w[e] = (oc64){orc_uniform(seed, stream, 2 * (uint64_t)e, lim), orc_uniform(seed, stream, 2 * (uint64_t)e + 1, lim)};
+}
+
+static inline uint64_t stream_id(uint32_t layer, uint32_t slot) { return ((uint64_t)layer << 12) | slot; }
+
+int orc_init_seeded(orc_net* net, uint64_t seed) {
+  if (!net) return fail(ORC_ERR_ARG, "null net");
+  for (int li = 0; li < net->n; ++li) {
+    orc_layer* L = &net->layers[li];
+    switch (L->kind) {
+      case ORC_EMBEDDING: xavier_fill(L->table, L->vocab, L->d_out, seed, stream_id(li, 0)); break;
+      case ORC_NORM:
+        for (uint32_t i = 0; i < L->d_in; ++i) L->gamma[i] = (oc64){1.0, 0.0}, L->beta[i] = (oc64){0.0, 0.0};
+        break;
+      case ORC_SELF_ATTENTION: {
+        size_t wn = (size_t)L->d_in * L->dh, bn = (size_t)L->max_ctx * L->max_ctx;
+        for (uint32_t h = 0; h < L->heads; ++h) {
+          xavier_fill(L->wq + h * wn, L->d_in, L->dh, seed, stream_id(li, 1 + 4 * h));
+          xavier_fill(L->wk + h * wn, L->d_in, L->dh, seed, stream_id(li, 2 + 4 * h));
+          xavier_fill(L->wv + h * wn, L->d_in, L->dh, seed, stream_id(li, 3 + 4 * h));
+          xavier_fill(L->bias_pos + h * bn, L->max_ctx, L->max_ctx, seed, stream_id(li, 4 + 4 * h));
+        }
+        for (uint32_t i = 0; i < L->d_in; ++i) L->gamma[i] = (oc64){1.0, 0.0}, L->beta[i] = (oc64){0.0, 0.0};
+        break;
+      }
+      case ORC_FEED_FORWARD:
+        xavier_fill(L->w1, L->d_in, L->hidden, seed, stream_id(li, 1));
+        xavier_fill(L->w2, L->hidden, L->d_out, seed, stream_id(li, 2));
+        for (uint32_t i = 0; i < L->hidden; ++i) L->b1[i] = (oc64){1.0, 0.0};
+        for (uint32_t i = 0; i < L->d_out; ++i) L->b2[i] = (oc64){1.0, 0.0};
+        break;
+      case ORC_LINEAR:
+        xavier_fill(L->w1, L->d_in, L->d_out, seed, stream_id(li, 1));
+        for (uint32_t i = 0; i < L->d_out; ++i) L->b1[i] = (oc64){1.0, 0.0};
+        break;
+      default: break;
+    }
+  }
+  return ORC_OK;
+}
+
+int orc_get_tensor(const orc_net* net, uint32_t layer, uint32_t slot, oc64* out, uint64_t n) {
+  if (!net || layer >= (uint32_t)net->n) return fail(ORC_ERR_ARG, "bad layer index");
+  const orc_layer* L = &net->layers[layer];
+  const oc64* src = NULL;
+  uint64_t len = 0;
+  switch (slot) {
+    case 0:
+      if (L->kind == ORC_EMBEDDING) src = L->table, len = (uint64_t)L->vocab * L->d_out;
+      else if (L->kind == ORC_SELF_ATTENTION) src = L->wq, len = (uint64_t)L->heads * L->d_in * L->dh;
+      else if (L->kind == ORC_FEED_FORWARD) src = L->w1, len = (uint64_t)L->d_in * L->hidden;
+      else if (L->kind == ORC_LINEAR) src = L->w1, len = (uint64_t)L->d_in * L->d_out;
+      break;
+    case 1:
+      if (L->kind == ORC_SELF_ATTENTION) src = L->wk, len = (uint64_t)L->heads * L->d_in * L->dh;
+      else if (L->kind == ORC_FEED_FORWARD) src = L->w2, len = (uint64_t)L->hidden * L->d_out;
+      break;
+    case 2:
+      if (L->kind == ORC_SELF_ATTENTION) src = L->wv, len = (uint64_t)L->heads * L->d_in * L->dh;
+      break;
+    case 3:
+      if (L->kind == ORC_SELF_ATTENTION) src = L->bias_pos, len = (uint64_t)L->heads * L->max_ctx * L->max_ctx;
+      break;
+    case 4:
+      if (L->kind == ORC_FEED_FORWARD) src = L->b1, len = L->hidden;
+      else if (L->kind == ORC_LINEAR) src = L->b1, len = L->d_out;
+      break;
+    case 5:
+      if (L->kind == ORC_FEED_FORWARD) src = L->b2, len = L->d_out;
+      break;
+    case 6:
+      if (L->gamma) src = L->gamma, len = L->d_in;
+      break;
+    case 7:
+      if (L->beta) src = L->beta, len = L->d_in;
+      break;
+  }
+  if (!src) return fail(ORC_ERR_ARG, "layer %u has no tensor in slot %u", layer, slot);
+  if (n != len) return fail(ORC_ERR_ARG, "tensor size %llu != %llu", (unsigned long long)n, (unsigned long long)len);
+  memcpy(out, src, len * sizeof(oc64));
+  return ORC_OK;
+}
+
+int orc_reset(orc_net* net) {
+  if (!net) return fail(ORC_ERR_ARG, "null net");
+  for (int i = 0; i < net->n; ++i)
+    if (net->layers[i].kind == ORC_SELF_ATTENTION) free_cache(&net->layers[i]);
+  return ORC_OK;
+}
+
+/* ------------------------------------------------------------------------ */
+/* layer forwards                                                           */
+/* ------------------------------------------------------------------------ */
+
+/* EmbeddingLayer::forward + apply_padding_to_batch (embedding_layer.rs:112-211):
+ * right-pad with PAD=1, mask 1/0; id 1 always yields the zero vector. */
+static int embedding_forward(const orc_layer* L, const uint32_t* ids, const uint32_t* lens, uint32_t B, uint32_t S,
+                             oc64* out, uint32_t* mask) {
+  const uint32_t d = L->d_out;
+  for (uint32_t b = 0; b < B; ++b)
+    for (uint32_t s = 0; s < S; ++s) {
+      uint32_t id = s < lens[b] ? ids[(size_t)b * S + s] : 1;
+      mask[(size_t)b * S + s] = s < lens[b] ? 1 : 0;
+      oc64* o = out + ((size_t)b * S + s) * d;
+      if (id == 1) {
+        for (uint32_t i = 0; i < d; ++i) o[i] = (oc64){0.0, 0.0};
+      } else {
+        if (id >= L->vocab) return fail(ORC_ERR_ARG, "No token embedding found: %u", id);
+        memcpy(o, L->table + (size_t)id * d, d * sizeof(oc64));
+      }
+    }
+  return ORC_OK;
+}
+
+/* PositionalEncodingLayer::forward (positional_encoding_layer.rs:35-99):
+ * position = row index, or time_step when forward_only and time_step > 0. */
+static void posenc_forward(const orc_layer* L, oc64* x, uint32_t B, uint32_t S, const uint32_t* ts, int forward_only) {
+  const uint32_t d = L->d_in;
+  oc64* tmp = (oc64*)malloc(d * sizeof(oc64));
+  for (uint32_t b = 0; b < B; ++b)
+    for (uint32_t s = 0; s < S; ++s) {
+      uint64_t pos = s;
+      uint32_t t = ts ? ts[b] : 0;
+      if (forward_only && t > 0) pos = t;
+      oc64* row = x + ((size_t)b * S + s) * d;
+      orc_rope_row(row, d, L->base, pos, tmp);
+      memcpy(row, tmp, d * sizeof(oc64));
+    }
+  free(tmp);
+}
+
+/* NormalNormLayer::forward (norm_layer.rs:84-130).  With `before`, the input
+ * first becomes Re(x + before) + 0i (add_matrix_3d_c, utils/matrix.rs:600-613). */
+static void norm_forward(double eps, const oc64* gamma, const oc64* beta, const oc64* x, const oc64* before,
+                         uint64_t rows, uint32_t d, oc64* out) {
+#pragma omp parallel
+  {
+    oc64* tmp = (oc64*)malloc(d * sizeof(oc64));
+#pragma omp for schedule(static)
+    for (int64_t r = 0; r < (int64_t)rows; ++r) {
+      const oc64* xr = x + (size_t)r * d;
+      if (before) {
+        const oc64* br = before + (size_t)r * d;
+        for (uint32_t i = 0; i < d; ++i) tmp[i] = (oc64){xr[i].re + br[i].re, 0.0};
+        xr = tmp;
+      }
+      orc_layernorm_row(xr, d, eps, gamma, beta, out + (size_t)r * d);
+    }
+    free(tmp);
+  }
+}
+
+/* MaskedAttentionHead::forward for all heads + SelfAttentionLayer::forward
+ * (masked_attention_head.rs:122-220, self_attention_layer.rs:55-133). */
+static int self_attention_forward(orc_layer* L, const oc64* x, const uint32_t* mask, const uint32_t* lens,
+                                  uint32_t B, uint32_t S, int forward_only, oc64* out) {
+  const uint32_t d = L->d_in, H = L->heads, dh = L->dh, mc = L->max_ctx;
+  const int decode = forward_only && L->cache_valid;
+  if (decode && B != L->cache_B) return fail(ORC_ERR_STATE, "cached batch %u != %u; reset first", L->cache_B, B);
+  if (S > mc) return fail(ORC_ERR_ARG, "sequence %u exceeds max context %u", S, mc);
+  if (decode)
+    for (uint32_t b = 0; b < B; ++b)
+      if (L->clen[b] + 1 > mc) return fail(ORC_ERR_ARG, "context %u exceeds max context %u", L->clen[b] + 1, mc);
+  if (forward_only && !L->cache_valid) {
+    free_cache(L);
+    size_t cn = (size_t)H * B * mc * dh;
+    L->kc = (oc64*)calloc(cn, sizeof(oc64));
+    L->vc = (oc64*)calloc(cn, sizeof(oc64));
+    L->clen = (uint32_t*)calloc(B, sizeof(uint32_t));
+    if (!L->kc || !L->vc || !L->clen) return fail(ORC_ERR_NOMEM, "kv cache: out of memory");
+    L->cache_B = B;
+  }
+  const double scale = 1.0 / (1e-8 + sqrt((double)dh)); /* scale_attention_scores :453-465 */
+  const size_t wn = (size_t)d * dh;
+  const uint32_t T_fresh = S;
+  oc64* concat = (oc64*)malloc((size_t)B * S * d * sizeof(oc64));
+  oc64* knew = NULL;
+  oc64* vnew = NULL;
+  if (!decode) {
+    knew = (oc64*)malloc((size_t)H * B * S * dh * sizeof(oc64));
+    vnew = (oc64*)malloc((size_t)H * B * S * dh * sizeof(oc64));
+  }
+  /* K/V: all rows without a cache (:135-139), else only the last token (:140-156) */
+#pragma omp parallel for collapse(2) schedule(dynamic)
+  for (int64_t h = 0; h < (int64_t)H; ++h)
+    for (int64_t b = 0; b < (int64_t)B; ++b) {
+      const oc64* xb = x + (size_t)b * S * d;
+      if (!decode) {
+        zgemm_serial(S, dh, d, xb, L->wk + h * wn, knew + ((size_t)h * B + b) * S * dh);
+        zgemm_serial(S, dh, d, xb, L->wv + h * wn, vnew + ((size_t)h * B + b) * S * dh);
+      } else {
+        const oc64* last = xb + (size_t)(lens[b] - 1) * d;
+        size_t off = (((size_t)h * B + b) * mc + L->clen[b]) * dh;
+        zgemm_row(dh, d, last, L->wk + h * wn, L->kc + off);
+        zgemm_row(dh, d, last, L->wv + h * wn, L->vc + off);
+      }
+    }
+  if (decode)
+    for (uint32_t b = 0; b < B; ++b) L->clen[b] += 1;
+  else if (forward_only) {
+    /* the cache keeps each sequence's own lens[b] rows (:159-163) */
+    for (uint32_t h = 0; h < H; ++h)
+      for (uint32_t b = 0; b < B; ++b) {
+        size_t src = ((size_t)h * B + b) * S * dh, dst = ((size_t)h * B + b) * mc * dh;
+        memcpy(L->kc + dst, knew + src, (size_t)lens[b] * dh * sizeof(oc64));
+        memcpy(L->vc + dst, vnew + src, (size_t)lens[b] * dh * sizeof(oc64));
+      }
+    for (uint32_t b = 0; b < B; ++b) L->clen[b] = lens[b];
+    L->cache_valid = 1;
+  }
+#pragma omp parallel
+  {
+    oc64* q = (oc64*)malloc((size_t)S * dh * sizeof(oc64));
+    double* sc = (double*)malloc((size_t)mc * sizeof(double));
+#pragma omp for collapse(2) schedule(dynamic)
+    for (int64_t h = 0; h < (int64_t)H; ++h)
+      for (int64_t b = 0; b < (int64_t)B; ++b) {
+        const oc64* xb = x + (size_t)b * S * d;
+        zgemm_serial(S, dh, d, xb, L->wq + h * wn, q); /* :132 */
+        const oc64 *K, *V;
+        uint32_t T;
+        if (decode) {
+          K = L->kc + ((size_t)h * B + b) * mc * dh;
+          V = L->vc + ((size_t)h * B + b) * mc * dh;
+          T = L->clen[b];
+        } else {
+          K = knew + ((size_t)h * B + b) * S * dh;
+          V = vnew + ((size_t)h * B + b) * S * dh;
+          T = T_fresh;
+        }
+        const oc64* bp = L->bias_pos + (size_t)h * mc * mc;
+        for (uint32_t r = 0; r < S; ++r) {
+          oc64* o = concat + ((size_t)b * S + r) * d + (size_t)h * dh;
+          if (mask[(size_t)b * S + r] == 0) { /* softmax_complex_padding_real :369-388 */
+            for (uint32_t e = 0; e < dh; ++e) o[e] = (oc64){0.0, 0.0};
+            continue;
+          }
+          const oc64* qr = q + (size_t)r * dh;
+          /* scores (:190-196): Re(q.k^T) * scale + bias_pos[r][c]; the causal
+           * mask of S x S rows is applied modulo its size (:494-503) */
+          for (uint32_t c = 0; c < T; ++c) {
+            if ((c % S) > r) {
+              sc[c] = -1e12;
+              continue;
+            }
+            const oc64* kr = K + (size_t)c * dh;
+            double acc = 0.0;
+            for (uint32_t e = 0; e < dh; ++e) acc = acc + (qr[e].re * kr[e].re - qr[e].im * kr[e].im);
+            sc[c] = acc * scale + bp[(size_t)r * mc + c].re;
+          }
+          double mx = -INFINITY;
+          for (uint32_t c = 0; c < T; ++c) mx = fmax(mx, sc[c]);
+          double sum = 0.0;
+          for (uint32_t c = 0; c < T; ++c) {
+            sc[c] = exp(sc[c] - mx);
+            sum += sc[c];
+          }
+          for (uint32_t c = 0; c < T; ++c) sc[c] = sc[c] / sum;
+          /* multiply_f64_complex (utils/matrix.rs:356-380) */
+          for (uint32_t e = 0; e < dh; ++e) {
+            oc64 acc = {0.0, 0.0};
+            for (uint32_t c = 0; c < T; ++c) acc = c_add(acc, c_scale(V[(size_t)c * dh + e], sc[c]));
+            o[e] = acc;
+          }
+        }
+      }
+    free(q);
+    free(sc);
+  }
+  /* residual + LayerNorm (:101-124) */
+  norm_forward(L->eps, L->gamma, L->beta, concat, x, (uint64_t)B * S, d, out);
+  free(concat);
+  free(knew);
+  free(vnew);
+  return ORC_OK;
+}
+
+static int check_finite(const oc64* y, uint64_t n, const char* what) {
+  for (uint64_t i = 0; i < n; ++i)
+    if (!isfinite(y[i].re) || !isfinite(y[i].im)) return fail(ORC_ERR_NAN, "%s: The value is Not Valid", what);
+  return ORC_OK;
+}
+
+/* FeedForwardLayer::forward (feedforward_layer.rs:56-138): Dense(GELU) with
+ * pad rows zeroed (layer.rs:132-166, activation.rs:268-284), then Linear. */
+static int ffn_forward(const orc_layer* L, const oc64* x, const uint32_t* mask, uint64_t rows, oc64* out) {
+  const uint32_t d = L->d_in, F = L->hidden;
+  int nan_flag = 0;
+#pragma omp parallel
+  {
+    oc64* h = (oc64*)malloc((size_t)F * sizeof(oc64));
+    int local_nan = 0;
+#pragma omp for schedule(static)
+    for (int64_t r = 0; r < (int64_t)rows; ++r) {
+      zgemm_row(F, d, x + (size_t)r * d, L->w1, h);
+      for (uint32_t j = 0; j < F; ++j) {
+        oc64 z = c_add(h[j], L->b1[j]); /* add_vector */
+        h[j] = (!mask || mask[r]) ? gelu_c(z, &local_nan) : (oc64){0.0, 0.0};
+      }
+      oc64* o = out + (size_t)r * d;
+      zgemm_row(d, F, h, L->w2, o);
+      for (uint32_t j = 0; j < d; ++j) o[j] = c_add(o[j], L->b2[j]);
+    }
+    if (local_nan) {
+#pragma omp atomic write
+      nan_flag = 1;
+    }
+    free(h);
+  }
+  if (nan_flag) return fail(ORC_ERR_NAN, "NaN detected in tanh(f(z))");
+  return check_finite(out, rows * d, "output ffn dense"); /* transformer_network.rs:408 */
+}
+
+/* LinearLayer::forward (linear_layer.rs:55-75) */
+static void linear_forward(const orc_layer* L, const oc64* x, uint64_t rows, oc64* out) {
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < (int64_t)rows; ++r) {
+    oc64* o = out + (size_t)r * L->d_out;
+    zgemm_row(L->d_out, L->d_in, x + (size_t)r * L->d_in, L->w1, o);
+    for (uint32_t j = 0; j < L->d_out; ++j) o[j] = c_add(o[j], L->b1[j]);
+  }
+}
+
+/* Runs one hidden-state layer in place-or-swap. */
+static int run_layer(orc_layer* L, oc64** cur, oc64** nxt, uint64_t* cap, const uint32_t* mask, const uint32_t* lens,
+                     uint32_t B, uint32_t S, const uint32_t* ts, int forward_only) {
+  const uint64_t rows = (uint64_t)B * S;
+  if (L->kind == ORC_POSITIONAL_ENCODING) {
+    posenc_forward(L, *cur, B, S, ts, forward_only);
+    return ORC_OK;
+  }
+  uint64_t need = rows * (L->d_out > L->d_in ? L->d_out : L->d_in);
+  if (need > *cap) {
+    free(*nxt);
+    *nxt = (oc64*)malloc(need * sizeof(oc64));
+    if (!*nxt) return fail(ORC_ERR_NOMEM, "activation: out of memory");
+    *cap = need;
+  }
+  int rc = ORC_OK;
+  switch (L->kind) {
+    case ORC_NORM: norm_forward(L->eps, L->gamma, L->beta, *cur, NULL, rows, L->d_in, *nxt); break;
+    case ORC_SELF_ATTENTION: rc = self_attention_forward(L, *cur, mask, lens, B, S, forward_only, *nxt); break;
+    case ORC_FEED_FORWARD: rc = ffn_forward(L, *cur, mask, rows, *nxt); break;
+    case ORC_LINEAR: linear_forward(L, *cur, rows, *nxt); break;
+    default: return fail(ORC_ERR_ARG, "layer kind %d is not a hidden-state layer", L->kind);
+  }
+  oc64* t = *cur;
+  *cur = *nxt;
+  *nxt = t;
+  /* both buffers must hold `need` after the swap */
+  return rc;
+}
+
+static int check_lens(const uint32_t* lens, uint32_t B, uint32_t S) {
+  if (!B || !S) return fail(ORC_ERR_ARG, "batch_ids is empty");
+  for (uint32_t b = 0; b < B; ++b)
+    if (lens[b] == 0 || lens[b] > S) return fail(ORC_ERR_ARG, "lens[%u]=%u outside [1,%u]", b, lens[b], S);
+  return ORC_OK;
+}
+
+int orc_predict(orc_net* net, const uint32_t* ids, const uint32_t* lens, uint32_t B, uint32_t S,
+                const uint32_t* time_steps, int forward_only, int out_rows, double* out, uint32_t* out_mask) {
+  if (!net || !ids || !lens || !out) return fail(ORC_ERR_ARG, "null argument");
+  int rc = check_lens(lens, B, S);
+  if (rc) return rc;
+  if (net->n < 2 || net->layers[0].kind != ORC_EMBEDDING || net->layers[net->n - 1].kind != ORC_SOFTMAX)
+    return fail(ORC_ERR_STATE, "network must start with Embedding and end with Softmax");
+  const uint64_t rows = (uint64_t)B * S;
+  uint32_t dmax = 0;
+  for (int i = 0; i < net->n; ++i) {
+    if (net->layers[i].d_in > dmax) dmax = net->layers[i].d_in;
+    if (net->layers[i].d_out > dmax) dmax = net->layers[i].d_out;
+  }
+  uint64_t cap = rows * dmax;
+  oc64* cur = (oc64*)malloc(cap * sizeof(oc64));
+  oc64* nxt = (oc64*)malloc(cap * sizeof(oc64));
+  uint32_t* mask = (uint32_t*)malloc(rows * sizeof(uint32_t));
+  if (!cur || !nxt || !mask) {
+    free(cur), free(nxt), free(mask);
+    return fail(ORC_ERR_NOMEM, "activation: out of memory");
+  }
+  rc = embedding_forward(&net->layers[0], ids, lens, B, S, cur, mask);
+  int gathered = 0; /* rows reduced to one per sequence before the vocab Linear */
+  for (int li = 1; rc == ORC_OK && li < net->n - 1; ++li) {
+    orc_layer* L = &net->layers[li];
+    if (out_rows == 1 && forward_only && L->kind == ORC_LINEAR && li == net->n - 2) {
+      for (uint32_t b = 0; b < B; ++b)
+        memmove(cur + (size_t)b * L->d_in, cur + ((size_t)b * S + lens[b] - 1) * L->d_in, L->d_in * sizeof(oc64));
+      uint64_t need = (uint64_t)B * L->d_out;
+      if (need > cap) {
+        free(nxt);
+        nxt = (oc64*)malloc(need * sizeof(oc64));
+        oc64* c2 = (oc64*)realloc(cur, need * sizeof(oc64));
+        if (!nxt || !c2) {
+          rc = fail(ORC_ERR_NOMEM, "logits: out of memory");
+          break;
+        }
+        cur = c2;
+        cap = need;
+      }
+      linear_forward(L, cur, B, nxt);
+      oc64* t = cur;
+      cur = nxt;
+      nxt = t;
+      gathered = 1;
+      continue;
+    }
+    if (L->kind == ORC_EMBEDDING || L->kind == ORC_SOFTMAX) {
+      rc = fail(ORC_ERR_STATE, "unexpected layer kind %d inside the stack", L->kind);
+      break;
+    }
+    rc = run_layer(L, &cur, &nxt, &cap, mask, lens, B, S, time_steps, forward_only);
+  }
+  if (rc == ORC_OK) {
+    const orc_layer* SM = &net->layers[net->n - 1];
+    uint32_t V = net->layers[net->n - 2].d_out;
+    uint32_t out_S = gathered ? 1 : S;
+    /* Softmax arm of predict (:472-489) */
+    const uint32_t n_out = out_rows == 1 ? 1 : S;
+    for (uint32_t b = 0; b < B; ++b) {
+      for (uint32_t k = 0; k < n_out; ++k) {
+        const uint32_t src_s = out_rows == 1 ? lens[b] - 1 : k; /* row in the padded batch */
+        const oc64* row = gathered ? cur + (size_t)b * V : cur + ((size_t)b * out_S + src_s) * V;
+        double* o = out + ((size_t)b * n_out + k) * V;
+        if (forward_only) { /* convert_c_to_f64_3d (src/utils/data_converter.rs:244-256) */
+          for (uint32_t v = 0; v < V; ++v) o[v] = row[v].re;
+        } else if (SM->mode == ORC_TRAINING) { /* softmax_complex_padding_real */
+          if (mask[(size_t)b * S + src_s] == 0)
+            for (uint32_t v = 0; v < V; ++v) o[v] = 0.0;
+          else
+            orc_softmax_row_real(row, V, o);
+        } else { /* softmax_last_row (activation.rs:409-419): only row S-1 */
+          if (src_s == S - 1)
+            orc_softmax_row_real(row, V, o);
+          else
+            for (uint32_t v = 0; v < V; ++v) o[v] = 0.0;
+        }
+      }
+    }
+    if (out_mask) memcpy(out_mask, mask, rows * sizeof(uint32_t));
+  }
+  free(cur);
+  free(nxt);
+  free(mask);
+  return rc;
+}
+
+int orc_forward_layers(orc_net* net, uint32_t first, uint32_t last, const oc64* in, const uint32_t* mask_in,
+                       uint32_t B, uint32_t S, const uint32_t* time_steps, int forward_only, oc64* out) {
+  if (!net || !in || !out || first >= last || last > (uint32_t)net->n) return fail(ORC_ERR_ARG, "bad layer range");
+  if (!B || !S) return fail(ORC_ERR_ARG, "empty batch");
+  const uint64_t rows = (uint64_t)B * S;
+  uint32_t dmax = 0;
+  for (uint32_t i = first; i < last; ++i) {
+    if (net->layers[i].d_in > dmax) dmax = net->layers[i].d_in;
+    if (net->layers[i].d_out > dmax) dmax = net->layers[i].d_out;
+  }
+  uint64_t cap = rows * dmax;
+  oc64* cur = (oc64*)malloc(cap * sizeof(oc64));
+  oc64* nxt = (oc64*)malloc(cap * sizeof(oc64));
+  uint32_t* mask = (uint32_t*)malloc(rows * sizeof(uint32_t));
+  uint32_t* lens = (uint32_t*)malloc(B * sizeof(uint32_t));
+  int rc = ORC_OK;
+  if (!cur || !nxt || !mask || !lens) rc = fail(ORC_ERR_NOMEM, "activation: out of memory");
+  if (rc == ORC_OK) {
+    memcpy(cur, in, rows * net->layers[first].d_in * sizeof(oc64));
+    for (uint32_t b = 0; b < B; ++b) {
+      lens[b] = 0;
+      for (uint32_t s = 0; s < S; ++s) {
+        mask[(size_t)b * S + s] = mask_in ? mask_in[(size_t)b * S + s] : 1;
+        lens[b] += mask[(size_t)b * S + s] ? 1 : 0;
+      }
+      if (!lens[b]) lens[b] = 1;
+    }
+  }
+  for (uint32_t li = first; rc == ORC_OK && li < last; ++li)
+    rc = run_layer(&net->layers[li], &cur, &nxt, &cap, mask, lens, B, S, time_steps, forward_only);
+  if (rc == ORC_OK) memcpy(out, cur, rows * net->layers[last - 1].d_out * sizeof(oc64));
+  free(cur);
+  free(nxt);
+  free(mask);
+  free(lens);
+  return rc;
+}
+
+int orc_generate(orc_net* net, const uint32_t* prompt, const uint32_t* lens, uint32_t B, uint32_t S,
+                 uint32_t n_new, uint32_t* out_ids, double* out_logits) {
+  if (!net || !prompt || !lens || !out_ids) return fail(ORC_ERR_ARG, "null argument");
+  int rc = check_lens(lens, B, S);
+  if (rc) return rc;
+  if (n_new == 0) return ORC_OK;
+  if (net->n < 2) return fail(ORC_ERR_STATE, "empty network");
+  const uint32_t V = net->layers[net->n - 2].d_out;
+  double* logits = (double*)malloc((size_t)B * V * sizeof(double));
+  uint32_t* ids = (uint32_t*)malloc(B * sizeof(uint32_t));
+  uint32_t* ones = (uint32_t*)malloc(B * sizeof(uint32_t));
+  uint32_t* ts = (uint32_t*)malloc(B * sizeof(uint32_t));
+  if (!logits || !ids || !ones || !ts) rc = fail(ORC_ERR_NOMEM, "generate: out of memory");
+  if (rc == ORC_OK) rc = orc_reset(net); /* predict_by_text reloads the model per request (:638-652) */
+  for (uint32_t t = 0; rc == ORC_OK && t < n_new; ++t) {
+    if (t == 0) {
+      rc = orc_predict(net, prompt, lens, B, S, NULL, 1, 1, logits, NULL);
+    } else {
+      for (uint32_t b = 0; b < B; ++b) {
+        ones[b] = 1;
+        ts[b] = lens[b] + t - 1; /* time_step of the fed token (:300-304) */
+      }
+      rc = orc_predict(net, ids, ones, B, 1, ts, 1, 1, logits, NULL);
+    }
+    if (rc) break;
+    for (uint32_t b = 0; b < B; ++b) {
+      int64_t id = orc_greedy_row(logits + (size_t)b * V, V);
+      if (id < 0) {
+        rc = fail(ORC_ERR_NAN, "greedy_decoding: NaN in logits");
+        break;
+      }
+      ids[b] = (uint32_t)id;
+      out_ids[(size_t)b * n_new + t] = (uint32_t)id;
+    }
+    if (out_logits) memcpy(out_logits + (size_t)t * B * V, logits, (size_t)B * V * sizeof(double));
+  }
+  free(logits);
+  free(ids);
+  free(ones);
+  free(ts);
+  return rc;
+}

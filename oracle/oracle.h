@@ -1,0 +1,111 @@
+/*
+ * oracle.h — CPU restatement of the rustCrates transformer token loop.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker for the HIP path in
+ * rustcrates_amd/: only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load it.  The product path never links or calls it.
+ *
+ * Every function restates the Rust source it cites (paths relative to the
+ * reference crate root, src/neural_networks/...).  Arithmetic follows the Rust
+ * expression order exactly and is compiled with -ffp-contract=off (Rust never
+ * fuses a*b+c), against glibc libm (what Rust's f64 methods call on Linux).
+ *
+ * Complex<f64> is num-complex 0.4.6: #[repr(C)] {re, im}, 16 bytes.
+ */
+#ifndef RUSTCRATES_ORACLE_H
+#define RUSTCRATES_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct { double re, im; } oc64;
+
+/* Layer kinds, in the order of LayerEnum (network_components/layer.rs:75-88)
+ * restricted to the variants on the token-loop path. */
+enum {
+  ORC_EMBEDDING = 0,
+  ORC_POSITIONAL_ENCODING = 1,
+  ORC_NORM = 2,
+  ORC_SELF_ATTENTION = 3,
+  ORC_FEED_FORWARD = 4,
+  ORC_LINEAR = 5,
+  ORC_SOFTMAX = 6
+};
+
+/* OperationMode (network_types/neural_network_generic.rs:17-20) */
+enum { ORC_TRAINING = 0, ORC_PRODUCTION = 1 };
+
+/* status codes (match include/mitok.h) */
+enum { ORC_OK = 0, ORC_ERR_ARG = 1, ORC_ERR_STATE = 3, ORC_ERR_NAN = 4, ORC_ERR_NOMEM = 5 };
+
+typedef struct orc_net orc_net;
+
+const char* orc_last_error(void);
+
+/* ---- num-complex 0.4.6 scalar ops (exported for pinning tests) ---- */
+oc64 orc_cmul(oc64 a, oc64 b);
+oc64 orc_cdiv(oc64 a, oc64 b);
+oc64 orc_csqrt(oc64 z);
+oc64 orc_ctanh(oc64 z);
+oc64 orc_gelu(oc64 z, int* nan_flag);
+
+/* ---- L1 numeric kernels ---- */
+/* multiply_complex (utils/matrix.rs:16-65): C[m][n] = A[m][k] * B[k][n], row-major */
+void orc_zgemm(uint32_t m, uint32_t n, uint32_t k, const oc64* A, const oc64* B, oc64* C);
+/* NormalNormLayer::normalize (norm_layer.rs:64-82) on one row; out is Re + 0i */
+void orc_layernorm_row(const oc64* x, uint32_t d, double eps, const oc64* gamma, const oc64* beta, oc64* out);
+/* softmax_row_real (utils/activation.rs:431-439) */
+void orc_softmax_row_real(const oc64* x, uint32_t n, double* out);
+/* greedy_decoding row argmax (utils/sampling_methods.rs:5-18); -1 on NaN */
+int64_t orc_greedy_row(const double* row, uint32_t n);
+/* apply_rotary_positional_encoding (positional_encoding_layer.rs:181-209) */
+void orc_rope_row(const oc64* x, uint32_t d, double base, uint64_t position, oc64* out);
+
+/* ---- seeded synthetic data (counter generator shared with the HIP path) ---- */
+uint64_t orc_draw(uint64_t seed, uint64_t stream, uint64_t index);
+double orc_uniform(uint64_t seed, uint64_t stream, uint64_t index, double lim);
+void orc_gen_prompts(uint64_t seed, uint32_t batch, uint32_t max_len, const uint32_t* lens, uint32_t vocab, uint32_t* ids);
+void orc_gen_normal(uint64_t seed, uint64_t n, oc64* out);
+
+/* ---- network (NeuralNetwork, network_types/neural_network_generic.rs:23-31) ---- */
+orc_net* orc_net_create(void);
+void orc_net_destroy(orc_net* net);
+int orc_num_layers(const orc_net* net);
+/* Tensors may be NULL and filled later by orc_init_seeded. Layouts are the
+ * reference's: row-major [in][out], per-head [h][d][dh], bias_pos [h][max_ctx][max_ctx]. */
+int orc_add_embedding(orc_net* net, uint32_t vocab, uint32_t dim, const oc64* table);
+int orc_add_positional_encoding(orc_net* net, uint32_t dim, double base);
+int orc_add_norm(orc_net* net, uint32_t dim, double eps, const oc64* gamma, const oc64* beta);
+int orc_add_self_attention(orc_net* net, uint32_t heads, uint32_t dim, uint32_t max_ctx, double eps,
+                           const oc64* wq, const oc64* wk, const oc64* wv, const oc64* bias_pos,
+                           const oc64* gamma, const oc64* beta);
+int orc_add_feed_forward(orc_net* net, uint32_t dim, uint32_t hidden, const oc64* w1, const oc64* b1,
+                         const oc64* w2, const oc64* b2);
+int orc_add_linear(orc_net* net, uint32_t in, uint32_t out, const oc64* w, const oc64* b);
+int orc_add_softmax(orc_net* net, int operation_mode);
+int orc_init_seeded(orc_net* net, uint64_t seed);
+/* reads back a weight tensor (slot: 0 table/w/w1/wq, 1 wk/w2, 2 wv, 3 bias_pos, 4 b/b1, 5 b2, 6 gamma, 7 beta) */
+int orc_get_tensor(const orc_net* net, uint32_t layer, uint32_t slot, oc64* out, uint64_t n);
+int orc_reset(orc_net* net);
+void orc_set_threads(int n);
+
+/* predict (transformer_network.rs:315-504).  ids [B][S] right-padded (entries
+ * at or beyond lens[b] are replaced by PAD=1).  time_steps [B] or NULL.
+ * out_rows 0: out [B][S][V];  out_rows 1: out [B][V] (row lens[b]-1). */
+int orc_predict(orc_net* net, const uint32_t* ids, const uint32_t* lens, uint32_t B, uint32_t S,
+                const uint32_t* time_steps, int forward_only, int out_rows, double* out, uint32_t* out_mask);
+/* Layers [first, last) over hidden states in [B][S][d_in] -> out [B][S][d_out]. */
+int orc_forward_layers(orc_net* net, uint32_t first, uint32_t last, const oc64* in, const uint32_t* mask,
+                       uint32_t B, uint32_t S, const uint32_t* time_steps, int forward_only, oc64* out);
+/* Greedy token loop (predict_token_by_token, transformer_network.rs:165-313) on ids:
+ * out_ids [B][n_new]; out_logits [n_new][B][V] Re-logits of the row each token came from (or NULL). */
+int orc_generate(orc_net* net, const uint32_t* prompt, const uint32_t* lens, uint32_t B, uint32_t S,
+                 uint32_t n_new, uint32_t* out_ids, double* out_logits);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,226 @@
+"""rustcrates_amd — MI355X token loop for the rustCrates complex-valued transformer.
+
+Python handle over libmitok.so (include/mitok.h).  The methods mirror the
+reference's model API (src/neural_networks/...):
+
+    Network.add_embedding / add_norm / add_self_attention / ...   LayerEnum variants (layer.rs:75-88)
+    Network.predict                                               predict (transformer_network.rs:315-504)
+    Network.forward_layers                                        Layer::forward chains
+    Network.generate                                              predict_token_by_token on ids (:165-313)
+
+All compute runs in the HIP library; importing this package never falls back
+to a CPU path: if libmitok.so is missing or no GPU is present, the calls raise.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+from . import configs, seeded  # noqa: F401
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libmitok.so")
+
+TRAINING, PRODUCTION = 0, 1
+TIME_VOCAB, TIME_LAYER_GEMM, TIME_ATTENTION, TIME_STEP = 1, 2, 3, 4
+
+ERRORS = {1: "ERR_ARG", 2: "ERR_HIP", 3: "ERR_STATE", 4: "ERR_NAN", 5: "ERR_NOMEM"}
+
+# every entry point declared in include/mitok.h: name -> (restype, argtypes)
+_P = C.c_void_p
+_u32, _u64, _i32, _f64 = C.c_uint32, C.c_uint64, C.c_int, C.c_double
+SIGNATURES = {
+    "mitok_version": (_i32, []),
+    "mitok_last_error": (C.c_char_p, []),
+    "mitok_device_count": (_i32, [_P]),
+    "mitok_network_create": (_i32, [_i32, _P]),
+    "mitok_network_destroy": (None, [_P]),
+    "mitok_num_layers": (_i32, [_P]),
+    "mitok_add_embedding": (_i32, [_P, _u32, _u32, _P]),
+    "mitok_add_positional_encoding": (_i32, [_P, _u32, _f64]),
+    "mitok_add_norm": (_i32, [_P, _u32, _f64, _P, _P]),
+    "mitok_add_self_attention": (_i32, [_P, _u32, _u32, _u32, _f64, _P, _P, _P, _P, _P, _P]),
+    "mitok_add_feed_forward": (_i32, [_P, _u32, _u32, _P, _P, _P, _P]),
+    "mitok_add_linear": (_i32, [_P, _u32, _u32, _P, _P]),
+    "mitok_add_softmax": (_i32, [_P, _i32]),
+    "mitok_init_seeded": (_i32, [_P, _u64]),
+    "mitok_get_tensor": (_i32, [_P, _u32, _u32, _P, _u64]),
+    "mitok_reset": (_i32, [_P]),
+    "mitok_predict": (_i32, [_P, _P, _P, _u32, _u32, _P, _i32, _i32, _P, _P]),
+    "mitok_forward_layers": (_i32, [_P, _u32, _u32, _P, _P, _u32, _u32, _P, _i32, _P]),
+    "mitok_generate": (_i32, [_P, _P, _P, _u32, _u32, _u32, _P, _P]),
+    "mitok_greedy_decoding": (_i32, [_P, _P, _u32, _u32, _P]),
+    "mitok_last_timings": (_i32, [_P, _P]),
+    "mitok_timing_enable": (_i32, [_P, _i32]),
+    "mitok_timing_read": (_i32, [_P, _P, _P, _P]),
+    "mitok_set_graph_mode": (_i32, [_P, _i32]),
+}
+
+
+class MitokError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"{ERRORS.get(code, code)}: {msg}")
+        self.code = code
+
+
+_lib = None
+
+
+def load_library():
+    """Loads libmitok.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is missing: run `python -m rustcrates_amd.build` first")
+        lib = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def _check(rc: int):
+    if rc != 0:
+        raise MitokError(rc, load_library().mitok_last_error().decode())
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+def _c128(a):
+    return None if a is None else np.ascontiguousarray(a, dtype=np.complex128)
+
+
+def device_count() -> int:
+    n = C.c_int(0)
+    _check(load_library().mitok_device_count(C.byref(n)))
+    return n.value
+
+
+class Network:
+    """NeuralNetwork on one GPU (neural_network_generic.rs:23-31)."""
+
+    def __init__(self, device: int = 0):
+        lib = load_library()
+        h = C.c_void_p()
+        _check(lib.mitok_network_create(device, C.byref(h)))
+        self._h = h
+        self._lib = lib
+        self.vocab = None
+
+    def close(self):
+        if getattr(self, "_h", None):
+            self._lib.mitok_network_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def num_layers(self) -> int:
+        return self._lib.mitok_num_layers(self._h)
+
+    # ---- LayerEnum variants ----
+    def add_embedding(self, vocab, dim, table=None):
+        _check(self._lib.mitok_add_embedding(self._h, vocab, dim, _ptr(_c128(table))))
+
+    def add_positional_encoding(self, dim, base=1250.0):
+        _check(self._lib.mitok_add_positional_encoding(self._h, dim, base))
+
+    def add_norm(self, dim, eps, gamma=None, beta=None):
+        _check(self._lib.mitok_add_norm(self._h, dim, eps, _ptr(_c128(gamma)), _ptr(_c128(beta))))
+
+    def add_self_attention(self, heads, dim, max_ctx, eps=1e-12, wq=None, wk=None, wv=None, bias_pos=None,
+                           gamma=None, beta=None):
+        _check(self._lib.mitok_add_self_attention(self._h, heads, dim, max_ctx, eps, _ptr(_c128(wq)),
+                                                  _ptr(_c128(wk)), _ptr(_c128(wv)), _ptr(_c128(bias_pos)),
+                                                  _ptr(_c128(gamma)), _ptr(_c128(beta))))
+
+    def add_feed_forward(self, dim, hidden, w1=None, b1=None, w2=None, b2=None):
+        _check(self._lib.mitok_add_feed_forward(self._h, dim, hidden, _ptr(_c128(w1)), _ptr(_c128(b1)),
+                                                _ptr(_c128(w2)), _ptr(_c128(b2))))
+
+    def add_linear(self, d_in, d_out, w=None, b=None):
+        self.vocab = d_out
+        _check(self._lib.mitok_add_linear(self._h, d_in, d_out, _ptr(_c128(w)), _ptr(_c128(b))))
+
+    def add_softmax(self, mode=PRODUCTION):
+        _check(self._lib.mitok_add_softmax(self._h, mode))
+
+    def init_seeded(self, seed):
+        _check(self._lib.mitok_init_seeded(self._h, seed))
+
+    def get_tensor(self, layer, slot, n):
+        if slot == 3:
+            out = np.empty(n, np.float64)
+        else:
+            out = np.empty(n, np.complex128)
+        _check(self._lib.mitok_get_tensor(self._h, layer, slot, _ptr(out), n))
+        return out
+
+    def reset(self):
+        _check(self._lib.mitok_reset(self._h))
+
+    # ---- forward paths ----
+    def predict(self, ids, lens=None, time_steps=None, forward_only=True, last_row_only=False):
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        B, S = ids.shape
+        lens = np.full(B, S, np.uint32) if lens is None else np.ascontiguousarray(lens, dtype=np.uint32)
+        ts = None if time_steps is None else np.ascontiguousarray(time_steps, dtype=np.uint32)
+        V = self.vocab
+        out = np.empty((B, V) if last_row_only else (B, S, V), np.float64)
+        mask = np.empty((B, S), np.uint32)
+        _check(self._lib.mitok_predict(self._h, _ptr(ids), _ptr(lens), B, S, _ptr(ts), int(forward_only),
+                                       int(last_row_only), _ptr(out), _ptr(mask)))
+        return out, mask
+
+    def forward_layers(self, first, last, x, mask=None, time_steps=None, forward_only=True, d_out=None):
+        x = _c128(x)
+        B, S, _ = x.shape
+        m = None if mask is None else np.ascontiguousarray(mask, dtype=np.uint32)
+        ts = None if time_steps is None else np.ascontiguousarray(time_steps, dtype=np.uint32)
+        out = np.empty((B, S, d_out if d_out else x.shape[2]), np.complex128)
+        _check(self._lib.mitok_forward_layers(self._h, first, last, _ptr(x), _ptr(m), B, S, _ptr(ts),
+                                              int(forward_only), _ptr(out)))
+        return out
+
+    def generate(self, prompt, lens=None, n_new=1, want_logits=False):
+        prompt = np.ascontiguousarray(prompt, dtype=np.uint32)
+        B, S = prompt.shape
+        lens = np.full(B, S, np.uint32) if lens is None else np.ascontiguousarray(lens, dtype=np.uint32)
+        ids = np.empty((B, n_new), np.uint32)
+        logits = np.empty((n_new, B, self.vocab), np.float64) if want_logits else None
+        _check(self._lib.mitok_generate(self._h, _ptr(prompt), _ptr(lens), B, S, n_new, _ptr(ids), _ptr(logits)))
+        return (ids, logits) if want_logits else ids
+
+    def greedy_decoding(self, logits):
+        logits = np.ascontiguousarray(logits, dtype=np.float64)
+        rows, V = logits.shape
+        out = np.empty(rows, np.uint32)
+        _check(self._lib.mitok_greedy_decoding(self._h, _ptr(logits), rows, V, _ptr(out)))
+        return out
+
+    # ---- measurement ----
+    def last_timings(self):
+        t = np.zeros(3, np.float64)
+        _check(self._lib.mitok_last_timings(self._h, _ptr(t)))
+        return {"prefill_ms": float(t[0]), "decode_ms": float(t[1]), "graph": bool(t[2])}
+
+    def timing_enable(self, kernel_class: int):
+        _check(self._lib.mitok_timing_enable(self._h, kernel_class))
+
+    def timing_read(self):
+        ms, n, b = C.c_double(), C.c_uint64(), C.c_double()
+        _check(self._lib.mitok_timing_read(self._h, C.byref(ms), C.byref(n), C.byref(b)))
+        return {"total_ms": ms.value, "launches": n.value, "alg_bytes": b.value}
+
+    def set_graph_mode(self, direct_launch: bool):
+        _check(self._lib.mitok_set_graph_mode(self._h, int(direct_launch)))

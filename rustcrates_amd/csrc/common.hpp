@@ -1,0 +1,105 @@
+// common.hpp — shared definitions of the MI355X token-loop library (libmitok).
+//
+// Complex<f64> is stored as HIP double2 {x = re, y = im}: the same 16-byte
+// #[repr(C)] {re, im} layout as num-complex 0.4.6, so host buffers from the
+// reference cross the C ABI without conversion.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mitok {
+
+// ---- status codes (include/mitok.h) ----
+enum Status : int {
+  OK = 0,
+  ERR_ARG = 1,
+  ERR_HIP = 2,
+  ERR_STATE = 3,
+  ERR_NAN = 4,
+  ERR_NOMEM = 5,
+};
+
+// ---- device error word bits, set by kernels, read by the host after a step ----
+enum ErrBits : uint32_t {
+  EB_GELU_NAN = 1u,      // gelu_complex panics on NaN (utils/activation.rs:207-209)
+  EB_FFN_NONFINITE = 2u, // check_nan_or_inf_3d after the FFN (transformer_network.rs:408)
+  EB_BAD_TOKEN = 4u,     // id >= vocab: no embedding (embedding_layer.rs:305)
+  EB_ARGMAX_NAN = 8u,    // greedy_decoding partial_cmp().unwrap() (sampling_methods.rs:12)
+  EB_CTX_OVERFLOW = 16u, // a cached sequence outgrew max_ctx
+};
+
+// ---- counter generator (identical to oracle.c / seeded.py) ----
+__host__ __device__ inline uint64_t mix64(uint64_t z) {
+  z += 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+__host__ __device__ inline uint64_t stream_key(uint64_t seed, uint64_t stream) { return mix64(mix64(seed) ^ stream); }
+// uniform on [-lim, lim): (2u - 1) is exact, the product is the only rounding
+__host__ __device__ inline double uniform_from_key(uint64_t key, uint64_t index, double lim) {
+  double u = (double)(mix64(key ^ index) >> 11) * 0x1.0p-53;
+  return (2.0 * u - 1.0) * lim;
+}
+inline uint64_t stream_id(uint32_t layer, uint32_t slot) { return ((uint64_t)layer << 12) | slot; }
+
+// ---- num-complex 0.4.6 arithmetic on double2 ----
+__device__ __forceinline__ double2 cadd(double2 a, double2 b) { return make_double2(a.x + b.x, a.y + b.y); }
+__device__ __forceinline__ double2 csub(double2 a, double2 b) { return make_double2(a.x - b.x, a.y - b.y); }
+__device__ __forceinline__ double2 cmul(double2 a, double2 b) {
+  return make_double2(a.x * b.x - a.y * b.y, a.x * b.y + a.y * b.x);
+}
+__device__ __forceinline__ double2 cscale(double2 a, double t) { return make_double2(a.x * t, a.y * t); }
+__device__ __forceinline__ double2 cunscale(double2 a, double t) { return make_double2(a.x / t, a.y / t); }
+// impl Div for Complex: (a * conj(b)) / norm_sqr(b)
+__device__ __forceinline__ double2 cdiv(double2 a, double2 b) {
+  double n = b.x * b.x + b.y * b.y;
+  return make_double2((a.x * b.x + a.y * b.y) / n, (a.y * b.x - a.x * b.y) / n);
+}
+// Complex::sqrt: positive-real / imaginary-axis shortcuts, else polar form
+__device__ inline double2 csqrt_nc(double2 z) {
+  if (z.y == 0.0) {
+    if (!signbit(z.x)) return make_double2(sqrt(z.x), z.y);
+    double im = sqrt(-z.x);
+    return signbit(z.y) ? make_double2(0.0, -im) : make_double2(0.0, im);
+  }
+  if (z.x == 0.0) {
+    double x = sqrt(fabs(z.y) / 2.0);
+    return signbit(z.y) ? make_double2(x, -x) : make_double2(x, x);
+  }
+  double r = hypot(z.x, z.y);
+  double th = atan2(z.y, z.x) / 2.0;
+  double rs = sqrt(r);
+  return make_double2(rs * cos(th), rs * sin(th));
+}
+// Complex::tanh: (sinh 2a + i sin 2b) / (cosh 2a + cos 2b)
+__device__ inline double2 ctanh_nc(double2 z) {
+  double a2 = z.x + z.x, b2 = z.y + z.y;
+  double den = cosh(a2) + cos(b2);
+  return make_double2(sinh(a2) / den, sin(b2) / den);
+}
+// gelu_complex (utils/activation.rs:195-212); powi(3) = z * (z * z)
+__device__ inline double2 gelu_nc(double2 z, bool* nan) {
+  const double s = 0x1.9884533d43651p-1;  // (2.0 / PI).sqrt() as f64 (correctly rounded sqrt)
+  double2 z3 = cmul(z, cmul(z, z));
+  double2 f = cscale(cadd(z, cmul(make_double2(0.044715, 0.0), z3)), s);
+  double2 cl = make_double2(fmin(fmax(f.x, -30.0), 30.0), fmin(fmax(f.y, -30.0), 30.0));
+  double2 t = ctanh_nc(cl);
+  if (isnan(t.x) || isnan(t.y)) *nan = true;
+  return cmul(cscale(z, 0.5), make_double2(1.0 + t.x, 0.0 + t.y));
+}
+
+// ---- wavefront reductions (wave64) ----
+__device__ __forceinline__ double wave_sum(double v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ double wave_max(double v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmax(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+}  // namespace mitok

@@ -1,0 +1,1227 @@
+// network.hip — host side of libmitok: the reference's layer/model API over
+// device tensors, the forward executor, the greedy token loop and the C ABI
+// declared in include/mitok.h.
+//
+// Reference structure mirrored here (paths relative to src/neural_networks/):
+//   NeuralNetwork { layers: Vec<LayerEnum> }   network_types/neural_network_generic.rs:23-31
+//   LayerEnum                                  network_components/layer.rs:75-88
+//   predict                                    network_types/transformer/transformer_network.rs:315-504
+//   predict_token_by_token                     network_types/transformer/transformer_network.rs:165-313
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "../../include/mitok.h"
+#include "kernels.hpp"
+
+namespace mitok {
+
+// ---------------------------------------------------------------------------
+// errors
+// ---------------------------------------------------------------------------
+static thread_local char g_err[1024];
+
+static int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+#define HIP_TRY(expr)                                                                          \
+  do {                                                                                         \
+    hipError_t e_ = (expr);                                                                    \
+    if (e_ != hipSuccess) return fail(ERR_HIP, "%s: %s (%s:%d)", #expr, hipGetErrorString(e_), \
+                                      __FILE__, __LINE__);                                     \
+  } while (0)
+
+#define TRY(expr)          \
+  do {                     \
+    int rc_ = (expr);      \
+    if (rc_) return rc_;   \
+  } while (0)
+
+// ---------------------------------------------------------------------------
+// device buffers
+// ---------------------------------------------------------------------------
+struct DevBuf {
+  void* p = nullptr;
+  size_t bytes = 0;
+  DevBuf() = default;
+  DevBuf(const DevBuf&) = delete;
+  DevBuf& operator=(const DevBuf&) = delete;
+  ~DevBuf() { release(); }
+  void release() {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    bytes = 0;
+  }
+  // grows only; returns 1 in *grew when the address changed
+  int reserve(size_t n, bool* grew = nullptr) {
+    if (n <= bytes && p) return OK;
+    release();
+    size_t want = std::max<size_t>(n, 256);
+    hipError_t e = hipMalloc(&p, want);
+    if (e != hipSuccess) {
+      p = nullptr;
+      return fail(ERR_NOMEM, "hipMalloc(%zu bytes): %s", want, hipGetErrorString(e));
+    }
+    bytes = want;
+    if (grew) *grew = true;
+    return OK;
+  }
+  template <class T>
+  T* as() const {
+    return (T*)p;
+  }
+};
+
+// ---------------------------------------------------------------------------
+// layers (LayerEnum variants on the token-loop path)
+// ---------------------------------------------------------------------------
+enum Kind { K_EMBEDDING = 0, K_POSENC = 1, K_NORM = 2, K_SELF_ATTENTION = 3, K_FEED_FORWARD = 4, K_LINEAR = 5, K_SOFTMAX = 6 };
+
+struct Layer {
+  int kind;
+  uint32_t d_in = 0, d_out = 0;
+  explicit Layer(int k) : kind(k) {}
+  virtual ~Layer() = default;
+};
+
+struct EmbeddingLayer : Layer {  // embedding_layer.rs:24-36
+  uint32_t vocab = 0;
+  DevBuf table;  // [vocab][d]
+  EmbeddingLayer() : Layer(K_EMBEDDING) {}
+};
+
+struct PositionalEncodingLayer : Layer {  // positional_encoding_layer.rs:15-22
+  double base = 1250.0;
+  DevBuf cs;  // [positions][d/2] (cos, sin) of the clamped angle
+  int positions = 0;
+  PositionalEncodingLayer() : Layer(K_POSENC) {}
+};
+
+struct NormLayer : Layer {  // norm_layer.rs:17-42
+  double eps = 0.0;
+  DevBuf gamma, beta;  // [d]
+  NormLayer() : Layer(K_NORM) {}
+};
+
+struct SelfAttentionLayer : Layer {  // self_attention_layer.rs:16-25 + masked_attention_head.rs:23-61
+  uint32_t heads = 0, dh = 0, max_ctx = 0;
+  double eps = 0.0;
+  DevBuf wqkv;     // [d][3d]: columns [q heads | k heads | v heads], head h at h*dh
+  DevBuf bias_re;  // [heads][max_ctx][max_ctx]  Re(bias_pos): only the real part reaches the softmax
+  DevBuf gamma, beta;
+  DevBuf kc, vc;  // [cache_B][heads][max_ctx][dh]
+  SelfAttentionLayer() : Layer(K_SELF_ATTENTION) {}
+};
+
+struct FeedForwardLayer : Layer {  // feedforward_layer.rs:14-26, layer.rs:91-112, linear_layer.rs:18-34
+  uint32_t hidden = 0;
+  DevBuf w1, b1, w2, b2;
+  FeedForwardLayer() : Layer(K_FEED_FORWARD) {}
+};
+
+struct LinearLayer : Layer {  // linear_layer.rs:18-34
+  DevBuf w, b;
+  LinearLayer() : Layer(K_LINEAR) {}
+};
+
+struct SoftmaxLayer : Layer {  // softmax_output_layer.rs:15-27
+  int mode = 1;
+  SoftmaxLayer() : Layer(K_SOFTMAX) {}
+};
+
+enum RunMode { MODE_PREFILL = 0, MODE_CACHED = 1, MODE_STATELESS = 2 };
+
+struct Spec {
+  int B = 0, S = 0;
+  int mode = MODE_STATELESS;
+  bool forward_only = true;
+  bool last_row = false;
+  uint32_t first = 0, last = 0;      // layer range
+  const double2* in = nullptr;       // hidden-state input when first > 0
+  const uint32_t* ids = nullptr;     // [B*S] padded ids (first == 0)
+  const uint32_t* mask = nullptr;    // [B*S]
+  const uint32_t* lens = nullptr;    // [B]
+  const int* pos = nullptr;          // [B*S] RoPE positions, or null -> kv_len (S == 1)
+  const int* kv_row = nullptr;       // [B] cached append row (S > 1), or null
+  double* out_re = nullptr;          // vocab Re-logits
+  double* out_prob = nullptr;        // softmax output (not forward_only)
+  double2* out_hidden = nullptr;     // result of a hidden-state range
+};
+
+struct Timing {
+  int cls = 0;
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> pending;
+  std::vector<double> pending_bytes;
+  std::vector<hipEvent_t> pool;
+  double total_ms = 0.0, bytes = 0.0;
+  uint64_t launches = 0;
+};
+
+}  // namespace mitok
+
+struct mitok_network {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::vector<std::unique_ptr<mitok::Layer>> layers;
+  // session (KV cache) state
+  bool cache_valid = false;
+  uint32_t cache_B = 0;
+  std::vector<uint32_t> kv_len_h;
+  mitok::DevBuf kv_len_d, err_d;
+  // workspaces
+  mitok::DevBuf act0, act1, qbuf, concat, hbuf, gath, logits_c, logits_re, probs, gemm_ws, attn_ws, kv_scratch;
+  mitok::DevBuf ids_d, mask_d, lens_d, pos_d, kv_row_d, ones_d, dec_ids_d, hist_d, cnt_d, logit_hist_d;
+  // decode-step graph
+  hipGraphExec_t graph = nullptr;
+  uint32_t graph_B = 0, graph_nnew = 0;
+  bool graph_logits = false;
+  uint64_t ws_generation = 0, graph_generation = 0;
+  int direct_launch = 0;
+  double last_t[3] = {0, 0, 0};
+  mitok::Timing timing;
+};
+
+namespace mitok {
+
+using Net = mitok_network;
+
+static int set_device(Net* n) {
+  HIP_TRY(hipSetDevice(n->device));
+  return OK;
+}
+
+static void drop_graph(Net* n) {
+  if (n->graph) (void)hipGraphExecDestroy(n->graph);
+  n->graph = nullptr;
+}
+
+static int reserve(Net* n, DevBuf& b, size_t bytes) {
+  bool grew = false;
+  TRY(b.reserve(bytes, &grew));
+  if (grew) {
+    n->ws_generation++;
+    drop_graph(n);
+  }
+  return OK;
+}
+
+static int upload(Net* n, DevBuf& b, const void* src, size_t bytes) {
+  TRY(reserve(n, b, bytes));
+  HIP_TRY(hipMemcpyAsync(b.p, src, bytes, hipMemcpyHostToDevice, n->stream));
+  return OK;
+}
+
+static int check_err_word(Net* n) {
+  uint32_t e = 0;
+  HIP_TRY(hipMemcpyAsync(&e, n->err_d.p, sizeof e, hipMemcpyDeviceToHost, n->stream));
+  HIP_TRY(hipStreamSynchronize(n->stream));
+  if (!e) return OK;
+  fill_u32(n->stream, n->err_d.as<uint32_t>(), 1, 0);
+  HIP_TRY(hipStreamSynchronize(n->stream));
+  if (e & EB_BAD_TOKEN) return fail(ERR_ARG, "No token embedding found: token id >= vocab (embedding_layer.rs:305)");
+  if (e & EB_GELU_NAN) return fail(ERR_NAN, "NaN detected in tanh(f(z)) (activation.rs:207-209)");
+  if (e & EB_FFN_NONFINITE) return fail(ERR_NAN, "output ffn dense: The value is Not Valid (transformer_network.rs:408)");
+  if (e & EB_ARGMAX_NAN) return fail(ERR_NAN, "greedy_decoding: NaN in logits (sampling_methods.rs:12)");
+  if (e & EB_CTX_OVERFLOW) return fail(ERR_ARG, "context exceeds max_ctx");
+  return fail(ERR_STATE, "device error word 0x%x", e);
+}
+
+// ---------------------------------------------------------------------------
+// timing
+// ---------------------------------------------------------------------------
+static hipEvent_t take_event(Timing& t) {
+  if (!t.pool.empty()) {
+    hipEvent_t e = t.pool.back();
+    t.pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  (void)hipEventCreate(&e);
+  return e;
+}
+
+struct TimeScope {
+  Net* n;
+  bool on;
+  hipEvent_t a = nullptr;
+  double bytes;
+  TimeScope(Net* net, int cls, double alg_bytes) : n(net), on(net->timing.cls == cls), bytes(alg_bytes) {
+    if (on) {
+      a = take_event(n->timing);
+      (void)hipEventRecord(a, n->stream);
+    }
+  }
+  ~TimeScope() {
+    if (!on) return;
+    hipEvent_t b = take_event(n->timing);
+    (void)hipEventRecord(b, n->stream);
+    n->timing.pending.push_back({a, b});
+    n->timing.pending_bytes.push_back(bytes);
+  }
+};
+
+static void collect_timing(Net* n) {
+  Timing& t = n->timing;
+  for (size_t i = 0; i < t.pending.size(); ++i) {
+    float ms = 0.f;
+    if (hipEventElapsedTime(&ms, t.pending[i].first, t.pending[i].second) == hipSuccess) {
+      t.total_ms += ms;
+      t.bytes += t.pending_bytes[i];
+      t.launches++;
+    }
+    t.pool.push_back(t.pending[i].first);
+    t.pool.push_back(t.pending[i].second);
+  }
+  t.pending.clear();
+  t.pending_bytes.clear();
+}
+
+static double gemm_bytes(long M, long N, long K, bool re_out) {
+  return 16.0 * (double)K * N + 16.0 * (double)M * K + (re_out ? 8.0 : 16.0) * (double)M * N;
+}
+
+// ---------------------------------------------------------------------------
+// workspace sizing for one forward shape
+// ---------------------------------------------------------------------------
+struct Dims {
+  uint32_t dmax = 0, dsa = 0, hmax = 0, fmax = 0, vocab = 0, mc_max = 0, dh_max = 0;
+};
+
+static Dims net_dims(const Net* n) {
+  Dims d;
+  for (auto& L : n->layers) {
+    d.dmax = std::max({d.dmax, L->d_in, L->d_out});
+    if (L->kind == K_SELF_ATTENTION) {
+      auto* A = (SelfAttentionLayer*)L.get();
+      d.dsa = std::max(d.dsa, A->d_in);
+      d.hmax = std::max(d.hmax, A->heads);
+      d.mc_max = std::max(d.mc_max, A->max_ctx);
+      d.dh_max = std::max(d.dh_max, A->dh);
+    }
+    if (L->kind == K_FEED_FORWARD) d.fmax = std::max(d.fmax, ((FeedForwardLayer*)L.get())->hidden);
+    if (L->kind == K_LINEAR) d.vocab = std::max(d.vocab, L->d_out);
+  }
+  return d;
+}
+
+static bool is_vocab_linear(const Net* n, uint32_t li) {
+  return n->layers[li]->kind == K_LINEAR && li + 2 == n->layers.size() && n->layers.back()->kind == K_SOFTMAX;
+}
+
+static int prepare(Net* n, const Spec& sp) {
+  const Dims dm = net_dims(n);
+  const size_t rows = (size_t)sp.B * sp.S;
+  const size_t c16 = sizeof(double2);
+  TRY(reserve(n, n->act0, rows * dm.dmax * c16));
+  TRY(reserve(n, n->act1, rows * dm.dmax * c16));
+  TRY(reserve(n, n->qbuf, rows * std::max(1u, dm.dsa) * c16));
+  TRY(reserve(n, n->concat, rows * std::max(1u, dm.dsa) * c16));
+  TRY(reserve(n, n->hbuf, rows * std::max(1u, dm.fmax) * c16));
+  TRY(reserve(n, n->gath, (size_t)sp.B * dm.dmax * c16));
+  size_t gws = 0;
+  for (uint32_t li = sp.first; li < sp.last; ++li) {
+    Layer* L = n->layers[li].get();
+    const int M = (int)rows;
+    if (L->kind == K_SELF_ATTENTION) gws = std::max(gws, gemm_ws_bytes(M, 3 * L->d_in, L->d_in, EPI_QKV));
+    if (L->kind == K_FEED_FORWARD) {
+      auto* F = (FeedForwardLayer*)L;
+      gws = std::max(gws, gemm_ws_bytes(M, F->hidden, F->d_in, EPI_GELU));
+      gws = std::max(gws, gemm_ws_bytes(M, F->d_out, F->hidden, EPI_STORE));
+    }
+    if (L->kind == K_LINEAR) {
+      bool vocab = is_vocab_linear(n, li) && sp.first == 0;
+      int Mv = (vocab && sp.last_row) ? sp.B : M;
+      int mode = (vocab && sp.forward_only) ? EPI_RE : EPI_STORE;
+      gws = std::max(gws, gemm_ws_bytes(Mv, L->d_out, L->d_in, mode));
+      if (vocab && !sp.forward_only) {
+        TRY(reserve(n, n->logits_c, (size_t)Mv * L->d_out * c16));
+        TRY(reserve(n, n->probs, (size_t)Mv * L->d_out * sizeof(double)));
+      }
+      if (vocab && sp.forward_only) TRY(reserve(n, n->logits_re, (size_t)Mv * L->d_out * sizeof(double)));
+    }
+  }
+  TRY(reserve(n, n->gemm_ws, gws));
+  if (dm.hmax) {
+    TRY(reserve(n, n->attn_ws, attention_decode_ws_bytes(sp.B, dm.hmax, dm.dh_max, dm.mc_max)));
+    if (sp.mode == MODE_STATELESS) TRY(reserve(n, n->kv_scratch, 2 * rows * dm.dsa * c16));
+  }
+  TRY(reserve(n, n->kv_len_d, (size_t)sp.B * sizeof(int)));
+  TRY(reserve(n, n->ones_d, std::max<size_t>(rows, sp.B) * sizeof(uint32_t)));
+  TRY(reserve(n, n->dec_ids_d, (size_t)sp.B * sizeof(uint32_t)));
+  return OK;
+}
+
+// RoPE table: (cos, sin) of clamp(pos / base^(2i/d), -1, 1) with the host libm,
+// exactly as positional_encoding_layer.rs:188-198 evaluates it.
+static int ensure_rope_table(Net* n, PositionalEncodingLayer* P, int positions) {
+  if (P->positions >= positions) return OK;
+  const uint32_t d = P->d_in, half = d / 2;
+  std::vector<double2> cs((size_t)positions * half);
+  for (int p = 0; p < positions; ++p)
+    for (uint32_t i = 0; i < half; ++i) {
+      double theta = (double)p / pow(P->base * 1.0, 2.0 * (double)i / (double)d);
+      theta = std::min(1.0, std::max(-1.0, theta));
+      cs[(size_t)p * half + i] = make_double2(cos(theta), sin(theta));
+    }
+  TRY(reserve(n, P->cs, cs.size() * sizeof(double2)));
+  HIP_TRY(hipMemcpy(P->cs.p, cs.data(), cs.size() * sizeof(double2), hipMemcpyHostToDevice));
+  P->positions = positions;
+  return OK;
+}
+
+// ---------------------------------------------------------------------------
+// the forward executor: predict's layer walk (transformer_network.rs:335-492)
+// ---------------------------------------------------------------------------
+static int enqueue_forward(Net* n, const Spec& sp) {
+  hipStream_t st = n->stream;
+  uint32_t* err = n->err_d.as<uint32_t>();
+  const int B = sp.B, S = sp.S, rows = B * S;
+  double2* cur = n->act0.as<double2>();
+  double2* nxt = n->act1.as<double2>();
+  if (sp.first > 0) HIP_TRY(hipMemcpyAsync(cur, sp.in, (size_t)rows * n->layers[sp.first]->d_in * sizeof(double2),
+                                          hipMemcpyDeviceToDevice, st));
+  for (uint32_t li = sp.first; li < sp.last; ++li) {
+    Layer* L = n->layers[li].get();
+    switch (L->kind) {
+      case K_EMBEDDING: {
+        auto* E = (EmbeddingLayer*)L;
+        embed(st, E->table.as<double2>(), E->vocab, E->d_out, sp.ids, rows, cur, err);
+        break;
+      }
+      case K_POSENC: {
+        auto* P = (PositionalEncodingLayer*)L;
+        rope(st, cur, rows, P->d_in, P->cs.as<double2>(), P->positions, sp.pos, sp.pos ? nullptr : n->kv_len_d.as<int>(),
+             err);
+        break;
+      }
+      case K_NORM: {
+        auto* N = (NormLayer*)L;
+        layernorm(st, cur, nullptr, nxt, rows, N->d_in, N->eps, N->gamma.as<double2>(), N->beta.as<double2>());
+        std::swap(cur, nxt);
+        break;
+      }
+      case K_SELF_ATTENTION: {
+        auto* A = (SelfAttentionLayer*)L;
+        const int d = A->d_in, H = A->heads, dh = A->dh;
+        Epi e;
+        e.mode = EPI_QKV;
+        e.out = n->qbuf.as<double2>();
+        e.ldo = d;
+        e.d = d;
+        e.dh = dh;
+        e.heads = H;
+        e.S = S;
+        e.err = err;
+        Attn a;
+        a.q = n->qbuf.as<double2>();
+        a.ldq = d;
+        if (sp.mode == MODE_STATELESS) {
+          e.kc = n->kv_scratch.as<double2>();
+          e.vc = e.kc + (size_t)rows * d;
+          e.ctx = S;
+          a.T_const = S;
+          a.T_max = S;
+        } else {
+          e.kc = A->kc.as<double2>();
+          e.vc = A->vc.as<double2>();
+          e.ctx = A->max_ctx;
+          if (sp.mode == MODE_PREFILL) {
+            a.T_const = S;
+            a.T_max = S;
+          } else {
+            e.kv_base = n->kv_len_d.as<int>();
+            e.kv_row = sp.kv_row;
+            a.kv_len = n->kv_len_d.as<int>();
+            a.T_add = 1;
+            a.T_max = A->max_ctx;
+          }
+        }
+        {
+          TimeScope ts(n, MITOK_TIME_LAYER_GEMM, gemm_bytes(rows, 3 * d, d, false));
+          gemm(st, rows, 3 * d, d, cur, d, A->wqkv.as<double2>(), 3 * d, e, n->gemm_ws.p);
+        }
+        a.kc = e.kc;
+        a.vc = e.vc;
+        a.ctx = e.ctx;
+        a.bias_re = A->bias_re.as<double>();
+        a.mc = A->max_ctx;
+        a.row_mask = sp.mask;
+        a.out = n->concat.as<double2>();
+        a.ldo = d;
+        a.B = B;
+        a.S = S;
+        a.H = H;
+        a.dh = dh;
+        a.scale = 1.0 / (1e-8 + sqrt((double)dh));  // scale_attention_scores (masked_attention_head.rs:453-465)
+        {
+          TimeScope ts(n, MITOK_TIME_ATTENTION, 0.0);
+          if (sp.mode == MODE_CACHED && S == 1) attention_decode(st, a, n->attn_ws.p);
+          else attention_rows(st, a);
+        }
+        layernorm(st, n->concat.as<double2>(), cur, nxt, rows, d, A->eps, A->gamma.as<double2>(), A->beta.as<double2>());
+        std::swap(cur, nxt);
+        break;
+      }
+      case K_FEED_FORWARD: {
+        auto* F = (FeedForwardLayer*)L;
+        Epi e1;
+        e1.mode = EPI_GELU;
+        e1.bias = F->b1.as<double2>();
+        e1.out = n->hbuf.as<double2>();
+        e1.ldo = F->hidden;
+        e1.row_mask = sp.mask;
+        e1.err = err;
+        Epi e2;
+        e2.mode = EPI_STORE;
+        e2.bias = F->b2.as<double2>();
+        e2.out = nxt;
+        e2.ldo = F->d_out;
+        e2.check_finite = 1;
+        e2.err = err;
+        {
+          TimeScope ts(n, MITOK_TIME_LAYER_GEMM, gemm_bytes(rows, F->hidden, F->d_in, false));
+          gemm(st, rows, F->hidden, F->d_in, cur, F->d_in, F->w1.as<double2>(), F->hidden, e1, n->gemm_ws.p);
+        }
+        {
+          TimeScope ts(n, MITOK_TIME_LAYER_GEMM, gemm_bytes(rows, F->d_out, F->hidden, false));
+          gemm(st, rows, F->d_out, F->hidden, n->hbuf.as<double2>(), F->hidden, F->w2.as<double2>(), F->d_out, e2,
+               n->gemm_ws.p);
+        }
+        std::swap(cur, nxt);
+        break;
+      }
+      case K_LINEAR: {
+        auto* Ln = (LinearLayer*)L;
+        const bool vocab = is_vocab_linear(n, li) && sp.first == 0;
+        if (!vocab) {
+          Epi e;
+          e.mode = EPI_STORE;
+          e.bias = Ln->b.as<double2>();
+          e.out = nxt;
+          e.ldo = Ln->d_out;
+          e.err = err;
+          gemm(st, rows, Ln->d_out, Ln->d_in, cur, Ln->d_in, Ln->w.as<double2>(), Ln->d_out, e, n->gemm_ws.p);
+          std::swap(cur, nxt);
+          break;
+        }
+        const double2* x = cur;
+        int M = rows;
+        if (sp.last_row) {
+          gather_rows(st, cur, S, Ln->d_in, sp.lens, B, n->gath.as<double2>());
+          x = n->gath.as<double2>();
+          M = B;
+        }
+        Epi e;
+        e.bias = Ln->b.as<double2>();
+        e.ldo = Ln->d_out;
+        e.err = err;
+        if (sp.forward_only) {
+          e.mode = EPI_RE;
+          e.out_re = sp.out_re;
+          TimeScope ts(n, MITOK_TIME_VOCAB, gemm_bytes(M, Ln->d_out, Ln->d_in, true));
+          gemm(st, M, Ln->d_out, Ln->d_in, x, Ln->d_in, Ln->w.as<double2>(), Ln->d_out, e, n->gemm_ws.p);
+        } else {
+          e.mode = EPI_STORE;
+          e.out = n->logits_c.as<double2>();
+          gemm(st, M, Ln->d_out, Ln->d_in, x, Ln->d_in, Ln->w.as<double2>(), Ln->d_out, e, n->gemm_ws.p);
+          auto* SM = (SoftmaxLayer*)n->layers.back().get();
+          softmax_rows(st, n->logits_c.as<double2>(), M, S, Ln->d_out, sp.mask, SM->mode == MITOK_TRAINING ? 0 : 1,
+                       sp.out_prob);
+        }
+        break;
+      }
+      case K_SOFTMAX: break;  // applied together with the vocab Linear
+    }
+  }
+  if (sp.out_hidden && cur != sp.out_hidden) {
+    const uint32_t dout = n->layers[sp.last - 1]->d_out;
+    HIP_TRY(hipMemcpyAsync(sp.out_hidden, cur, (size_t)rows * dout * sizeof(double2), hipMemcpyDeviceToDevice, st));
+  }
+  HIP_TRY(hipGetLastError());
+  return OK;
+}
+
+// ---------------------------------------------------------------------------
+// session helpers
+// ---------------------------------------------------------------------------
+static int alloc_caches(Net* n, uint32_t B) {
+  for (auto& L : n->layers)
+    if (L->kind == K_SELF_ATTENTION) {
+      auto* A = (SelfAttentionLayer*)L.get();
+      size_t bytes = (size_t)B * A->heads * A->max_ctx * A->dh * sizeof(double2);
+      TRY(reserve(n, A->kc, bytes));
+      TRY(reserve(n, A->vc, bytes));
+    }
+  return OK;
+}
+
+static uint32_t min_ctx(const Net* n) {
+  uint32_t m = UINT32_MAX;
+  for (auto& L : n->layers)
+    if (L->kind == K_SELF_ATTENTION) m = std::min(m, ((SelfAttentionLayer*)L.get())->max_ctx);
+  return m;
+}
+
+static int check_stack(const Net* n) {
+  if (n->layers.size() < 2 || n->layers[0]->kind != K_EMBEDDING || n->layers.back()->kind != K_SOFTMAX ||
+      n->layers[n->layers.size() - 2]->kind != K_LINEAR)
+    return fail(ERR_STATE, "network must be Embedding ... Linear, Softmax");
+  for (size_t i = 1; i + 2 < n->layers.size(); ++i)
+    if (n->layers[i]->kind == K_EMBEDDING || n->layers[i]->kind == K_SOFTMAX)
+      return fail(ERR_STATE, "Embedding/Softmax only at the ends of the stack");
+  return OK;
+}
+
+static int ensure_rope_for(Net* n, uint32_t first, uint32_t last, int positions) {
+  for (uint32_t li = first; li < last; ++li)
+    if (n->layers[li]->kind == K_POSENC) TRY(ensure_rope_table(n, (PositionalEncodingLayer*)n->layers[li].get(), positions));
+  return OK;
+}
+
+static int rope_positions_needed(const Net* n) {
+  uint32_t m = min_ctx(n);
+  return (int)std::max<uint32_t>(m == UINT32_MAX ? 512u : m, 512u);
+}
+
+}  // namespace mitok
+
+using namespace mitok;
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+extern "C" {
+
+int mitok_version(void) { return 1; }
+
+const char* mitok_last_error(void) { return g_err; }
+
+int mitok_device_count(int* count) {
+  if (!count) return fail(ERR_ARG, "null count");
+  HIP_TRY(hipGetDeviceCount(count));
+  return OK;
+}
+
+int mitok_network_create(int device, mitok_network** out) {
+  if (!out) return fail(ERR_ARG, "null out");
+  *out = nullptr;
+  int nd = 0;
+  HIP_TRY(hipGetDeviceCount(&nd));
+  if (device < 0 || device >= nd) return fail(ERR_ARG, "device %d not present (%d devices)", device, nd);
+  auto* n = new (std::nothrow) mitok_network();
+  if (!n) return fail(ERR_NOMEM, "out of host memory");
+  n->device = device;
+  int rc = set_device(n);
+  if (!rc && hipStreamCreateWithFlags(&n->stream, hipStreamNonBlocking) != hipSuccess)
+    rc = fail(ERR_HIP, "hipStreamCreate failed");
+  if (!rc) rc = n->err_d.reserve(sizeof(uint32_t));
+  if (!rc) {
+    fill_u32(n->stream, n->err_d.as<uint32_t>(), 1, 0);
+    if (hipStreamSynchronize(n->stream) != hipSuccess) rc = fail(ERR_HIP, "stream sync failed");
+  }
+  if (rc) {
+    mitok_network_destroy(n);
+    return rc;
+  }
+  *out = n;
+  return OK;
+}
+
+void mitok_network_destroy(mitok_network* n) {
+  if (!n) return;
+  (void)hipSetDevice(n->device);
+  if (n->stream) (void)hipStreamSynchronize(n->stream);
+  drop_graph(n);
+  collect_timing(n);
+  for (hipEvent_t e : n->timing.pool) (void)hipEventDestroy(e);
+  n->layers.clear();
+  if (n->stream) (void)hipStreamDestroy(n->stream);
+  delete n;
+}
+
+int mitok_num_layers(const mitok_network* n) { return n ? (int)n->layers.size() : 0; }
+
+static int upload_c(Net* n, DevBuf& b, const double* src, size_t count, double2 dflt, bool has_default) {
+  TRY(reserve(n, b, count * sizeof(double2)));
+  if (src) HIP_TRY(hipMemcpy(b.p, src, count * sizeof(double2), hipMemcpyHostToDevice));
+  else fill_const(n->stream, b.as<double2>(), count, has_default ? dflt : make_double2(0.0, 0.0));
+  HIP_TRY(hipStreamSynchronize(n->stream));
+  return OK;
+}
+
+static int add_layer(Net* n, Layer* L) {
+  n->layers.emplace_back(L);
+  n->cache_valid = false;
+  drop_graph(n);
+  return OK;
+}
+
+int mitok_add_embedding(mitok_network* n, uint32_t vocab, uint32_t dim, const double* table) {
+  if (!n || !vocab || !dim) return fail(ERR_ARG, "embedding: bad arguments");
+  TRY(set_device(n));
+  auto* L = new EmbeddingLayer();
+  L->vocab = vocab;
+  L->d_in = L->d_out = dim;
+  add_layer(n, L);
+  return upload_c(n, L->table, table, (size_t)vocab * dim, {}, false);
+}
+
+int mitok_add_positional_encoding(mitok_network* n, uint32_t dim, double base) {
+  if (!n || !dim || dim % 2) return fail(ERR_ARG, "positional encoding: dim must be even (positional_encoding_layer.rs:183)");
+  TRY(set_device(n));
+  auto* L = new PositionalEncodingLayer();
+  L->d_in = L->d_out = dim;
+  L->base = base;
+  return add_layer(n, L);
+}
+
+int mitok_add_norm(mitok_network* n, uint32_t dim, double eps, const double* gamma, const double* beta) {
+  if (!n || !dim) return fail(ERR_ARG, "norm: bad arguments");
+  if (dim > 1024) return fail(ERR_ARG, "norm: dim %u > 1024 unsupported", dim);
+  TRY(set_device(n));
+  auto* L = new NormLayer();
+  L->d_in = L->d_out = dim;
+  L->eps = eps;
+  add_layer(n, L);
+  TRY(upload_c(n, L->gamma, gamma, dim, make_double2(1.0, 0.0), true));
+  return upload_c(n, L->beta, beta, dim, make_double2(0.0, 0.0), true);
+}
+
+int mitok_add_self_attention(mitok_network* n, uint32_t heads, uint32_t dim, uint32_t max_ctx, double eps,
+                             const double* wq, const double* wk, const double* wv, const double* bias_pos,
+                             const double* gamma, const double* beta) {
+  if (!n || !heads || !dim || dim % heads || !max_ctx) return fail(ERR_ARG, "self-attention: bad arguments");
+  const uint32_t dh = dim / heads;
+  if (dh > 256) return fail(ERR_ARG, "self-attention: head dim %u > 256 unsupported", dh);
+  if (dim > 1024) return fail(ERR_ARG, "self-attention: dim %u > 1024 unsupported", dim);
+  if (max_ctx > 6144) return fail(ERR_ARG, "self-attention: max_ctx %u > 6144 unsupported", max_ctx);
+  TRY(set_device(n));
+  auto* L = new SelfAttentionLayer();
+  L->heads = heads;
+  L->d_in = L->d_out = dim;
+  L->dh = dh;
+  L->max_ctx = max_ctx;
+  L->eps = eps;
+  add_layer(n, L);
+  const size_t d = dim;
+  TRY(reserve(n, L->wqkv, d * 3 * d * sizeof(double2)));
+  fill_const(n->stream, L->wqkv.as<double2>(), d * 3 * d, make_double2(0.0, 0.0));
+  HIP_TRY(hipStreamSynchronize(n->stream));
+  const double* srcs[3] = {wq, wk, wv};
+  for (int p = 0; p < 3; ++p) {
+    if (!srcs[p]) continue;
+    // [h][d][dh] -> columns p*d + h*dh of [d][3d]
+    std::vector<double2> packed(d * 3 * d);
+    HIP_TRY(hipMemcpy(packed.data(), L->wqkv.p, packed.size() * sizeof(double2), hipMemcpyDeviceToHost));
+    const double2* s = (const double2*)srcs[p];
+    for (uint32_t h = 0; h < heads; ++h)
+      for (size_t r = 0; r < d; ++r)
+        for (uint32_t e = 0; e < dh; ++e) packed[r * 3 * d + p * d + h * dh + e] = s[((size_t)h * d + r) * dh + e];
+    HIP_TRY(hipMemcpy(L->wqkv.p, packed.data(), packed.size() * sizeof(double2), hipMemcpyHostToDevice));
+  }
+  const size_t bn = (size_t)heads * max_ctx * max_ctx;
+  TRY(reserve(n, L->bias_re, bn * sizeof(double)));
+  if (bias_pos) {
+    std::vector<double> re(bn);
+    for (size_t i = 0; i < bn; ++i) re[i] = bias_pos[2 * i];
+    HIP_TRY(hipMemcpy(L->bias_re.p, re.data(), bn * sizeof(double), hipMemcpyHostToDevice));
+  } else {
+    HIP_TRY(hipMemset(L->bias_re.p, 0, bn * sizeof(double)));
+  }
+  TRY(upload_c(n, L->gamma, gamma, dim, make_double2(1.0, 0.0), true));
+  return upload_c(n, L->beta, beta, dim, make_double2(0.0, 0.0), true);
+}
+
+int mitok_add_feed_forward(mitok_network* n, uint32_t dim, uint32_t hidden, const double* w1, const double* b1,
+                           const double* w2, const double* b2) {
+  if (!n || !dim || !hidden) return fail(ERR_ARG, "feed-forward: bad arguments");
+  TRY(set_device(n));
+  auto* L = new FeedForwardLayer();
+  L->d_in = L->d_out = dim;
+  L->hidden = hidden;
+  add_layer(n, L);
+  TRY(upload_c(n, L->w1, w1, (size_t)dim * hidden, {}, false));
+  TRY(upload_c(n, L->b1, b1, hidden, make_double2(1.0, 0.0), true));
+  TRY(upload_c(n, L->w2, w2, (size_t)hidden * dim, {}, false));
+  return upload_c(n, L->b2, b2, dim, make_double2(1.0, 0.0), true);
+}
+
+int mitok_add_linear(mitok_network* n, uint32_t in, uint32_t out, const double* w, const double* b) {
+  if (!n || !in || !out) return fail(ERR_ARG, "linear: bad arguments");
+  TRY(set_device(n));
+  auto* L = new LinearLayer();
+  L->d_in = in;
+  L->d_out = out;
+  add_layer(n, L);
+  TRY(upload_c(n, L->w, w, (size_t)in * out, {}, false));
+  return upload_c(n, L->b, b, out, make_double2(1.0, 0.0), true);
+}
+
+int mitok_add_softmax(mitok_network* n, int operation_mode) {
+  if (!n) return fail(ERR_ARG, "null network");
+  if (operation_mode != MITOK_TRAINING && operation_mode != MITOK_PRODUCTION) return fail(ERR_ARG, "bad operation mode");
+  auto* L = new SoftmaxLayer();
+  L->mode = operation_mode;
+  return add_layer(n, L);
+}
+
+int mitok_init_seeded(mitok_network* n, uint64_t seed) {
+  if (!n) return fail(ERR_ARG, "null network");
+  TRY(set_device(n));
+  hipStream_t st = n->stream;
+  auto lim = [](uint64_t r, uint64_t c) { return sqrt(6.0 / (double)(r + c)); };
+  for (uint32_t li = 0; li < n->layers.size(); ++li) {
+    Layer* L = n->layers[li].get();
+    switch (L->kind) {
+      case K_EMBEDDING: {
+        auto* E = (EmbeddingLayer*)L;
+        fill_seeded(st, E->table.as<double2>(), E->vocab, E->d_out, E->d_out, stream_key(seed, stream_id(li, 0)),
+                    lim(E->vocab, E->d_out));
+        break;
+      }
+      case K_NORM: {
+        auto* N = (NormLayer*)L;
+        fill_const(st, N->gamma.as<double2>(), N->d_in, make_double2(1.0, 0.0));
+        fill_const(st, N->beta.as<double2>(), N->d_in, make_double2(0.0, 0.0));
+        break;
+      }
+      case K_SELF_ATTENTION: {
+        auto* A = (SelfAttentionLayer*)L;
+        const long d = A->d_in;
+        for (uint32_t h = 0; h < A->heads; ++h) {
+          for (int p = 0; p < 3; ++p)
+            fill_seeded(st, A->wqkv.as<double2>() + p * d + (long)h * A->dh, (int)d, A->dh, 3 * d,
+                        stream_key(seed, stream_id(li, 1 + p + 4 * h)), lim(d, A->dh));
+          fill_seeded_re(st, A->bias_re.as<double>() + (size_t)h * A->max_ctx * A->max_ctx, A->max_ctx, A->max_ctx,
+                         A->max_ctx, stream_key(seed, stream_id(li, 4 + 4 * h)), lim(A->max_ctx, A->max_ctx));
+        }
+        fill_const(st, A->gamma.as<double2>(), A->d_in, make_double2(1.0, 0.0));
+        fill_const(st, A->beta.as<double2>(), A->d_in, make_double2(0.0, 0.0));
+        break;
+      }
+      case K_FEED_FORWARD: {
+        auto* F = (FeedForwardLayer*)L;
+        fill_seeded(st, F->w1.as<double2>(), F->d_in, F->hidden, F->hidden, stream_key(seed, stream_id(li, 1)),
+                    lim(F->d_in, F->hidden));
+        fill_seeded(st, F->w2.as<double2>(), F->hidden, F->d_out, F->d_out, stream_key(seed, stream_id(li, 2)),
+                    lim(F->hidden, F->d_out));
+        fill_const(st, F->b1.as<double2>(), F->hidden, make_double2(1.0, 0.0));
+        fill_const(st, F->b2.as<double2>(), F->d_out, make_double2(1.0, 0.0));
+        break;
+      }
+      case K_LINEAR: {
+        auto* Ln = (LinearLayer*)L;
+        fill_seeded(st, Ln->w.as<double2>(), Ln->d_in, Ln->d_out, Ln->d_out, stream_key(seed, stream_id(li, 1)),
+                    lim(Ln->d_in, Ln->d_out));
+        fill_const(st, Ln->b.as<double2>(), Ln->d_out, make_double2(1.0, 0.0));
+        break;
+      }
+      default: break;
+    }
+  }
+  HIP_TRY(hipGetLastError());
+  HIP_TRY(hipStreamSynchronize(st));
+  n->cache_valid = false;
+  return OK;
+}
+
+int mitok_get_tensor(mitok_network* n, uint32_t layer, uint32_t slot, double* out, uint64_t count) {
+  if (!n || !out || layer >= n->layers.size()) return fail(ERR_ARG, "bad layer index");
+  TRY(set_device(n));
+  HIP_TRY(hipStreamSynchronize(n->stream));
+  Layer* L = n->layers[layer].get();
+  auto copy = [&](const DevBuf& b, uint64_t len, size_t elem) -> int {
+    if (count != len) return fail(ERR_ARG, "tensor size %llu != %llu", (unsigned long long)count, (unsigned long long)len);
+    HIP_TRY(hipMemcpy(out, b.p, len * elem, hipMemcpyDeviceToHost));
+    return OK;
+  };
+  switch (L->kind) {
+    case K_EMBEDDING:
+      if (slot == 0) return copy(((EmbeddingLayer*)L)->table, (uint64_t)((EmbeddingLayer*)L)->vocab * L->d_out, 16);
+      break;
+    case K_NORM:
+      if (slot == 6) return copy(((NormLayer*)L)->gamma, L->d_in, 16);
+      if (slot == 7) return copy(((NormLayer*)L)->beta, L->d_in, 16);
+      break;
+    case K_SELF_ATTENTION: {
+      auto* A = (SelfAttentionLayer*)L;
+      if (slot <= 2) {
+        const size_t d = A->d_in;
+        if (count != (uint64_t)A->heads * d * A->dh) return fail(ERR_ARG, "tensor size mismatch");
+        std::vector<double2> packed(d * 3 * d);
+        HIP_TRY(hipMemcpy(packed.data(), A->wqkv.p, packed.size() * sizeof(double2), hipMemcpyDeviceToHost));
+        double2* o = (double2*)out;
+        for (uint32_t h = 0; h < A->heads; ++h)
+          for (size_t r = 0; r < d; ++r)
+            for (uint32_t e = 0; e < A->dh; ++e) o[((size_t)h * d + r) * A->dh + e] = packed[r * 3 * d + slot * d + h * A->dh + e];
+        return OK;
+      }
+      if (slot == 3) return copy(A->bias_re, (uint64_t)A->heads * A->max_ctx * A->max_ctx, 8);
+      if (slot == 6) return copy(A->gamma, A->d_in, 16);
+      if (slot == 7) return copy(A->beta, A->d_in, 16);
+      break;
+    }
+    case K_FEED_FORWARD: {
+      auto* F = (FeedForwardLayer*)L;
+      if (slot == 0) return copy(F->w1, (uint64_t)F->d_in * F->hidden, 16);
+      if (slot == 1) return copy(F->w2, (uint64_t)F->hidden * F->d_out, 16);
+      if (slot == 4) return copy(F->b1, F->hidden, 16);
+      if (slot == 5) return copy(F->b2, F->d_out, 16);
+      break;
+    }
+    case K_LINEAR: {
+      auto* Ln = (LinearLayer*)L;
+      if (slot == 0) return copy(Ln->w, (uint64_t)Ln->d_in * Ln->d_out, 16);
+      if (slot == 4) return copy(Ln->b, Ln->d_out, 16);
+      break;
+    }
+  }
+  return fail(ERR_ARG, "layer %u has no tensor in slot %u", layer, slot);
+}
+
+int mitok_reset(mitok_network* n) {
+  if (!n) return fail(ERR_ARG, "null network");
+  n->cache_valid = false;
+  n->cache_B = 0;
+  n->kv_len_h.clear();
+  return OK;
+}
+
+static int validate_batch(const uint32_t* lens, uint32_t B, uint32_t S) {
+  if (!B || !S) return fail(ERR_ARG, "batch_ids is empty (transformer_network.rs:198-208)");
+  for (uint32_t b = 0; b < B; ++b)
+    if (!lens[b] || lens[b] > S) return fail(ERR_ARG, "lens[%u]=%u outside [1, %u]", b, lens[b], S);
+  return OK;
+}
+
+// Host-side part of a predict/forward call: mode, bounds, uploads.
+static int begin_call(Net* n, const uint32_t* lens, uint32_t B, uint32_t S, const uint32_t* ts, bool forward_only,
+                      bool hidden_path, Spec& sp, std::vector<uint32_t>& mask_h) {
+  sp.B = B;
+  sp.S = S;
+  sp.forward_only = forward_only;
+  const uint32_t mc = min_ctx(n);
+  if (mc != UINT32_MAX && S > mc) return fail(ERR_ARG, "sequence %u exceeds max context %u", S, mc);
+  if (forward_only && n->cache_valid) {
+    if (B != n->cache_B) return fail(ERR_STATE, "cached batch %u != %u; reset first", n->cache_B, B);
+    for (uint32_t b = 0; b < B; ++b)
+      if (n->kv_len_h[b] + 1 > mc) return fail(ERR_ARG, "context %u exceeds max context %u", n->kv_len_h[b] + 1, mc);
+    sp.mode = MODE_CACHED;
+  } else if (forward_only) {
+    sp.mode = MODE_PREFILL;
+  } else {
+    sp.mode = MODE_STATELESS;
+  }
+  TRY(prepare(n, sp));
+  if (sp.mode == MODE_PREFILL) TRY(alloc_caches(n, B));
+  const size_t rows = (size_t)B * S;
+  mask_h.assign(rows, 0);
+  std::vector<int> pos(rows);
+  for (uint32_t b = 0; b < B; ++b)
+    for (uint32_t s = 0; s < S; ++s) {
+      mask_h[(size_t)b * S + s] = s < lens[b] ? 1 : 0;
+      uint32_t t = ts ? ts[b] : 0;
+      pos[(size_t)b * S + s] = (forward_only && t > 0) ? (int)t : (int)s;  // positional_encoding_layer.rs:61-65
+    }
+  int maxpos = 0;
+  for (int p : pos) maxpos = std::max(maxpos, p);
+  TRY(ensure_rope_for(n, sp.first, sp.last, std::max(rope_positions_needed(n), maxpos + 1)));
+  TRY(upload(n, n->mask_d, mask_h.data(), rows * sizeof(uint32_t)));
+  TRY(upload(n, n->lens_d, lens, B * sizeof(uint32_t)));
+  TRY(upload(n, n->pos_d, pos.data(), rows * sizeof(int)));
+  sp.mask = n->mask_d.as<uint32_t>();
+  sp.lens = n->lens_d.as<uint32_t>();
+  sp.pos = n->pos_d.as<int>();
+  if (sp.mode == MODE_CACHED) {
+    std::vector<int> kv(n->kv_len_h.begin(), n->kv_len_h.end());
+    TRY(upload(n, n->kv_len_d, kv.data(), B * sizeof(int)));
+    if (S > 1) {
+      std::vector<int> kr(B);
+      for (uint32_t b = 0; b < B; ++b) kr[b] = (int)lens[b] - 1;  // the last token (masked_attention_head.rs:141-153)
+      TRY(upload(n, n->kv_row_d, kr.data(), B * sizeof(int)));
+      sp.kv_row = n->kv_row_d.as<int>();
+    }
+  }
+  (void)hidden_path;
+  HIP_TRY(hipStreamSynchronize(n->stream));  // the host staging vectors above go out of scope
+  return OK;
+}
+
+static void end_call(Net* n, const Spec& sp, const uint32_t* lens) {
+  if (sp.mode == MODE_PREFILL) {
+    n->cache_valid = true;
+    n->cache_B = sp.B;
+    n->kv_len_h.assign(lens, lens + sp.B);  // the cache keeps each sequence's own rows
+  } else if (sp.mode == MODE_CACHED) {
+    for (uint32_t b = 0; b < (uint32_t)sp.B; ++b) n->kv_len_h[b] += 1;
+  }
+}
+
+int mitok_predict(mitok_network* n, const uint32_t* ids, const uint32_t* lens, uint32_t B, uint32_t S,
+                  const uint32_t* time_steps, int forward_only, int last_row_only, double* out, uint32_t* out_mask) {
+  if (!n || !ids || !lens || !out) return fail(ERR_ARG, "null argument");
+  TRY(validate_batch(lens, B, S));
+  TRY(check_stack(n));
+  TRY(set_device(n));
+  Spec sp;
+  sp.first = 0;
+  sp.last = (uint32_t)n->layers.size();
+  sp.last_row = last_row_only && forward_only;
+  std::vector<uint32_t> mask_h;
+  TRY(begin_call(n, lens, B, S, time_steps, forward_only != 0, false, sp, mask_h));
+  const size_t rows = (size_t)B * S;
+  std::vector<uint32_t> padded(rows);
+  for (uint32_t b = 0; b < B; ++b)
+    for (uint32_t s = 0; s < S; ++s) padded[(size_t)b * S + s] = s < lens[b] ? ids[(size_t)b * S + s] : 1u;
+  TRY(upload(n, n->ids_d, padded.data(), rows * sizeof(uint32_t)));
+  sp.ids = n->ids_d.as<uint32_t>();
+  const uint32_t V = n->layers[n->layers.size() - 2]->d_out;
+  sp.out_re = n->logits_re.as<double>();
+  sp.out_prob = n->probs.as<double>();
+  TRY(enqueue_forward(n, sp));
+  if (forward_only) {
+    size_t cnt = (sp.last_row ? (size_t)B : rows) * V;
+    HIP_TRY(hipMemcpyAsync(out, sp.out_re, cnt * sizeof(double), hipMemcpyDeviceToHost, n->stream));
+    HIP_TRY(hipStreamSynchronize(n->stream));
+  } else {
+    std::vector<double> all(rows * V);
+    HIP_TRY(hipMemcpyAsync(all.data(), sp.out_prob, all.size() * sizeof(double), hipMemcpyDeviceToHost, n->stream));
+    HIP_TRY(hipStreamSynchronize(n->stream));
+    if (last_row_only)
+      for (uint32_t b = 0; b < B; ++b)
+        memcpy(out + (size_t)b * V, all.data() + ((size_t)b * S + lens[b] - 1) * V, V * sizeof(double));
+    else memcpy(out, all.data(), all.size() * sizeof(double));
+  }
+  collect_timing(n);
+  TRY(check_err_word(n));
+  end_call(n, sp, lens);
+  if (out_mask) memcpy(out_mask, mask_h.data(), rows * sizeof(uint32_t));
+  return OK;
+}
+
+int mitok_forward_layers(mitok_network* n, uint32_t first, uint32_t last, const double* in, const uint32_t* mask_in,
+                         uint32_t B, uint32_t S, const uint32_t* time_steps, int forward_only, double* out) {
+  if (!n || !in || !out || first >= last || last > n->layers.size()) return fail(ERR_ARG, "bad layer range");
+  if (!B || !S) return fail(ERR_ARG, "empty batch");
+  for (uint32_t li = first; li < last; ++li) {
+    int k = n->layers[li]->kind;
+    if (k == K_EMBEDDING || k == K_SOFTMAX) return fail(ERR_ARG, "layer %u is not a hidden-state layer", li);
+  }
+  TRY(set_device(n));
+  std::vector<uint32_t> lens(B);
+  for (uint32_t b = 0; b < B; ++b) {
+    uint32_t c = 0;
+    for (uint32_t s = 0; s < S; ++s) c += (mask_in ? mask_in[(size_t)b * S + s] : 1) ? 1 : 0;
+    lens[b] = c ? c : 1;
+  }
+  Spec sp;
+  sp.first = first;
+  sp.last = last;
+  std::vector<uint32_t> mask_h;
+  TRY(begin_call(n, lens.data(), B, S, time_steps, forward_only != 0, true, sp, mask_h));
+  const size_t rows = (size_t)B * S;
+  if (mask_in) {
+    TRY(upload(n, n->mask_d, mask_in, rows * sizeof(uint32_t)));
+  } else {
+    fill_u32(n->stream, n->mask_d.as<uint32_t>(), rows, 1);
+  }
+  const uint32_t din = n->layers[first]->d_in, dout = n->layers[last - 1]->d_out;
+  DevBuf xin, xout;
+  TRY(xin.reserve(rows * din * sizeof(double2)));
+  TRY(xout.reserve(rows * dout * sizeof(double2)));
+  HIP_TRY(hipMemcpyAsync(xin.p, in, rows * din * sizeof(double2), hipMemcpyHostToDevice, n->stream));
+  sp.in = xin.as<double2>();
+  sp.out_hidden = xout.as<double2>();
+  TRY(enqueue_forward(n, sp));
+  HIP_TRY(hipMemcpyAsync(out, xout.p, rows * dout * sizeof(double2), hipMemcpyDeviceToHost, n->stream));
+  HIP_TRY(hipStreamSynchronize(n->stream));
+  collect_timing(n);
+  TRY(check_err_word(n));
+  end_call(n, sp, lens.data());
+  return OK;
+}
+
+// One decode step for every sequence: embed the previous greedy ids, run the
+// stack with the cache, vocab Re-logits, greedy ids (+history), kv advance.
+static int enqueue_decode_step(Net* n, const Spec& sp, bool want_logits, uint32_t n_new) {
+  TRY(enqueue_forward(n, sp));
+  const uint32_t V = n->layers[n->layers.size() - 2]->d_out;
+  if (want_logits) store_logits(n->stream, sp.out_re, sp.B, V, n->logit_hist_d.as<double>(), n->cnt_d.as<int>());
+  argmax_rows(n->stream, sp.out_re, sp.B, V, n->dec_ids_d.as<uint32_t>(), n->hist_d.as<uint32_t>(), n_new,
+              n->cnt_d.as<int>(), n->kv_len_d.as<int>(), 1, n->err_d.as<uint32_t>());
+  return OK;
+}
+
+int mitok_generate(mitok_network* n, const uint32_t* prompt, const uint32_t* lens, uint32_t B, uint32_t S,
+                   uint32_t n_new, uint32_t* out_ids, double* out_logits) {
+  if (!n || !prompt || !lens || !out_ids) return fail(ERR_ARG, "null argument");
+  TRY(validate_batch(lens, B, S));
+  TRY(check_stack(n));
+  TRY(set_device(n));
+  if (n_new == 0) return OK;
+  const uint32_t mc = min_ctx(n);
+  for (uint32_t b = 0; b < B; ++b)
+    if (mc != UINT32_MAX && (uint64_t)lens[b] + n_new - 1 > mc)
+      return fail(ERR_ARG, "prompt %u + %u new tokens exceed max context %u", lens[b], n_new, mc);
+  TRY(mitok_reset(n));
+  hipStream_t st = n->stream;
+  const uint32_t V = n->layers[n->layers.size() - 2]->d_out;
+  const bool want_logits = out_logits != nullptr;
+
+  // workspaces for both shapes first, so nothing moves once the graph exists
+  Spec dec;
+  dec.B = B;
+  dec.S = 1;
+  dec.mode = MODE_CACHED;
+  dec.first = 0;
+  dec.last = (uint32_t)n->layers.size();
+  TRY(prepare(n, dec));
+  TRY(reserve(n, n->hist_d, (size_t)B * n_new * sizeof(uint32_t)));
+  TRY(reserve(n, n->cnt_d, (size_t)B * sizeof(int)));
+  if (want_logits) TRY(reserve(n, n->logit_hist_d, (size_t)n_new * B * V * sizeof(double)));
+
+  Spec pre;
+  pre.first = 0;
+  pre.last = (uint32_t)n->layers.size();
+  pre.last_row = true;
+  std::vector<uint32_t> mask_h;
+  TRY(begin_call(n, lens, B, S, nullptr, true, false, pre, mask_h));
+  TRY(ensure_rope_for(n, 0, pre.last, (int)std::max<uint32_t>(rope_positions_needed(n), S + n_new)));
+  std::vector<uint32_t> padded((size_t)B * S);
+  for (uint32_t b = 0; b < B; ++b)
+    for (uint32_t s = 0; s < S; ++s) padded[(size_t)b * S + s] = s < lens[b] ? prompt[(size_t)b * S + s] : 1u;
+  TRY(upload(n, n->ids_d, padded.data(), padded.size() * sizeof(uint32_t)));
+  // decode-shape buffers (prepare above may have been superseded by the prefill's larger shape)
+  TRY(prepare(n, dec));
+  pre.ids = n->ids_d.as<uint32_t>();
+  pre.out_re = n->logits_re.as<double>();
+  fill_int(st, n->cnt_d.as<int>(), B, 0);
+  fill_u32(st, n->ones_d.as<uint32_t>(), B, 1);
+
+  hipEvent_t ev[3];
+  for (auto& e : ev) HIP_TRY(hipEventCreate(&e));
+  HIP_TRY(hipEventRecord(ev[0], st));
+  // ---- prompt: full forward, vocab on each sequence's last row, first ids ----
+  TRY(enqueue_forward(n, pre));
+  if (want_logits) store_logits(st, pre.out_re, B, V, n->logit_hist_d.as<double>(), n->cnt_d.as<int>());
+  argmax_rows(st, pre.out_re, B, V, n->dec_ids_d.as<uint32_t>(), n->hist_d.as<uint32_t>(), n_new, n->cnt_d.as<int>(),
+              nullptr, 0, n->err_d.as<uint32_t>());
+  {
+    std::vector<int> kv(lens, lens + B);
+    HIP_TRY(hipMemcpyAsync(n->kv_len_d.p, kv.data(), B * sizeof(int), hipMemcpyHostToDevice, st));
+    HIP_TRY(hipStreamSynchronize(st));  // kv is a stack vector
+  }
+  HIP_TRY(hipEventRecord(ev[1], st));
+  end_call(n, pre, lens);
+
+  // ---- decode steps ----
+  dec.ids = n->dec_ids_d.as<uint32_t>();
+  dec.mask = n->ones_d.as<uint32_t>();
+  dec.lens = n->ones_d.as<uint32_t>();
+  dec.pos = nullptr;  // RoPE position = kv_len (the fed token's index)
+  dec.out_re = n->logits_re.as<double>();
+  bool used_graph = false;
+  if (n_new > 1) {
+    const bool direct = n->direct_launch || n->timing.cls != 0;
+    if (!direct) {
+      if (!n->graph || n->graph_B != B || n->graph_nnew != n_new || n->graph_logits != want_logits ||
+          n->graph_generation != n->ws_generation) {
+        drop_graph(n);
+        hipGraph_t g = nullptr;
+        HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+        int rc = enqueue_decode_step(n, dec, want_logits, n_new);
+        hipError_t ce = hipStreamEndCapture(st, &g);
+        if (rc) return rc;
+        if (ce != hipSuccess) return fail(ERR_HIP, "hipStreamEndCapture: %s", hipGetErrorString(ce));
+        hipError_t ie = hipGraphInstantiate(&n->graph, g, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(g);
+        if (ie != hipSuccess) return fail(ERR_HIP, "hipGraphInstantiate: %s", hipGetErrorString(ie));
+        n->graph_B = B;
+        n->graph_nnew = n_new;
+        n->graph_logits = want_logits;
+        n->graph_generation = n->ws_generation;
+      }
+      for (uint32_t t = 1; t < n_new; ++t) HIP_TRY(hipGraphLaunch(n->graph, st));
+      used_graph = true;
+    } else {
+      for (uint32_t t = 1; t < n_new; ++t) {
+        TimeScope ts(n, MITOK_TIME_STEP, 0.0);
+        TRY(enqueue_decode_step(n, dec, want_logits, n_new));
+      }
+    }
+  }
+  HIP_TRY(hipEventRecord(ev[2], st));
+  HIP_TRY(hipMemcpyAsync(out_ids, n->hist_d.p, (size_t)B * n_new * sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+  if (want_logits)
+    HIP_TRY(hipMemcpyAsync(out_logits, n->logit_hist_d.p, (size_t)n_new * B * V * sizeof(double), hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  float a = 0.f, b2 = 0.f;
+  (void)hipEventElapsedTime(&a, ev[0], ev[1]);
+  (void)hipEventElapsedTime(&b2, ev[1], ev[2]);
+  for (auto& e : ev) (void)hipEventDestroy(e);
+  n->last_t[0] = a;
+  n->last_t[1] = b2;
+  n->last_t[2] = used_graph ? 1.0 : 0.0;
+  collect_timing(n);
+  TRY(check_err_word(n));
+  for (uint32_t b = 0; b < B; ++b) n->kv_len_h[b] += n_new - 1;
+  return OK;
+}
+
+int mitok_greedy_decoding(mitok_network* n, const double* logits, uint32_t rows, uint32_t V, uint32_t* out_ids) {
+  if (!n || !logits || !out_ids || !rows || !V) return fail(ERR_ARG, "bad arguments");
+  TRY(set_device(n));
+  DevBuf lg, ids;
+  TRY(lg.reserve((size_t)rows * V * sizeof(double)));
+  TRY(ids.reserve((size_t)rows * sizeof(uint32_t)));
+  HIP_TRY(hipMemcpyAsync(lg.p, logits, (size_t)rows * V * sizeof(double), hipMemcpyHostToDevice, n->stream));
+  argmax_rows(n->stream, lg.as<double>(), rows, V, ids.as<uint32_t>(), nullptr, 0, nullptr, nullptr, 0,
+              n->err_d.as<uint32_t>());
+  HIP_TRY(hipMemcpyAsync(out_ids, ids.p, rows * sizeof(uint32_t), hipMemcpyDeviceToHost, n->stream));
+  HIP_TRY(hipStreamSynchronize(n->stream));
+  return check_err_word(n);
+}
+
+int mitok_last_timings(mitok_network* n, double* t3) {
+  if (!n || !t3) return fail(ERR_ARG, "null argument");
+  memcpy(t3, n->last_t, sizeof n->last_t);
+  return OK;
+}
+
+int mitok_timing_enable(mitok_network* n, int cls) {
+  if (!n) return fail(ERR_ARG, "null network");
+  collect_timing(n);
+  n->timing.cls = cls;
+  n->timing.total_ms = 0.0;
+  n->timing.bytes = 0.0;
+  n->timing.launches = 0;
+  return OK;
+}
+
+int mitok_timing_read(mitok_network* n, double* total_ms, uint64_t* launches, double* alg_bytes) {
+  if (!n) return fail(ERR_ARG, "null network");
+  collect_timing(n);
+  if (total_ms) *total_ms = n->timing.total_ms;
+  if (launches) *launches = n->timing.launches;
+  if (alg_bytes) *alg_bytes = n->timing.bytes;
+  return OK;
+}
+
+int mitok_set_graph_mode(mitok_network* n, int direct_launch) {
+  if (!n) return fail(ERR_ARG, "null network");
+  n->direct_launch = direct_launch;
+  return OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,292 @@
+"""GPU parity: the HIP path (libmitok.so through the C ABI) against the CPU oracle.
+
+Bar (north_star): generated token ids bit-exact, logits and hidden states
+within REL_TOL = 1e-9 max relative error (conftest.max_rel_err); seeded
+weights bit-exact.  Sizes are those the oracle finishes in seconds; the full
+batch-32 run is checked through batch independence (each sequence equals its
+own batch-1 run).
+"""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+import rustcrates_amd as ra
+from conftest import REL_TOL, max_rel_err
+from rustcrates_amd import configs, seeded
+
+pytestmark = pytest.mark.gpu
+
+
+def log(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _threads():
+    oracle.set_threads(16)
+
+
+def pair(cfg):
+    """(gpu network, oracle network) with identical seeded weights."""
+    return configs.build_network(ra.Network(0), cfg), configs.build_network(oracle.Network(), cfg)
+
+
+SMALL = configs.ModelConfig("small", layers=2, d=32, heads=4, ffn=64, vocab=211, max_ctx=64, seed=9)
+
+
+# ---------------------------------------------------------------------------
+# building blocks
+# ---------------------------------------------------------------------------
+def test_seeded_weights_bit_exact():
+    cfg = configs.C1
+    g, o = pair(cfg)
+    d, V, F, h, mc = cfg.d, cfg.vocab, cfg.ffn, cfg.heads, cfg.max_ctx
+    assert np.array_equal(g.get_tensor(0, 0, V * d), o.get_tensor(0, 0, V * d))
+    for slot in range(3):
+        assert np.array_equal(g.get_tensor(2, slot, h * d * (d // h)), o.get_tensor(2, slot, h * d * (d // h)))
+    bp = o.get_tensor(2, 3, h * mc * mc)
+    assert np.array_equal(g.get_tensor(2, 3, h * mc * mc), bp.real)
+    assert np.array_equal(g.get_tensor(3, 0, d * F), o.get_tensor(3, 0, d * F))
+    assert np.array_equal(g.get_tensor(3, 1, F * d), o.get_tensor(3, 1, F * d))
+    last = o.num_layers - 2
+    assert np.array_equal(g.get_tensor(last, 0, d * V), o.get_tensor(last, 0, d * V))
+
+
+def test_greedy_decoding_ties_nan():
+    g = ra.Network(0)
+    rows = np.array([[1.0, 3.0, 2.0, 3.0, 0.5], [-np.inf, -np.inf, -np.inf, -np.inf, -np.inf],
+                     [0.0, 0.0, 0.0, 0.0, 0.0], [5.0, 1.0, 1.0, 1.0, 1.0]])
+    assert list(g.greedy_decoding(rows)) == [3, 4, 4, 0]  # last index among equal maxima
+    big = np.zeros((3, 32000))
+    big[0, 17] = big[0, 31999] = 2.0
+    big[1, 100] = 1.0
+    big[2, :] = -1.0
+    assert list(g.greedy_decoding(big)) == [31999, 100, 31999]
+    bad = np.zeros((1, 10))
+    bad[0, 4] = np.nan
+    with pytest.raises(ra.MitokError) as e:
+        g.greedy_decoding(bad)
+    assert e.value.code == 4
+
+
+def _linear_net(W, b=None):
+    g = ra.Network(0)
+    K, N = W.shape
+    g.add_linear(K, N, W, b)
+    return g
+
+
+@pytest.mark.parametrize("M", [1, 3, 8, 16, 37, 130])
+def test_linear_integer_products_exact(M):
+    # the reference's zgemm known answers generalised: integer data is exact in f64
+    rng = np.random.default_rng(M)
+    K, N = 45, 70
+    A = (rng.integers(-8, 9, (M, K)) + 1j * rng.integers(-8, 9, (M, K))).astype(complex)
+    W = (rng.integers(-8, 9, (K, N)) + 1j * rng.integers(-8, 9, (K, N))).astype(complex)
+    g = _linear_net(W, np.zeros(N, complex))
+    log(f"linear exact M={M}")
+    out = g.forward_layers(0, 1, A.reshape(1, M, K), forward_only=False, d_out=N)
+    assert np.array_equal(out[0], A @ W)
+
+
+def test_linear_reference_known_answer():
+    # utils/tests.rs:75-114 (3x2 * 2x6) through a LinearLayer with zero bias
+    a = np.array([[1, 2], [3, 4], [5, 6]], dtype=complex)
+    w = np.array([[1, 2, 3, 4, 5, 6], [7, 8, 9, 10, 11, 12]], dtype=complex)
+    g = _linear_net(w, np.zeros(6, complex))
+    out = g.forward_layers(0, 1, a.reshape(1, 3, 2), forward_only=False, d_out=6)
+    assert np.array_equal(out[0].real, [[15, 18, 21, 24, 27, 30], [31, 38, 45, 52, 59, 66], [47, 58, 69, 80, 91, 102]])
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 512, 1536), (2, 300, 77), (8, 2048, 512), (32, 512, 2048), (100, 96, 130),
+                                   (4096, 64, 64)])
+def test_gemm_random_vs_oracle(M, K, N):
+    rng = np.random.default_rng(M * 7 + K)
+    A = rng.standard_normal((M, K)) + 1j * rng.standard_normal((M, K))
+    W = rng.standard_normal((K, N)) + 1j * rng.standard_normal((K, N))
+    bias = rng.standard_normal(N) + 1j * rng.standard_normal(N)
+    g = _linear_net(W, bias)
+    log(f"gemm M={M} K={K} N={N}")
+    out = g.forward_layers(0, 1, A.reshape(1, M, K), forward_only=False, d_out=N)[0]
+    want = oracle.zgemm(A, W) + bias
+    assert max_rel_err(out, want) < 1e-12
+
+
+# ---------------------------------------------------------------------------
+# layers and the model
+# ---------------------------------------------------------------------------
+def test_c2_single_layer_forward():
+    """Config 2: one layer (Norm -> SelfAttention -> FeedForward), hidden states N(0,1), B8 x S256."""
+    cfg = configs.C2
+    g = ra.Network(0)
+    o = oracle.Network()
+    for net in (g, o):
+        net.add_norm(cfg.d, cfg.norm_eps)
+        net.add_self_attention(cfg.heads, cfg.d, cfg.max_ctx, cfg.attn_eps)
+        net.add_feed_forward(cfg.d, cfg.ffn)
+        net.init_seeded(cfg.seed)
+    x = seeded.normal(1, (8, 256, cfg.d))
+    log("c2 gpu forward")
+    got = g.forward_layers(0, 3, x, forward_only=False)
+    log("c2 oracle forward")
+    want = o.forward_layers(0, 3, x, forward_only=False)
+    err = max_rel_err(got, want)
+    log(f"c2 max rel err {err:.3e}")
+    assert err < REL_TOL
+
+
+def test_small_model_predict_all_rows_and_softmax_modes():
+    g, o = pair(SMALL)
+    lens = [7, 12, 4]
+    ids = seeded.prompts(5, lens, SMALL.vocab)
+    lg, mg = g.predict(ids, lens, forward_only=True)
+    lo, mo = o.predict(ids, lens, forward_only=True)
+    assert np.array_equal(mg, mo)
+    assert max_rel_err(lg, lo) < REL_TOL
+    # stateless forward with the PRODUCTION softmax (softmax_last_row)
+    pg, _ = g.predict(ids, lens, forward_only=False)
+    po, _ = o.predict(ids, lens, forward_only=False)
+    assert max_rel_err(pg, po) < REL_TOL
+
+
+def test_training_mode_softmax_padded_rows():
+    cfg = SMALL
+    g, o = ra.Network(0), oracle.Network()
+    for net in (g, o):
+        net.add_embedding(cfg.vocab, cfg.d)
+        net.add_norm(cfg.d, 1e-5)
+        net.add_self_attention(cfg.heads, cfg.d, cfg.max_ctx)
+        net.add_feed_forward(cfg.d, cfg.ffn)
+        net.add_linear(cfg.d, cfg.vocab)
+        net.add_softmax(ra.TRAINING)
+        net.init_seeded(4)
+    lens = [9, 3]
+    ids = seeded.prompts(6, lens, cfg.vocab)
+    pg, _ = g.predict(ids, lens, forward_only=False)
+    po, _ = o.predict(ids, lens, forward_only=False)
+    assert np.all(pg[1, 3:] == 0.0)
+    assert max_rel_err(pg, po) < REL_TOL
+
+
+def test_c1_generate_parity():
+    cfg = configs.C1
+    w = configs.WORKLOADS["c1"]
+    g, o = pair(cfg)
+    prompt = seeded.prompts(0, [w.prompt_len], cfg.vocab)
+    ig, lg = g.generate(prompt, n_new=w.n_new, want_logits=True)
+    io, lo = o.generate(prompt, n_new=w.n_new, want_logits=True)
+    log(f"c1 ids {ig[0][:8]} err {max_rel_err(lg, lo):.3e}")
+    assert np.array_equal(ig, io)
+    assert max_rel_err(lg, lo) < REL_TOL
+
+
+def test_graph_replay_equals_direct_launch():
+    g = configs.build_network(ra.Network(0), SMALL)
+    prompt = seeded.prompts(2, [10], SMALL.vocab)
+    i1, l1 = g.generate(prompt, n_new=12, want_logits=True)
+    assert g.last_timings()["graph"]
+    i2, l2 = g.generate(prompt, n_new=12, want_logits=True)  # replays the cached graph
+    g.set_graph_mode(True)
+    i3, l3 = g.generate(prompt, n_new=12, want_logits=True)
+    assert not g.last_timings()["graph"]
+    assert np.array_equal(i1, i2) and np.array_equal(i1, i3)
+    assert np.array_equal(l1, l2) and np.array_equal(l1, l3)
+
+
+def test_rope_model_parity():
+    cfg = configs.ModelConfig("rope", layers=2, d=64, heads=4, ffn=128, vocab=500, max_ctx=96, seed=12, rope=True)
+    g, o = pair(cfg)
+    prompt = seeded.prompts(3, [20], cfg.vocab)
+    ig, lg = g.generate(prompt, n_new=24, want_logits=True)
+    io, lo = o.generate(prompt, n_new=24, want_logits=True)
+    assert np.array_equal(ig, io)
+    assert max_rel_err(lg, lo) < REL_TOL
+
+
+def test_cached_predict_with_several_rows():
+    """The reference's cached branch with S > 1: q for every row, K/V only for the
+    last token, causal mask applied modulo S (masked_attention_head.rs:140-203)."""
+    g, o = pair(SMALL)
+    ids = seeded.prompts(8, [9], SMALL.vocab)
+    for net in (g, o):
+        net.reset()
+    a_g, _ = g.predict(ids[:, :5], forward_only=True)
+    a_o, _ = o.predict(ids[:, :5], forward_only=True)
+    b_g, _ = g.predict(ids[:, 5:9], time_steps=[5], forward_only=True)
+    b_o, _ = o.predict(ids[:, 5:9], time_steps=[5], forward_only=True)
+    assert max_rel_err(a_g, a_o) < REL_TOL
+    assert max_rel_err(b_g, b_o) < REL_TOL
+
+
+def test_ragged_batch_generate_parity():
+    cfg = configs.ModelConfig("rag", layers=2, d=64, heads=4, ffn=256, vocab=1000, max_ctx=80, seed=13)
+    g, o = pair(cfg)
+    lens = [17, 40, 5, 33]
+    prompt = seeded.prompts(4, lens, cfg.vocab)
+    ig, lg = g.generate(prompt, lens=lens, n_new=20, want_logits=True)
+    io, lo = o.generate(prompt, lens=lens, n_new=20, want_logits=True)
+    assert np.array_equal(ig, io)
+    assert max_rel_err(lg, lo) < REL_TOL
+
+
+def test_c3_batch1_generate_parity():
+    cfg = configs.C3
+    w = configs.WORKLOADS["c3b1"]
+    g, o = pair(cfg)
+    prompt = seeded.prompts(0, [w.prompt_len], cfg.vocab)
+    log("c3 b1 gpu generate")
+    ig, lg = g.generate(prompt, n_new=w.n_new, want_logits=True)
+    log("c3 b1 oracle generate")
+    io, lo = o.generate(prompt, n_new=w.n_new, want_logits=True)
+    err = max_rel_err(lg, lo)
+    log(f"c3 b1 max rel err {err:.3e}; ids match {np.array_equal(ig, io)}")
+    assert np.array_equal(ig, io)
+    assert err < REL_TOL
+
+
+def test_c3_ragged_subset_vs_oracle():
+    cfg = configs.C3
+    g, o = pair(cfg)
+    lens = [128, 77, 100]
+    prompt = seeded.prompts(1, lens, cfg.vocab)
+    ig, lg = g.generate(prompt, lens=lens, n_new=12, want_logits=True)
+    io, lo = o.generate(prompt, lens=lens, n_new=12, want_logits=True)
+    assert np.array_equal(ig, io)
+    assert max_rel_err(lg, lo) < REL_TOL
+
+
+def test_c3_batch32_equals_batch1_runs():
+    cfg = configs.C3
+    w = configs.WORKLOADS["c3b32"]
+    g = configs.build_network(ra.Network(0), cfg)
+    prompt = seeded.prompts(0, [w.prompt_len] * w.batch, cfg.vocab)
+    log("c3 b32 generate")
+    ids, lg = g.generate(prompt, n_new=w.n_new, want_logits=True)
+    for b in (0, 13, 31):
+        i1, l1 = g.generate(prompt[b:b + 1], n_new=w.n_new, want_logits=True)
+        assert np.array_equal(i1[0], ids[b])
+        assert max_rel_err(l1[:, 0], lg[:, b]) < REL_TOL
+
+
+# ---------------------------------------------------------------------------
+# error paths (reference panics -> status codes)
+# ---------------------------------------------------------------------------
+def test_unknown_token_id_is_an_error():
+    g = configs.build_network(ra.Network(0), SMALL)
+    with pytest.raises(ra.MitokError) as e:
+        g.predict(np.array([[3, SMALL.vocab + 5]], np.uint32))
+    assert e.value.code == 1
+
+
+def test_context_overflow_is_an_error():
+    g = configs.build_network(ra.Network(0), SMALL)
+    prompt = seeded.prompts(1, [60], SMALL.vocab)
+    with pytest.raises(ra.MitokError):
+        g.generate(prompt, n_new=10)  # 60 + 9 cached > max_ctx 64
+    ids = g.generate(prompt, n_new=5)  # the network stays usable
+    assert ids.shape == (1, 5)

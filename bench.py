@@ -1,0 +1,205 @@
+"""Benchmark of the greedy token loop (predict_token_by_token on ids) on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3b32] [--no-cpu]
+
+One step is one full mitok_generate call on the workload: the prompt forward
+of every sequence plus (n_new - 1) cached decode steps, greedy ids chosen on
+the device, only ids copied back.  Inputs (seeded weights, prompts) are
+resident before the timed region.  The timed region is bracketed by device
+synchronisation; `value` is generated tokens per second (batch x n_new per
+step).  Prints ONE JSON line.
+
+Besides the timed region the run measures, with HIP events on the library's
+stream, the average duration of the dominant kernel class (roofline), and
+times the CPU oracle on a bounded sample of the same workload (cpu_baseline).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+import rustcrates_amd as ra  # noqa: E402
+from rustcrates_amd import configs, seeded  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
+FP64_MFMA_PEAK_TFS = 78.6  # MI355X dense FP64 matrix, TFLOP/s
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def workload_prompt(w):
+    lens = configs.prompt_lengths(w)
+    return seeded.prompts(w.prompt_seed, lens, w.model.vocab, max_len=w.prompt_len), np.array(lens, np.uint32)
+
+
+def time_generate(net, prompt, lens, n_new, steps, warmup):
+    for _ in range(warmup):
+        net.generate(prompt, lens=lens, n_new=n_new)
+    ra.device_synchronize(0)
+    t0 = time.perf_counter()
+    pre = dec = 0.0
+    ids = None
+    for _ in range(steps):
+        ids = net.generate(prompt, lens=lens, n_new=n_new)
+        t = net.last_timings()
+        pre += t["prefill_ms"]
+        dec += t["decode_ms"]
+    ra.device_synchronize(0)
+    wall = time.perf_counter() - t0
+    return wall, pre / steps, dec / steps, ids
+
+
+def kernel_class(net, prompt, lens, n_new, cls, reps=2):
+    """HIP-event totals of one kernel class over `reps` generate calls (direct launches)."""
+    net.timing_enable(cls)
+    for _ in range(reps):
+        net.generate(prompt, lens=lens, n_new=n_new)
+    r = net.timing_read()
+    net.timing_enable(0)
+    return r
+
+
+def roofline_entry(r, bound):
+    n = max(r["launches"], 1)
+    avg_s = r["total_ms"] / n / 1e3
+    if bound == "hbm":
+        achieved = r["alg_bytes"] / n / avg_s / 1e9
+        peak, unit = HBM_PEAK_GBS, "GB/s"
+    else:
+        achieved = r["alg_flops"] / n / avg_s / 1e12
+        peak, unit = FP64_MFMA_PEAK_TFS, "TFLOP/s"
+    return {"bound": bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4), "traffic": None, "avg_launch_us": round(avg_s * 1e6, 3),
+            "launches": r["launches"], "alg_bytes_per_launch": r["alg_bytes"] / n,
+            "alg_flops_per_launch": r["alg_flops"] / n}
+
+
+def cpu_baseline(w, budget_s=20.0):
+    """The CPU oracle (a port of the reference's forward, OpenMP over the
+    reference's rayon axes) on the first sequences of the same workload."""
+    import oracle
+
+    threads = min(16, os.cpu_count() or 1)
+    oracle.set_threads(threads)
+    cfg = w.model
+    o = configs.build_network(oracle.Network(), cfg)
+    prompt, lens = workload_prompt(w)
+    nseq, n_new = 1, w.n_new
+    t0 = time.perf_counter()
+    o.generate(prompt[:1], lens=lens[:1], n_new=n_new)
+    t1 = time.perf_counter() - t0
+    if t1 < budget_s / 3 and w.batch > 1:
+        nseq = int(min(w.batch, max(1, budget_s // max(t1, 1e-3))))
+        t0 = time.perf_counter()
+        o.generate(prompt[:nseq], lens=lens[:nseq], n_new=n_new)
+        t1 = time.perf_counter() - t0
+    o.close()
+    return {"value": round(nseq * n_new / t1, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{nseq} of {w.batch} sequences, full prompt + {n_new} greedy tokens, {t1:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--workload", default="c3b32", choices=sorted(configs.WORKLOADS))
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--no-b1", action="store_true", help="skip the batch-1 companion measurement")
+    ap.add_argument("--direct", action="store_true",
+                    help="launch decode kernels directly instead of replaying HIP graphs (for profilers)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(sequences shard data-parallel with no exchange; only the one-GPU share is built)", file=sys.stderr)
+        sys.exit(2)
+
+    w = configs.WORKLOADS[args.workload]
+    cfg = w.model
+    log(f"workload {args.workload}: building seeded network")
+    net = configs.build_network(ra.Network(0), cfg)
+    net.set_graph_mode(args.direct)
+    prompt, lens = workload_prompt(w)
+    B, n_new = w.batch, w.n_new
+
+    log(f"timing {args.steps} steps after {args.warmup} warmup")
+    wall, pre_ms, dec_ms, _ = time_generate(net, prompt, lens, n_new, args.steps, args.warmup)
+    ms_step = wall / args.steps * 1e3
+    tokens = B * n_new
+    value = tokens * args.steps / wall
+    decode_tok_s = B * (n_new - 1) / (dec_ms / 1e3) if dec_ms > 0 else None
+
+    # roofline of the dominant kernel classes, HIP events on the library stream
+    log("kernel-class timing")
+    classes = {}
+    for name, cls, bound in (("vocab", ra.TIME_VOCAB, None), ("layer_gemm", ra.TIME_LAYER_GEMM, None),
+                             ("attention", ra.TIME_ATTENTION, None)):
+        classes[name] = kernel_class(net, prompt, lens, n_new, cls)
+    dominant = max(("vocab", "layer_gemm"), key=lambda k: classes[k]["total_ms"])
+    r = classes[dominant]
+    # a GEMM class is MFMA-bound when its arithmetic intensity exceeds the ridge point
+    intensity = r["alg_flops"] / max(r["alg_bytes"], 1.0)
+    bound = "mfma" if intensity > FP64_MFMA_PEAK_TFS * 1e12 / (HBM_PEAK_GBS * 1e9) else "hbm"
+    roof = roofline_entry(r, bound)
+    roof["kernel_class"] = dominant
+    class_ms = {k: round(v["total_ms"] / 2, 3) for k, v in classes.items()}
+
+    out = {
+        "metric": "generated tokens/s",
+        "value": round(value, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "c128",
+        "data": "synthetic (seeded Xavier-uniform weights, uniform-random prompt ids)",
+        "config": {"workload": args.workload, "layers": cfg.layers, "d_model": cfg.d, "heads": cfg.heads,
+                   "ffn": cfg.ffn, "vocab": cfg.vocab, "batch": B, "prompt_len": w.prompt_len,
+                   "n_new": n_new, "parallelism": "single GPU"},
+        "prefill_ms": round(pre_ms, 3),
+        "decode_ms": round(dec_ms, 3),
+        "decode_tokens_per_s": round(decode_tok_s, 2) if decode_tok_s else None,
+        "kernel_class_ms_per_step": class_ms,
+        "roofline": roof,
+    }
+
+    if not args.no_b1 and B > 1 and args.workload.startswith("c3"):
+        log("batch-1 companion")
+        w1 = configs.WORKLOADS["c3b1"]
+        p1, l1 = workload_prompt(w1)
+        wall1, pre1, dec1, _ = time_generate(net, p1, l1, w1.n_new, max(3, args.steps), 1)
+        rv = kernel_class(net, p1, l1, w1.n_new, ra.TIME_VOCAB)
+        out["batch1"] = {
+            "tokens_per_s": round(w1.n_new * max(3, args.steps) / wall1, 2),
+            "decode_tokens_per_s": round((w1.n_new - 1) / (dec1 / 1e3), 2),
+            "decode_ms_per_token": round(dec1 / (w1.n_new - 1), 4),
+            "prefill_ms": round(pre1, 3),
+            "vocab_roofline": roofline_entry(rv, "hbm"),
+        }
+        # whole decode step against the HBM roofline: weights + KV + bias rows per token
+        step_bytes = 16.0 * cfg.weight_elems() + 16.0 * cfg.vocab  # weights + bias vector
+        out["batch1"]["decode_step_hbm_frac"] = round(step_bytes / (dec1 / (w1.n_new - 1) / 1e3) / 1e9 / HBM_PEAK_GBS, 4)
+
+    if not args.no_cpu:
+        log("cpu baseline (oracle)")
+        out["cpu_baseline"] = cpu_baseline(w)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -132,8 +132,11 @@ int mitok_last_timings(mitok_network* net, double* t3);
 /* HIP-event timing of one kernel class during the following calls (0 disables;
  * decode steps then run without graph replay so each launch is bracketed). */
 int mitok_timing_enable(mitok_network* net, int kernel_class);
-/* Accumulated since enable: total ms, launches, algorithmic HBM bytes of those launches. */
-int mitok_timing_read(mitok_network* net, double* total_ms, uint64_t* launches, double* alg_bytes);
+/* Accumulated since enable: total ms, launches, and the algorithmic HBM bytes
+ * and real flops of those launches (any pointer may be NULL). */
+int mitok_timing_read(mitok_network* net, double* total_ms, uint64_t* launches, double* alg_bytes, double* alg_flops);
+/* hipDeviceSynchronize on `device` (bench brackets its timed region with it). */
+int mitok_device_synchronize(int device);
 /* 0 = replay decode steps as HIP graphs (default), 1 = launch kernels directly. */
 int mitok_set_graph_mode(mitok_network* net, int direct_launch);
 

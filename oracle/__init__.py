@@ -70,6 +70,7 @@ def _load():
         "orc_get_tensor": (i32, [P, u32, u32, P, u64]),
         "orc_reset": (i32, [P]),
         "orc_set_threads": (None, [i32]),
+        "orc_set_gemm_order": (None, [i32]),
         "orc_predict": (i32, [P, P, P, u32, u32, P, i32, i32, P, P]),
         "orc_forward_layers": (i32, [P, u32, u32, P, P, u32, u32, P, i32, P]),
         "orc_generate": (i32, [P, P, P, u32, u32, u32, P, P]),
@@ -106,6 +107,13 @@ def _check(rc):
 
 def set_threads(n: int) -> None:
     lib().orc_set_threads(int(n))
+
+
+def set_gemm_order(order: int) -> None:
+    """0: zgemm sums k ascending (default); 1: k descending; 2: eight k chunks
+    summed separately then combined.  All are valid restatements of OpenBLAS
+    zgemm_, whose order is unspecified."""
+    lib().orc_set_gemm_order(int(order))
 
 
 # ---- scalar / row helpers (for pinning tests) ----

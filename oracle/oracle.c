@@ -120,14 +120,43 @@ oc64 orc_gelu(oc64 z, int* nan_flag) {
 /* One output row of multiply_complex: acc[j] = sum_k a[k] * B[k][j], each sum a
  * sequential complex fold from 0 in k order (zgemm_ alpha=1, beta=0;
  * utils/matrix.rs:16-65). */
-static void zgemm_row(uint32_t n, uint32_t k, const oc64* a, const oc64* B, oc64* c) {
+/* 0: k ascending (default), 1: k descending, 2: k split into 8 contiguous
+ * chunks, each summed ascending, the 8 partials then summed in order */
+static int g_gemm_order = 0;
+
+static void zgemm_range(uint32_t n, uint32_t k0, uint32_t k1, int desc, const oc64* a, const oc64* B, oc64* c) {
   for (uint32_t j = 0; j < n; ++j) c[j] = (oc64){0.0, 0.0};
-  for (uint32_t kk = 0; kk < k; ++kk) {
+  for (uint32_t i = k0; i < k1; ++i) {
+    const uint32_t kk = desc ? k0 + k1 - 1 - i : i;
     const oc64 av = a[kk];
     const oc64* b = B + (size_t)kk * n;
     for (uint32_t j = 0; j < n; ++j) c[j] = c_add(c[j], c_mul(av, b[j]));
   }
 }
+
+static void zgemm_row(uint32_t n, uint32_t k, const oc64* a, const oc64* B, oc64* c) {
+  if (g_gemm_order != 2) {
+    zgemm_range(n, 0, k, g_gemm_order == 1, a, B, c);
+    return;
+  }
+  enum { P = 8 };
+  oc64* part = (oc64*)malloc(sizeof(oc64) * n);
+  for (uint32_t j = 0; j < n; ++j) c[j] = (oc64){0.0, 0.0};
+  const uint32_t chunk = (k + P - 1) / P;
+  for (uint32_t p = 0; p < P; ++p) {
+    uint32_t k0 = p * chunk, k1 = k0 + chunk < k ? k0 + chunk : k;
+    if (k0 >= k1) break;
+    zgemm_range(n, k0, k1, 0, a, B, part);
+    for (uint32_t j = 0; j < n; ++j) c[j] = c_add(c[j], part[j]);
+  }
+  free(part);
+}
+
+/* OpenBLAS fixes no summation order for zgemm_ (its kernels block and fuse
+ * differently per CPU), so any order is an equally valid restatement of
+ * utils/matrix.rs:16-65.  Orders 1 and 2 exist to measure the reference's
+ * own rounding noise floor: the spread between valid orders. */
+void orc_set_gemm_order(int order) { g_gemm_order = (order == 1 || order == 2) ? order : 0; }
 
 static void zgemm_serial(uint32_t m, uint32_t n, uint32_t k, const oc64* A, const oc64* B, oc64* C) {
   for (uint32_t i = 0; i < m; ++i) zgemm_row(n, k, A + (size_t)i * k, B, C + (size_t)i * n);

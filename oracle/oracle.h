@@ -91,6 +91,9 @@ int orc_init_seeded(orc_net* net, uint64_t seed);
 int orc_get_tensor(const orc_net* net, uint32_t layer, uint32_t slot, oc64* out, uint64_t n);
 int orc_reset(orc_net* net);
 void orc_set_threads(int n);
+/* zgemm summation order: 0 k ascending (default); 1 k descending; 2 eight
+ * contiguous k chunks summed separately, then combined (noise-floor measurement) */
+void orc_set_gemm_order(int order);
 
 /* predict (transformer_network.rs:315-504).  ids [B][S] right-padded (entries
  * at or beyond lens[b] are replaced by PAD=1).  time_steps [B] or NULL.

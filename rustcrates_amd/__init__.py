@@ -54,7 +54,8 @@ SIGNATURES = {
     "mitok_greedy_decoding": (_i32, [_P, _P, _u32, _u32, _P]),
     "mitok_last_timings": (_i32, [_P, _P]),
     "mitok_timing_enable": (_i32, [_P, _i32]),
-    "mitok_timing_read": (_i32, [_P, _P, _P, _P]),
+    "mitok_timing_read": (_i32, [_P, _P, _P, _P, _P]),
+    "mitok_device_synchronize": (_i32, [_i32]),
     "mitok_set_graph_mode": (_i32, [_P, _i32]),
 }
 
@@ -94,6 +95,11 @@ def _ptr(a):
 
 def _c128(a):
     return None if a is None else np.ascontiguousarray(a, dtype=np.complex128)
+
+
+def device_synchronize(device: int = 0) -> None:
+    """hipDeviceSynchronize on `device`."""
+    _check(load_library().mitok_device_synchronize(device))
 
 
 def device_count() -> int:
@@ -218,9 +224,9 @@ class Network:
         _check(self._lib.mitok_timing_enable(self._h, kernel_class))
 
     def timing_read(self):
-        ms, n, b = C.c_double(), C.c_uint64(), C.c_double()
-        _check(self._lib.mitok_timing_read(self._h, C.byref(ms), C.byref(n), C.byref(b)))
-        return {"total_ms": ms.value, "launches": n.value, "alg_bytes": b.value}
+        ms, n, b, f = C.c_double(), C.c_uint64(), C.c_double(), C.c_double()
+        _check(self._lib.mitok_timing_read(self._h, C.byref(ms), C.byref(n), C.byref(b), C.byref(f)))
+        return {"total_ms": ms.value, "launches": n.value, "alg_bytes": b.value, "alg_flops": f.value}
 
     def set_graph_mode(self, direct_launch: bool):
         _check(self._lib.mitok_set_graph_mode(self._h, int(direct_launch)))

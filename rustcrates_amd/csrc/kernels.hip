@@ -150,7 +150,8 @@ __global__ __launch_bounds__(256) void k_reduce_epi_re(const double* __restrict_
 // a wave issues 4 v_mfma_f64_16x16x4_f64 per output tile:
 //     Cr += Ar*Br;  Cr += (-Ai)*Bi;  Ci += Ar*Bi;  Ci += Ai*Br
 // Lane layout of v_mfma_f64_16x16x4_f64 (wave64): A[i][k] at lane i+16k,
-// B[k][j] at lane j+16k, D[i][j] at lane j+16*(i/4), element i%4.
+// B[k][j] at lane j+16k, D[i][j] at lane j+16*(i%4), element i/4 (unlike the
+// f32 16x16x4 form, consecutive output rows sit in consecutive lane groups).
 // ===========================================================================
 constexpr int GBM = 64, GBN = 64, GBK = 16, GPAD = 4;
 
@@ -234,7 +235,7 @@ __global__ __launch_bounds__(256) void k_zgemm_mfma(const double2* __restrict__ 
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int m = m0 + wm + 16 * i + 4 * (lane >> 4) + r;
+        const int m = m0 + wm + 16 * i + (lane >> 4) + 4 * r;
         const int n = n0 + wn + 16 * j + (lane & 15);
         if (m < M && n < N) {
           double2 v = make_double2(cr[i][j][r], ci[i][j][r]);

@@ -164,7 +164,8 @@ struct Timing {
   std::vector<std::pair<hipEvent_t, hipEvent_t>> pending;
   std::vector<double> pending_bytes;
   std::vector<hipEvent_t> pool;
-  double total_ms = 0.0, bytes = 0.0;
+  std::vector<double> pending_flops;
+  double total_ms = 0.0, bytes = 0.0, flops = 0.0;
   uint64_t launches = 0;
 };
 
@@ -255,8 +256,9 @@ struct TimeScope {
   Net* n;
   bool on;
   hipEvent_t a = nullptr;
-  double bytes;
-  TimeScope(Net* net, int cls, double alg_bytes) : n(net), on(net->timing.cls == cls), bytes(alg_bytes) {
+  double bytes, flops;
+  TimeScope(Net* net, int cls, double alg_bytes, double alg_flops = 0.0)
+      : n(net), on(net->timing.cls == cls), bytes(alg_bytes), flops(alg_flops) {
     if (on) {
       a = take_event(n->timing);
       (void)hipEventRecord(a, n->stream);
@@ -268,6 +270,7 @@ struct TimeScope {
     (void)hipEventRecord(b, n->stream);
     n->timing.pending.push_back({a, b});
     n->timing.pending_bytes.push_back(bytes);
+    n->timing.pending_flops.push_back(flops);
   }
 };
 
@@ -278,6 +281,7 @@ static void collect_timing(Net* n) {
     if (hipEventElapsedTime(&ms, t.pending[i].first, t.pending[i].second) == hipSuccess) {
       t.total_ms += ms;
       t.bytes += t.pending_bytes[i];
+      t.flops += t.pending_flops[i];
       t.launches++;
     }
     t.pool.push_back(t.pending[i].first);
@@ -285,11 +289,15 @@ static void collect_timing(Net* n) {
   }
   t.pending.clear();
   t.pending_bytes.clear();
+  t.pending_flops.clear();
 }
 
+// algorithmic HBM bytes of C[M][N] = A[M][K] * B[K][N]: B once, A once, C once
 static double gemm_bytes(long M, long N, long K, bool re_out) {
   return 16.0 * (double)K * N + 16.0 * (double)M * K + (re_out ? 8.0 : 16.0) * (double)M * N;
 }
+// real flops of a complex product: 4 multiplies + 4 adds per complex MAC
+static double gemm_flops(long M, long N, long K) { return 8.0 * (double)M * N * K; }
 
 // ---------------------------------------------------------------------------
 // workspace sizing for one forward shape
@@ -389,8 +397,8 @@ static int enqueue_forward(Net* n, const Spec& sp) {
   const int B = sp.B, S = sp.S, rows = B * S;
   double2* cur = n->act0.as<double2>();
   double2* nxt = n->act1.as<double2>();
-  if (sp.first > 0) HIP_TRY(hipMemcpyAsync(cur, sp.in, (size_t)rows * n->layers[sp.first]->d_in * sizeof(double2),
-                                          hipMemcpyDeviceToDevice, st));
+  if (sp.in) HIP_TRY(hipMemcpyAsync(cur, sp.in, (size_t)rows * n->layers[sp.first]->d_in * sizeof(double2),
+                                   hipMemcpyDeviceToDevice, st));
   for (uint32_t li = sp.first; li < sp.last; ++li) {
     Layer* L = n->layers[li].get();
     switch (L->kind) {
@@ -448,7 +456,7 @@ static int enqueue_forward(Net* n, const Spec& sp) {
           }
         }
         {
-          TimeScope ts(n, MITOK_TIME_LAYER_GEMM, gemm_bytes(rows, 3 * d, d, false));
+          TimeScope ts(n, MITOK_TIME_LAYER_GEMM, gemm_bytes(rows, 3 * d, d, false), gemm_flops(rows, 3 * d, d));
           gemm(st, rows, 3 * d, d, cur, d, A->wqkv.as<double2>(), 3 * d, e, n->gemm_ws.p);
         }
         a.kc = e.kc;
@@ -490,11 +498,13 @@ static int enqueue_forward(Net* n, const Spec& sp) {
         e2.check_finite = 1;
         e2.err = err;
         {
-          TimeScope ts(n, MITOK_TIME_LAYER_GEMM, gemm_bytes(rows, F->hidden, F->d_in, false));
+          TimeScope ts(n, MITOK_TIME_LAYER_GEMM, gemm_bytes(rows, F->hidden, F->d_in, false),
+                       gemm_flops(rows, F->hidden, F->d_in));
           gemm(st, rows, F->hidden, F->d_in, cur, F->d_in, F->w1.as<double2>(), F->hidden, e1, n->gemm_ws.p);
         }
         {
-          TimeScope ts(n, MITOK_TIME_LAYER_GEMM, gemm_bytes(rows, F->d_out, F->hidden, false));
+          TimeScope ts(n, MITOK_TIME_LAYER_GEMM, gemm_bytes(rows, F->d_out, F->hidden, false),
+                       gemm_flops(rows, F->d_out, F->hidden));
           gemm(st, rows, F->d_out, F->hidden, n->hbuf.as<double2>(), F->hidden, F->w2.as<double2>(), F->d_out, e2,
                n->gemm_ws.p);
         }
@@ -529,7 +539,7 @@ static int enqueue_forward(Net* n, const Spec& sp) {
         if (sp.forward_only) {
           e.mode = EPI_RE;
           e.out_re = sp.out_re;
-          TimeScope ts(n, MITOK_TIME_VOCAB, gemm_bytes(M, Ln->d_out, Ln->d_in, true));
+          TimeScope ts(n, MITOK_TIME_VOCAB, gemm_bytes(M, Ln->d_out, Ln->d_in, true), gemm_flops(M, Ln->d_out, Ln->d_in));
           gemm(st, M, Ln->d_out, Ln->d_in, x, Ln->d_in, Ln->w.as<double2>(), Ln->d_out, e, n->gemm_ws.p);
         } else {
           e.mode = EPI_STORE;
@@ -1205,16 +1215,24 @@ int mitok_timing_enable(mitok_network* n, int cls) {
   n->timing.cls = cls;
   n->timing.total_ms = 0.0;
   n->timing.bytes = 0.0;
+  n->timing.flops = 0.0;
   n->timing.launches = 0;
   return OK;
 }
 
-int mitok_timing_read(mitok_network* n, double* total_ms, uint64_t* launches, double* alg_bytes) {
+int mitok_timing_read(mitok_network* n, double* total_ms, uint64_t* launches, double* alg_bytes, double* alg_flops) {
   if (!n) return fail(ERR_ARG, "null network");
   collect_timing(n);
   if (total_ms) *total_ms = n->timing.total_ms;
   if (launches) *launches = n->timing.launches;
   if (alg_bytes) *alg_bytes = n->timing.bytes;
+  if (alg_flops) *alg_flops = n->timing.flops;
+  return OK;
+}
+
+int mitok_device_synchronize(int device) {
+  HIP_TRY(hipSetDevice(device));
+  HIP_TRY(hipDeviceSynchronize());
   return OK;
 }
 

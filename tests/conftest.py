@@ -32,6 +32,41 @@ def max_rel_err(got, want) -> float:
     return float(np.max(np.abs(got - want) / den)) if want.size else 0.0
 
 
+def normwise_rel_err(got, want) -> float:
+    """max over rows of ||got - want||_inf / ||want||_inf (last axis = one logits row)."""
+    got = np.asarray(got).reshape(-1, np.shape(want)[-1])
+    want = np.asarray(want).reshape(-1, np.shape(want)[-1])
+    num = np.max(np.abs(got - want), axis=1)
+    den = np.maximum(np.max(np.abs(want), axis=1), np.finfo(float).tiny)
+    return float(np.max(num / den))
+
+
+# Deep configurations (config 3 and up) are ill-conditioned in the reference's
+# own arithmetic: each complex pre-LayerNorm amplifies incoming rounding
+# several-fold (its complex variance partly cancels), compounding per layer.
+# There the logits are judged against the oracle's own noise floor: the
+# difference between two equally valid zgemm summation orders of the oracle
+# (OpenBLAS fixes none).  NOISE_FACTOR is the allowed multiple of that floor.
+NOISE_FACTOR = 4.0
+
+
+def oracle_noise_floor(onet, prompt, lens, n_new, want):
+    """(elementwise, normwise) spread of the oracle run `want` (zgemm k
+    ascending) against the same run under the other valid zgemm orders
+    (k descending; k in eight chunks), the larger of the two."""
+    import oracle
+
+    floor = [0.0, 0.0]
+    for order in (1, 2):
+        oracle.set_gemm_order(order)
+        try:
+            _, alt = onet.generate(prompt, lens=lens, n_new=n_new, want_logits=True)
+        finally:
+            oracle.set_gemm_order(0)
+        floor = [max(floor[0], max_rel_err(alt, want)), max(floor[1], normwise_rel_err(alt, want))]
+    return tuple(floor)
+
+
 @pytest.fixture(scope="session")
 def oracle_mod():
     import oracle

@@ -139,6 +139,9 @@ int mitok_timing_read(mitok_network* net, double* total_ms, uint64_t* launches, 
 int mitok_device_synchronize(int device);
 /* 0 = replay decode steps as HIP graphs (default), 1 = launch kernels directly. */
 int mitok_set_graph_mode(mitok_network* net, int direct_launch);
+/* 1 = decode steps of up to 8 sequences run the fused plan (row transforms in
+ * the product prologues, default); 0 = one launch per reference operation. */
+int mitok_set_decode_plan(mitok_network* net, int fused);
 
 #ifdef __cplusplus
 }

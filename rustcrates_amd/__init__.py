@@ -57,6 +57,7 @@ SIGNATURES = {
     "mitok_timing_read": (_i32, [_P, _P, _P, _P, _P]),
     "mitok_device_synchronize": (_i32, [_i32]),
     "mitok_set_graph_mode": (_i32, [_P, _i32]),
+    "mitok_set_decode_plan": (_i32, [_P, _i32]),
 }
 
 
@@ -230,3 +231,6 @@ class Network:
 
     def set_graph_mode(self, direct_launch: bool):
         _check(self._lib.mitok_set_graph_mode(self._h, int(direct_launch)))
+
+    def set_decode_plan(self, fused: bool):
+        _check(self._lib.mitok_set_decode_plan(self._h, int(fused)))

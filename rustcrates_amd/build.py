@@ -17,7 +17,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 SRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libmitok.so")
-SOURCES = ["kernels.hip", "network.hip"]
+SOURCES = ["kernels.hip", "gemm.hip", "attention.hip", "network.hip"]
 ARCH = os.environ.get("MITOK_ARCH", "gfx950")
 
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"

@@ -102,4 +102,43 @@ __device__ __forceinline__ double wave_max(double v) {
   return v;
 }
 
+// ---- split completion ----
+// Every block of a split calls this once after writing its partial result;
+// it returns true in exactly one block, the last to arrive, after which that
+// block sees every other block's writes.  The counter is reset by that block,
+// so the next launch on the stream starts from zero.  All threads of the block
+// must call it (it contains barriers).
+__device__ __forceinline__ bool arrive_last(uint32_t* counter, uint32_t expected) {
+  __shared__ uint32_t s_last;
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t old = atomicAdd(counter, 1u);
+    const uint32_t last = (old + 1u == expected) ? 1u : 0u;
+    if (last) atomicExch(counter, 0u);
+    s_last = last;
+  }
+  __syncthreads();
+  const bool last = s_last != 0u;
+  if (last) __threadfence();
+  return last;
+}
+
+// greedy_decoding order: the larger value wins, equal values go to the larger
+// index (Rust max_by keeps the last maximum); index -1 marks "no value"
+__device__ __forceinline__ void argmax_combine(double& bv, int& bi, double ov, int oi) {
+  if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi > bi))) {
+    bv = ov;
+    bi = oi;
+  }
+}
+__device__ __forceinline__ void wave_argmax(double& v, int& i) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const double ov = __shfl_xor(v, o, 64);
+    const int oi = __shfl_xor(i, o, 64);
+    argmax_combine(v, i, ov, oi);
+  }
+}
+
 }  // namespace mitok

@@ -1,12 +1,47 @@
-// kernels.hpp — launch wrappers of the gfx950 kernels (kernels.hip).
+// kernels.hpp — launch wrappers of the gfx950 kernels (gemm.hip, attention.hip,
+// kernels.hip).
 //
 // Every wrapper enqueues on `st` and never synchronises or allocates, so the
-// decode step built from them can be captured into a HIP graph.
+// decode step built from them can be captured into a HIP graph.  Kernels that
+// split work across blocks finish it in the block that arrives last at a
+// per-tile counter (Sync); counters return to zero before the kernel ends, so
+// launches on one stream can share them.
 #pragma once
 
 #include "common.hpp"
 
 namespace mitok {
+
+// ---- scratch shared by the launches of one stream ----
+struct Sync {
+  uint32_t* counters = nullptr;  // zero-initialised, SYNC_COUNTERS entries
+  void* ws = nullptr;            // split partials
+  size_t ws_bytes = 0;
+};
+constexpr int SYNC_COUNTERS = 1 << 16;
+
+// ---- the row transform a GEMV applies to its input rows (prologue) ----
+// source (rows, or an embedding gather) -> RoPE -> residual Re(x + r) -> LayerNorm
+struct RowOps {
+  const double2* x = nullptr;  // [M][ldx] rows, or
+  long ldx = 0;
+  const double2* table = nullptr;  // [vocab][K] embedding table gathered by ids (PAD id 1 -> 0)
+  const uint32_t* ids = nullptr;
+  int vocab = 0;
+  const double2* rope_cs = nullptr;  // [rope_max][K/2] (cos, sin); position of row m = rope_pos[m]
+  const int* rope_pos = nullptr;
+  int rope_max = 0;
+  const double2* resid = nullptr;  // x = Re(x + resid) + 0i  (add_matrix_3d_c, utils/matrix.rs:600-613)
+  long ldr = 0;
+  int ln = 0;  // NormalNormLayer over the K elements of each row (norm_layer.rs:64-130)
+  double eps = 0.0;
+  const double2* gamma = nullptr;
+  const double2* beta = nullptr;
+  double2* save = nullptr;  // optional copy of the transformed rows [M][ldsave]
+  long ldsave = 0;
+  uint32_t* err = nullptr;
+  bool plain() const { return !table && !rope_cs && !resid && !ln && !save; }
+};
 
 // ---- GEMM epilogue: what happens to C[m][n] after the complex dot product ----
 enum EpiMode : int {
@@ -22,6 +57,8 @@ struct Epi {
   double2* out = nullptr;         // STORE / GELU / QKV(q part)
   double* out_re = nullptr;       // RE
   long ldo = 0;
+  double* hist_re = nullptr;       // RE: also hist_re[hist_cnt[0]][m][n] (logits history, ld N)
+  const int* hist_cnt = nullptr;
   const uint32_t* row_mask = nullptr;  // GELU: rows with mask 0 become 0
   int check_finite = 0;
   uint32_t* err = nullptr;
@@ -34,12 +71,31 @@ struct Epi {
   const int* kv_row = nullptr;   // [B] only this row is appended (null: every row)
 };
 
-// GEMM C[M][N] = A[M][K] * B[K][N] (complex, row-major), then the epilogue.
-// Small M uses a bandwidth GEMV, larger M the MFMA-tiled kernel; split-K
-// partial sums go to `ws`.  gemm_ws_bytes() is the workspace it needs.
-size_t gemm_ws_bytes(int M, int N, int K, int mode);
-void gemm(hipStream_t st, int M, int N, int K, const double2* A, long lda, const double2* B, long ldb, const Epi& ep,
-          void* ws);
+// ---- greedy_decoding fused into an EPI_RE GEMM (src/utils/sampling_methods.rs:5-18) ----
+// Per-tile (max, last index) partials, then the block that finishes last
+// reduces them per row: ids[m], optional history append and KV advance.
+struct Argmax {
+  double* part_v = nullptr;  // [M][tiles]
+  int* part_i = nullptr;
+  uint32_t* ids = nullptr;
+  uint32_t* hist = nullptr;
+  int hist_stride = 0;
+  int* hist_cnt = nullptr;
+  int* kv_len = nullptr;
+  int advance_kv = 0;
+  uint32_t* err = nullptr;
+};
+
+// GEMM C[M][N] = rowops(A)[M][K] * W[K][N] (complex, row-major), then the epilogue
+// and the optional fused argmax.  M <= 8 runs the bandwidth GEMV (any RowOps);
+// larger M the MFMA-tiled kernel (plain rows only).  gemm_ws_bytes() is the split
+// workspace it needs; argmax_part_elems() the size of Argmax::part_v/part_i.
+size_t gemm_ws_bytes(int M, int N, int K);
+size_t argmax_part_elems(int M, int N);
+int gemm(hipStream_t st, int M, int N, int K, const RowOps& ro, const double2* W, long ldw, const Epi& ep,
+         const Argmax* am, const Sync& sy);
+// The prologue alone: out[m][k] = rowops(x)[m][k]  (materialises a pending row transform)
+void rowops_apply(hipStream_t st, int M, int K, const RowOps& ro, double2* out, long ldo);
 
 // ---- attention ----
 struct Attn {
@@ -61,9 +117,9 @@ struct Attn {
 };
 // One query row per block (prefill and the general reference case).
 void attention_rows(hipStream_t st, const Attn& a);
-// Split-key decode (S == 1): partial softmax per key chunk, then a combine.
+// Decode (S == 1): key chunks in parallel, combined by the last chunk to finish.
 size_t attention_decode_ws_bytes(int B, int H, int dh, int T_max);
-void attention_decode(hipStream_t st, const Attn& a, void* ws);
+int attention_decode(hipStream_t st, const Attn& a, const Sync& sy);
 
 // ---- row kernels ----
 void embed(hipStream_t st, const double2* table, int V, int d, const uint32_t* ids, int rows, double2* out,
@@ -74,12 +130,10 @@ void rope(hipStream_t st, double2* x, int rows, int d, const double2* cs_table, 
 void layernorm(hipStream_t st, const double2* x, const double2* before, double2* out, int rows, int d, double eps,
                const double2* gamma, const double2* beta);
 void gather_rows(hipStream_t st, const double2* src, int S, int d, const uint32_t* lens, int B, double2* dst);
-// argmax per row with last-index ties; ids[b]; optional history append and kv advance
-void argmax_rows(hipStream_t st, const double* logits, int rows, int V, uint32_t* ids, uint32_t* hist, int hist_stride,
-                 int* hist_cnt, int* kv_len, int advance_kv, uint32_t* err);
+// argmax per row with last-index ties (greedy_decoding on host-provided logits)
+void argmax_rows(hipStream_t st, const double* logits, int rows, int V, uint32_t* ids, uint32_t* err);
 void softmax_rows(hipStream_t st, const double2* logits, int rows, int S, int V, const uint32_t* row_mask, int mode,
                   double* out);
-void store_logits(hipStream_t st, const double* logits, int rows, int V, double* hist, const int* hist_cnt);
 
 // ---- initialisation ----
 void fill_seeded(hipStream_t st, double2* dst, int rows, int cols, long ld, uint64_t key, double lim);
@@ -87,6 +141,5 @@ void fill_seeded_re(hipStream_t st, double* dst, int rows, int cols, long ld, ui
 void fill_const(hipStream_t st, double2* dst, size_t n, double2 v);
 void fill_int(hipStream_t st, int* dst, size_t n, int v);
 void fill_u32(hipStream_t st, uint32_t* dst, size_t n, uint32_t v);
-void copy_re(hipStream_t st, const double2* src, double* dst, size_t n);
 
 }  // namespace mitok

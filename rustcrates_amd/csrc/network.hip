@@ -157,6 +157,9 @@ struct Spec {
   double* out_re = nullptr;          // vocab Re-logits
   double* out_prob = nullptr;        // softmax output (not forward_only)
   double2* out_hidden = nullptr;     // result of a hidden-state range
+  const Argmax* am = nullptr;        // greedy ids fused into the vocab GEMM (token loop)
+  double* hist_re = nullptr;         // Re-logits history [step][B][V] at hist_cnt[0] (token loop)
+  const int* hist_cnt = nullptr;
 };
 
 struct Timing {
@@ -181,8 +184,11 @@ struct mitok_network {
   std::vector<uint32_t> kv_len_h;
   mitok::DevBuf kv_len_d, err_d;
   // workspaces
-  mitok::DevBuf act0, act1, qbuf, concat, hbuf, gath, logits_c, logits_re, probs, gemm_ws, attn_ws, kv_scratch;
+  mitok::DevBuf act0, act1, qbuf, concat, hbuf, gath, mat0, mat1, logits_c, logits_re, probs, kv_scratch;
   mitok::DevBuf ids_d, mask_d, lens_d, pos_d, kv_row_d, ones_d, dec_ids_d, hist_d, cnt_d, logit_hist_d;
+  // split-completion counters (zeroed once, self-resetting), split partials, argmax partials
+  mitok::DevBuf sync_cnt, sync_ws, am_v, am_i;
+  int fused_decode = 1;  // B <= 8 decode steps use the fused GEMV plan
   // decode-step graph
   hipGraphExec_t graph = nullptr;
   uint32_t graph_B = 0, graph_nnew = 0;
@@ -337,36 +343,63 @@ static int prepare(Net* n, const Spec& sp) {
   TRY(reserve(n, n->concat, rows * std::max(1u, dm.dsa) * c16));
   TRY(reserve(n, n->hbuf, rows * std::max(1u, dm.fmax) * c16));
   TRY(reserve(n, n->gath, (size_t)sp.B * dm.dmax * c16));
-  size_t gws = 0;
+  TRY(reserve(n, n->mat0, rows * dm.dmax * c16));
+  TRY(reserve(n, n->mat1, rows * dm.dmax * c16));
+  size_t ws = 0;
   for (uint32_t li = sp.first; li < sp.last; ++li) {
     Layer* L = n->layers[li].get();
     const int M = (int)rows;
-    if (L->kind == K_SELF_ATTENTION) gws = std::max(gws, gemm_ws_bytes(M, 3 * L->d_in, L->d_in, EPI_QKV));
+    if (L->kind == K_SELF_ATTENTION) ws = std::max(ws, gemm_ws_bytes(M, 3 * L->d_in, L->d_in));
     if (L->kind == K_FEED_FORWARD) {
       auto* F = (FeedForwardLayer*)L;
-      gws = std::max(gws, gemm_ws_bytes(M, F->hidden, F->d_in, EPI_GELU));
-      gws = std::max(gws, gemm_ws_bytes(M, F->d_out, F->hidden, EPI_STORE));
+      ws = std::max(ws, gemm_ws_bytes(M, F->hidden, F->d_in));
+      ws = std::max(ws, gemm_ws_bytes(M, F->d_out, F->hidden));
     }
     if (L->kind == K_LINEAR) {
-      bool vocab = is_vocab_linear(n, li) && sp.first == 0;
-      int Mv = (vocab && sp.last_row) ? sp.B : M;
-      int mode = (vocab && sp.forward_only) ? EPI_RE : EPI_STORE;
-      gws = std::max(gws, gemm_ws_bytes(Mv, L->d_out, L->d_in, mode));
+      const bool vocab = is_vocab_linear(n, li) && sp.first == 0;
+      const int Mv = (vocab && sp.last_row) ? sp.B : M;
+      ws = std::max(ws, gemm_ws_bytes(Mv, L->d_out, L->d_in));
       if (vocab && !sp.forward_only) {
         TRY(reserve(n, n->logits_c, (size_t)Mv * L->d_out * c16));
         TRY(reserve(n, n->probs, (size_t)Mv * L->d_out * sizeof(double)));
       }
-      if (vocab && sp.forward_only) TRY(reserve(n, n->logits_re, (size_t)Mv * L->d_out * sizeof(double)));
+      if (vocab && sp.forward_only) {
+        TRY(reserve(n, n->logits_re, (size_t)Mv * L->d_out * sizeof(double)));
+        TRY(reserve(n, n->am_v, argmax_part_elems(Mv, L->d_out) * sizeof(double)));
+        TRY(reserve(n, n->am_i, argmax_part_elems(Mv, L->d_out) * sizeof(int)));
+      }
     }
   }
-  TRY(reserve(n, n->gemm_ws, gws));
   if (dm.hmax) {
-    TRY(reserve(n, n->attn_ws, attention_decode_ws_bytes(sp.B, dm.hmax, dm.dh_max, dm.mc_max)));
+    if (sp.mode == MODE_CACHED && sp.S == 1)
+      ws = std::max(ws, attention_decode_ws_bytes(sp.B, dm.hmax, dm.dh_max, dm.mc_max));
     if (sp.mode == MODE_STATELESS) TRY(reserve(n, n->kv_scratch, 2 * rows * dm.dsa * c16));
   }
+  TRY(reserve(n, n->sync_ws, ws));
   TRY(reserve(n, n->kv_len_d, (size_t)sp.B * sizeof(int)));
   TRY(reserve(n, n->ones_d, std::max<size_t>(rows, sp.B) * sizeof(uint32_t)));
   TRY(reserve(n, n->dec_ids_d, (size_t)sp.B * sizeof(uint32_t)));
+  return OK;
+}
+
+static Sync sync_of(Net* n) {
+  Sync s;
+  s.counters = n->sync_cnt.as<uint32_t>();
+  s.ws = n->sync_ws.p;
+  s.ws_bytes = n->sync_ws.bytes;
+  return s;
+}
+
+static RowOps rows_of(const double2* x, long ldx) {
+  RowOps r;
+  r.x = x;
+  r.ldx = ldx;
+  return r;
+}
+
+// a launch wrapper's refusal (shape beyond the workspace or counters) as an error
+static int launch_rc(int rc, const char* what) {
+  if (rc) return fail(rc, "%s: launch refused (workspace or shape limit)", what);
   return OK;
 }
 
@@ -394,6 +427,7 @@ static int ensure_rope_table(Net* n, PositionalEncodingLayer* P, int positions) 
 static int enqueue_forward(Net* n, const Spec& sp) {
   hipStream_t st = n->stream;
   uint32_t* err = n->err_d.as<uint32_t>();
+  const Sync sy = sync_of(n);
   const int B = sp.B, S = sp.S, rows = B * S;
   double2* cur = n->act0.as<double2>();
   double2* nxt = n->act1.as<double2>();
@@ -457,7 +491,7 @@ static int enqueue_forward(Net* n, const Spec& sp) {
         }
         {
           TimeScope ts(n, MITOK_TIME_LAYER_GEMM, gemm_bytes(rows, 3 * d, d, false), gemm_flops(rows, 3 * d, d));
-          gemm(st, rows, 3 * d, d, cur, d, A->wqkv.as<double2>(), 3 * d, e, n->gemm_ws.p);
+          TRY(launch_rc(gemm(st, rows, 3 * d, d, rows_of(cur, d), A->wqkv.as<double2>(), 3 * d, e, nullptr, sy), "qkv"));
         }
         a.kc = e.kc;
         a.vc = e.vc;
@@ -474,7 +508,7 @@ static int enqueue_forward(Net* n, const Spec& sp) {
         a.scale = 1.0 / (1e-8 + sqrt((double)dh));  // scale_attention_scores (masked_attention_head.rs:453-465)
         {
           TimeScope ts(n, MITOK_TIME_ATTENTION, 0.0);
-          if (sp.mode == MODE_CACHED && S == 1) attention_decode(st, a, n->attn_ws.p);
+          if (sp.mode == MODE_CACHED && S == 1) TRY(launch_rc(attention_decode(st, a, sy), "attention"));
           else attention_rows(st, a);
         }
         layernorm(st, n->concat.as<double2>(), cur, nxt, rows, d, A->eps, A->gamma.as<double2>(), A->beta.as<double2>());
@@ -500,13 +534,14 @@ static int enqueue_forward(Net* n, const Spec& sp) {
         {
           TimeScope ts(n, MITOK_TIME_LAYER_GEMM, gemm_bytes(rows, F->hidden, F->d_in, false),
                        gemm_flops(rows, F->hidden, F->d_in));
-          gemm(st, rows, F->hidden, F->d_in, cur, F->d_in, F->w1.as<double2>(), F->hidden, e1, n->gemm_ws.p);
+          TRY(launch_rc(gemm(st, rows, F->hidden, F->d_in, rows_of(cur, F->d_in), F->w1.as<double2>(), F->hidden, e1,
+                             nullptr, sy), "ffn1"));
         }
         {
           TimeScope ts(n, MITOK_TIME_LAYER_GEMM, gemm_bytes(rows, F->d_out, F->hidden, false),
                        gemm_flops(rows, F->d_out, F->hidden));
-          gemm(st, rows, F->d_out, F->hidden, n->hbuf.as<double2>(), F->hidden, F->w2.as<double2>(), F->d_out, e2,
-               n->gemm_ws.p);
+          TRY(launch_rc(gemm(st, rows, F->d_out, F->hidden, rows_of(n->hbuf.as<double2>(), F->hidden),
+                             F->w2.as<double2>(), F->d_out, e2, nullptr, sy), "ffn2"));
         }
         std::swap(cur, nxt);
         break;
@@ -521,7 +556,8 @@ static int enqueue_forward(Net* n, const Spec& sp) {
           e.out = nxt;
           e.ldo = Ln->d_out;
           e.err = err;
-          gemm(st, rows, Ln->d_out, Ln->d_in, cur, Ln->d_in, Ln->w.as<double2>(), Ln->d_out, e, n->gemm_ws.p);
+          TRY(launch_rc(gemm(st, rows, Ln->d_out, Ln->d_in, rows_of(cur, Ln->d_in), Ln->w.as<double2>(), Ln->d_out, e,
+                             nullptr, sy), "linear"));
           std::swap(cur, nxt);
           break;
         }
@@ -539,12 +575,16 @@ static int enqueue_forward(Net* n, const Spec& sp) {
         if (sp.forward_only) {
           e.mode = EPI_RE;
           e.out_re = sp.out_re;
+          e.hist_re = sp.hist_re;
+          e.hist_cnt = sp.hist_cnt;
           TimeScope ts(n, MITOK_TIME_VOCAB, gemm_bytes(M, Ln->d_out, Ln->d_in, true), gemm_flops(M, Ln->d_out, Ln->d_in));
-          gemm(st, M, Ln->d_out, Ln->d_in, x, Ln->d_in, Ln->w.as<double2>(), Ln->d_out, e, n->gemm_ws.p);
+          TRY(launch_rc(gemm(st, M, Ln->d_out, Ln->d_in, rows_of(x, Ln->d_in), Ln->w.as<double2>(), Ln->d_out, e,
+                             sp.am, sy), "vocab"));
         } else {
           e.mode = EPI_STORE;
           e.out = n->logits_c.as<double2>();
-          gemm(st, M, Ln->d_out, Ln->d_in, x, Ln->d_in, Ln->w.as<double2>(), Ln->d_out, e, n->gemm_ws.p);
+          TRY(launch_rc(gemm(st, M, Ln->d_out, Ln->d_in, rows_of(x, Ln->d_in), Ln->w.as<double2>(), Ln->d_out, e,
+                             nullptr, sy), "vocab"));
           auto* SM = (SoftmaxLayer*)n->layers.back().get();
           softmax_rows(st, n->logits_c.as<double2>(), M, S, Ln->d_out, sp.mask, SM->mode == MITOK_TRAINING ? 0 : 1,
                        sp.out_prob);
@@ -560,6 +600,195 @@ static int enqueue_forward(Net* n, const Spec& sp) {
   }
   HIP_TRY(hipGetLastError());
   return OK;
+}
+
+// ---------------------------------------------------------------------------
+// fused decode step for B <= 8 sequences (one row each): the row transforms
+// of Embedding / PositionalEncoding / Norm and the residual LayerNorm inside
+// SelfAttention are carried as a pending prologue into the next product, so a
+// transformer block is 4 launches: QKV (+KV append), attention, FFN Dense
+// (+GELU), FFN Linear; the vocab Linear ends the step with the greedy id.
+// ---------------------------------------------------------------------------
+static bool fused_decode_ok(const Net* n, const Spec& sp) {
+  if (!n->fused_decode || sp.mode != MODE_CACHED || sp.S != 1 || sp.B > 8 || !sp.forward_only) return false;
+  if (sp.first != 0 || sp.last != n->layers.size() || sp.kv_row || sp.out_hidden) return false;
+  return true;
+}
+
+static int enqueue_decode_fused(Net* n, const Spec& sp) {
+  hipStream_t st = n->stream;
+  uint32_t* err = n->err_d.as<uint32_t>();
+  const Sync sy = sync_of(n);
+  const int B = sp.B;
+  int* kv_len = n->kv_len_d.as<int>();
+  RowOps pro;  // pending prologue of the next product
+  pro.err = err;
+  int width = 0;  // row length the pending prologue produces
+  double2* mats[2] = {n->mat0.as<double2>(), n->mat1.as<double2>()};
+  int mat_next = 0;
+  auto materialize = [&]() {
+    double2* out = mats[mat_next];
+    mat_next ^= 1;
+    rowops_apply(st, B, width, pro, out, width);
+    RowOps r = rows_of(out, width);
+    r.err = err;
+    pro = r;
+  };
+  for (uint32_t li = 0; li < n->layers.size(); ++li) {
+    Layer* L = n->layers[li].get();
+    switch (L->kind) {
+      case K_EMBEDDING: {
+        auto* E = (EmbeddingLayer*)L;
+        pro = RowOps();
+        pro.err = err;
+        pro.table = E->table.as<double2>();
+        pro.ids = sp.ids;
+        pro.vocab = (int)E->vocab;
+        width = (int)E->d_out;
+        break;
+      }
+      case K_POSENC: {
+        auto* P = (PositionalEncodingLayer*)L;
+        if (pro.rope_cs || pro.resid || pro.ln) materialize();
+        pro.rope_cs = P->cs.as<double2>();
+        pro.rope_pos = sp.pos ? sp.pos : kv_len;
+        pro.rope_max = P->positions;
+        break;
+      }
+      case K_NORM: {
+        auto* N = (NormLayer*)L;
+        if (pro.ln) materialize();
+        pro.ln = 1;
+        pro.eps = N->eps;
+        pro.gamma = N->gamma.as<double2>();
+        pro.beta = N->beta.as<double2>();
+        break;
+      }
+      case K_SELF_ATTENTION: {
+        auto* A = (SelfAttentionLayer*)L;
+        const int d = A->d_in, H = A->heads, dh = A->dh;
+        if (pro.resid) materialize();           // its residual source is about to be overwritten
+        double2* x1 = n->act0.as<double2>();  // the block input, kept for the residual
+        pro.save = x1;
+        pro.ldsave = d;
+        Epi e;
+        e.mode = EPI_QKV;
+        e.out = n->qbuf.as<double2>();
+        e.ldo = d;
+        e.d = d;
+        e.dh = dh;
+        e.heads = H;
+        e.S = 1;
+        e.err = err;
+        e.kc = A->kc.as<double2>();
+        e.vc = A->vc.as<double2>();
+        e.ctx = A->max_ctx;
+        e.kv_base = kv_len;
+        {
+          TimeScope ts(n, MITOK_TIME_LAYER_GEMM, gemm_bytes(B, 3 * d, d, false), gemm_flops(B, 3 * d, d));
+          TRY(launch_rc(gemm(st, B, 3 * d, d, pro, A->wqkv.as<double2>(), 3 * d, e, nullptr, sy), "qkv"));
+        }
+        Attn a;
+        a.q = n->qbuf.as<double2>();
+        a.ldq = d;
+        a.kc = e.kc;
+        a.vc = e.vc;
+        a.ctx = A->max_ctx;
+        a.kv_len = kv_len;
+        a.T_add = 1;
+        a.T_max = A->max_ctx;
+        a.bias_re = A->bias_re.as<double>();
+        a.mc = A->max_ctx;
+        a.row_mask = sp.mask;
+        a.out = n->concat.as<double2>();
+        a.ldo = d;
+        a.B = B;
+        a.S = 1;
+        a.H = H;
+        a.dh = dh;
+        a.scale = 1.0 / (1e-8 + sqrt((double)dh));  // masked_attention_head.rs:453-465
+        {
+          TimeScope ts(n, MITOK_TIME_ATTENTION, 0.0);
+          TRY(launch_rc(attention_decode(st, a, sy), "attention"));
+        }
+        pro = rows_of(n->concat.as<double2>(), d);  // residual + Norm (self_attention_layer.rs:101-124)
+        pro.err = err;
+        pro.resid = x1;
+        pro.ldr = d;
+        pro.ln = 1;
+        pro.eps = A->eps;
+        pro.gamma = A->gamma.as<double2>();
+        pro.beta = A->beta.as<double2>();
+        width = d;
+        break;
+      }
+      case K_FEED_FORWARD: {
+        auto* F = (FeedForwardLayer*)L;
+        Epi e1;
+        e1.mode = EPI_GELU;
+        e1.bias = F->b1.as<double2>();
+        e1.out = n->hbuf.as<double2>();
+        e1.ldo = F->hidden;
+        e1.row_mask = sp.mask;
+        e1.err = err;
+        double2* out = n->act1.as<double2>();
+        Epi e2;
+        e2.mode = EPI_STORE;
+        e2.bias = F->b2.as<double2>();
+        e2.out = out;
+        e2.ldo = F->d_out;
+        e2.check_finite = 1;
+        e2.err = err;
+        {
+          TimeScope ts(n, MITOK_TIME_LAYER_GEMM, gemm_bytes(B, F->hidden, F->d_in, false),
+                       gemm_flops(B, F->hidden, F->d_in));
+          TRY(launch_rc(gemm(st, B, F->hidden, F->d_in, pro, F->w1.as<double2>(), F->hidden, e1, nullptr, sy), "ffn1"));
+        }
+        {
+          TimeScope ts(n, MITOK_TIME_LAYER_GEMM, gemm_bytes(B, F->d_out, F->hidden, false),
+                       gemm_flops(B, F->d_out, F->hidden));
+          TRY(launch_rc(gemm(st, B, F->d_out, F->hidden, rows_of(n->hbuf.as<double2>(), F->hidden), F->w2.as<double2>(),
+                             F->d_out, e2, nullptr, sy), "ffn2"));
+        }
+        pro = rows_of(out, F->d_out);
+        pro.err = err;
+        width = (int)F->d_out;
+        break;
+      }
+      case K_LINEAR: {
+        auto* Ln = (LinearLayer*)L;
+        Epi e;
+        e.bias = Ln->b.as<double2>();
+        e.ldo = Ln->d_out;
+        e.err = err;
+        if (is_vocab_linear(n, li)) {
+          e.mode = EPI_RE;
+          e.out_re = sp.out_re;
+          e.hist_re = sp.hist_re;
+          e.hist_cnt = sp.hist_cnt;
+          TimeScope ts(n, MITOK_TIME_VOCAB, gemm_bytes(B, Ln->d_out, Ln->d_in, true), gemm_flops(B, Ln->d_out, Ln->d_in));
+          TRY(launch_rc(gemm(st, B, Ln->d_out, Ln->d_in, pro, Ln->w.as<double2>(), Ln->d_out, e, sp.am, sy), "vocab"));
+        } else {
+          double2* out = mats[mat_next];
+          mat_next ^= 1;
+          e.mode = EPI_STORE;
+          e.out = out;
+          TRY(launch_rc(gemm(st, B, Ln->d_out, Ln->d_in, pro, Ln->w.as<double2>(), Ln->d_out, e, nullptr, sy), "linear"));
+          pro = rows_of(out, Ln->d_out);
+          pro.err = err;
+          width = (int)Ln->d_out;
+        }
+        break;
+      }
+      case K_SOFTMAX: break;
+    }
+  }
+  HIP_TRY(hipGetLastError());
+  return OK;
+}
+
+static int enqueue_step(Net* n, const Spec& sp) {
+  return fused_decode_ok(n, sp) ? enqueue_decode_fused(n, sp) : enqueue_forward(n, sp);
 }
 
 // ---------------------------------------------------------------------------
@@ -636,8 +865,10 @@ int mitok_network_create(int device, mitok_network** out) {
   if (!rc && hipStreamCreateWithFlags(&n->stream, hipStreamNonBlocking) != hipSuccess)
     rc = fail(ERR_HIP, "hipStreamCreate failed");
   if (!rc) rc = n->err_d.reserve(sizeof(uint32_t));
+  if (!rc) rc = n->sync_cnt.reserve((size_t)SYNC_COUNTERS * sizeof(uint32_t));
   if (!rc) {
     fill_u32(n->stream, n->err_d.as<uint32_t>(), 1, 0);
+    fill_u32(n->stream, n->sync_cnt.as<uint32_t>(), SYNC_COUNTERS, 0);
     if (hipStreamSynchronize(n->stream) != hipSuccess) rc = fail(ERR_HIP, "stream sync failed");
   }
   if (rc) {
@@ -999,7 +1230,7 @@ int mitok_predict(mitok_network* n, const uint32_t* ids, const uint32_t* lens, u
   const uint32_t V = n->layers[n->layers.size() - 2]->d_out;
   sp.out_re = n->logits_re.as<double>();
   sp.out_prob = n->probs.as<double>();
-  TRY(enqueue_forward(n, sp));
+  TRY(enqueue_step(n, sp));
   if (forward_only) {
     size_t cnt = (sp.last_row ? (size_t)B : rows) * V;
     HIP_TRY(hipMemcpyAsync(out, sp.out_re, cnt * sizeof(double), hipMemcpyDeviceToHost, n->stream));
@@ -1063,14 +1294,24 @@ int mitok_forward_layers(mitok_network* n, uint32_t first, uint32_t last, const 
 }
 
 // One decode step for every sequence: embed the previous greedy ids, run the
-// stack with the cache, vocab Re-logits, greedy ids (+history), kv advance.
-static int enqueue_decode_step(Net* n, const Spec& sp, bool want_logits, uint32_t n_new) {
-  TRY(enqueue_forward(n, sp));
-  const uint32_t V = n->layers[n->layers.size() - 2]->d_out;
-  if (want_logits) store_logits(n->stream, sp.out_re, sp.B, V, n->logit_hist_d.as<double>(), n->cnt_d.as<int>());
-  argmax_rows(n->stream, sp.out_re, sp.B, V, n->dec_ids_d.as<uint32_t>(), n->hist_d.as<uint32_t>(), n_new,
-              n->cnt_d.as<int>(), n->kv_len_d.as<int>(), 1, n->err_d.as<uint32_t>());
-  return OK;
+// stack with the cache, vocab Re-logits (+history) and the greedy ids fused
+// into the vocab product, which also appends to the id history and advances
+// every sequence's KV length.
+static int enqueue_decode_step(Net* n, Spec sp, bool want_logits, uint32_t n_new) {
+  Argmax am;
+  am.part_v = n->am_v.as<double>();
+  am.part_i = n->am_i.as<int>();
+  am.ids = n->dec_ids_d.as<uint32_t>();
+  am.hist = n->hist_d.as<uint32_t>();
+  am.hist_stride = (int)n_new;
+  am.hist_cnt = n->cnt_d.as<int>();
+  am.kv_len = n->kv_len_d.as<int>();
+  am.advance_kv = 1;
+  am.err = n->err_d.as<uint32_t>();
+  sp.am = &am;
+  sp.hist_re = want_logits ? n->logit_hist_d.as<double>() : nullptr;
+  sp.hist_cnt = n->cnt_d.as<int>();
+  return enqueue_step(n, sp);
 }
 
 int mitok_generate(mitok_network* n, const uint32_t* prompt, const uint32_t* lens, uint32_t B, uint32_t S,
@@ -1123,10 +1364,18 @@ int mitok_generate(mitok_network* n, const uint32_t* prompt, const uint32_t* len
   for (auto& e : ev) HIP_TRY(hipEventCreate(&e));
   HIP_TRY(hipEventRecord(ev[0], st));
   // ---- prompt: full forward, vocab on each sequence's last row, first ids ----
+  Argmax am0;
+  am0.part_v = n->am_v.as<double>();
+  am0.part_i = n->am_i.as<int>();
+  am0.ids = n->dec_ids_d.as<uint32_t>();
+  am0.hist = n->hist_d.as<uint32_t>();
+  am0.hist_stride = (int)n_new;
+  am0.hist_cnt = n->cnt_d.as<int>();
+  am0.err = n->err_d.as<uint32_t>();
+  pre.am = &am0;
+  pre.hist_re = want_logits ? n->logit_hist_d.as<double>() : nullptr;
+  pre.hist_cnt = n->cnt_d.as<int>();
   TRY(enqueue_forward(n, pre));
-  if (want_logits) store_logits(st, pre.out_re, B, V, n->logit_hist_d.as<double>(), n->cnt_d.as<int>());
-  argmax_rows(st, pre.out_re, B, V, n->dec_ids_d.as<uint32_t>(), n->hist_d.as<uint32_t>(), n_new, n->cnt_d.as<int>(),
-              nullptr, 0, n->err_d.as<uint32_t>());
   {
     std::vector<int> kv(lens, lens + B);
     HIP_TRY(hipMemcpyAsync(n->kv_len_d.p, kv.data(), B * sizeof(int), hipMemcpyHostToDevice, st));
@@ -1196,8 +1445,7 @@ int mitok_greedy_decoding(mitok_network* n, const double* logits, uint32_t rows,
   TRY(lg.reserve((size_t)rows * V * sizeof(double)));
   TRY(ids.reserve((size_t)rows * sizeof(uint32_t)));
   HIP_TRY(hipMemcpyAsync(lg.p, logits, (size_t)rows * V * sizeof(double), hipMemcpyHostToDevice, n->stream));
-  argmax_rows(n->stream, lg.as<double>(), rows, V, ids.as<uint32_t>(), nullptr, 0, nullptr, nullptr, 0,
-              n->err_d.as<uint32_t>());
+  argmax_rows(n->stream, lg.as<double>(), rows, V, ids.as<uint32_t>(), n->err_d.as<uint32_t>());
   HIP_TRY(hipMemcpyAsync(out_ids, ids.p, rows * sizeof(uint32_t), hipMemcpyDeviceToHost, n->stream));
   HIP_TRY(hipStreamSynchronize(n->stream));
   return check_err_word(n);
@@ -1239,6 +1487,13 @@ int mitok_device_synchronize(int device) {
 int mitok_set_graph_mode(mitok_network* n, int direct_launch) {
   if (!n) return fail(ERR_ARG, "null network");
   n->direct_launch = direct_launch;
+  return OK;
+}
+
+int mitok_set_decode_plan(mitok_network* n, int fused) {
+  if (!n) return fail(ERR_ARG, "null network");
+  n->fused_decode = fused ? 1 : 0;
+  drop_graph(n);
   return OK;
 }
 

@@ -101,7 +101,8 @@ void attention_rows(hipStream_t st, const Attn& a) {
 // (sequence, head) to finish rescales the chunks to the common max, in
 // chunk order: out = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M).
 // ===========================================================================
-constexpr int DEC_LPK = 16;  // lanes per key in the score phase
+constexpr int DEC_LPK = 16;          // lanes per key in the score phase
+constexpr int DEC_MAX_SPLITS = 256;  // key chunks per (sequence, head)
 
 static int decode_chunk(int B, int H) { return B * H <= 64 ? 32 : 64; }
 
@@ -111,6 +112,7 @@ __global__ __launch_bounds__(256) void k_attention_decode(Attn a, int CH, int ns
   __shared__ double sc[64];
   __shared__ double2 pv[256];
   __shared__ double stat[2];
+  __shared__ double cw[DEC_MAX_SPLITS], cl[DEC_MAX_SPLITS];
   const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int T = a.kv_len ? a.kv_len[b] + a.T_add : a.T_const;
@@ -166,9 +168,12 @@ __global__ __launch_bounds__(256) void k_attention_decode(Attn a, int CH, int ns
   if (tid < a.dh) {
     double2 s = pv[tid];
     for (int gg = 1; gg < G; ++gg) s = cadd(s, pv[gg * a.dh + tid]);
-    po[pidx * a.dh + tid] = s;
+    st_dev(&po[pidx * a.dh + tid], s);
   }
-  if (tid == 0) pm[pidx] = stat[0], pl[pidx] = stat[1];
+  if (tid == 0) {
+    st_dev(&pm[pidx], stat[0]);
+    st_dev(&pl[pidx], stat[1]);
+  }
   if (!arrive_last(&cnt[bh], (uint32_t)ns)) return;
 
   double2* out = a.out + (long)b * a.ldo + (long)h * a.dh;
@@ -177,17 +182,37 @@ __global__ __launch_bounds__(256) void k_attention_decode(Attn a, int CH, int ns
     return;
   }
   const long base = bh * nsplit;
+  // chunk statistics through LDS: cw[s] = e^(m_s - M), L = sum_s l_s cw[s] in chunk order
+  if (tid < ns) cw[tid] = ld_dev(&pm[base + tid]);
+  __syncthreads();
   double M = -INFINITY;
-  for (int s = 0; s < ns; ++s) M = fmax(M, pm[base + s]);
+  for (int s = 0; s < ns; ++s) M = fmax(M, cw[s]);
+  __syncthreads();
+  if (tid < ns) {
+    const double w = exp(cw[tid] - M);
+    cw[tid] = w;
+    cl[tid] = ld_dev(&pl[base + tid]) * w;
+  }
+  __syncthreads();
   double L = 0.0;
-  for (int s = 0; s < ns; ++s) L += pl[base + s] * exp(pm[base + s] - M);
+  for (int s = 0; s < ns; ++s) L += cl[s];
   for (int t = tid; t < a.dh; t += 256) {
     double2 o = make_double2(0.0, 0.0);
-    for (int s = 0; s < ns; ++s) {
-      const double w = exp(pm[base + s] - M);
-      const double2 v = po[(base + s) * a.dh + t];
-      o.x += v.x * w;
-      o.y += v.y * w;
+    int s = 0;
+    for (; s + 4 <= ns; s += 4) {
+      const double2 v0 = ld_dev(&po[(base + s) * a.dh + t]);
+      const double2 v1 = ld_dev(&po[(base + s + 1) * a.dh + t]);
+      const double2 v2 = ld_dev(&po[(base + s + 2) * a.dh + t]);
+      const double2 v3 = ld_dev(&po[(base + s + 3) * a.dh + t]);
+      o.x += v0.x * cw[s], o.y += v0.y * cw[s];
+      o.x += v1.x * cw[s + 1], o.y += v1.y * cw[s + 1];
+      o.x += v2.x * cw[s + 2], o.y += v2.y * cw[s + 2];
+      o.x += v3.x * cw[s + 3], o.y += v3.y * cw[s + 3];
+    }
+    for (; s < ns; ++s) {
+      const double2 v = ld_dev(&po[(base + s) * a.dh + t]);
+      o.x += v.x * cw[s];
+      o.y += v.y * cw[s];
     }
     out[t] = make_double2(o.x / L, o.y / L);
   }
@@ -202,7 +227,7 @@ int attention_decode(hipStream_t st, const Attn& a, const Sync& sy) {
   const int CH = decode_chunk(a.B, a.H);
   const int ns = cdiv_i(a.T_max, CH);
   if (attention_decode_ws_bytes(a.B, a.H, a.dh, a.T_max) > sy.ws_bytes) return ERR_STATE;
-  if ((long)a.B * a.H >= SYNC_COUNTERS - 1 || a.dh > 256 || a.S != 1) return ERR_ARG;
+  if ((long)a.B * a.H >= SYNC_COUNTERS - 1 || a.dh > 256 || a.S != 1 || ns > DEC_MAX_SPLITS) return ERR_ARG;
   double* pm = (double*)sy.ws;
   double* pl = pm + (long)a.B * a.H * ns;
   double2* po = (double2*)(pl + (long)a.B * a.H * ns);

@@ -102,26 +102,51 @@ __device__ __forceinline__ double wave_max(double v) {
   return v;
 }
 
+// ---- cross-block results (split partials) ----
+// MI355X has one L2 per XCD and they are not coherent with each other, so the
+// partial results one block leaves for another (split-K, key chunks, argmax
+// tiles) are written and read at device coherence (relaxed agent-scope
+// atomics: the sc1 stores/loads that reach past the XCD's L2).  An
+// agent-scope fence would instead write back and invalidate the whole L2,
+// which measured several times slower than the whole product.
+__device__ __forceinline__ void st_dev(double* p, double v) {
+  __hip_atomic_store((unsigned long long*)p, (unsigned long long)__double_as_longlong(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ double ld_dev(const double* p) {
+  return __longlong_as_double(
+      (long long)__hip_atomic_load((unsigned long long*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+__device__ __forceinline__ void st_dev(double2* p, double2 v) {
+  st_dev(&p->x, v.x);
+  st_dev(&p->y, v.y);
+}
+__device__ __forceinline__ double2 ld_dev(const double2* p) { return make_double2(ld_dev(&p->x), ld_dev(&p->y)); }
+__device__ __forceinline__ void st_dev(int* p, int v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ int ld_dev(const int* p) {
+  return __hip_atomic_load((int*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // ---- split completion ----
-// Every block of a split calls this once after writing its partial result;
-// it returns true in exactly one block, the last to arrive, after which that
-// block sees every other block's writes.  The counter is reset by that block,
-// so the next launch on the stream starts from zero.  All threads of the block
-// must call it (it contains barriers).
+// Every block of a split calls this once after writing its partial result
+// with st_dev; it returns true in exactly one block, the last to arrive, which
+// then reads every partial with ld_dev.  Each wave first waits for its stores
+// to be acknowledged (vmcnt counts stores on gfx9), so they are device-visible
+// before the counter moves.  The counter is reset by the last block, so the
+// next launch on the stream starts from zero.  All threads of the block must
+// call it (it contains barriers).
 __device__ __forceinline__ bool arrive_last(uint32_t* counter, uint32_t expected) {
   __shared__ uint32_t s_last;
-  __threadfence();
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (threadIdx.x == 0) {
-    const uint32_t old = atomicAdd(counter, 1u);
+    const uint32_t old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const uint32_t last = (old + 1u == expected) ? 1u : 0u;
-    if (last) atomicExch(counter, 0u);
+    if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = last;
   }
   __syncthreads();
-  const bool last = s_last != 0u;
-  if (last) __threadfence();
-  return last;
+  return s_last != 0u;
 }
 
 // greedy_decoding order: the larger value wins, equal values go to the larger

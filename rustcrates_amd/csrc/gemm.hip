@@ -70,28 +70,32 @@ __device__ __forceinline__ double apply_epi(const Epi& ep, int M, int N, int m, 
   return v.x;
 }
 
-// The block that finished last reduces the per-tile argmax partials of each
-// row: one wave per row, lanes striding over tiles.  All threads call it.
-__device__ void argmax_finish(const Argmax& am, int M, int tiles) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  for (int m = wave; m < M; m += 4) {
-    double bv = -INFINITY;
-    int bi = -1;
-    for (int t = lane; t < tiles; t += 64) argmax_combine(bv, bi, am.part_v[(long)m * tiles + t], am.part_i[(long)m * tiles + t]);
-    wave_argmax(bv, bi);
-    if (lane == 0) {
-      if (bi < 0) {  // every logit was NaN (the reference panics)
-        atomicOr(am.err, (uint32_t)EB_ARGMAX_NAN);
-        bi = 0;
-      }
-      am.ids[m] = (uint32_t)bi;
-      if (am.hist) {
-        const int t = am.hist_cnt[m];
-        am.hist[(long)m * am.hist_stride + t] = (uint32_t)bi;
-        am.hist_cnt[m] = t + 1;
-      }
-      if (am.advance_kv) am.kv_len[m] += 1;
+// greedy_decoding finish: one block per row reduces that row's per-tile
+// (max, last index) partials, then stores the id, appends it to the history
+// and advances the sequence's KV length.
+__global__ __launch_bounds__(256) void k_argmax_finalize(Argmax am, int tiles) {
+  __shared__ double sv[4];
+  __shared__ int si[4];
+  const int m = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  double bv = -INFINITY;
+  int bi = -1;
+  for (int t = tid; t < tiles; t += 256) argmax_combine(bv, bi, am.part_v[(long)m * tiles + t], am.part_i[(long)m * tiles + t]);
+  wave_argmax(bv, bi);
+  if (lane == 0) sv[wave] = bv, si[wave] = bi;
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < 4; ++w) argmax_combine(bv, bi, sv[w], si[w]);
+    if (bi < 0) {  // every logit was NaN (the reference panics)
+      atomicOr(am.err, (uint32_t)EB_ARGMAX_NAN);
+      bi = 0;
     }
+    am.ids[m] = (uint32_t)bi;
+    if (am.hist) {
+      const int t = am.hist_cnt[m];
+      am.hist[(long)m * am.hist_stride + t] = (uint32_t)bi;
+      am.hist_cnt[m] = t + 1;
+    }
+    if (am.advance_kv) am.kv_len[m] += 1;
   }
 }
 
@@ -193,29 +197,40 @@ __device__ void ro_stats(const RowOps& r, int m0, int M, int K, double2* mean_s,
 }
 
 // ===========================================================================
-// GEMV for M <= 8 rows: HBM-bound weight stream.  Block = 4 waves x 64
-// columns; wave w walks kw rows of W (first 8 in flight before the prologue
-// runs), the 4 waves are summed in LDS, blockIdx.y splits K.
+// GEMV for M <= 8 rows: HBM-bound weight stream.  A block owns C columns and a
+// K range of 4*kw rows; lane (r, c) = (lane / C, lane % C) reads row r of each
+// group of 64/C rows, so one wave instruction covers 64/C rows x C columns.
+// The first 8 weight loads per lane are in flight while the prologue builds
+// the block's input rows in LDS.  Lanes of a column are summed by shuffles,
+// the 4 waves through LDS; blockIdx.y splits K (at most 8 ways, so few blocks
+// meet at each completion counter).
 // ===========================================================================
-template <int MR>
+constexpr int GEMV_MAX_SPLIT = 8;
+constexpr int SKINNY_MAX_SPLIT = 8;
+
+template <int MR, int C>
 __global__ __launch_bounds__(256) void k_gemv(RowOps ro, int M, const double2* __restrict__ W, long ldw, int N, int K,
                                               int kw, Epi ep, Argmax am, double2* __restrict__ ws,
                                               uint32_t* __restrict__ cnt) {
+  constexpr int RPW = 64 / C;  // rows per wave instruction
   extern __shared__ double2 xs[];  // [MR][4*kw]
-  __shared__ double2 red[3][MR][64];
+  __shared__ double2 red[3][MR][C];
   __shared__ double2 st_mean[MR], st_sd[MR];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane / C, c = lane - (lane / C) * C;
   const int KB = 4 * kw;
   const int kb0 = blockIdx.y * KB;
-  const int n = blockIdx.x * 64 + lane;
+  const int n = blockIdx.x * C + c;
   const bool col_ok = n < N;
   const int k0 = kb0 + wave * kw;
   const int kmax = max(0, min(kw, K - k0));
-  const double2* wp = W + (long)k0 * ldw + n;
+  const int nu = kmax > r ? (kmax - r + RPW - 1) / RPW : 0;  // rows k0 + r + u*RPW, u < nu
+  const double2* wp = W + (long)(k0 + r) * ldw + n;
+  const long wstep = (long)RPW * ldw;
 
   double2 w[8];
 #pragma unroll
-  for (int u = 0; u < 8; ++u) w[u] = (col_ok && u < kmax) ? wp[(long)u * ldw] : make_double2(0.0, 0.0);
+  for (int u = 0; u < 8; ++u) w[u] = (col_ok && u < nu) ? wp[u * wstep] : make_double2(0.0, 0.0);
 
   if (ro.ln) ro_stats<MR>(ro, 0, M, K, st_mean, st_sd);
   if (blockIdx.x == 0 && blockIdx.y == 0 && tid < M) ro_check(ro, tid);
@@ -235,76 +250,88 @@ __global__ __launch_bounds__(256) void k_gemv(RowOps ro, int M, const double2* _
 #pragma unroll
   for (int m = 0; m < MR; ++m) acc[m] = make_double2(0.0, 0.0);
   if (col_ok) {
-    const double2* xw = xs + wave * kw;
+    const double2* xw = xs + wave * kw + r;  // row u of this lane: xw[m * KB + u * RPW]
 #pragma unroll
     for (int u = 0; u < 8; ++u)
-      if (u < kmax)
+      if (u < nu)
 #pragma unroll
-        for (int m = 0; m < MR; ++m) acc[m] = cadd(acc[m], cmul(xw[m * KB + u], w[u]));
-    int kk = 8;
-    for (; kk + 8 <= kmax; kk += 8) {
+        for (int m = 0; m < MR; ++m) acc[m] = cadd(acc[m], cmul(xw[m * KB + u * RPW], w[u]));
+    int u0 = 8;
+    for (; u0 + 8 <= nu; u0 += 8) {
 #pragma unroll
-      for (int u = 0; u < 8; ++u) w[u] = wp[(long)(kk + u) * ldw];
+      for (int u = 0; u < 8; ++u) w[u] = wp[(u0 + u) * wstep];
 #pragma unroll
       for (int u = 0; u < 8; ++u)
 #pragma unroll
-        for (int m = 0; m < MR; ++m) acc[m] = cadd(acc[m], cmul(xw[m * KB + kk + u], w[u]));
+        for (int m = 0; m < MR; ++m) acc[m] = cadd(acc[m], cmul(xw[m * KB + (u0 + u) * RPW], w[u]));
     }
-    for (; kk < kmax; ++kk) {
-      const double2 wv = wp[(long)kk * ldw];
+    for (; u0 < nu; ++u0) {
+      const double2 wv = wp[u0 * wstep];
 #pragma unroll
-      for (int m = 0; m < MR; ++m) acc[m] = cadd(acc[m], cmul(xw[m * KB + kk], wv));
+      for (int m = 0; m < MR; ++m) acc[m] = cadd(acc[m], cmul(xw[m * KB + u0 * RPW], wv));
     }
   }
-  if (wave > 0)
+  // lanes of one column (same c, r = 0 .. RPW-1) -> r = 0
+#pragma unroll
+  for (int o = C; o < 64; o <<= 1)
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      acc[m].x += __shfl_xor(acc[m].x, o, 64);
+      acc[m].y += __shfl_xor(acc[m].y, o, 64);
+    }
+  if (wave > 0 && lane < C)
 #pragma unroll
     for (int m = 0; m < MR; ++m) red[wave - 1][m][lane] = acc[m];
   __syncthreads();
-  if (wave == 0)
+  const bool owner = wave == 0 && lane < C;  // lane c of wave 0 owns column n
+  if (owner)
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m] = cadd(cadd(cadd(acc[m], red[0][m][lane]), red[1][m][lane]), red[2][m][lane]);
 
   const int P = gridDim.y;
   if (P > 1) {
-    if (wave == 0 && col_ok)
+    if (owner && col_ok)
 #pragma unroll
       for (int m = 0; m < MR; ++m)
-        if (m < M) ws[((long)blockIdx.y * M + m) * N + n] = acc[m];
+        if (m < M) st_dev(&ws[((long)blockIdx.y * M + m) * N + n], acc[m]);
     if (!arrive_last(&cnt[blockIdx.x], (uint32_t)P)) return;
-    if (wave == 0 && col_ok)
+    if (owner && col_ok)
 #pragma unroll
       for (int m = 0; m < MR; ++m)
         if (m < M) {
-          double2 v = ws[(long)m * N + n];
-          for (int p = 1; p < P; ++p) v = cadd(v, ws[((long)p * M + m) * N + n]);
+          double2 pv[GEMV_MAX_SPLIT];  // all loads in flight, then summed in split order
+#pragma unroll
+          for (int p = 0; p < GEMV_MAX_SPLIT; ++p)
+            pv[p] = p < P ? ld_dev(&ws[((long)p * M + m) * N + n]) : make_double2(0.0, 0.0);
+          double2 v = pv[0];
+#pragma unroll
+          for (int p = 1; p < GEMV_MAX_SPLIT; ++p)
+            if (p < P) v = cadd(v, pv[p]);
           acc[m] = v;
         }
   }
 
   double re[MR];
-  if (wave == 0 && col_ok)
+  if (owner && col_ok)
 #pragma unroll
     for (int m = 0; m < MR; ++m)
       if (m < M) re[m] = apply_epi(ep, M, N, m, n, acc[m]);
-  if (!am.part_v) return;
-  if (wave == 0)
+  if (!am.part_v || wave != 0) return;
 #pragma unroll
-    for (int m = 0; m < MR; ++m)
-      if (m < M) {
-        double bv = -INFINITY;
-        int bi = -1;
-        if (col_ok) {
-          if (isnan(re[m])) atomicOr(am.err, (uint32_t)EB_ARGMAX_NAN);
-          else bv = re[m], bi = n;
-        }
-        wave_argmax(bv, bi);
-        if (lane == 0) {
-          am.part_v[(long)m * gridDim.x + blockIdx.x] = bv;
-          am.part_i[(long)m * gridDim.x + blockIdx.x] = bi;
-        }
+  for (int m = 0; m < MR; ++m)
+    if (m < M) {
+      double bv = -INFINITY;
+      int bi = -1;
+      if (lane < C && col_ok) {
+        if (isnan(re[m])) atomicOr(am.err, (uint32_t)EB_ARGMAX_NAN);
+        else bv = re[m], bi = n;
       }
-  if (!arrive_last(&cnt[SYNC_COUNTERS - 1], gridDim.x)) return;
-  argmax_finish(am, M, gridDim.x);
+      wave_argmax(bv, bi);
+      if (lane == 0) {
+        am.part_v[(long)m * gridDim.x + blockIdx.x] = bv;
+        am.part_i[(long)m * gridDim.x + blockIdx.x] = bi;
+      }
+    }
 }
 
 // The prologue alone, one block per row.
@@ -437,17 +464,27 @@ __global__ __launch_bounds__(256) void k_zgemm_mfma(const double2* __restrict__ 
         for (int r = 0; r < 4; ++r) {
           const int m = m0 + wm + 16 * i + (lane >> 4) + 4 * r;
           const int n = n0 + wn + 16 * j + (lane & 15);
-          if (m < M && n < N) ws[((long)blockIdx.z * M + m) * N + n] = make_double2(cr[i][j][r], ci[i][j][r]);
+          if (m < M && n < N) st_dev(&ws[((long)blockIdx.z * M + m) * N + n], make_double2(cr[i][j][r], ci[i][j][r]));
         }
     if (!arrive_last(&cnt[blockIdx.y * gridDim.x + blockIdx.x], gridDim.z)) return;
+    // thread t owns tile elements t + 256 i (row t/64 + 4i, column t%64); the
+    // splits are summed in order, 16 independent loads in flight per split
     const int P = gridDim.z;
-    for (int e = tid; e < GBM * GBN; e += 256) {
-      const int ml = e / GBN, nl = e - ml * GBN;
-      const int m = m0 + ml, n = n0 + nl;
+    const int nl = tid & 63, n = n0 + nl;
+    double2 v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = make_double2(0.0, 0.0);
+    for (int p = 0; p < P; ++p)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int m = m0 + (tid >> 6) + 4 * i;
+        if (m < M && n < N) v[i] = cadd(v[i], ld_dev(&ws[((long)p * M + m) * N + n]));
+      }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int ml = (tid >> 6) + 4 * i, m = m0 + ml;
       if (m < M && n < N) {
-        double2 v = ws[(long)m * N + n];
-        for (int p = 1; p < P; ++p) v = cadd(v, ws[((long)p * M + m) * N + n]);
-        const double re = apply_epi(ep, M, N, m, n, v);
+        const double re = apply_epi(ep, M, N, m, n, v[i]);
         if (argmax) stage[ml * 65 + nl] = re;
       }
     }
@@ -455,7 +492,6 @@ __global__ __launch_bounds__(256) void k_zgemm_mfma(const double2* __restrict__ 
   if (!argmax) return;
   __syncthreads();
   // per-row (max, last index) over the tile's columns: wave w takes rows w, w+4, ...
-  const int tiles_n = gridDim.x;
   for (int ml = wave; ml < GBM; ml += 4) {
     const int m = m0 + ml, n = n0 + lane;
     if (m >= M) break;
@@ -468,25 +504,168 @@ __global__ __launch_bounds__(256) void k_zgemm_mfma(const double2* __restrict__ 
     }
     wave_argmax(bv, bi);
     if (lane == 0) {
-      am.part_v[(long)m * tiles_n + blockIdx.x] = bv;
-      am.part_i[(long)m * tiles_n + blockIdx.x] = bi;
+      am.part_v[(long)m * gridDim.x + blockIdx.x] = bv;
+      am.part_i[(long)m * gridDim.x + blockIdx.x] = bi;
     }
   }
-  if (!arrive_last(&cnt[SYNC_COUNTERS - 1], gridDim.x * gridDim.y)) return;
-  argmax_finish(am, M, tiles_n);
+}
+
+// ===========================================================================
+// Skinny MFMA GEMM for 9 <= M <= 64 rows (batched decode): a block owns all M
+// rows (RT tiles of 16) and 16 columns; its K range is split over the 4 waves,
+// each accumulating the whole 16RT x 16 tile with v_mfma_f64_16x16x4_f64 from
+// operands loaded straight from global memory (A: row i, k offset lane/16;
+// B: column i, k offset lane/16).  Waves are summed through LDS, blockIdx.y
+// splits K at most 8 ways.
+// ===========================================================================
+template <int RT>
+__global__ __launch_bounds__(256) void k_zgemm_skinny(const double2* __restrict__ X, long ldx, int M,
+                                                        const double2* __restrict__ W, long ldw, int N, int K, int kc,
+                                                        Epi ep, Argmax am, double2* __restrict__ ws,
+                                                        uint32_t* __restrict__ cnt) {
+  __shared__ double2 red[4][16 * RT][16];
+  __shared__ double stage[16 * RT][17];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int i = lane & 15, kq = lane >> 4;
+  const int n0 = blockIdx.x * 16, n = n0 + i;
+  const int kb0 = blockIdx.y * kc, kb1 = min(K, kb0 + kc);
+  const int q = kc / 4;  // multiple of 16
+  const int ka = kb0 + wave * q, kz = min(kb1, ka + q);
+
+  v4d cr[RT], ci[RT];
+#pragma unroll
+  for (int t = 0; t < RT; ++t) cr[t] = ci[t] = v4d{0.0, 0.0, 0.0, 0.0};
+
+  constexpr int U = 4;  // k-steps of 4 per batch
+  for (int k = ka; k < kz; k += 4 * U) {
+    double2 b[U], a[RT][U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int kk = k + 4 * u + kq;
+      b[u] = (kk < kz && n < N) ? W[(long)kk * ldw + n] : make_double2(0.0, 0.0);
+#pragma unroll
+      for (int t = 0; t < RT; ++t) {
+        const int m = 16 * t + i;
+        a[t][u] = (kk < kz && m < M) ? X[(long)m * ldx + kk] : make_double2(0.0, 0.0);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int t = 0; t < RT; ++t) {
+        cr[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[t][u].x, b[u].x, cr[t], 0, 0, 0);
+        ci[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[t][u].x, b[u].y, ci[t], 0, 0, 0);
+        cr[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(-a[t][u].y, b[u].y, cr[t], 0, 0, 0);
+        ci[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[t][u].y, b[u].x, ci[t], 0, 0, 0);
+      }
+  }
+  // D[i][j] of row tile t at lane j + 16*(i%4), element i/4
+#pragma unroll
+  for (int t = 0; t < RT; ++t)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) red[wave][16 * t + 4 * e + kq][i] = make_double2(cr[t][e], ci[t][e]);
+  __syncthreads();
+  // thread tid owns tile elements tid + 256 j: row (tid >> 4) + 16 j, column tid & 15
+  const int col = tid & 15, n1 = n0 + col;
+  double2 v[RT];
+#pragma unroll
+  for (int j = 0; j < RT; ++j) {
+    const int row = (tid >> 4) + 16 * j;
+    v[j] = cadd(cadd(cadd(red[0][row][col], red[1][row][col]), red[2][row][col]), red[3][row][col]);
+  }
+  const int P = gridDim.y;
+  if (P > 1) {
+#pragma unroll
+    for (int j = 0; j < RT; ++j) {
+      const int m = (tid >> 4) + 16 * j;
+      if (m < M && n1 < N) st_dev(&ws[((long)blockIdx.y * M + m) * N + n1], v[j]);
+    }
+    if (!arrive_last(&cnt[blockIdx.x], (uint32_t)P)) return;
+#pragma unroll
+    for (int j = 0; j < RT; ++j) {
+      const int m = (tid >> 4) + 16 * j;
+      if (m < M && n1 < N) {
+        double2 pv[SKINNY_MAX_SPLIT];
+#pragma unroll
+        for (int p = 0; p < SKINNY_MAX_SPLIT; ++p)
+          pv[p] = p < P ? ld_dev(&ws[((long)p * M + m) * N + n1]) : make_double2(0.0, 0.0);
+        double2 s = pv[0];
+#pragma unroll
+        for (int p = 1; p < SKINNY_MAX_SPLIT; ++p)
+          if (p < P) s = cadd(s, pv[p]);
+        v[j] = s;
+      }
+    }
+  }
+  const bool argmax = am.part_v != nullptr;
+#pragma unroll
+  for (int j = 0; j < RT; ++j) {
+    const int row = (tid >> 4) + 16 * j;
+    if (row < M && n1 < N) {
+      const double re = apply_epi(ep, M, N, row, n1, v[j]);
+      if (argmax) stage[row][col] = re;
+    }
+  }
+  if (!argmax) return;
+  __syncthreads();
+  // per row over the 16 columns: 16-lane groups, (max, last index)
+#pragma unroll
+  for (int j = 0; j < RT; ++j) {
+    const int row = (tid >> 4) + 16 * j;
+    double bv = -INFINITY;
+    int bi = -1;
+    if (row < M && n1 < N) {
+      const double x = stage[row][col];
+      if (isnan(x)) atomicOr(am.err, (uint32_t)EB_ARGMAX_NAN);
+      else bv = x, bi = n1;
+    }
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) {
+      const double ov = __shfl_xor(bv, o, 64);
+      const int oi = __shfl_xor(bi, o, 64);
+      argmax_combine(bv, bi, ov, oi);
+    }
+    if (col == 0 && row < M) {
+      am.part_v[(long)row * gridDim.x + blockIdx.x] = bv;
+      am.part_i[(long)row * gridDim.x + blockIdx.x] = bi;
+    }
+  }
 }
 
 // ---- planning and dispatch ------------------------------------------------
+// GEMV: C columns per block (16, or 64 for wide outputs), K split so that the
+// grid has about 512 blocks, at most GEMV_MAX_SPLIT ways.
 struct GemvPlan {
-  int mr, kw, P, ncb;
+  int mr, C, kw, P, ncb;
 };
 static GemvPlan plan_gemv(int M, int N, int K) {
   GemvPlan p;
   p.mr = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
-  p.ncb = cdiv_i(N, 64);
-  const int P0 = std::max(1, cdiv_i(1024, p.ncb));  // about 4 blocks per CU
-  p.kw = std::min(128, std::max(2, cdiv_i(cdiv_i(K, P0), 4)));
-  p.P = cdiv_i(K, 4 * p.kw);
+  p.C = cdiv_i(N, 64) >= 256 ? 64 : 16;
+  const int rpw = 64 / p.C;
+  p.ncb = cdiv_i(N, p.C);
+  int P = std::min(GEMV_MAX_SPLIT, std::max(1, cdiv_i(512, p.ncb)));
+  // rows per block: a multiple of 4 waves x rpw, and its input rows fit 64 KB of LDS
+  const int unit = 4 * rpw;
+  int KB = cdiv_i(cdiv_i(K, P), unit) * unit;
+  const int kb_max = std::max(unit, (65536 / (16 * p.mr)) / unit * unit);
+  KB = std::min(KB, kb_max);
+  p.kw = KB / 4;
+  p.P = cdiv_i(K, KB);
+  return p;
+}
+// skinny MFMA: 16 columns per block, K split in chunks that are multiples of
+// 64 (16 per wave), about 512 blocks, at most SKINNY_MAX_SPLIT ways
+struct SkinnyPlan {
+  int rt, ncb, kc, P;
+};
+static SkinnyPlan plan_skinny(int M, int N, int K) {
+  SkinnyPlan p;
+  p.rt = cdiv_i(M, 16);
+  p.ncb = cdiv_i(N, 16);
+  const int P = std::min(SKINNY_MAX_SPLIT, std::max(1, cdiv_i(512, p.ncb)));
+  p.kc = cdiv_i(cdiv_i(K, P), 64) * 64;
+  p.P = cdiv_i(K, p.kc);
   return p;
 }
 struct MfmaPlan {
@@ -504,24 +683,32 @@ static MfmaPlan plan_mfma(int M, int N, int K) {
   return p;
 }
 
+constexpr int SKINNY_MAX_M = 64;
+
 size_t gemm_ws_bytes(int M, int N, int K) {
-  if (M <= 8) {
-    const GemvPlan p = plan_gemv(M, N, K);
-    return p.P > 1 ? (size_t)p.P * M * N * sizeof(double2) : 0;
-  }
-  const MfmaPlan p = plan_mfma(M, N, K);
-  return p.P > 1 ? (size_t)p.P * M * N * sizeof(double2) : 0;
+  int P;
+  if (M <= 8) P = plan_gemv(M, N, K).P;
+  else if (M <= SKINNY_MAX_M) P = plan_skinny(M, N, K).P;
+  else P = plan_mfma(M, N, K).P;
+  return P > 1 ? (size_t)P * M * N * sizeof(double2) : 0;
 }
 
-size_t argmax_part_elems(int M, int N) { return (size_t)M * cdiv_i(N, 64); }
+// argmax partials: one per row and 16-column tile covers every product shape
+size_t argmax_part_elems(int M, int N) { return (size_t)M * cdiv_i(N, 16); }
 
-template <int MR>
+template <int MR, int C>
 static void launch_gemv(hipStream_t st, const GemvPlan& p, const RowOps& ro, int M, const double2* W, long ldw, int N,
                         int K, const Epi& ep, const Argmax& am, const Sync& sy) {
   dim3 grid(p.ncb, p.P);
   const size_t shm = (size_t)MR * 4 * p.kw * sizeof(double2);
-  hipLaunchKernelGGL((k_gemv<MR>), grid, dim3(256), shm, st, ro, M, W, ldw, N, K, p.kw, ep, am, (double2*)sy.ws,
+  hipLaunchKernelGGL((k_gemv<MR, C>), grid, dim3(256), shm, st, ro, M, W, ldw, N, K, p.kw, ep, am, (double2*)sy.ws,
                      sy.counters);
+}
+template <int MR>
+static void launch_gemv_c(hipStream_t st, const GemvPlan& p, const RowOps& ro, int M, const double2* W, long ldw, int N,
+                          int K, const Epi& ep, const Argmax& am, const Sync& sy) {
+  if (p.C == 64) launch_gemv<MR, 64>(st, p, ro, M, W, ldw, N, K, ep, am, sy);
+  else launch_gemv<MR, 16>(st, p, ro, M, W, ldw, N, K, ep, am, sy);
 }
 
 int gemm(hipStream_t st, int M, int N, int K, const RowOps& ro, const double2* W, long ldw, const Epi& ep,
@@ -529,25 +716,40 @@ int gemm(hipStream_t st, int M, int N, int K, const RowOps& ro, const double2* W
   if (M <= 0 || N <= 0) return OK;
   const Argmax am = amp ? *amp : Argmax();
   if (gemm_ws_bytes(M, N, K) > sy.ws_bytes) return ERR_STATE;
+  int tiles = 0;  // column tiles of the argmax partials
   if (M <= 8) {
     const GemvPlan p = plan_gemv(M, N, K);
-    if (p.ncb >= SYNC_COUNTERS - 1) return ERR_ARG;
+    if (p.ncb >= SYNC_COUNTERS) return ERR_ARG;
     switch (p.mr) {
-      case 1: launch_gemv<1>(st, p, ro, M, W, ldw, N, K, ep, am, sy); break;
-      case 2: launch_gemv<2>(st, p, ro, M, W, ldw, N, K, ep, am, sy); break;
-      case 4: launch_gemv<4>(st, p, ro, M, W, ldw, N, K, ep, am, sy); break;
-      default: launch_gemv<8>(st, p, ro, M, W, ldw, N, K, ep, am, sy); break;
+      case 1: launch_gemv_c<1>(st, p, ro, M, W, ldw, N, K, ep, am, sy); break;
+      case 2: launch_gemv_c<2>(st, p, ro, M, W, ldw, N, K, ep, am, sy); break;
+      case 4: launch_gemv_c<4>(st, p, ro, M, W, ldw, N, K, ep, am, sy); break;
+      default: launch_gemv_c<8>(st, p, ro, M, W, ldw, N, K, ep, am, sy); break;
     }
-    return OK;
+    tiles = p.ncb;
+  } else {
+    if (!ro.plain()) return ERR_ARG;  // the MFMA paths read plain rows; materialise the prologue first
+    if (M <= SKINNY_MAX_M) {
+      const SkinnyPlan p = plan_skinny(M, N, K);
+      if (p.ncb >= SYNC_COUNTERS) return ERR_ARG;
+      dim3 grid(p.ncb, p.P);
+      switch (p.rt) {
+        case 1: hipLaunchKernelGGL((k_zgemm_skinny<1>), grid, dim3(256), 0, st, ro.x, ro.ldx, M, W, ldw, N, K, p.kc, ep, am, (double2*)sy.ws, sy.counters); break;
+        case 2: hipLaunchKernelGGL((k_zgemm_skinny<2>), grid, dim3(256), 0, st, ro.x, ro.ldx, M, W, ldw, N, K, p.kc, ep, am, (double2*)sy.ws, sy.counters); break;
+        case 3: hipLaunchKernelGGL((k_zgemm_skinny<3>), grid, dim3(256), 0, st, ro.x, ro.ldx, M, W, ldw, N, K, p.kc, ep, am, (double2*)sy.ws, sy.counters); break;
+        default: hipLaunchKernelGGL((k_zgemm_skinny<4>), grid, dim3(256), 0, st, ro.x, ro.ldx, M, W, ldw, N, K, p.kc, ep, am, (double2*)sy.ws, sy.counters); break;
+      }
+      tiles = p.ncb;
+    } else {
+      const MfmaPlan p = plan_mfma(M, N, K);
+      if (p.P > 1 && (long)p.mt * p.nt >= SYNC_COUNTERS) return ERR_ARG;
+      dim3 grid(p.nt, p.mt, p.P);
+      hipLaunchKernelGGL(k_zgemm_mfma, grid, dim3(256), 0, st, ro.x, ro.ldx, W, ldw, M, N, K, p.kchunk, ep, am,
+                         (double2*)sy.ws, sy.counters);
+      tiles = p.nt;
+    }
   }
-  if (!ro.plain()) return ERR_ARG;  // the MFMA path reads plain rows; materialise the prologue first
-  const MfmaPlan p = plan_mfma(M, N, K);
-  if ((long)p.mt * p.nt >= SYNC_COUNTERS - 1) {
-    if (p.P > 1 || am.part_v) return ERR_ARG;
-  }
-  dim3 grid(p.nt, p.mt, p.P);
-  hipLaunchKernelGGL(k_zgemm_mfma, grid, dim3(256), 0, st, ro.x, ro.ldx, W, ldw, M, N, K, p.kchunk, ep, am,
-                     (double2*)sy.ws, sy.counters);
+  if (am.part_v) hipLaunchKernelGGL(k_argmax_finalize, dim3(M), dim3(256), 0, st, am, tiles);
   return OK;
 }
 

@@ -103,8 +103,9 @@ def test_linear_reference_known_answer():
     assert np.array_equal(out[0].real, [[15, 18, 21, 24, 27, 30], [31, 38, 45, 52, 59, 66], [47, 58, 69, 80, 91, 102]])
 
 
-@pytest.mark.parametrize("M,K,N", [(1, 512, 1536), (2, 300, 77), (8, 2048, 512), (32, 512, 2048), (100, 96, 130),
-                                   (4096, 64, 64)])
+@pytest.mark.parametrize("M,K,N", [(1, 512, 1536), (2, 300, 77), (8, 2048, 512), (1, 512, 32000), (5, 768, 20000),
+                                   (9, 64, 33), (16, 512, 1536), (32, 512, 2048), (40, 300, 77), (64, 2048, 512),
+                                   (100, 96, 130), (4096, 64, 64)])
 def test_gemm_random_vs_oracle(M, K, N):
     rng = np.random.default_rng(M * 7 + K)
     A = rng.standard_normal((M, K)) + 1j * rng.standard_normal((M, K))

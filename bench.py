@@ -117,6 +117,8 @@ def main():
     ap.add_argument("--workload", default="c3b32", choices=sorted(configs.WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-b1", action="store_true", help="skip the batch-1 companion measurement")
+    ap.add_argument("--no-classes", action="store_true",
+                    help="skip the per-kernel-class HIP-event pass (profiler runs of the timed region only)")
     ap.add_argument("--direct", action="store_true",
                     help="launch decode kernels directly instead of replaying HIP graphs (for profilers)")
     args = ap.parse_args()
@@ -141,19 +143,21 @@ def main():
     decode_tok_s = B * (n_new - 1) / (dec_ms / 1e3) if dec_ms > 0 else None
 
     # roofline of the dominant kernel classes, HIP events on the library stream
-    log("kernel-class timing")
-    classes = {}
-    for name, cls, bound in (("vocab", ra.TIME_VOCAB, None), ("layer_gemm", ra.TIME_LAYER_GEMM, None),
-                             ("attention", ra.TIME_ATTENTION, None)):
-        classes[name] = kernel_class(net, prompt, lens, n_new, cls)
-    dominant = max(("vocab", "layer_gemm"), key=lambda k: classes[k]["total_ms"])
-    r = classes[dominant]
-    # a GEMM class is MFMA-bound when its arithmetic intensity exceeds the ridge point
-    intensity = r["alg_flops"] / max(r["alg_bytes"], 1.0)
-    bound = "mfma" if intensity > FP64_MFMA_PEAK_TFS * 1e12 / (HBM_PEAK_GBS * 1e9) else "hbm"
-    roof = roofline_entry(r, bound)
-    roof["kernel_class"] = dominant
-    class_ms = {k: round(v["total_ms"] / 2, 3) for k, v in classes.items()}
+    roof, class_ms = None, None
+    if not args.no_classes:
+        log("kernel-class timing")
+        classes = {}
+        for name, cls in (("vocab", ra.TIME_VOCAB), ("layer_gemm", ra.TIME_LAYER_GEMM),
+                          ("attention", ra.TIME_ATTENTION)):
+            classes[name] = kernel_class(net, prompt, lens, n_new, cls)
+        dominant = max(("vocab", "layer_gemm"), key=lambda k: classes[k]["total_ms"])
+        r = classes[dominant]
+        # a GEMM class is MFMA-bound when its arithmetic intensity exceeds the ridge point
+        intensity = r["alg_flops"] / max(r["alg_bytes"], 1.0)
+        bound = "mfma" if intensity > FP64_MFMA_PEAK_TFS * 1e12 / (HBM_PEAK_GBS * 1e9) else "hbm"
+        roof = roofline_entry(r, bound)
+        roof["kernel_class"] = dominant
+        class_ms = {k: round(v["total_ms"] / 2, 3) for k, v in classes.items()}
 
     out = {
         "metric": "generated tokens/s",

@@ -96,54 +96,157 @@ void attention_rows(hipStream_t st, const Attn& a) {
 // Decode (one query row per sequence, masked_attention_head.rs:135-208 with
 // the cache): keys are split in chunks of CH, one block per (chunk, head,
 // sequence).  No causal mask in this branch; bias_pos row 0.  A block scores
-// its chunk (16 lanes per key, 4 keys per wave), keeps the chunk's max m,
-// sum l of exp(s - m) and o = sum exp(s - m) v, and the last chunk of each
-// (sequence, head) to finish rescales the chunks to the common max, in
-// chunk order: out = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M).
+// its chunk (16 lanes per key, 4 keys per wave) and leaves the chunk's max m,
+// sum l of exp(s - m) and o = sum exp(s - m) v; the rows are finished by the
+// row transform (rowops.hpp), which rescales the chunks to the common max:
+// out = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M), then the residual and
+// LayerNorm of the attention layer.  No block waits for another.
 // ===========================================================================
 constexpr int DEC_LPK = 16;          // lanes per key in the score phase
 constexpr int DEC_MAX_SPLITS = 256;  // key chunks per (sequence, head)
 
-static int decode_chunk(int B, int H) { return B * H <= 64 ? 32 : 64; }
+// keys per chunk: 32 reads the cache at ~7 TB/s where 64 reached under 4
+// (the same bytes, fewer blocks in flight); 16 when there are few heads in all
+constexpr int DEC_MAX_CHUNK = 32;
+static int decode_chunk(int B, int H) { return B * H <= 16 ? 16 : 32; }
 
-__global__ __launch_bounds__(256) void k_attention_decode(Attn a, int CH, int nsplit, double* __restrict__ pm,
-                                                          double* __restrict__ pl, double2* __restrict__ po,
-                                                          uint32_t* __restrict__ cnt) {
-  __shared__ double sc[64];
+// q is the sum of npart partials (row b at q + b * ldq, partial stride
+// pstride).  With `append`, the partials hold [q | k | v] of the new token
+// (the fused decode plan): the chunk of position T-1 sums that token's k and
+// v, appends them to the cache and uses them directly.
+// DH > 0: head dim known at compile time; every key, value and bias_pos
+// load of the chunk is issued at entry, before q is summed, so the chunk
+// costs one memory round trip.  DH == 0: any head dim up to 256.
+template <int DH>
+__global__ __launch_bounds__(256) void k_attention_split(Attn a, const double2* __restrict__ qkv, long ldq, int npart,
+                                                         long pstride, int append, AttnSplit o) {
+  constexpr int NP = DEC_MAX_CHUNK / 16;  // score passes (16 keys each)
+  __shared__ double sc[DEC_MAX_CHUNK];
   __shared__ double2 pv[256];
+  __shared__ double2 qs[256], kn[256], vn[256];
   __shared__ double stat[2];
-  __shared__ double cw[DEC_MAX_SPLITS], cl[DEC_MAX_SPLITS];
+  const int dh = DH > 0 ? DH : a.dh;
   const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int T = a.kv_len ? a.kv_len[b] + a.T_add : a.T_const;
+  const int T = a.kv_len[b] + 1;
+  const int CH = o.CH;
   const int c0 = split * CH;
-  if (c0 >= T) return;  // not part of this sequence's split count
+  if (c0 >= T) return;  // the consumer reads only this sequence's chunks
   const int nc = min(CH, T - c0);
-  const int ns = (T + CH - 1) / CH;
+  const bool has_new = append && c0 + nc == T;  // chunk of the new token, position T-1, still to append
+  const int d = a.H * dh;
   const long bh = (long)b * a.H + h;
-  const double2* qrow = a.q + (long)b * a.ldq + (long)h * a.dh;
-  const double2* K = a.kc + bh * a.ctx * a.dh;
-  const double2* V = a.vc + bh * a.ctx * a.dh;
+  const double2* K = a.kc + bh * a.ctx * dh;
+  const double2* V = a.vc + bh * a.ctx * dh;
   const double* bias0 = a.bias_re + (long)h * a.mc * a.mc;  // bias_pos row 0
 
-  // scores: key j = it + 4*w + (lane / 16) of the chunk, lanes j%16 split the head dim
-  const int sub = lane & (DEC_LPK - 1), kw = lane / DEC_LPK;
-  for (int j0 = 0; j0 < nc; j0 += 16) {
-    const int j = j0 + wave * 4 + kw;
-    double acc = 0.0;
-    if (j < nc) {
-      const double2* kr = K + (long)(c0 + j) * a.dh;
-      for (int e = sub; e < a.dh; e += DEC_LPK) {
-        const double2 kv = kr[e], qv = qrow[e];
-        acc += qv.x * kv.x - qv.y * kv.y;
+  // score lanes: 16 per key, 4 keys per wave and pass
+  const int sub = lane & (DEC_LPK - 1), kq = lane / DEC_LPK;
+  constexpr int EPL = DH > 0 ? (DH + DEC_LPK - 1) / DEC_LPK : 1;
+  // value lanes: element e, key group g of G
+  const int G = 256 / dh;
+  const int e = tid % dh, g = tid / dh;
+  constexpr int VG = 256 / (DH > 0 ? DH : 256);
+  constexpr int VU = DH > 0 ? (DEC_MAX_CHUNK + VG - 1) / VG : 1;  // keys per value lane
+  // keys and bias rows are in flight while q is summed; values are loaded after
+  // the softmax, which keeps the register count (and the blocks per CU) high
+  double2 kv[NP][EPL];
+  double bj[NP];
+  if (DH > 0) {
+#pragma unroll
+    for (int pass = 0; pass < NP; ++pass) {
+      const int j = pass * 16 + wave * 4 + kq;
+      const double2* kr = K + (long)(c0 + j) * dh;
+#pragma unroll
+      for (int t = 0; t < EPL; ++t) {
+        const int ee = sub + t * DEC_LPK;
+        kv[pass][t] = (j < nc && ee < dh) ? kr[ee] : make_double2(0.0, 0.0);
+      }
+      bj[pass] = (j < nc && sub == 0) ? bias0[c0 + j] : 0.0;
+    }
+  }
+
+  const double2* row = qkv + (long)b * ldq + (long)h * dh;
+  for (int ee = tid; ee < dh; ee += 256) {
+    double2 q = make_double2(0.0, 0.0), kk = q, vx = q;
+    for (int p0 = 0; p0 < npart; p0 += 4) {  // partials summed in order, four loads in flight
+      double2 t[4];
+#pragma unroll
+      for (int p = 0; p < 4; ++p) t[p] = p0 + p < npart ? row[(p0 + p) * pstride + ee] : make_double2(0.0, 0.0);
+#pragma unroll
+      for (int p = 0; p < 4; ++p)
+        if (p0 + p < npart) q = (p0 + p == 0) ? t[p] : cadd(q, t[p]);
+      if (has_new) {
+#pragma unroll
+        for (int p = 0; p < 4; ++p) t[p] = p0 + p < npart ? row[(p0 + p) * pstride + d + ee] : make_double2(0.0, 0.0);
+#pragma unroll
+        for (int p = 0; p < 4; ++p)
+          if (p0 + p < npart) kk = (p0 + p == 0) ? t[p] : cadd(kk, t[p]);
+#pragma unroll
+        for (int p = 0; p < 4; ++p) t[p] = p0 + p < npart ? row[(p0 + p) * pstride + 2 * d + ee] : make_double2(0.0, 0.0);
+#pragma unroll
+        for (int p = 0; p < 4; ++p)
+          if (p0 + p < npart) vx = (p0 + p == 0) ? t[p] : cadd(vx, t[p]);
+      }
+    }
+    qs[ee] = q;
+    if (has_new) {
+      kn[ee] = kk;
+      vn[ee] = vx;
+      if (T - 1 < a.ctx) {  // append (masked_attention_head.rs:159-178)
+        a.kc_w[(bh * a.ctx + (T - 1)) * dh + ee] = kk;
+        a.vc_w[(bh * a.ctx + (T - 1)) * dh + ee] = vx;
+      } else if (ee == 0) {
+        atomicOr(a.err, (uint32_t)EB_CTX_OVERFLOW);
+      }
+    }
+  }
+  __syncthreads();
+
+  if (DH > 0) {
+    if (has_new) {  // the new token's row from LDS (its cache row was written just above)
+#pragma unroll
+      for (int pass = 0; pass < NP; ++pass) {
+        const int j = pass * 16 + wave * 4 + kq;
+#pragma unroll
+        for (int t = 0; t < EPL; ++t) {
+          const int ee = sub + t * DEC_LPK;
+          if (c0 + j == T - 1 && ee < dh) kv[pass][t] = kn[ee];
+        }
       }
     }
 #pragma unroll
-    for (int o = DEC_LPK / 2; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
-    if (j < nc && sub == 0) sc[j] = acc * a.scale + bias0[c0 + j];
+    for (int pass = 0; pass < NP; ++pass) {
+      const int j = pass * 16 + wave * 4 + kq;
+      double acc = 0.0;
+#pragma unroll
+      for (int t = 0; t < EPL; ++t) {
+        const int ee = sub + t * DEC_LPK;
+        if (ee < dh) acc += qs[ee].x * kv[pass][t].x - qs[ee].y * kv[pass][t].y;
+      }
+#pragma unroll
+      for (int off = DEC_LPK / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+      if (j < nc && sub == 0) sc[j] = acc * a.scale + bj[pass];
+    }
+  } else {
+    for (int j0 = 0; j0 < nc; j0 += 16) {
+      const int j = j0 + wave * 4 + kq;
+      double acc = 0.0;
+      if (j < nc) {
+        const bool is_new = has_new && c0 + j == T - 1;
+        const double2* kr = K + (long)(c0 + j) * dh;
+        for (int ee = sub; ee < dh; ee += DEC_LPK) {
+          const double2 k2 = is_new ? kn[ee] : kr[ee], qv = qs[ee];
+          acc += qv.x * k2.x - qv.y * k2.y;
+        }
+      }
+#pragma unroll
+      for (int off = DEC_LPK / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+      if (j < nc && sub == 0) sc[j] = acc * a.scale + bias0[c0 + j];
+    }
   }
   __syncthreads();
-  if (wave == 0) {
+  if (wave == 0) {  // nc <= 32 < 64 lanes
     const double s = lane < nc ? sc[lane] : -INFINITY;
     const double m = wave_max(s);
     const double p = lane < nc ? exp(s - m) : 0.0;
@@ -152,86 +255,80 @@ __global__ __launch_bounds__(256) void k_attention_decode(Attn a, int CH, int ns
     if (lane == 0) stat[0] = m, stat[1] = l;
   }
   __syncthreads();
-  const int G = 256 / a.dh;
-  const int e = tid % a.dh, g = tid / a.dh;
+  // out[e] over the chunk's keys: group g takes keys g, g + G, ...
   double2 acc = make_double2(0.0, 0.0);
-  if (g < G)
+  if (DH > 0) {
+    double2 vv[VU];
+#pragma unroll
+    for (int u = 0; u < VU; ++u) {
+      const int j = g + u * G;
+      vv[u] = (g < G && j < nc) ? V[(long)(c0 + j) * dh + e] : make_double2(0.0, 0.0);
+    }
+    if (has_new)
+#pragma unroll
+      for (int u = 0; u < VU; ++u)
+        if (g < G && c0 + g + u * G == T - 1) vv[u] = vn[e];
+#pragma unroll
+    for (int u = 0; u < VU; ++u) {
+      const int j = g + u * G;
+      if (g < G && j < nc) {
+        const double p = sc[j];
+        acc.x += p * vv[u].x;
+        acc.y += p * vv[u].y;
+      }
+    }
+  } else if (g < G) {
     for (int j = g; j < nc; j += G) {
       const double p = sc[j];
-      const double2 v = V[(long)(c0 + j) * a.dh + e];
+      const double2 v = (has_new && c0 + j == T - 1) ? vn[e] : V[(long)(c0 + j) * dh + e];
       acc.x += p * v.x;
       acc.y += p * v.y;
     }
+  }
   pv[tid] = acc;
   __syncthreads();
-  const long pidx = bh * nsplit + split;
-  if (tid < a.dh) {
+  const long pidx = bh * o.nsplit + split;
+  if (tid < dh) {
     double2 s = pv[tid];
-    for (int gg = 1; gg < G; ++gg) s = cadd(s, pv[gg * a.dh + tid]);
-    st_dev(&po[pidx * a.dh + tid], s);
+    for (int gg = 1; gg < G; ++gg) s = cadd(s, pv[gg * dh + tid]);
+    ((double2*)o.po)[pidx * dh + tid] = s;
   }
   if (tid == 0) {
-    st_dev(&pm[pidx], stat[0]);
-    st_dev(&pl[pidx], stat[1]);
-  }
-  if (!arrive_last(&cnt[bh], (uint32_t)ns)) return;
-
-  double2* out = a.out + (long)b * a.ldo + (long)h * a.dh;
-  if (a.row_mask && a.row_mask[b] == 0) {
-    for (int t = tid; t < a.dh; t += 256) out[t] = make_double2(0.0, 0.0);
-    return;
-  }
-  const long base = bh * nsplit;
-  // chunk statistics through LDS: cw[s] = e^(m_s - M), L = sum_s l_s cw[s] in chunk order
-  if (tid < ns) cw[tid] = ld_dev(&pm[base + tid]);
-  __syncthreads();
-  double M = -INFINITY;
-  for (int s = 0; s < ns; ++s) M = fmax(M, cw[s]);
-  __syncthreads();
-  if (tid < ns) {
-    const double w = exp(cw[tid] - M);
-    cw[tid] = w;
-    cl[tid] = ld_dev(&pl[base + tid]) * w;
-  }
-  __syncthreads();
-  double L = 0.0;
-  for (int s = 0; s < ns; ++s) L += cl[s];
-  for (int t = tid; t < a.dh; t += 256) {
-    double2 o = make_double2(0.0, 0.0);
-    int s = 0;
-    for (; s + 4 <= ns; s += 4) {
-      const double2 v0 = ld_dev(&po[(base + s) * a.dh + t]);
-      const double2 v1 = ld_dev(&po[(base + s + 1) * a.dh + t]);
-      const double2 v2 = ld_dev(&po[(base + s + 2) * a.dh + t]);
-      const double2 v3 = ld_dev(&po[(base + s + 3) * a.dh + t]);
-      o.x += v0.x * cw[s], o.y += v0.y * cw[s];
-      o.x += v1.x * cw[s + 1], o.y += v1.y * cw[s + 1];
-      o.x += v2.x * cw[s + 2], o.y += v2.y * cw[s + 2];
-      o.x += v3.x * cw[s + 3], o.y += v3.y * cw[s + 3];
-    }
-    for (; s < ns; ++s) {
-      const double2 v = ld_dev(&po[(base + s) * a.dh + t]);
-      o.x += v.x * cw[s];
-      o.y += v.y * cw[s];
-    }
-    out[t] = make_double2(o.x / L, o.y / L);
+    ((double*)o.pm)[pidx] = stat[0];
+    ((double*)o.pl)[pidx] = stat[1];
   }
 }
 
-size_t attention_decode_ws_bytes(int B, int H, int dh, int T_max) {
+AttnSplit attention_split_plan(const Attn& a) {
+  AttnSplit o;
+  o.H = a.H;
+  o.dh = a.dh;
+  o.CH = decode_chunk(a.B, a.H);
+  o.nsplit = cdiv_i(a.T_max, o.CH);
+  o.kv_len = a.kv_len;
+  return o;
+}
+
+size_t attention_split_ws_bytes(int B, int H, int dh, int T_max) {
   const int ns = cdiv_i(T_max, decode_chunk(B, H));
   return (size_t)B * H * ns * (2 * sizeof(double) + dh * sizeof(double2));
 }
 
-int attention_decode(hipStream_t st, const Attn& a, const Sync& sy) {
-  const int CH = decode_chunk(a.B, a.H);
-  const int ns = cdiv_i(a.T_max, CH);
-  if (attention_decode_ws_bytes(a.B, a.H, a.dh, a.T_max) > sy.ws_bytes) return ERR_STATE;
-  if ((long)a.B * a.H >= SYNC_COUNTERS - 1 || a.dh > 256 || a.S != 1 || ns > DEC_MAX_SPLITS) return ERR_ARG;
-  double* pm = (double*)sy.ws;
-  double* pl = pm + (long)a.B * a.H * ns;
-  double2* po = (double2*)(pl + (long)a.B * a.H * ns);
-  hipLaunchKernelGGL(k_attention_decode, dim3(ns, a.H, a.B), dim3(256), 0, st, a, CH, ns, pm, pl, po, sy.counters);
+int attention_decode_split(hipStream_t st, const Attn& a, const double2* q, long ldq, int npart, long part_stride,
+                           bool append, const AttnSplit& o) {
+  if (a.S != 1 || a.dh > 256 || o.nsplit > DEC_MAX_SPLITS || o.CH > DEC_MAX_CHUNK || !a.kv_len || npart > 8 ||
+      npart < 1)
+    return ERR_ARG;
+  if (append && (!a.kc_w || !a.vc_w)) return ERR_ARG;
+  const dim3 grid(o.nsplit, a.H, a.B);
+  const int ap = append ? 1 : 0;
+  switch (a.dh) {
+    case 16: hipLaunchKernelGGL(k_attention_split<16>, grid, dim3(256), 0, st, a, q, ldq, npart, part_stride, ap, o); break;
+    case 32: hipLaunchKernelGGL(k_attention_split<32>, grid, dim3(256), 0, st, a, q, ldq, npart, part_stride, ap, o); break;
+    case 64: hipLaunchKernelGGL(k_attention_split<64>, grid, dim3(256), 0, st, a, q, ldq, npart, part_stride, ap, o); break;
+    case 128: hipLaunchKernelGGL(k_attention_split<128>, grid, dim3(256), 0, st, a, q, ldq, npart, part_stride, ap, o); break;
+    default: hipLaunchKernelGGL(k_attention_split<0>, grid, dim3(256), 0, st, a, q, ldq, npart, part_stride, ap, o); break;
+  }
   return OK;
 }
 

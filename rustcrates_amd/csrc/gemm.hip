@@ -17,7 +17,7 @@
 // on arrival order.
 #include <algorithm>
 
-#include "kernels.hpp"
+#include "rowops.hpp"
 
 namespace mitok {
 
@@ -100,103 +100,6 @@ __global__ __launch_bounds__(256) void k_argmax_finalize(Argmax am, int tiles) {
 }
 
 // ===========================================================================
-// prologue (row transform) on the fly
-// ===========================================================================
-__device__ __forceinline__ double2 ro_raw(const RowOps& r, int m, int k, int K) {
-  if (r.table) {
-    const uint32_t id = r.ids[m];
-    if (id == 1u || id >= (uint32_t)r.vocab) return make_double2(0.0, 0.0);  // PAD; bad ids flagged by ro_check
-    return r.table[(long)id * K + k];
-  }
-  return r.x[(long)m * r.ldx + k];
-}
-
-// source element with RoPE (pairs (2i, 2i+1) rotate by the tabulated angle)
-__device__ __forceinline__ double2 ro_source(const RowOps& r, int m, int k, int K) {
-  if (!r.rope_cs) return ro_raw(r, m, k, K);
-  const int p = min(r.rope_pos[m], r.rope_max - 1);  // overflow flagged by ro_check
-  const int i = k >> 1;
-  const double2 t = r.rope_cs[(long)p * (K >> 1) + i];
-  const double2 e = ro_raw(r, m, 2 * i, K), o = ro_raw(r, m, 2 * i + 1, K);
-  return (k & 1) ? make_double2(e.x * t.y + o.x * t.x, e.y * t.y + o.y * t.x)
-                 : make_double2(e.x * t.x - o.x * t.y, e.y * t.x - o.y * t.y);
-}
-
-__device__ __forceinline__ double2 ro_value(const RowOps& r, int m, int k, int K) {
-  double2 v = ro_source(r, m, k, K);
-  if (r.resid) v = make_double2(v.x + r.resid[(long)m * r.ldr + k].x, 0.0);
-  return v;
-}
-
-__device__ __forceinline__ void ro_check(const RowOps& r, int m) {
-  if (r.table && r.ids[m] != 1u && r.ids[m] >= (uint32_t)r.vocab) atomicOr(r.err, (uint32_t)EB_BAD_TOKEN);
-  if (r.rope_cs && r.rope_pos[m] >= r.rope_max) atomicOr(r.err, (uint32_t)EB_CTX_OVERFLOW);
-}
-
-// normalize (norm_layer.rs:77): Re(((x - mean) / sd) * gamma + beta) + 0i
-__device__ __forceinline__ double2 ln_apply(double2 v, double2 mean, double2 sd, double2 g, double2 b) {
-  const double2 o = cadd(cmul(cdiv(csub(v, mean), sd), g), b);
-  return make_double2(o.x, 0.0);
-}
-
-// LayerNorm statistics of rows m0 .. m0+M-1 (M <= MR) over K elements:
-// mean = sum(x) / K, var = sum((x - mean)^2) / K (complex square),
-// sd = csqrt(var + eps) (norm_layer.rs:64-80).  Block-wide; all threads call it.
-template <int MR>
-__device__ void ro_stats(const RowOps& r, int m0, int M, int K, double2* mean_s, double2* sd_s) {
-  __shared__ double red_s[4][2 * MR];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  double a[2 * MR];
-  const double len = (double)K;
-#pragma unroll
-  for (int j = 0; j < 2 * MR; ++j) a[j] = 0.0;
-  for (int k = tid; k < K; k += 256)
-#pragma unroll
-    for (int m = 0; m < MR; ++m)
-      if (m < M) {
-        const double2 v = ro_value(r, m0 + m, k, K);
-        a[2 * m] += v.x;
-        a[2 * m + 1] += v.y;
-      }
-#pragma unroll
-  for (int j = 0; j < 2 * MR; ++j) a[j] = wave_sum(a[j]);
-  if (lane == 0)
-#pragma unroll
-    for (int j = 0; j < 2 * MR; ++j) red_s[wave][j] = a[j];
-  __syncthreads();
-  if (tid < M) {
-    const double sre = (red_s[0][2 * tid] + red_s[1][2 * tid]) + (red_s[2][2 * tid] + red_s[3][2 * tid]);
-    const double sim = (red_s[0][2 * tid + 1] + red_s[1][2 * tid + 1]) + (red_s[2][2 * tid + 1] + red_s[3][2 * tid + 1]);
-    mean_s[tid] = make_double2(sre / len, sim / len);
-  }
-  __syncthreads();
-#pragma unroll
-  for (int j = 0; j < 2 * MR; ++j) a[j] = 0.0;
-  for (int k = tid; k < K; k += 256)
-#pragma unroll
-    for (int m = 0; m < MR; ++m)
-      if (m < M) {
-        const double2 t = csub(ro_value(r, m0 + m, k, K), mean_s[m]);
-        const double2 tt = cmul(t, t);
-        a[2 * m] += tt.x;
-        a[2 * m + 1] += tt.y;
-      }
-#pragma unroll
-  for (int j = 0; j < 2 * MR; ++j) a[j] = wave_sum(a[j]);
-  __syncthreads();  // red_s reuse
-  if (lane == 0)
-#pragma unroll
-    for (int j = 0; j < 2 * MR; ++j) red_s[wave][j] = a[j];
-  __syncthreads();
-  if (tid < M) {
-    const double vre = (red_s[0][2 * tid] + red_s[1][2 * tid]) + (red_s[2][2 * tid] + red_s[3][2 * tid]);
-    const double vim = (red_s[0][2 * tid + 1] + red_s[1][2 * tid + 1]) + (red_s[2][2 * tid + 1] + red_s[3][2 * tid + 1]);
-    sd_s[tid] = csqrt_nc(make_double2(vre / len + r.eps, vim / len + 0.0));
-  }
-  __syncthreads();
-}
-
-// ===========================================================================
 // GEMV for M <= 8 rows: HBM-bound weight stream.  A block owns C columns and a
 // K range of 4*kw rows; lane (r, c) = (lane / C, lane % C) reads row r of each
 // group of 64/C rows, so one wave instruction covers 64/C rows x C columns.
@@ -213,7 +116,7 @@ __global__ __launch_bounds__(256) void k_gemv(RowOps ro, int M, const double2* _
                                               int kw, Epi ep, Argmax am, double2* __restrict__ ws,
                                               uint32_t* __restrict__ cnt) {
   constexpr int RPW = 64 / C;  // rows per wave instruction
-  extern __shared__ double2 xs[];  // [MR][4*kw]
+  extern __shared__ double2 lds2[];  // input rows [MR][RL], then the attention-combine weights
   __shared__ double2 red[3][MR][C];
   __shared__ double2 st_mean[MR], st_sd[MR];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -227,35 +130,37 @@ __global__ __launch_bounds__(256) void k_gemv(RowOps ro, int M, const double2* _
   const int nu = kmax > r ? (kmax - r + RPW - 1) / RPW : 0;  // rows k0 + r + u*RPW, u < nu
   const double2* wp = W + (long)(k0 + r) * ldw + n;
   const long wstep = (long)RPW * ldw;
+  // a LayerNorm needs the whole row in LDS; otherwise the block's K range
+  const int ka = ro.ln ? 0 : kb0, RL = ro.ln ? K : KB;
+  RoLds L;
+  L.wts = (double*)(lds2 + MR * RL);
+  L.lsum = L.wts + (ro.att.po ? (size_t)M * ro.att.H * ro.att.nsplit : 0);
+  L.m0 = 0;
 
   double2 w[8];
 #pragma unroll
   for (int u = 0; u < 8; ++u) w[u] = (col_ok && u < nu) ? wp[u * wstep] : make_double2(0.0, 0.0);
 
-  if (ro.ln) ro_stats<MR>(ro, 0, M, K, st_mean, st_sd);
+  ro_prepare(ro, M, L);
+  ro_build<MR>(ro, M, K, ka, RL, kb0, min(K, kb0 + KB), lds2, L, st_mean, st_sd);
   if (blockIdx.x == 0 && blockIdx.y == 0 && tid < M) ro_check(ro, tid);
-  for (int i = tid; i < MR * KB; i += 256) {
-    const int m = i / KB, kk = i - m * KB, k = kb0 + kk;
-    double2 v = make_double2(0.0, 0.0);
-    if (m < M && k < K) {
-      v = ro_value(ro, m, k, K);
-      if (ro.ln) v = ln_apply(v, st_mean[m], st_sd[m], ro.gamma[k], ro.beta[k]);
-      if (ro.save && blockIdx.x == 0) ro.save[(long)m * ro.ldsave + k] = v;
+  const double2* xs = lds2 + (kb0 - ka);  // row m of the block's range at xs[m * RL]
+  if (ro.save && blockIdx.x == 0)
+    for (int i = tid; i < MR * KB; i += 256) {
+      const int m = i / KB, k = kb0 + (i - m * KB);
+      if (m < M && k < K) ro.save[(long)m * ro.ldsave + k] = xs[m * RL + (k - kb0)];
     }
-    xs[i] = v;
-  }
-  __syncthreads();
 
   double2 acc[MR];
 #pragma unroll
   for (int m = 0; m < MR; ++m) acc[m] = make_double2(0.0, 0.0);
   if (col_ok) {
-    const double2* xw = xs + wave * kw + r;  // row u of this lane: xw[m * KB + u * RPW]
+    const double2* xw = xs + wave * kw + r;  // row u of this lane: xw[m * RL + u * RPW]
 #pragma unroll
     for (int u = 0; u < 8; ++u)
       if (u < nu)
 #pragma unroll
-        for (int m = 0; m < MR; ++m) acc[m] = cadd(acc[m], cmul(xw[m * KB + u * RPW], w[u]));
+        for (int m = 0; m < MR; ++m) acc[m] = cadd(acc[m], cmul(xw[m * RL + u * RPW], w[u]));
     int u0 = 8;
     for (; u0 + 8 <= nu; u0 += 8) {
 #pragma unroll
@@ -263,12 +168,12 @@ __global__ __launch_bounds__(256) void k_gemv(RowOps ro, int M, const double2* _
 #pragma unroll
       for (int u = 0; u < 8; ++u)
 #pragma unroll
-        for (int m = 0; m < MR; ++m) acc[m] = cadd(acc[m], cmul(xw[m * KB + (u0 + u) * RPW], w[u]));
+        for (int m = 0; m < MR; ++m) acc[m] = cadd(acc[m], cmul(xw[m * RL + (u0 + u) * RPW], w[u]));
     }
     for (; u0 < nu; ++u0) {
       const double2 wv = wp[u0 * wstep];
 #pragma unroll
-      for (int m = 0; m < MR; ++m) acc[m] = cadd(acc[m], cmul(xw[m * KB + u0 * RPW], wv));
+      for (int m = 0; m < MR; ++m) acc[m] = cadd(acc[m], cmul(xw[m * RL + u0 * RPW], wv));
     }
   }
   // lanes of one column (same c, r = 0 .. RPW-1) -> r = 0
@@ -289,6 +194,13 @@ __global__ __launch_bounds__(256) void k_gemv(RowOps ro, int M, const double2* _
     for (int m = 0; m < MR; ++m) acc[m] = cadd(cadd(cadd(acc[m], red[0][m][lane]), red[1][m][lane]), red[2][m][lane]);
 
   const int P = gridDim.y;
+  if (ep.mode == EPI_PART) {  // the consumer sums the partials and applies what follows
+    if (owner && col_ok)
+#pragma unroll
+      for (int m = 0; m < MR; ++m)
+        if (m < M) ep.out[((long)blockIdx.y * M + m) * N + n] = acc[m];
+    return;
+  }
   if (P > 1) {
     if (owner && col_ok)
 #pragma unroll
@@ -336,20 +248,26 @@ __global__ __launch_bounds__(256) void k_gemv(RowOps ro, int M, const double2* _
 
 // The prologue alone, one block per row.
 __global__ __launch_bounds__(256) void k_rowops(RowOps ro, int K, double2* __restrict__ out, long ldo) {
+  extern __shared__ double2 lds2[];  // the row [K], then the attention-combine weights
   __shared__ double2 st_mean[1], st_sd[1];
   const int m = blockIdx.x;
-  if (ro.ln) ro_stats<1>(ro, m, 1, K, st_mean, st_sd);
+  RoLds L;
+  L.wts = (double*)(lds2 + K);
+  L.lsum = L.wts + (ro.att.po ? (size_t)ro.att.H * ro.att.nsplit : 0);
+  L.m0 = m;
+  ro_prepare(ro, 1, L);
+  ro_build<1>(ro, 1, K, 0, K, 0, K, lds2, L, st_mean, st_sd);
   if (threadIdx.x == 0) ro_check(ro, m);
   for (int k = threadIdx.x; k < K; k += 256) {
-    double2 v = ro_value(ro, m, k, K);
-    if (ro.ln) v = ln_apply(v, st_mean[0], st_sd[0], ro.gamma[k], ro.beta[k]);
+    const double2 v = lds2[k];
     out[(long)m * ldo + k] = v;
     if (ro.save) ro.save[(long)m * ro.ldsave + k] = v;
   }
 }
 
 void rowops_apply(hipStream_t st, int M, int K, const RowOps& ro, double2* out, long ldo) {
-  if (M > 0) hipLaunchKernelGGL(k_rowops, dim3(M), dim3(256), 0, st, ro, K, out, ldo);
+  const size_t shm = (size_t)K * sizeof(double2) + (ro.att.po ? (size_t)ro.att.H * (ro.att.nsplit + 1) * sizeof(double) : 0);
+  if (M > 0) hipLaunchKernelGGL(k_rowops, dim3(M), dim3(256), shm, st, ro, K, out, ldo);
 }
 
 // ===========================================================================
@@ -510,15 +428,7 @@ __global__ __launch_bounds__(256) void k_zgemm_mfma(const double2* __restrict__ 
   }
 }
 
-// ===========================================================================
-// Skinny MFMA GEMM for 9 <= M <= 64 rows (batched decode): a block owns all M
-// rows (RT tiles of 16) and 16 columns; its K range is split over the 4 waves,
-// each accumulating the whole 16RT x 16 tile with v_mfma_f64_16x16x4_f64 from
-// operands loaded straight from global memory (A: row i, k offset lane/16;
-// B: column i, k offset lane/16).  Waves are summed through LDS, blockIdx.y
-// splits K at most 8 ways.
-// ===========================================================================
-template <int RT>
+template <int RT, bool RE>
 __global__ __launch_bounds__(256) void k_zgemm_skinny(const double2* __restrict__ X, long ldx, int M,
                                                         const double2* __restrict__ W, long ldw, int N, int K, int kc,
                                                         Epi ep, Argmax am, double2* __restrict__ ws,
@@ -536,28 +446,41 @@ __global__ __launch_bounds__(256) void k_zgemm_skinny(const double2* __restrict_
 #pragma unroll
   for (int t = 0; t < RT; ++t) cr[t] = ci[t] = v4d{0.0, 0.0, 0.0, 0.0};
 
-  constexpr int U = 4;  // k-steps of 4 per batch
-  for (int k = ka; k < kz; k += 4 * U) {
-    double2 b[U], a[RT][U];
+  constexpr int U = 4;  // k-steps of 4 per batch, double-buffered
+  double2 b[2][U], a[2][RT][U];
+  auto load = [&](int buf, int k) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int kk = k + 4 * u + kq;
-      b[u] = (kk < kz && n < N) ? W[(long)kk * ldw + n] : make_double2(0.0, 0.0);
+      b[buf][u] = (kk < kz && n < N) ? W[(long)kk * ldw + n] : make_double2(0.0, 0.0);
 #pragma unroll
       for (int t = 0; t < RT; ++t) {
         const int m = 16 * t + i;
-        a[t][u] = (kk < kz && m < M) ? X[(long)m * ldx + kk] : make_double2(0.0, 0.0);
+        a[buf][t][u] = (kk < kz && m < M) ? X[(long)m * ldx + kk] : make_double2(0.0, 0.0);
       }
     }
+  };
+  auto mma = [&](int buf) {
 #pragma unroll
     for (int u = 0; u < U; ++u)
 #pragma unroll
       for (int t = 0; t < RT; ++t) {
-        cr[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[t][u].x, b[u].x, cr[t], 0, 0, 0);
-        ci[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[t][u].x, b[u].y, ci[t], 0, 0, 0);
-        cr[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(-a[t][u].y, b[u].y, cr[t], 0, 0, 0);
-        ci[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[t][u].y, b[u].x, ci[t], 0, 0, 0);
+        cr[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[buf][t][u].x, b[buf][u].x, cr[t], 0, 0, 0);
+        cr[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(-a[buf][t][u].y, b[buf][u].y, cr[t], 0, 0, 0);
+        if (!RE) {
+          ci[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[buf][t][u].x, b[buf][u].y, ci[t], 0, 0, 0);
+          ci[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[buf][t][u].y, b[buf][u].x, ci[t], 0, 0, 0);
+        }
       }
+  };
+  constexpr int KS = 4 * U;  // unrolled by two: both buffer indices are constants
+  if (ka < kz) load(0, ka);
+  for (int k = ka; k < kz; k += 2 * KS) {
+    if (k + KS < kz) load(1, k + KS);
+    mma(0);
+    if (k + KS >= kz) break;
+    if (k + 2 * KS < kz) load(0, k + 2 * KS);
+    mma(1);
   }
   // D[i][j] of row tile t at lane j + 16*(i%4), element i/4
 #pragma unroll
@@ -632,19 +555,176 @@ __global__ __launch_bounds__(256) void k_zgemm_skinny(const double2* __restrict_
   }
 }
 
+// ===========================================================================
+// Wide skinny variant (outputs of 16K+ columns, no K split): a block owns all M
+// rows (RT tiles of 16) and 16*CW columns; its 4 waves are CW column groups x
+// (4/CW) K groups.  Each wave accumulates its 16RT x 16 tile with
+// v_mfma_f64_16x16x4_f64 from operands loaded straight from global memory
+// (A: row i, k offset lane/16; B: column i, k offset lane/16), double-buffered.
+// Waves sharing columns are summed through LDS; blockIdx.y splits K at most 8
+// ways (last-arrival completion).  Waves of one column group share the A rows
+// in L1, so wide outputs use CW = 4.  RE: only the real part is formed.
+// D[i][j] of row tile t sits at lane j + 16*(i%4), element i/4.
+// ===========================================================================
+template <int RT, bool RE, int CW>
+__global__ __launch_bounds__(256) void k_zgemm_skinny_cols(const double2* __restrict__ X, long ldx, int M,
+                                                        const double2* __restrict__ W, long ldw, int N, int K, int kc,
+                                                        Epi ep, Argmax am, double2* __restrict__ ws,
+                                                        uint32_t* __restrict__ cnt) {
+  constexpr int KG = 4 / CW;  // K groups
+  __shared__ double2 red[KG > 1 ? KG - 1 : 1][CW][RT * 4][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int cg = wave % CW, kg = wave / CW;
+  const int i = lane & 15, kq = lane >> 4;
+  const int n0 = blockIdx.x * 16 * CW + 16 * cg, n = n0 + i;
+  const int kb0 = blockIdx.y * kc, kb1 = min(K, kb0 + kc);
+  const int q = kc / KG;  // multiple of 16
+  const int ka = kb0 + kg * q, kz = min(kb1, ka + q);
+
+  v4d cr[RT], ci[RT];
+#pragma unroll
+  for (int t = 0; t < RT; ++t) cr[t] = ci[t] = v4d{0.0, 0.0, 0.0, 0.0};
+
+  constexpr int U = 4;  // k-steps of 4 per batch
+  double2 b[2][U], a[2][RT][U];
+  auto load = [&](int buf, int k) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int kk = k + 4 * u + kq;
+      b[buf][u] = (kk < kz && n < N) ? W[(long)kk * ldw + n] : make_double2(0.0, 0.0);
+#pragma unroll
+      for (int t = 0; t < RT; ++t) {
+        const int m = 16 * t + i;
+        a[buf][t][u] = (kk < kz && m < M) ? X[(long)m * ldx + kk] : make_double2(0.0, 0.0);
+      }
+    }
+  };
+  auto mma = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int t = 0; t < RT; ++t) {
+        // Cr += Ar*Br + (-Ai)*Bi; Ci += Ar*Bi + Ai*Br (only Cr when the real part is all that is used)
+        cr[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[buf][t][u].x, b[buf][u].x, cr[t], 0, 0, 0);
+        cr[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(-a[buf][t][u].y, b[buf][u].y, cr[t], 0, 0, 0);
+        if (!RE) {
+          ci[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[buf][t][u].x, b[buf][u].y, ci[t], 0, 0, 0);
+          ci[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[buf][t][u].y, b[buf][u].x, ci[t], 0, 0, 0);
+        }
+      }
+  };
+  // double buffer unrolled by two so both buffer indices are constants (registers, not scratch)
+  constexpr int KS = 4 * U;
+  if (ka < kz) load(0, ka);
+  for (int k = ka; k < kz; k += 2 * KS) {
+    if (k + KS < kz) load(1, k + KS);
+    mma(0);
+    if (k + KS >= kz) break;
+    if (k + 2 * KS < kz) load(0, k + 2 * KS);
+    mma(1);
+  }
+
+  // K groups of a column group -> the kg == 0 wave, in group order
+  if (KG > 1) {
+    if (kg > 0)
+#pragma unroll
+      for (int t = 0; t < RT; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) red[kg - 1][cg][t * 4 + e][lane] = make_double2(cr[t][e], ci[t][e]);
+    __syncthreads();
+    if (kg == 0)
+#pragma unroll
+      for (int g = 0; g < KG - 1; ++g)
+#pragma unroll
+        for (int t = 0; t < RT; ++t)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const double2 v = red[g][cg][t * 4 + e][lane];
+            cr[t][e] += v.x;
+            ci[t][e] += v.y;
+          }
+  }
+  const bool owner = kg == 0;
+  const int P = gridDim.y;
+  if (P > 1) {
+    if (owner)
+#pragma unroll
+      for (int t = 0; t < RT; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int m = 16 * t + 4 * e + kq;
+          if (m < M && n < N) st_dev(&ws[((long)blockIdx.y * M + m) * N + n], make_double2(cr[t][e], ci[t][e]));
+        }
+    if (!arrive_last(&cnt[blockIdx.x], (uint32_t)P)) return;
+    if (owner)
+#pragma unroll
+      for (int t = 0; t < RT; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int m = 16 * t + 4 * e + kq;
+          if (m < M && n < N) {
+            double2 pv[SKINNY_MAX_SPLIT];  // all loads in flight, then summed in split order
+#pragma unroll
+            for (int p = 0; p < SKINNY_MAX_SPLIT; ++p)
+              pv[p] = p < P ? ld_dev(&ws[((long)p * M + m) * N + n]) : make_double2(0.0, 0.0);
+            double2 s = pv[0];
+#pragma unroll
+            for (int p = 1; p < SKINNY_MAX_SPLIT; ++p)
+              if (p < P) s = cadd(s, pv[p]);
+            cr[t][e] = s.x;
+            ci[t][e] = s.y;
+          }
+        }
+  }
+  if (!owner) return;
+  const bool argmax = am.part_v != nullptr;
+  const int tiles16 = (N + 15) / 16;
+#pragma unroll
+  for (int t = 0; t < RT; ++t)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int m = 16 * t + 4 * e + kq;
+      double re = 0.0;
+      if (m < M && n < N) re = apply_epi(ep, M, N, m, n, make_double2(cr[t][e], ci[t][e]));
+      if (argmax) {  // (max, last index) of row m over this wave's 16 columns
+        double bv = -INFINITY;
+        int bi = -1;
+        if (m < M && n < N) {
+          if (isnan(re)) atomicOr(am.err, (uint32_t)EB_ARGMAX_NAN);
+          else bv = re, bi = n;
+        }
+#pragma unroll
+        for (int o = 8; o > 0; o >>= 1) {
+          const double ov = __shfl_xor(bv, o, 64);
+          const int oi = __shfl_xor(bi, o, 64);
+          argmax_combine(bv, bi, ov, oi);
+        }
+        if (i == 0 && m < M) {
+          am.part_v[(long)m * tiles16 + n0 / 16] = bv;
+          am.part_i[(long)m * tiles16 + n0 / 16] = bi;
+        }
+      }
+    }
+}
+
 // ---- planning and dispatch ------------------------------------------------
 // GEMV: C columns per block (16, or 64 for wide outputs), K split so that the
 // grid has about 512 blocks, at most GEMV_MAX_SPLIT ways.
 struct GemvPlan {
   int mr, C, kw, P, ncb;
 };
-static GemvPlan plan_gemv(int M, int N, int K) {
+// part: EPI_PART (no completion, the consumer sums): 8-column blocks and a
+// split that brings the grid to about 256 blocks -- the fastest shapes of a
+// sweep over columns {4, 8, 16, 64} x splits {1, 2, 4, 8} at config 3.
+// Otherwise 16 columns (64 for wide outputs) and a completion counter.
+static GemvPlan plan_gemv(int M, int N, int K, bool part) {
   GemvPlan p;
   p.mr = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
-  p.C = cdiv_i(N, 64) >= 256 ? 64 : 16;
+  const bool wide = cdiv_i(N, 64) >= 256;
+  p.C = wide ? 64 : (part ? 8 : 16);
   const int rpw = 64 / p.C;
   p.ncb = cdiv_i(N, p.C);
-  int P = std::min(GEMV_MAX_SPLIT, std::max(1, cdiv_i(512, p.ncb)));
+  const int P = std::min(GEMV_MAX_SPLIT, std::max(1, cdiv_i(256, p.ncb)));
   // rows per block: a multiple of 4 waves x rpw, and its input rows fit 64 KB of LDS
   const int unit = 4 * rpw;
   int KB = cdiv_i(cdiv_i(K, P), unit) * unit;
@@ -652,16 +732,27 @@ static GemvPlan plan_gemv(int M, int N, int K) {
   KB = std::min(KB, kb_max);
   p.kw = KB / 4;
   p.P = cdiv_i(K, KB);
+  if (!part && p.P > GEMV_MAX_SPLIT) p.P = -1;  // not reachable for the supported widths
   return p;
 }
-// skinny MFMA: 16 columns per block, K split in chunks that are multiples of
-// 64 (16 per wave), about 512 blocks, at most SKINNY_MAX_SPLIT ways
+// skinny MFMA: wide outputs take 64-column blocks whose 4 waves share the A
+// rows (no K split); the rest 16-column blocks, K split over the waves and in
+// chunks of multiples of 64 over blocks (about 512 blocks, at most
+// SKINNY_MAX_SPLIT ways)
 struct SkinnyPlan {
-  int rt, ncb, kc, P;
+  int rt, cw, ncb, kc, P;  // cw 4: the wide variant
 };
 static SkinnyPlan plan_skinny(int M, int N, int K) {
   SkinnyPlan p;
   p.rt = cdiv_i(M, 16);
+  if (cdiv_i(N, 64) >= 256) {
+    p.cw = 4;
+    p.ncb = cdiv_i(N, 64);
+    p.kc = cdiv_i(K, 64) * 64;
+    p.P = 1;
+    return p;
+  }
+  p.cw = 0;
   p.ncb = cdiv_i(N, 16);
   const int P = std::min(SKINNY_MAX_SPLIT, std::max(1, cdiv_i(512, p.ncb)));
   p.kc = cdiv_i(cdiv_i(K, P), 64) * 64;
@@ -685,9 +776,11 @@ static MfmaPlan plan_mfma(int M, int N, int K) {
 
 constexpr int SKINNY_MAX_M = 64;
 
+int gemm_parts(int M, int N, int K) { return M <= 8 ? plan_gemv(M, N, K, true).P : 0; }
+
 size_t gemm_ws_bytes(int M, int N, int K) {
   int P;
-  if (M <= 8) P = plan_gemv(M, N, K).P;
+  if (M <= 8) P = plan_gemv(M, N, K, false).P;
   else if (M <= SKINNY_MAX_M) P = plan_skinny(M, N, K).P;
   else P = plan_mfma(M, N, K).P;
   return P > 1 ? (size_t)P * M * N * sizeof(double2) : 0;
@@ -696,11 +789,17 @@ size_t gemm_ws_bytes(int M, int N, int K) {
 // argmax partials: one per row and 16-column tile covers every product shape
 size_t argmax_part_elems(int M, int N) { return (size_t)M * cdiv_i(N, 16); }
 
+static size_t gemv_lds_bytes(const GemvPlan& p, const RowOps& ro, int M, int K) {
+  const size_t rl = ro.ln ? (size_t)K : (size_t)4 * p.kw;
+  return (size_t)p.mr * rl * sizeof(double2) +
+         (ro.att.po ? (size_t)M * ro.att.H * (ro.att.nsplit + 1) * sizeof(double) : 0);
+}
+
 template <int MR, int C>
 static void launch_gemv(hipStream_t st, const GemvPlan& p, const RowOps& ro, int M, const double2* W, long ldw, int N,
                         int K, const Epi& ep, const Argmax& am, const Sync& sy) {
   dim3 grid(p.ncb, p.P);
-  const size_t shm = (size_t)MR * 4 * p.kw * sizeof(double2);
+  const size_t shm = gemv_lds_bytes(p, ro, M, K);
   hipLaunchKernelGGL((k_gemv<MR, C>), grid, dim3(256), shm, st, ro, M, W, ldw, N, K, p.kw, ep, am, (double2*)sy.ws,
                      sy.counters);
 }
@@ -708,18 +807,43 @@ template <int MR>
 static void launch_gemv_c(hipStream_t st, const GemvPlan& p, const RowOps& ro, int M, const double2* W, long ldw, int N,
                           int K, const Epi& ep, const Argmax& am, const Sync& sy) {
   if (p.C == 64) launch_gemv<MR, 64>(st, p, ro, M, W, ldw, N, K, ep, am, sy);
-  else launch_gemv<MR, 16>(st, p, ro, M, W, ldw, N, K, ep, am, sy);
+  else if (p.C == 16) launch_gemv<MR, 16>(st, p, ro, M, W, ldw, N, K, ep, am, sy);
+  else launch_gemv<MR, 8>(st, p, ro, M, W, ldw, N, K, ep, am, sy);
+}
+
+template <bool RE>
+static void launch_skinny(hipStream_t st, const SkinnyPlan& p, const RowOps& ro, int M, const double2* W, long ldw,
+                          int N, int K, const Epi& ep, const Argmax& am, const Sync& sy) {
+  const dim3 grid(p.ncb, p.P), blk(256);
+  double2* ws = (double2*)sy.ws;
+  if (p.cw == 4) {
+    switch (p.rt) {
+      case 1: hipLaunchKernelGGL((k_zgemm_skinny_cols<1, RE, 4>), grid, blk, 0, st, ro.x, ro.ldx, M, W, ldw, N, K, p.kc, ep, am, ws, sy.counters); break;
+      case 2: hipLaunchKernelGGL((k_zgemm_skinny_cols<2, RE, 4>), grid, blk, 0, st, ro.x, ro.ldx, M, W, ldw, N, K, p.kc, ep, am, ws, sy.counters); break;
+      case 3: hipLaunchKernelGGL((k_zgemm_skinny_cols<3, RE, 4>), grid, blk, 0, st, ro.x, ro.ldx, M, W, ldw, N, K, p.kc, ep, am, ws, sy.counters); break;
+      default: hipLaunchKernelGGL((k_zgemm_skinny_cols<4, RE, 4>), grid, blk, 0, st, ro.x, ro.ldx, M, W, ldw, N, K, p.kc, ep, am, ws, sy.counters); break;
+    }
+    return;
+  }
+  switch (p.rt) {
+    case 1: hipLaunchKernelGGL((k_zgemm_skinny<1, RE>), grid, blk, 0, st, ro.x, ro.ldx, M, W, ldw, N, K, p.kc, ep, am, ws, sy.counters); break;
+    case 2: hipLaunchKernelGGL((k_zgemm_skinny<2, RE>), grid, blk, 0, st, ro.x, ro.ldx, M, W, ldw, N, K, p.kc, ep, am, ws, sy.counters); break;
+    case 3: hipLaunchKernelGGL((k_zgemm_skinny<3, RE>), grid, blk, 0, st, ro.x, ro.ldx, M, W, ldw, N, K, p.kc, ep, am, ws, sy.counters); break;
+    default: hipLaunchKernelGGL((k_zgemm_skinny<4, RE>), grid, blk, 0, st, ro.x, ro.ldx, M, W, ldw, N, K, p.kc, ep, am, ws, sy.counters); break;
+  }
 }
 
 int gemm(hipStream_t st, int M, int N, int K, const RowOps& ro, const double2* W, long ldw, const Epi& ep,
          const Argmax* amp, const Sync& sy) {
   if (M <= 0 || N <= 0) return OK;
   const Argmax am = amp ? *amp : Argmax();
-  if (gemm_ws_bytes(M, N, K) > sy.ws_bytes) return ERR_STATE;
+  if (ep.mode != EPI_PART && gemm_ws_bytes(M, N, K) > sy.ws_bytes) return ERR_STATE;
   int tiles = 0;  // column tiles of the argmax partials
   if (M <= 8) {
-    const GemvPlan p = plan_gemv(M, N, K);
-    if (p.ncb >= SYNC_COUNTERS) return ERR_ARG;
+    const bool part = ep.mode == EPI_PART;
+    const GemvPlan p = plan_gemv(M, N, K, part);
+    if (p.P < 1 || p.ncb >= SYNC_COUNTERS || (part && am.part_v)) return ERR_ARG;
+    if (gemv_lds_bytes(p, ro, M, K) > 120 * 1024) return ERR_ARG;
     switch (p.mr) {
       case 1: launch_gemv_c<1>(st, p, ro, M, W, ldw, N, K, ep, am, sy); break;
       case 2: launch_gemv_c<2>(st, p, ro, M, W, ldw, N, K, ep, am, sy); break;
@@ -728,18 +852,13 @@ int gemm(hipStream_t st, int M, int N, int K, const RowOps& ro, const double2* W
     }
     tiles = p.ncb;
   } else {
-    if (!ro.plain()) return ERR_ARG;  // the MFMA paths read plain rows; materialise the prologue first
+    if (!ro.plain() || ep.mode == EPI_PART) return ERR_ARG;  // the MFMA paths read plain rows
     if (M <= SKINNY_MAX_M) {
       const SkinnyPlan p = plan_skinny(M, N, K);
       if (p.ncb >= SYNC_COUNTERS) return ERR_ARG;
-      dim3 grid(p.ncb, p.P);
-      switch (p.rt) {
-        case 1: hipLaunchKernelGGL((k_zgemm_skinny<1>), grid, dim3(256), 0, st, ro.x, ro.ldx, M, W, ldw, N, K, p.kc, ep, am, (double2*)sy.ws, sy.counters); break;
-        case 2: hipLaunchKernelGGL((k_zgemm_skinny<2>), grid, dim3(256), 0, st, ro.x, ro.ldx, M, W, ldw, N, K, p.kc, ep, am, (double2*)sy.ws, sy.counters); break;
-        case 3: hipLaunchKernelGGL((k_zgemm_skinny<3>), grid, dim3(256), 0, st, ro.x, ro.ldx, M, W, ldw, N, K, p.kc, ep, am, (double2*)sy.ws, sy.counters); break;
-        default: hipLaunchKernelGGL((k_zgemm_skinny<4>), grid, dim3(256), 0, st, ro.x, ro.ldx, M, W, ldw, N, K, p.kc, ep, am, (double2*)sy.ws, sy.counters); break;
-      }
-      tiles = p.ncb;
+      if (ep.mode == EPI_RE) launch_skinny<true>(st, p, ro, M, W, ldw, N, K, ep, am, sy);
+      else launch_skinny<false>(st, p, ro, M, W, ldw, N, K, ep, am, sy);
+      tiles = cdiv_i(N, 16);  // argmax partials per 16 columns
     } else {
       const MfmaPlan p = plan_mfma(M, N, K);
       if (p.P > 1 && (long)p.mt * p.nt >= SYNC_COUNTERS) return ERR_ARG;

@@ -3,9 +3,10 @@
 //
 // Every wrapper enqueues on `st` and never synchronises or allocates, so the
 // decode step built from them can be captured into a HIP graph.  Kernels that
-// split work across blocks finish it in the block that arrives last at a
-// per-tile counter (Sync); counters return to zero before the kernel ends, so
-// launches on one stream can share them.
+// split work across blocks either leave partials for the next launch to sum,
+// or finish in the block that arrives last at a per-tile counter (Sync, at
+// most 8 arrivals per counter); counters return to zero before the kernel
+// ends, so launches on one stream can share them.
 #pragma once
 
 #include "common.hpp"
@@ -20,14 +21,32 @@ struct Sync {
 };
 constexpr int SYNC_COUNTERS = 1 << 16;
 
+// ---- split decode-attention partials, combined by the consumer's prologue ----
+// chunk s of (row m, head h): max m_s, sum l_s of exp(score - m_s), o_s[dh]
+struct AttnSplit {
+  const double* pm = nullptr;  // [M][H][nsplit]
+  const double* pl = nullptr;
+  const double2* po = nullptr;  // [M][H][nsplit][dh]
+  int H = 0, dh = 0, nsplit = 0, CH = 0;
+  const int* kv_len = nullptr;  // keys of row m: kv_len[m] + 1
+};
+
 // ---- the row transform a GEMV applies to its input rows (prologue) ----
-// source (rows, or an embedding gather) -> RoPE -> residual Re(x + r) -> LayerNorm
+// source (rows | sum of split partials | embedding gather | attention combine)
+//   -> + bias -> finite check -> GELU -> RoPE -> residual Re(x + r) -> LayerNorm
 struct RowOps {
-  const double2* x = nullptr;  // [M][ldx] rows, or
+  const double2* x = nullptr;  // [M][ldx] rows, or partial p at x + p * part_stride
   long ldx = 0;
+  int npart = 0;  // > 1: x[m][k] = sum over p < npart of the partials, in order
+  long part_stride = 0;
   const double2* table = nullptr;  // [vocab][K] embedding table gathered by ids (PAD id 1 -> 0)
   const uint32_t* ids = nullptr;
   int vocab = 0;
+  AttnSplit att;                     // att.po != null: the attention combine is the source
+  const double2* bias = nullptr;     // + bias[k] (utils/matrix.rs:615-625)
+  int finite_check = 0;              // flag non-finite values (FFN output, transformer_network.rs:408)
+  int gelu = 0;                      // gelu_complex, rows with mask 0 -> 0 (activation.rs:195-212,268-284)
+  const uint32_t* row_mask = nullptr;
   const double2* rope_cs = nullptr;  // [rope_max][K/2] (cos, sin); position of row m = rope_pos[m]
   const int* rope_pos = nullptr;
   int rope_max = 0;
@@ -40,7 +59,10 @@ struct RowOps {
   double2* save = nullptr;  // optional copy of the transformed rows [M][ldsave]
   long ldsave = 0;
   uint32_t* err = nullptr;
-  bool plain() const { return !table && !rope_cs && !resid && !ln && !save; }
+  bool plain() const {
+    return x && npart <= 1 && !table && !att.po && !bias && !finite_check && !gelu && !rope_cs && !resid && !ln &&
+           !save;
+  }
 };
 
 // ---- GEMM epilogue: what happens to C[m][n] after the complex dot product ----
@@ -49,6 +71,7 @@ enum EpiMode : int {
   EPI_GELU = 1,   // out[m][n] = mask[m] ? gelu(v + bias) : 0 (layer.rs:132-166)
   EPI_RE = 2,     // out_re[m][n] = Re(v + bias) (logits, data_converter.rs:244-256)
   EPI_QKV = 3,    // columns [q | k | v] of all heads: q -> out, k/v -> KV cache
+  EPI_PART = 4,   // GEMV only: split partial p of C to out + p * M * N (ld N); the consumer sums them
 };
 
 struct Epi {
@@ -94,6 +117,9 @@ size_t gemm_ws_bytes(int M, int N, int K);
 size_t argmax_part_elems(int M, int N);
 int gemm(hipStream_t st, int M, int N, int K, const RowOps& ro, const double2* W, long ldw, const Epi& ep,
          const Argmax* am, const Sync& sy);
+// EPI_PART products (M <= 8): the number of partials gemm() writes, and the
+// LDS the prologue needs for an attention-combine source
+int gemm_parts(int M, int N, int K);
 // The prologue alone: out[m][k] = rowops(x)[m][k]  (materialises a pending row transform)
 void rowops_apply(hipStream_t st, int M, int K, const RowOps& ro, double2* out, long ldo);
 
@@ -114,12 +140,21 @@ struct Attn {
   long ldo = 0;
   int B = 0, S = 0, H = 0, dh = 0;
   double scale = 1.0;
+  double2* kc_w = nullptr;  // writable cache (attention_decode_split appends the new token)
+  double2* vc_w = nullptr;
+  uint32_t* err = nullptr;
 };
 // One query row per block (prefill and the general reference case).
 void attention_rows(hipStream_t st, const Attn& a);
-// Decode (S == 1): key chunks in parallel, combined by the last chunk to finish.
-size_t attention_decode_ws_bytes(int B, int H, int dh, int T_max);
-int attention_decode(hipStream_t st, const Attn& a, const Sync& sy);
+// Decode (S == 1): key chunks in parallel; the chunk partials (AttnSplit) are
+// combined by a RowOps prologue (rowops_apply or a GEMV).  q is the sum of
+// npart partials (row b at q + b * ldq, partial stride part_stride); with
+// `append` the partials are [q | k | v] of the new token, whose k and v the
+// kernel appends to the cache (kc_w, vc_w).
+AttnSplit attention_split_plan(const Attn& a);
+size_t attention_split_ws_bytes(int B, int H, int dh, int T_max);
+int attention_decode_split(hipStream_t st, const Attn& a, const double2* q, long ldq, int npart, long part_stride,
+                           bool append, const AttnSplit& out);
 
 // ---- row kernels ----
 void embed(hipStream_t st, const double2* table, int V, int d, const uint32_t* ids, int rows, double2* out,

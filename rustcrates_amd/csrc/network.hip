@@ -188,6 +188,8 @@ struct mitok_network {
   mitok::DevBuf ids_d, mask_d, lens_d, pos_d, kv_row_d, ones_d, dec_ids_d, hist_d, cnt_d, logit_hist_d;
   // split-completion counters (zeroed once, self-resetting), split partials, argmax partials
   mitok::DevBuf sync_cnt, sync_ws, am_v, am_i;
+  // fused decode plan: split partials left for the next launch to sum
+  mitok::DevBuf dq, df1, dp0, dp1, datt;
   int fused_decode = 1;  // B <= 8 decode steps use the fused GEMV plan
   // decode-step graph
   hipGraphExec_t graph = nullptr;
@@ -372,10 +374,17 @@ static int prepare(Net* n, const Spec& sp) {
   }
   if (dm.hmax) {
     if (sp.mode == MODE_CACHED && sp.S == 1)
-      ws = std::max(ws, attention_decode_ws_bytes(sp.B, dm.hmax, dm.dh_max, dm.mc_max));
+      TRY(reserve(n, n->datt, attention_split_ws_bytes(sp.B, dm.hmax, dm.dh_max, dm.mc_max)));
     if (sp.mode == MODE_STATELESS) TRY(reserve(n, n->kv_scratch, 2 * rows * dm.dsa * c16));
   }
   TRY(reserve(n, n->sync_ws, ws));
+  if (sp.mode == MODE_CACHED && sp.S == 1 && sp.B <= 8) {
+    const size_t B = sp.B;
+    TRY(reserve(n, n->dq, 8 * B * 3 * std::max(1u, dm.dsa) * c16));
+    TRY(reserve(n, n->df1, 8 * B * std::max(1u, dm.fmax) * c16));
+    TRY(reserve(n, n->dp0, 8 * B * dm.dmax * c16));
+    TRY(reserve(n, n->dp1, 8 * B * dm.dmax * c16));
+  }
   TRY(reserve(n, n->kv_len_d, (size_t)sp.B * sizeof(int)));
   TRY(reserve(n, n->ones_d, std::max<size_t>(rows, sp.B) * sizeof(uint32_t)));
   TRY(reserve(n, n->dec_ids_d, (size_t)sp.B * sizeof(uint32_t)));
@@ -419,6 +428,14 @@ static int ensure_rope_table(Net* n, PositionalEncodingLayer* P, int positions) 
   HIP_TRY(hipMemcpy(P->cs.p, cs.data(), cs.size() * sizeof(double2), hipMemcpyHostToDevice));
   P->positions = positions;
   return OK;
+}
+
+// the chunk partials of decode attention live in n->datt
+static AttnSplit split_buffers(Net* n, AttnSplit o, int B, int H) {
+  o.pm = n->datt.as<double>();
+  o.pl = o.pm + (size_t)B * H * o.nsplit;
+  o.po = (const double2*)(o.pl + (size_t)B * H * o.nsplit);
+  return o;
 }
 
 // ---------------------------------------------------------------------------
@@ -506,12 +523,31 @@ static int enqueue_forward(Net* n, const Spec& sp) {
         a.H = H;
         a.dh = dh;
         a.scale = 1.0 / (1e-8 + sqrt((double)dh));  // scale_attention_scores (masked_attention_head.rs:453-465)
-        {
-          TimeScope ts(n, MITOK_TIME_ATTENTION, 0.0);
-          if (sp.mode == MODE_CACHED && S == 1) TRY(launch_rc(attention_decode(st, a, sy), "attention"));
-          else attention_rows(st, a);
+        if (sp.mode == MODE_CACHED && S == 1) {
+          // key chunks, then one row transform: chunk combine + residual + Norm (self_attention_layer.rs:101-124)
+          AttnSplit o = split_buffers(n, attention_split_plan(a), B, H);
+          {
+            TimeScope ts(n, MITOK_TIME_ATTENTION, 0.0);
+            TRY(launch_rc(attention_decode_split(st, a, n->qbuf.as<double2>(), d, 1, 0, false, o), "attention"));
+          }
+          RowOps r;
+          r.err = err;
+          r.att = o;
+          r.resid = cur;
+          r.ldr = d;
+          r.ln = 1;
+          r.eps = A->eps;
+          r.gamma = A->gamma.as<double2>();
+          r.beta = A->beta.as<double2>();
+          rowops_apply(st, B, d, r, nxt, d);
+        } else {
+          {
+            TimeScope ts(n, MITOK_TIME_ATTENTION, 0.0);
+            attention_rows(st, a);
+          }
+          layernorm(st, n->concat.as<double2>(), cur, nxt, rows, d, A->eps, A->gamma.as<double2>(),
+                    A->beta.as<double2>());
         }
-        layernorm(st, n->concat.as<double2>(), cur, nxt, rows, d, A->eps, A->gamma.as<double2>(), A->beta.as<double2>());
         std::swap(cur, nxt);
         break;
       }
@@ -612,9 +648,32 @@ static int enqueue_forward(Net* n, const Spec& sp) {
 static bool fused_decode_ok(const Net* n, const Spec& sp) {
   if (!n->fused_decode || sp.mode != MODE_CACHED || sp.S != 1 || sp.B > 8 || !sp.forward_only) return false;
   if (sp.first != 0 || sp.last != n->layers.size() || sp.kv_row || sp.out_hidden) return false;
+  // the GEMV prologue holds whole input rows of a LayerNorm in LDS
+  const size_t mr = sp.B <= 1 ? 1 : sp.B <= 2 ? 2 : sp.B <= 4 ? 4 : 8;
+  size_t row = 0;  // widest product input
+  for (auto& L : n->layers) row = std::max<size_t>(row, L->d_in);
+  if (mr * row * sizeof(double2) > 64 * 1024) return false;
+  for (auto& L : n->layers)
+    if (L->kind == K_SELF_ATTENTION) {
+      // the row transform keeps the chunk weights of every head in LDS
+      const auto* A = (const SelfAttentionLayer*)L.get();
+      Attn a;
+      a.B = sp.B;
+      a.H = A->heads;
+      a.T_max = A->max_ctx;
+      const AttnSplit o = attention_split_plan(a);
+      if (o.nsplit > 256) return false;
+    }
   return true;
 }
 
+// Every product of the plan writes split partials (EPI_PART) that the next
+// launch sums in its prologue, together with the operations that follow the
+// product in the reference (bias, GELU, finite check, residual, LayerNorm),
+// so no launch waits on another's blocks.  A transformer block is QKV
+// (+ LayerNorm of its input), attention (+ KV append), FFN Dense (+ attention
+// combine, residual, LayerNorm) and FFN Linear (+ bias, GELU); the vocab
+// Linear and the greedy id end the step.
 static int enqueue_decode_fused(Net* n, const Spec& sp) {
   hipStream_t st = n->stream;
   uint32_t* err = n->err_d.as<uint32_t>();
@@ -626,6 +685,8 @@ static int enqueue_decode_fused(Net* n, const Spec& sp) {
   int width = 0;  // row length the pending prologue produces
   double2* mats[2] = {n->mat0.as<double2>(), n->mat1.as<double2>()};
   int mat_next = 0;
+  double2* parts[2] = {n->dp0.as<double2>(), n->dp1.as<double2>()};
+  int part_next = 0;
   auto materialize = [&]() {
     double2* out = mats[mat_next];
     mat_next ^= 1;
@@ -633,6 +694,13 @@ static int enqueue_decode_fused(Net* n, const Spec& sp) {
     RowOps r = rows_of(out, width);
     r.err = err;
     pro = r;
+  };
+  auto part_rows = [&](double2* buf, int npart, int cols) {
+    RowOps r = rows_of(buf, cols);
+    r.npart = npart;
+    r.part_stride = (long)B * cols;
+    r.err = err;
+    return r;
   };
   for (uint32_t li = 0; li < n->layers.size(); ++li) {
     Layer* L = n->layers[li].get();
@@ -671,48 +739,41 @@ static int enqueue_decode_fused(Net* n, const Spec& sp) {
         double2* x1 = n->act0.as<double2>();  // the block input, kept for the residual
         pro.save = x1;
         pro.ldsave = d;
+        const int pq = gemm_parts(B, 3 * d, d);
         Epi e;
-        e.mode = EPI_QKV;
-        e.out = n->qbuf.as<double2>();
-        e.ldo = d;
-        e.d = d;
-        e.dh = dh;
-        e.heads = H;
-        e.S = 1;
+        e.mode = EPI_PART;
+        e.out = n->dq.as<double2>();
         e.err = err;
-        e.kc = A->kc.as<double2>();
-        e.vc = A->vc.as<double2>();
-        e.ctx = A->max_ctx;
-        e.kv_base = kv_len;
         {
           TimeScope ts(n, MITOK_TIME_LAYER_GEMM, gemm_bytes(B, 3 * d, d, false), gemm_flops(B, 3 * d, d));
           TRY(launch_rc(gemm(st, B, 3 * d, d, pro, A->wqkv.as<double2>(), 3 * d, e, nullptr, sy), "qkv"));
         }
         Attn a;
-        a.q = n->qbuf.as<double2>();
-        a.ldq = d;
-        a.kc = e.kc;
-        a.vc = e.vc;
+        a.kc = A->kc.as<double2>();
+        a.vc = A->vc.as<double2>();
+        a.kc_w = A->kc.as<double2>();
+        a.vc_w = A->vc.as<double2>();
         a.ctx = A->max_ctx;
         a.kv_len = kv_len;
         a.T_add = 1;
         a.T_max = A->max_ctx;
         a.bias_re = A->bias_re.as<double>();
         a.mc = A->max_ctx;
-        a.row_mask = sp.mask;
-        a.out = n->concat.as<double2>();
-        a.ldo = d;
         a.B = B;
         a.S = 1;
         a.H = H;
         a.dh = dh;
         a.scale = 1.0 / (1e-8 + sqrt((double)dh));  // masked_attention_head.rs:453-465
+        a.err = err;
+        const AttnSplit o = split_buffers(n, attention_split_plan(a), B, H);
         {
           TimeScope ts(n, MITOK_TIME_ATTENTION, 0.0);
-          TRY(launch_rc(attention_decode(st, a, sy), "attention"));
+          TRY(launch_rc(attention_decode_split(st, a, n->dq.as<double2>(), 3 * d, pq, (long)B * 3 * d, true, o),
+                        "attention"));
         }
-        pro = rows_of(n->concat.as<double2>(), d);  // residual + Norm (self_attention_layer.rs:101-124)
+        pro = RowOps();  // chunk combine + residual + Norm (self_attention_layer.rs:101-124), once per row
         pro.err = err;
+        pro.att = o;
         pro.resid = x1;
         pro.ldr = d;
         pro.ln = 1;
@@ -720,48 +781,50 @@ static int enqueue_decode_fused(Net* n, const Spec& sp) {
         pro.gamma = A->gamma.as<double2>();
         pro.beta = A->beta.as<double2>();
         width = d;
+        materialize();
         break;
       }
       case K_FEED_FORWARD: {
         auto* F = (FeedForwardLayer*)L;
+        const int p1 = gemm_parts(B, F->hidden, F->d_in);
         Epi e1;
-        e1.mode = EPI_GELU;
-        e1.bias = F->b1.as<double2>();
-        e1.out = n->hbuf.as<double2>();
-        e1.ldo = F->hidden;
-        e1.row_mask = sp.mask;
+        e1.mode = EPI_PART;
+        e1.out = n->df1.as<double2>();
         e1.err = err;
-        double2* out = n->act1.as<double2>();
-        Epi e2;
-        e2.mode = EPI_STORE;
-        e2.bias = F->b2.as<double2>();
-        e2.out = out;
-        e2.ldo = F->d_out;
-        e2.check_finite = 1;
-        e2.err = err;
         {
           TimeScope ts(n, MITOK_TIME_LAYER_GEMM, gemm_bytes(B, F->hidden, F->d_in, false),
                        gemm_flops(B, F->hidden, F->d_in));
           TRY(launch_rc(gemm(st, B, F->hidden, F->d_in, pro, F->w1.as<double2>(), F->hidden, e1, nullptr, sy), "ffn1"));
         }
+        RowOps h = part_rows(n->df1.as<double2>(), p1, F->hidden);  // Dense: + b1, GELU (layer.rs:132-166)
+        h.bias = F->b1.as<double2>();
+        h.gelu = 1;
+        h.row_mask = sp.mask;
+        double2* out = parts[part_next];
+        part_next ^= 1;
+        const int p2 = gemm_parts(B, F->d_out, F->hidden);
+        Epi e2;
+        e2.mode = EPI_PART;
+        e2.out = out;
+        e2.err = err;
         {
           TimeScope ts(n, MITOK_TIME_LAYER_GEMM, gemm_bytes(B, F->d_out, F->hidden, false),
                        gemm_flops(B, F->d_out, F->hidden));
-          TRY(launch_rc(gemm(st, B, F->d_out, F->hidden, rows_of(n->hbuf.as<double2>(), F->hidden), F->w2.as<double2>(),
-                             F->d_out, e2, nullptr, sy), "ffn2"));
+          TRY(launch_rc(gemm(st, B, F->d_out, F->hidden, h, F->w2.as<double2>(), F->d_out, e2, nullptr, sy), "ffn2"));
         }
-        pro = rows_of(out, F->d_out);
-        pro.err = err;
+        pro = part_rows(out, p2, F->d_out);  // Linear: + b2; non-finite check (transformer_network.rs:408)
+        pro.bias = F->b2.as<double2>();
+        pro.finite_check = 1;
         width = (int)F->d_out;
         break;
       }
       case K_LINEAR: {
         auto* Ln = (LinearLayer*)L;
-        Epi e;
-        e.bias = Ln->b.as<double2>();
-        e.ldo = Ln->d_out;
-        e.err = err;
         if (is_vocab_linear(n, li)) {
+          Epi e;
+          e.bias = Ln->b.as<double2>();
+          e.ldo = Ln->d_out;
+          e.err = err;
           e.mode = EPI_RE;
           e.out_re = sp.out_re;
           e.hist_re = sp.hist_re;
@@ -769,13 +832,16 @@ static int enqueue_decode_fused(Net* n, const Spec& sp) {
           TimeScope ts(n, MITOK_TIME_VOCAB, gemm_bytes(B, Ln->d_out, Ln->d_in, true), gemm_flops(B, Ln->d_out, Ln->d_in));
           TRY(launch_rc(gemm(st, B, Ln->d_out, Ln->d_in, pro, Ln->w.as<double2>(), Ln->d_out, e, sp.am, sy), "vocab"));
         } else {
-          double2* out = mats[mat_next];
-          mat_next ^= 1;
-          e.mode = EPI_STORE;
+          double2* out = parts[part_next];
+          part_next ^= 1;
+          const int pl = gemm_parts(B, Ln->d_out, Ln->d_in);
+          Epi e;
+          e.mode = EPI_PART;
           e.out = out;
+          e.err = err;
           TRY(launch_rc(gemm(st, B, Ln->d_out, Ln->d_in, pro, Ln->w.as<double2>(), Ln->d_out, e, nullptr, sy), "linear"));
-          pro = rows_of(out, Ln->d_out);
-          pro.err = err;
+          pro = part_rows(out, pl, Ln->d_out);
+          pro.bias = Ln->b.as<double2>();
           width = (int)Ln->d_out;
         }
         break;

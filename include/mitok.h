@@ -140,7 +140,8 @@ int mitok_device_synchronize(int device);
 /* 0 = replay decode steps as HIP graphs (default), 1 = launch kernels directly. */
 int mitok_set_graph_mode(mitok_network* net, int direct_launch);
 /* 1 = decode steps of up to 8 sequences run the fused plan (row transforms in
- * the product prologues, default); 0 = one launch per reference operation. */
+ * the product prologues) and prefill attention the tiled kernel (default);
+ * 0 = one launch per reference operation and one query row per attention block. */
 int mitok_set_decode_plan(mitok_network* net, int fused);
 
 #ifdef __cplusplus

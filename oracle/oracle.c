@@ -152,6 +152,25 @@ static void zgemm_row(uint32_t n, uint32_t k, const oc64* a, const oc64* B, oc64
   free(part);
 }
 
+/* Re(q . k) of one score: an entry of multiply_complex(q, transpose(K))
+ * (masked_attention_head.rs:190), so it follows the zgemm order above. */
+static double score_dot(uint32_t dh, const oc64* q, const oc64* k) {
+  double acc = 0.0;
+  if (g_gemm_order == 0) {
+    for (uint32_t e = 0; e < dh; ++e) acc = acc + (q[e].re * k[e].re - q[e].im * k[e].im);
+  } else if (g_gemm_order == 1) {
+    for (uint32_t e = dh; e-- > 0;) acc = acc + (q[e].re * k[e].re - q[e].im * k[e].im);
+  } else {
+    const uint32_t chunk = (dh + 7) / 8;
+    for (uint32_t e0 = 0; e0 < dh; e0 += chunk) {
+      double part = 0.0;
+      for (uint32_t e = e0; e < e0 + chunk && e < dh; ++e) part = part + (q[e].re * k[e].re - q[e].im * k[e].im);
+      acc = acc + part;
+    }
+  }
+  return acc;
+}
+
 /* OpenBLAS fixes no summation order for zgemm_ (its kernels block and fuse
  * differently per CPU), so any order is an equally valid restatement of
  * utils/matrix.rs:16-65.  Orders 1 and 2 exist to measure the reference's
@@ -695,10 +714,7 @@ static int self_attention_forward(orc_layer* L, const oc64* x, const uint32_t* m
               sc[c] = -1e12;
               continue;
             }
-            const oc64* kr = K + (size_t)c * dh;
-            double acc = 0.0;
-            for (uint32_t e = 0; e < dh; ++e) acc = acc + (qr[e].re * kr[e].re - qr[e].im * kr[e].im);
-            sc[c] = acc * scale + bp[(size_t)r * mc + c].re;
+            sc[c] = score_dot(dh, qr, K + (size_t)c * dh) * scale + bp[(size_t)r * mc + c].re;
           }
           double mx = -INFINITY;
           for (uint32_t c = 0; c < T; ++c) mx = fmax(mx, sc[c]);

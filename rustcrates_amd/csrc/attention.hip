@@ -332,4 +332,148 @@ int attention_decode_split(hipStream_t st, const Attn& a, const double2* q, long
   return OK;
 }
 
+// ===========================================================================
+// Prefill (keys = the S rows of the call, T == S): flash-style, one block per
+// (query tile of 16*NW rows, head, sequence), 32-key tiles up to the tile's
+// causal limit.  Re(q.k) = sum_e (qr kr - qi ki) is a real dot product of
+// length 2*dh: keys are staged in LDS as [kr | -ki], queries held as MFMA A
+// operands [qr | qi], and v_mfma_f64_16x16x4_f64 forms 16x16 score tiles.
+// Scores get the scale and Re(bias_pos[r][c]); keys c > r get -1e12
+// (masked_attention_head.rs:189-203).  The softmax runs online (running row
+// max m and sum l, the partial output rescaled by e^(m_old - m_new)); the
+// first tile always holds key 0, so m is a real score from then on and masked
+// keys contribute exactly 0.  P goes through LDS to become the A operand of
+// the P.V MFMAs (values staged in LDS).  out = acc / l; pad rows give 0.
+// D[i][j] of a 16x16 tile sits at lane j + 16*(i%4), element i/4.
+// ===========================================================================
+template <int DH, int NW>
+__global__ __launch_bounds__(64 * NW) void k_attention_prefill(Attn a) {
+  constexpr int KT = 32;          // keys per tile
+  constexpr int KD = 2 * DH;      // real dot length
+  constexpr int KSTR = KD + 1;    // LDS row stride of the key tile (doubles)
+  constexpr int NTH = 64 * NW;
+  constexpr int ET = DH / 16;     // 16-column tiles of the head dim
+  __shared__ double Ks[KT * KSTR];
+  __shared__ double2 Vs[KT * DH];
+  __shared__ double Ps[NW][16][KT + 1];
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int i = lane & 15, kq = lane >> 4;
+  const int S = a.S, T = a.T_const;
+  const int q0 = blockIdx.x * 16 * NW;  // block's first query row
+  const int r0 = q0 + 16 * wave;         // wave's first query row
+  const long rowbase = (long)b * S;
+  const double2* Kc = a.kc + ((long)b * a.H + h) * a.ctx * DH;
+  const double2* Vc = a.vc + ((long)b * a.H + h) * a.ctx * DH;
+  const double* bias = a.bias_re + (long)h * a.mc * a.mc;
+
+  // A operand of the scores: u[i][k] = k < DH ? qr[k] : qi[k - DH], k = 4s + kq
+  double uq[KD / 4];
+  {
+    const int r = r0 + i;
+    const double2* qrow = a.q + (rowbase + (r < S ? r : 0)) * a.ldq + (long)h * DH;
+#pragma unroll
+    for (int s2 = 0; s2 < KD / 4; ++s2) {
+      const int k = 4 * s2 + kq;
+      const double2 qv = r < S ? qrow[k % DH] : make_double2(0.0, 0.0);
+      uq[s2] = k < DH ? qv.x : qv.y;
+    }
+  }
+  v4d o_re[ET], o_im[ET];
+#pragma unroll
+  for (int t = 0; t < ET; ++t) o_re[t] = o_im[t] = v4d{0.0, 0.0, 0.0, 0.0};
+  double m[4], l[4];  // rows r0 + 4e + kq
+#pragma unroll
+  for (int e = 0; e < 4; ++e) m[e] = -INFINITY, l[e] = 0.0;
+
+  const int kend = min(T, q0 + 16 * NW);  // keys any row of the block can see
+  for (int c0 = 0; c0 < kend; c0 += KT) {
+    __syncthreads();  // the previous tile is consumed
+    for (int idx = tid; idx < KT * DH; idx += NTH) {
+      const int key = idx / DH, e = idx - key * DH, c = c0 + key;
+      const double2 kv = c < T ? Kc[(long)c * DH + e] : make_double2(0.0, 0.0);
+      const double2 vv = c < T ? Vc[(long)c * DH + e] : make_double2(0.0, 0.0);
+      Ks[key * KSTR + e] = kv.x;
+      Ks[key * KSTR + DH + e] = -kv.y;
+      Vs[key * DH + e] = vv;
+    }
+    __syncthreads();
+    // scores of 16 rows x 32 keys
+    v4d sc[2] = {v4d{0.0, 0.0, 0.0, 0.0}, v4d{0.0, 0.0, 0.0, 0.0}};
+#pragma unroll
+    for (int s2 = 0; s2 < KD / 4; ++s2)
+#pragma unroll
+      for (int jt = 0; jt < 2; ++jt)
+        sc[jt] = __builtin_amdgcn_mfma_f64_16x16x4f64(uq[s2], Ks[(16 * jt + i) * KSTR + 4 * s2 + kq], sc[jt], 0, 0, 0);
+    // scale, bias, causal mask; online softmax per row
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int r = r0 + 4 * e + kq;
+      double v[2];
+      double mt = -INFINITY;
+#pragma unroll
+      for (int jt = 0; jt < 2; ++jt) {
+        const int c = c0 + 16 * jt + i;
+        if (c > r || r >= S) v[jt] = -1e12;
+        else v[jt] = sc[jt][e] * a.scale + bias[(long)r * a.mc + c];
+        mt = fmax(mt, v[jt]);
+      }
+#pragma unroll
+      for (int o = 8; o > 0; o >>= 1) mt = fmax(mt, __shfl_xor(mt, o, 64));
+      const double mn = fmax(m[e], mt);
+      const double alpha = exp(m[e] - mn);
+      double ls = 0.0;
+#pragma unroll
+      for (int jt = 0; jt < 2; ++jt) {
+        const double p = exp(v[jt] - mn);
+        Ps[wave][4 * e + kq][16 * jt + i] = p;
+        ls += p;
+      }
+#pragma unroll
+      for (int o = 8; o > 0; o >>= 1) ls += __shfl_xor(ls, o, 64);
+      l[e] = l[e] * alpha + ls;
+      m[e] = mn;
+#pragma unroll
+      for (int t = 0; t < ET; ++t) o_re[t][e] *= alpha, o_im[t][e] *= alpha;
+    }
+    __syncthreads();  // P of every wave written
+    // out += P . V: A = P[row i][key 4s + kq], B = V[key 4s + kq][16t + i]
+#pragma unroll
+    for (int s2 = 0; s2 < KT / 4; ++s2) {
+      const double pa = Ps[wave][i][4 * s2 + kq];
+#pragma unroll
+      for (int t = 0; t < ET; ++t) {
+        const double2 vb = Vs[(4 * s2 + kq) * DH + 16 * t + i];
+        o_re[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(pa, vb.x, o_re[t], 0, 0, 0);
+        o_im[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(pa, vb.y, o_im[t], 0, 0, 0);
+      }
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int r = r0 + 4 * e + kq;
+    if (r >= S) continue;
+    const long row = rowbase + r;
+    const bool pad = a.row_mask && a.row_mask[row] == 0;
+    double2* out = a.out + row * a.ldo + (long)h * DH;
+#pragma unroll
+    for (int t = 0; t < ET; ++t)
+      out[16 * t + i] = pad ? make_double2(0.0, 0.0) : make_double2(o_re[t][e] / l[e], o_im[t][e] / l[e]);
+  }
+}
+
+bool attention_prefill(hipStream_t st, const Attn& a) {
+  if (a.kv_len || a.T_const != a.S || a.S <= 0) return false;
+  const auto launch = [&](auto kern, int nw) {
+    hipLaunchKernelGGL(kern, dim3(cdiv_i(a.S, 16 * nw), a.H, a.B), dim3(64 * nw), 0, st, a);
+  };
+  switch (a.dh) {
+    case 16: launch(k_attention_prefill<16, 8>, 8); return true;
+    case 32: launch(k_attention_prefill<32, 8>, 8); return true;
+    case 64: launch(k_attention_prefill<64, 8>, 8); return true;
+    case 128: launch(k_attention_prefill<128, 4>, 4); return true;
+    default: return false;
+  }
+}
+
 }  // namespace mitok

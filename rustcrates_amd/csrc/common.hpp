@@ -10,6 +10,9 @@
 
 namespace mitok {
 
+// accumulator of v_mfma_f64_16x16x4f64 (4 doubles per lane)
+typedef double v4d __attribute__((ext_vector_type(4)));
+
 // ---- status codes (include/mitok.h) ----
 enum Status : int {
   OK = 0,

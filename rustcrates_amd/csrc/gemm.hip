@@ -21,8 +21,6 @@
 
 namespace mitok {
 
-typedef double v4d __attribute__((ext_vector_type(4)));
-
 static inline int cdiv_i(long a, long b) { return (int)((a + b - 1) / b); }
 
 // ===========================================================================

@@ -144,8 +144,11 @@ struct Attn {
   double2* vc_w = nullptr;
   uint32_t* err = nullptr;
 };
-// One query row per block (prefill and the general reference case).
+// One query row per block (the general reference case, any T).
 void attention_rows(hipStream_t st, const Attn& a);
+// Prefill (T == S, no KV length): tiled MFMA kernel for head dims 16, 32, 64,
+// 128; returns false (nothing launched) for other shapes.
+bool attention_prefill(hipStream_t st, const Attn& a);
 // Decode (S == 1): key chunks in parallel; the chunk partials (AttnSplit) are
 // combined by a RowOps prologue (rowops_apply or a GEMV).  q is the sum of
 // npart partials (row b at q + b * ldq, partial stride part_stride); with

@@ -190,7 +190,8 @@ struct mitok_network {
   mitok::DevBuf sync_cnt, sync_ws, am_v, am_i;
   // fused decode plan: split partials left for the next launch to sum
   mitok::DevBuf dq, df1, dp0, dp1, datt;
-  int fused_decode = 1;  // B <= 8 decode steps use the fused GEMV plan
+  int fused_decode = 1;   // B <= 8 decode steps use the fused GEMV plan
+  int tiled_prefill = 1;  // prefill attention runs the tiled MFMA kernel where it applies
   // decode-step graph
   hipGraphExec_t graph = nullptr;
   uint32_t graph_B = 0, graph_nnew = 0;
@@ -543,7 +544,7 @@ static int enqueue_forward(Net* n, const Spec& sp) {
         } else {
           {
             TimeScope ts(n, MITOK_TIME_ATTENTION, 0.0);
-            attention_rows(st, a);
+            if (!n->tiled_prefill || !attention_prefill(st, a)) attention_rows(st, a);
           }
           layernorm(st, n->concat.as<double2>(), cur, nxt, rows, d, A->eps, A->gamma.as<double2>(),
                     A->beta.as<double2>());
@@ -1559,6 +1560,7 @@ int mitok_set_graph_mode(mitok_network* n, int direct_launch) {
 int mitok_set_decode_plan(mitok_network* n, int fused) {
   if (!n) return fail(ERR_ARG, "null network");
   n->fused_decode = fused ? 1 : 0;
+  n->tiled_prefill = fused ? 1 : 0;
   drop_graph(n);
   return OK;
 }

@@ -67,6 +67,22 @@ def oracle_noise_floor(onet, prompt, lens, n_new, want):
     return tuple(floor)
 
 
+def oracle_floor_of(run, want):
+    """oracle_noise_floor for any oracle computation: `run()` returns the
+    output array that `want` holds under the default order."""
+    import oracle
+
+    floor = [0.0, 0.0]
+    for order in (1, 2):
+        oracle.set_gemm_order(order)
+        try:
+            alt = run()
+        finally:
+            oracle.set_gemm_order(0)
+        floor = [max(floor[0], max_rel_err(alt, want)), max(floor[1], normwise_rel_err(alt, want))]
+    return tuple(floor)
+
+
 @pytest.fixture(scope="session")
 def oracle_mod():
     import oracle

@@ -139,10 +139,23 @@ int mitok_timing_read(mitok_network* net, double* total_ms, uint64_t* launches, 
 int mitok_device_synchronize(int device);
 /* 0 = replay decode steps as HIP graphs (default), 1 = launch kernels directly. */
 int mitok_set_graph_mode(mitok_network* net, int direct_launch);
-/* 1 = decode steps of up to 8 sequences run the fused plan (row transforms in
- * the product prologues) and prefill attention the tiled kernel (default);
- * 0 = one launch per reference operation and one query row per attention block. */
-int mitok_set_decode_plan(mitok_network* net, int fused);
+/* 3 = generate's decode loop for up to 8 sequences runs as one resident
+ *     cooperative launch (one block per CU, grid barriers between operations);
+ * 2 = the resident loop at batch 1, plan 1 for 2 to 8 sequences (default);
+ * 1 = decode steps of up to 8 sequences run the fused plan (row transforms in
+ *     the product prologues, one launch per product, replayed as a graph);
+ * 0 = one launch per reference operation and one query row per attention block.
+ * Plans 1 to 3 run prefill attention on the tiled kernel.
+ * No counterpart in the reference (a scheduling choice; results agree to the
+ * parity tolerance). */
+int mitok_set_decode_plan(mitok_network* net, int plan);
+/* Per-operation profile of the resident decode loop (plan 2).  enable = 1:
+ * later launches record block 0's clock after every grid barrier.  Then, if
+ * nops is not NULL, reports the last launch's operations (at most max_ops):
+ * kinds[i] (0 product, 1 attention chunks, 2 row transform, 3 chunk combine) and
+ * us[i], the microseconds from the previous barrier to the one after op i,
+ * averaged over the steps.  No counterpart in the reference (instrumentation). */
+int mitok_resident_profile(mitok_network* net, int enable, int max_ops, int* nops, int* kinds, double* us);
 
 #ifdef __cplusplus
 }

@@ -58,6 +58,7 @@ SIGNATURES = {
     "mitok_device_synchronize": (_i32, [_i32]),
     "mitok_set_graph_mode": (_i32, [_P, _i32]),
     "mitok_set_decode_plan": (_i32, [_P, _i32]),
+    "mitok_resident_profile": (_i32, [_P, _i32, _i32, C.POINTER(_i32), C.POINTER(_i32), C.POINTER(C.c_double)]),
 }
 
 
@@ -219,7 +220,8 @@ class Network:
     def last_timings(self):
         t = np.zeros(3, np.float64)
         _check(self._lib.mitok_last_timings(self._h, _ptr(t)))
-        return {"prefill_ms": float(t[0]), "decode_ms": float(t[1]), "graph": bool(t[2])}
+        plan = {0.0: "direct", 1.0: "graph", 2.0: "resident"}.get(float(t[2]), "direct")
+        return {"prefill_ms": float(t[0]), "decode_ms": float(t[1]), "graph": plan == "graph", "decode_loop": plan}
 
     def timing_enable(self, kernel_class: int):
         _check(self._lib.mitok_timing_enable(self._h, kernel_class))
@@ -232,5 +234,20 @@ class Network:
     def set_graph_mode(self, direct_launch: bool):
         _check(self._lib.mitok_set_graph_mode(self._h, int(direct_launch)))
 
-    def set_decode_plan(self, fused: bool):
-        _check(self._lib.mitok_set_decode_plan(self._h, int(fused)))
+    def resident_profile(self, enable: bool = True):
+        """Enables per-operation timing of the resident decode loop and returns
+        the last launch's [(kind, microseconds per step)]."""
+        mx = 512
+        n = _i32()
+        kinds = (_i32 * mx)()
+        us = (C.c_double * mx)()
+        _check(self._lib.mitok_resident_profile(self._h, int(enable), mx, C.byref(n), kinds, us))
+        names = {0: "gemv", 1: "attn", 2: "rows", 3: "combine"}
+        return [(names.get(kinds[i], "?"), us[i]) for i in range(n.value)]
+
+    def set_decode_plan(self, plan: int):
+        """3: generate's decode loop for up to 8 sequences as one resident
+        launch; 2: resident at batch 1, fused above (default); 1 (True):
+        fused launches, replayed as a graph; 0 (False): one launch per
+        reference operation."""
+        _check(self._lib.mitok_set_decode_plan(self._h, int(plan)))

@@ -17,7 +17,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 SRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libmitok.so")
-SOURCES = ["kernels.hip", "gemm.hip", "attention.hip", "network.hip"]
+SOURCES = ["kernels.hip", "gemm.hip", "attention.hip", "resident.hip", "resident_k1.hip", "resident_k2.hip",
+           "resident_k4.hip", "resident_k8.hip", "network.hip"]
 ARCH = os.environ.get("MITOK_ARCH", "gfx950")
 
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"

@@ -224,8 +224,7 @@ __global__ __launch_bounds__(256) void k_attention_split(Attn a, const double2* 
         const int ee = sub + t * DEC_LPK;
         if (ee < dh) acc += qs[ee].x * kv[pass][t].x - qs[ee].y * kv[pass][t].y;
       }
-#pragma unroll
-      for (int off = DEC_LPK / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+      acc = row16_sum(acc);  // the 16 lanes of key j
       if (j < nc && sub == 0) sc[j] = acc * a.scale + bj[pass];
     }
   } else {
@@ -240,8 +239,7 @@ __global__ __launch_bounds__(256) void k_attention_split(Attn a, const double2* 
           acc += qv.x * k2.x - qv.y * k2.y;
         }
       }
-#pragma unroll
-      for (int off = DEC_LPK / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+      acc = row16_sum(acc);  // the 16 lanes of key j
       if (j < nc && sub == 0) sc[j] = acc * a.scale + bias0[c0 + j];
     }
   }
@@ -418,8 +416,7 @@ __global__ __launch_bounds__(64 * NW) void k_attention_prefill(Attn a) {
         else v[jt] = sc[jt][e] * a.scale + bias[(long)r * a.mc + c];
         mt = fmax(mt, v[jt]);
       }
-#pragma unroll
-      for (int o = 8; o > 0; o >>= 1) mt = fmax(mt, __shfl_xor(mt, o, 64));
+      mt = row16_max(mt);
       const double mn = fmax(m[e], mt);
       const double alpha = exp(m[e] - mn);
       double ls = 0.0;
@@ -429,8 +426,7 @@ __global__ __launch_bounds__(64 * NW) void k_attention_prefill(Attn a) {
         Ps[wave][4 * e + kq][16 * jt + i] = p;
         ls += p;
       }
-#pragma unroll
-      for (int o = 8; o > 0; o >>= 1) ls += __shfl_xor(ls, o, 64);
+      ls = row16_sum(ls);
       l[e] = l[e] * alpha + ls;
       m[e] = mn;
 #pragma unroll

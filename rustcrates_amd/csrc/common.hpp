@@ -30,6 +30,7 @@ enum ErrBits : uint32_t {
   EB_BAD_TOKEN = 4u,     // id >= vocab: no embedding (embedding_layer.rs:305)
   EB_ARGMAX_NAN = 8u,    // greedy_decoding partial_cmp().unwrap() (sampling_methods.rs:12)
   EB_CTX_OVERFLOW = 16u, // a cached sequence outgrew max_ctx
+  EB_BARRIER = 32u,      // a grid barrier of the resident decode loop timed out
 };
 
 // ---- counter generator (identical to oracle.c / seeded.py) ----
@@ -94,15 +95,94 @@ __device__ inline double2 gelu_nc(double2 z, bool* nan) {
 }
 
 // ---- wavefront reductions (wave64) ----
-__device__ __forceinline__ double wave_sum(double v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+// ---- cross-lane reductions without the LDS crossbar ----
+// DPP moves inside rows of 16 lanes (quad swaps, half-row and row mirrors,
+// row rotate by 8) and gfx950's v_permlane16_swap / v_permlane32_swap across
+// rows take a few cycles each, where ds_bpermute (what __shfl_xor becomes)
+// is an LDS round trip.  Every step combines a lane with a partner that
+// combines the same two operands (mirrors pair uniform groups once the quads
+// are reduced; a swap hands both rows the same pair), so all lanes of a
+// group end with the same bits.
+constexpr int DPP_XOR1 = 0xB1;         // quad_perm [1, 0, 3, 2]
+constexpr int DPP_XOR2 = 0x4E;         // quad_perm [2, 3, 0, 1]
+constexpr int DPP_HALF_MIRROR = 0x141; // lane j of 8 <- 7 - j
+constexpr int DPP_MIRROR = 0x140;      // lane j of 16 <- 15 - j
+constexpr int DPP_ROR8 = 0x128;        // lane j of 16 <- (j + 8) % 16, i.e. j ^ 8
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i32(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, true); }
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+  return __hiloint2double(dpp_i32<CTRL>(__double2hiint(v)), dpp_i32<CTRL>(__double2loint(v)));
+}
+// a: the even 16-lane row of the lane's row pair, b: the odd one (same in both rows)
+__device__ __forceinline__ void pair16_f64(double v, double& a, double& b) {
+  const auto lo = __builtin_amdgcn_permlane16_swap((unsigned)__double2loint(v), (unsigned)__double2loint(v), false, false);
+  const auto hi = __builtin_amdgcn_permlane16_swap((unsigned)__double2hiint(v), (unsigned)__double2hiint(v), false, false);
+  a = __hiloint2double((int)hi[0], (int)lo[0]);
+  b = __hiloint2double((int)hi[1], (int)lo[1]);
+}
+// a: lanes 0-31, b: lanes 32-63 (same in both halves)
+__device__ __forceinline__ void pair32_f64(double v, double& a, double& b) {
+  const auto lo = __builtin_amdgcn_permlane32_swap((unsigned)__double2loint(v), (unsigned)__double2loint(v), false, false);
+  const auto hi = __builtin_amdgcn_permlane32_swap((unsigned)__double2hiint(v), (unsigned)__double2hiint(v), false, false);
+  a = __hiloint2double((int)hi[0], (int)lo[0]);
+  b = __hiloint2double((int)hi[1], (int)lo[1]);
+}
+__device__ __forceinline__ void pair16_i32(int v, int& a, int& b) {
+  const auto r = __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false);
+  a = (int)r[0];
+  b = (int)r[1];
+}
+__device__ __forceinline__ void pair32_i32(int v, int& a, int& b) {
+  const auto r = __builtin_amdgcn_permlane32_swap((unsigned)v, (unsigned)v, false, false);
+  a = (int)r[0];
+  b = (int)r[1];
+}
+
+// sum / max over each row of 16 lanes
+__device__ __forceinline__ double row16_sum(double v) {
+  v += dpp_f64<DPP_XOR1>(v);
+  v += dpp_f64<DPP_XOR2>(v);
+  v += dpp_f64<DPP_HALF_MIRROR>(v);
+  v += dpp_f64<DPP_MIRROR>(v);
   return v;
 }
-__device__ __forceinline__ double wave_max(double v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmax(v, __shfl_xor(v, o, 64));
+__device__ __forceinline__ double row16_max(double v) {
+  v = fmax(v, dpp_f64<DPP_XOR1>(v));
+  v = fmax(v, dpp_f64<DPP_XOR2>(v));
+  v = fmax(v, dpp_f64<DPP_HALF_MIRROR>(v));
+  v = fmax(v, dpp_f64<DPP_MIRROR>(v));
   return v;
+}
+// sums over lanes j, j ^ 16, j ^ 32, j ^ 48 (xor16), j ^ 32 (xor32), j ^ 8 (xor8)
+__device__ __forceinline__ double xor16_sum(double v) {
+  double a, b;
+  pair16_f64(v, a, b);
+  return a + b;
+}
+__device__ __forceinline__ double xor32_sum(double v) {
+  double a, b;
+  pair32_f64(v, a, b);
+  return a + b;
+}
+__device__ __forceinline__ double xor8_sum(double v) { return v + dpp_f64<DPP_ROR8>(v); }
+// sum of the lanes sharing lane % C (C in 8, 16, 32, 64)
+template <int C>
+__device__ __forceinline__ double col_sum(double v) {
+  if constexpr (C <= 8) v = xor8_sum(v);
+  if constexpr (C <= 16) v = xor16_sum(v);
+  if constexpr (C <= 32) v = xor32_sum(v);
+  return v;
+}
+__device__ __forceinline__ double wave_sum(double v) { return xor32_sum(xor16_sum(row16_sum(v))); }
+__device__ __forceinline__ double wave_max(double v) {
+  v = row16_max(v);
+  double a, b;
+  pair16_f64(v, a, b);
+  v = fmax(a, b);
+  pair32_f64(v, a, b);
+  return fmax(a, b);
 }
 
 // ---- cross-block results (split partials) ----
@@ -129,6 +209,32 @@ __device__ __forceinline__ void st_dev(int* p, int v) { __hip_atomic_store(p, v,
 __device__ __forceinline__ int ld_dev(const int* p) {
   return __hip_atomic_load((int*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ void st_dev(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ld_dev(const uint32_t* p) {
+  return __hip_atomic_load((uint32_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Access policy of the shared device code (rowops.hpp, epilogue.hpp) for
+// data that may change while a kernel runs.  AccPlain: ordinary loads and
+// stores, for kernels that only read what earlier launches wrote.  The
+// resident decode loop (resident.hip), where every block runs until the last
+// step, supplies a policy with device-coherent activations and the per-step
+// state (KV lengths, ids, history count) kept in each block's LDS.
+//   ld / st    activations and partial results
+//   kv(p, m)   KV length of sequence m (also the RoPE position of its new token)
+//   id(p, m)   token id of row m
+//   cnt(p)     decode-step count (the logits-history slot)
+struct AccPlain {
+  template <class T>
+  static __device__ __forceinline__ T ld(const T* p) { return *p; }
+  template <class T>
+  static __device__ __forceinline__ void st(T* p, T v) { *p = v; }
+  static __device__ __forceinline__ int kv(const int* p, int m) { return p[m]; }
+  static __device__ __forceinline__ uint32_t id(const uint32_t* p, int m) { return p[m]; }
+  static __device__ __forceinline__ int cnt(const int* p) { return p[0]; }
+};
 
 // ---- split completion ----
 // Every block of a split calls this once after writing its partial result
@@ -160,13 +266,27 @@ __device__ __forceinline__ void argmax_combine(double& bv, int& bi, double ov, i
     bi = oi;
   }
 }
+// the combine is symmetric (larger value, then larger index), so partners agree
+template <int CTRL>
+__device__ __forceinline__ void argmax_dpp(double& v, int& i) {
+  argmax_combine(v, i, dpp_f64<CTRL>(v), dpp_i32<CTRL>(i));
+}
+__device__ __forceinline__ void row16_argmax(double& v, int& i) {
+  argmax_dpp<DPP_XOR1>(v, i);
+  argmax_dpp<DPP_XOR2>(v, i);
+  argmax_dpp<DPP_HALF_MIRROR>(v, i);
+  argmax_dpp<DPP_MIRROR>(v, i);
+}
 __device__ __forceinline__ void wave_argmax(double& v, int& i) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const double ov = __shfl_xor(v, o, 64);
-    const int oi = __shfl_xor(i, o, 64);
-    argmax_combine(v, i, ov, oi);
-  }
+  row16_argmax(v, i);
+  double a, b;
+  int ia, ib;
+  pair16_f64(v, a, b);
+  pair16_i32(i, ia, ib);
+  argmax_combine(a, ia, b, ib);
+  pair32_f64(a, v, b);
+  pair32_i32(ia, i, ib);
+  argmax_combine(v, i, b, ib);
 }
 
 }  // namespace mitok

@@ -17,56 +17,11 @@
 // on arrival order.
 #include <algorithm>
 
-#include "rowops.hpp"
+#include "epilogue.hpp"
 
 namespace mitok {
 
 static inline int cdiv_i(long a, long b) { return (int)((a + b - 1) / b); }
-
-// ===========================================================================
-// epilogue: returns Re of the stored value (used by the fused argmax)
-// ===========================================================================
-__device__ __forceinline__ double apply_epi(const Epi& ep, int M, int N, int m, int n, double2 v) {
-  if (ep.bias) v = cadd(v, ep.bias[n]);
-  switch (ep.mode) {
-    case EPI_STORE:
-      if (ep.check_finite && !(isfinite(v.x) && isfinite(v.y))) atomicOr(ep.err, (uint32_t)EB_FFN_NONFINITE);
-      ep.out[(long)m * ep.ldo + n] = v;
-      break;
-    case EPI_GELU: {
-      bool nan = false;
-      if (ep.row_mask && ep.row_mask[m] == 0) v = make_double2(0.0, 0.0);  // activation.rs:268-284
-      else v = gelu_nc(v, &nan);
-      if (nan) atomicOr(ep.err, (uint32_t)EB_GELU_NAN);
-      ep.out[(long)m * ep.ldo + n] = v;
-      break;
-    }
-    case EPI_RE:
-      ep.out_re[(long)m * ep.ldo + n] = v.x;
-      if (ep.hist_re) ep.hist_re[((long)ep.hist_cnt[0] * M + m) * N + n] = v.x;
-      break;
-    case EPI_QKV: {
-      if (n < ep.d) {
-        ep.out[(long)m * ep.ldo + n] = v;
-        break;
-      }
-      const int part = n < 2 * ep.d ? 1 : 2;
-      const int c = n - part * ep.d;
-      const int h = c / ep.dh, e = c - h * ep.dh;
-      const int b = m / ep.S, s = m - b * ep.S;
-      if (ep.kv_row && ep.kv_row[b] != s) break;  // cached branch: only the last token (masked_attention_head.rs:140-156)
-      const int pos = (ep.kv_base ? ep.kv_base[b] : 0) + (ep.kv_row ? 0 : s);
-      if (pos >= ep.ctx) {
-        atomicOr(ep.err, (uint32_t)EB_CTX_OVERFLOW);
-        break;
-      }
-      double2* dst = part == 1 ? ep.kc : ep.vc;
-      dst[(((long)b * ep.heads + h) * ep.ctx + pos) * ep.dh + e] = v;
-      break;
-    }
-  }
-  return v.x;
-}
 
 // greedy_decoding finish: one block per row reduces that row's per-tile
 // (max, last index) partials, then stores the id, appends it to the history
@@ -176,12 +131,10 @@ __global__ __launch_bounds__(256) void k_gemv(RowOps ro, int M, const double2* _
   }
   // lanes of one column (same c, r = 0 .. RPW-1) -> r = 0
 #pragma unroll
-  for (int o = C; o < 64; o <<= 1)
-#pragma unroll
-    for (int m = 0; m < MR; ++m) {
-      acc[m].x += __shfl_xor(acc[m].x, o, 64);
-      acc[m].y += __shfl_xor(acc[m].y, o, 64);
-    }
+  for (int m = 0; m < MR; ++m) {
+    acc[m].x = col_sum<C>(acc[m].x);
+    acc[m].y = col_sum<C>(acc[m].y);
+  }
   if (wave > 0 && lane < C)
 #pragma unroll
     for (int m = 0; m < MR; ++m) red[wave - 1][m][lane] = acc[m];
@@ -540,12 +493,7 @@ __global__ __launch_bounds__(256) void k_zgemm_skinny(const double2* __restrict_
       if (isnan(x)) atomicOr(am.err, (uint32_t)EB_ARGMAX_NAN);
       else bv = x, bi = n1;
     }
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) {
-      const double ov = __shfl_xor(bv, o, 64);
-      const int oi = __shfl_xor(bi, o, 64);
-      argmax_combine(bv, bi, ov, oi);
-    }
+    row16_argmax(bv, bi);
     if (col == 0 && row < M) {
       am.part_v[(long)row * gridDim.x + blockIdx.x] = bv;
       am.part_i[(long)row * gridDim.x + blockIdx.x] = bi;
@@ -691,12 +639,7 @@ __global__ __launch_bounds__(256) void k_zgemm_skinny_cols(const double2* __rest
           if (isnan(re)) atomicOr(am.err, (uint32_t)EB_ARGMAX_NAN);
           else bv = re, bi = n;
         }
-#pragma unroll
-        for (int o = 8; o > 0; o >>= 1) {
-          const double ov = __shfl_xor(bv, o, 64);
-          const int oi = __shfl_xor(bi, o, 64);
-          argmax_combine(bv, bi, ov, oi);
-        }
+        row16_argmax(bv, bi);
         if (i == 0 && m < M) {
           am.part_v[(long)m * tiles16 + n0 / 16] = bv;
           am.part_i[(long)m * tiles16 + n0 / 16] = bi;

@@ -159,6 +159,67 @@ size_t attention_split_ws_bytes(int B, int H, int dh, int T_max);
 int attention_decode_split(hipStream_t st, const Attn& a, const double2* q, long ldq, int npart, long part_stride,
                            bool append, const AttnSplit& out);
 
+// ---- resident decode loop (resident.hip) ----
+// One cooperative launch runs `nsteps` decode steps; each step is the program
+// ops[0..nops), with a grid barrier after every operation.  Block b takes work
+// items b, b + grid, ... of each operation.  Every block keeps the step state
+// (KV lengths, the ids being fed, the step count) in LDS and finds the greedy
+// ids itself from the vocab product's argmax partials at the start of the next
+// step; block 0 writes ids, history, counts and KV lengths back.
+enum ROpKind : int { ROP_GEMV = 0, ROP_ATTN = 1, ROP_ROWS = 2, ROP_COMBINE = 3 };
+struct ROp {
+  int kind = ROP_GEMV;
+  int items = 0;
+  int M = 0;  // rows (sequences)
+  // GEMV: rowops(ro)[M][K] * W[K][N] -> ep; C columns x (4 kw) rows per item,
+  // ncb column blocks; EPI_PART leaves the K splits as partials, other modes
+  // need one split.  am.part_v != null: per column-block argmax partials.
+  RowOps ro;
+  const double2* W = nullptr;
+  long ldw = 0;
+  int N = 0, K = 0, C = 0, kw = 0, ncb = 0, P = 1, waves = 4;
+  Epi ep;
+  Argmax am;
+  // ATTN: chunks of attention_split_plan (items nsplit x H x B); q of sequence b at q + b * ldq
+  // COMBINE: out[b][h*dh + e] = Re(chunk combine + ro.resid) for item (b, h)
+  Attn a;
+  AttnSplit o;
+  const double2* q = nullptr;
+  long ldq = 0;
+  // ROWS: out[m][k] = rowops(ro)[m][k], k < K, in column chunks of cw (whole rows with a LayerNorm)
+  double2* out = nullptr;
+  long ldo = 0;
+  int cw = 0;
+};
+// the step state and greedy_decoding (sampling_methods.rs:5-18) of the loop
+struct RStep {
+  int B = 0;
+  const double* part_v = nullptr;  // [B][tiles] vocab argmax partials
+  const int* part_i = nullptr;
+  int tiles = 0;
+  uint32_t* ids = nullptr;   // [B] ids fed to the step
+  uint32_t* hist = nullptr;  // [B][hist_stride] generated ids
+  int hist_stride = 0;
+  int* hist_cnt = nullptr;  // [B] ids generated so far (also the logits-history slot)
+  int* kv_len = nullptr;    // [B]
+  uint32_t* err = nullptr;
+};
+struct ResGemvPlan {
+  int mr, C, kw, P, ncb, waves;
+};
+// narrowest column block with at most `grid` blocks; EPI_PART splits K up to
+// the grid (at most 8 ways); waves 3: one item per block whose weights fit the
+// prefetch registers of waves 1-3 (kw rows each), else 4 streaming waves
+ResGemvPlan resident_gemv_plan(int M, int N, int K, bool part, int grid);
+size_t resident_op_lds(const ROp& op);  // dynamic LDS of one operation
+// blocks of the launch (one per CU) if the kernel for (mr, dh) fits with `shm`
+int resident_grid(int device, int mr, int dh, size_t shm, int* grid);
+// flags: one word per block, epochs below epoch0 + 1 (zeroed at set-up); the
+// launch performs nsteps * nops barriers.  stamps (optional, nsteps * nops + 1
+// words): block 0's wall clock (100 MHz) after each barrier, then at the start.
+int resident_launch(hipStream_t st, const ROp* ops_d, int nops, int nsteps, const RStep& step, int mr, int dh,
+                    size_t shm, int grid, uint32_t* flags, uint32_t epoch0, uint32_t* err, uint64_t* stamps);
+
 // ---- row kernels ----
 void embed(hipStream_t st, const double2* table, int V, int d, const uint32_t* ids, int rows, double2* out,
            uint32_t* err);

@@ -192,6 +192,14 @@ struct mitok_network {
   mitok::DevBuf dq, df1, dp0, dp1, datt;
   int fused_decode = 1;   // B <= 8 decode steps use the fused GEMV plan
   int tiled_prefill = 1;  // prefill attention runs the tiled MFMA kernel where it applies
+  int resident = 1;       // generate's decode loop as one resident launch: 0 never, 1 B == 1, 2 B <= 8
+  // resident decode loop: operation table (host copy kept until the next build),
+  // one barrier flag per block (zeroed when allocated), the next barrier epoch
+  std::vector<mitok::ROp> res_ops_h;
+  mitok::DevBuf res_ops, res_flags, res_stamps;
+  uint32_t res_epoch = 0;
+  int res_profile = 0;  // record per-operation times of the next resident launches
+  uint32_t res_steps = 0;
   // decode-step graph
   hipGraphExec_t graph = nullptr;
   uint32_t graph_B = 0, graph_nnew = 0;
@@ -244,6 +252,7 @@ static int check_err_word(Net* n) {
   if (e & EB_FFN_NONFINITE) return fail(ERR_NAN, "output ffn dense: The value is Not Valid (transformer_network.rs:408)");
   if (e & EB_ARGMAX_NAN) return fail(ERR_NAN, "greedy_decoding: NaN in logits (sampling_methods.rs:12)");
   if (e & EB_CTX_OVERFLOW) return fail(ERR_ARG, "context exceeds max_ctx");
+  if (e & EB_BARRIER) return fail(ERR_STATE, "resident decode: a grid barrier timed out");
   return fail(ERR_STATE, "device error word 0x%x", e);
 }
 
@@ -859,6 +868,334 @@ static int enqueue_step(Net* n, const Spec& sp) {
 }
 
 // ---------------------------------------------------------------------------
+// resident decode loop (resident.hip): the decode step of generate for B <= 8
+// sequences as a program of operations that one cooperative launch runs for
+// every step.  Row transforms are materialised (ROP_ROWS) before a product
+// unless they fit its prologue: a LayerNorm of rows that fit LDS, split
+// partials + bias, an embedding gather, RoPE.  A transformer block is QKV
+// (+ KV append in the epilogue), attention chunks, chunk combine + residual,
+// FFN Dense (+ the attention block's LayerNorm in the prologue, GELU in the
+// epilogue), FFN Linear (split partials); the vocab product leaves argmax
+// partials that every block reduces at the start of the next step.
+// ---------------------------------------------------------------------------
+constexpr size_t RES_LN_ROWS_BYTES = 64 * 1024;  // LayerNorm prologue rows held in LDS
+constexpr size_t RES_MAX_DYN_LDS = 120 * 1024;
+
+static int res_mr(int B) { return B <= 1 ? 1 : B <= 2 ? 2 : B <= 4 ? 4 : 8; }
+
+// measured on MI355X at config 3: the resident loop wins at batch 1; from
+// batch 4 the fused launches (graph) are faster
+constexpr int RES_AUTO_MAX_B = 1;
+
+static bool resident_ok(const Net* n, const Spec& sp) {
+  const int max_b = n->resident == 2 ? 8 : n->resident == 1 ? RES_AUTO_MAX_B : 0;
+  if (sp.mode != MODE_CACHED || sp.S != 1 || sp.B > max_b || !sp.forward_only || !sp.am) return false;
+  if (sp.first != 0 || sp.last != n->layers.size() || sp.kv_row || sp.out_hidden) return false;
+  for (auto& L : n->layers)
+    if (L->kind == K_SELF_ATTENTION) {
+      const auto* A = (const SelfAttentionLayer*)L.get();
+      Attn a;
+      a.B = sp.B;
+      a.H = A->heads;
+      a.T_max = A->max_ctx;
+      a.dh = A->dh;
+      const AttnSplit o = attention_split_plan(a);
+      if (o.nsplit > 256 || A->dh > 256) return false;
+    }
+  return true;
+}
+
+// Builds the step program into n->res_ops_h; *dh = the head dim the kernel
+// is specialised for (0: generic), *shm = its dynamic LDS, *tiles = the vocab
+// product's argmax partials per row.
+static int resident_build(Net* n, const Spec& sp, int grid, int* dh_out, size_t* shm_out, int* tiles_out) {
+  std::vector<ROp>& ops = n->res_ops_h;
+  ops.clear();
+  uint32_t* err = n->err_d.as<uint32_t>();
+  const int B = sp.B, mr = res_mr(B);
+  int* kv_len = n->kv_len_d.as<int>();
+  RowOps pro;
+  pro.err = err;
+  int width = 0, dh_k = -1;
+  double2* mats[2] = {n->mat0.as<double2>(), n->mat1.as<double2>()};
+  int mat_next = 0;
+  double2* parts[2] = {n->dp0.as<double2>(), n->dp1.as<double2>()};
+  int part_next = 0;
+  auto materialize = [&]() {
+    ROp op;
+    op.kind = ROP_ROWS;
+    op.M = B;
+    op.ro = pro;
+    op.K = width;
+    op.out = mats[mat_next];
+    op.ldo = width;
+    op.cw = 256;
+    op.items = pro.ln ? B : B * ((width + op.cw - 1) / op.cw);
+    mat_next ^= 1;
+    ops.push_back(op);
+    pro = rows_of(op.out, width);
+    pro.err = err;
+  };
+  // a LayerNorm prologue holds whole input rows in LDS
+  auto fit_prologue = [&](int K) {
+    if (pro.att.po || (pro.ln && (size_t)mr * K * sizeof(double2) > RES_LN_ROWS_BYTES)) materialize();
+  };
+  auto gemv = [&](const RowOps& ro, const double2* W, int N, int K, const Epi& ep, const Argmax* am) -> ROp& {
+    const ResGemvPlan p = resident_gemv_plan(B, N, K, ep.mode == EPI_PART, grid);
+    ROp op;
+    op.kind = ROP_GEMV;
+    op.M = B;
+    op.ro = ro;
+    op.W = W;
+    op.ldw = N;
+    op.N = N;
+    op.K = K;
+    op.C = p.C;
+    op.kw = p.kw;
+    op.ncb = p.ncb;
+    op.P = p.P;
+    op.waves = p.waves;
+    op.ep = ep;
+    if (am) op.am = *am;
+    op.items = p.ncb * p.P;
+    ops.push_back(op);
+    return ops.back();
+  };
+  auto part_rows = [&](double2* buf, int npart, int cols) {
+    RowOps r = rows_of(buf, cols);
+    r.npart = npart;
+    r.part_stride = (long)B * cols;
+    r.err = err;
+    return r;
+  };
+  for (uint32_t li = 0; li < n->layers.size(); ++li) {
+    Layer* L = n->layers[li].get();
+    switch (L->kind) {
+      case K_EMBEDDING: {
+        auto* E = (EmbeddingLayer*)L;
+        pro = RowOps();
+        pro.err = err;
+        pro.table = E->table.as<double2>();
+        pro.ids = sp.ids;
+        pro.vocab = (int)E->vocab;
+        width = (int)E->d_out;
+        break;
+      }
+      case K_POSENC: {
+        auto* P = (PositionalEncodingLayer*)L;
+        if (pro.rope_cs || pro.resid || pro.ln || pro.att.po) materialize();
+        pro.rope_cs = P->cs.as<double2>();
+        pro.rope_pos = sp.pos ? sp.pos : kv_len;
+        pro.rope_max = P->positions;
+        break;
+      }
+      case K_NORM: {
+        auto* N = (NormLayer*)L;
+        if (pro.ln || pro.att.po) materialize();
+        pro.ln = 1;
+        pro.eps = N->eps;
+        pro.gamma = N->gamma.as<double2>();
+        pro.beta = N->beta.as<double2>();
+        break;
+      }
+      case K_SELF_ATTENTION: {
+        auto* A = (SelfAttentionLayer*)L;
+        const int d = A->d_in, H = A->heads, dh = A->dh;
+        dh_k = (dh_k < 0 || dh_k == dh) ? dh : 0;
+        if (pro.resid) materialize();  // its residual source is about to be overwritten
+        fit_prologue(d);
+        double2* x1 = n->act0.as<double2>();  // the block input, kept for the residual
+        pro.save = x1;
+        pro.ldsave = d;
+        Epi e;
+        e.mode = EPI_QKV;
+        e.out = n->qbuf.as<double2>();
+        e.ldo = d;
+        e.d = d;
+        e.dh = dh;
+        e.heads = H;
+        e.S = 1;
+        e.kc = A->kc.as<double2>();
+        e.vc = A->vc.as<double2>();
+        e.ctx = A->max_ctx;
+        e.kv_base = kv_len;
+        e.err = err;
+        gemv(pro, A->wqkv.as<double2>(), 3 * d, d, e, nullptr);
+        Attn a;
+        a.kc = A->kc.as<double2>();
+        a.vc = A->vc.as<double2>();
+        a.ctx = A->max_ctx;
+        a.kv_len = kv_len;
+        a.T_add = 1;
+        a.T_max = A->max_ctx;
+        a.bias_re = A->bias_re.as<double>();
+        a.mc = A->max_ctx;
+        a.B = B;
+        a.S = 1;
+        a.H = H;
+        a.dh = dh;
+        a.scale = 1.0 / (1e-8 + sqrt((double)dh));  // masked_attention_head.rs:453-465
+        a.err = err;
+        ROp at;
+        at.kind = ROP_ATTN;
+        at.M = B;
+        at.a = a;
+        at.o = split_buffers(n, attention_split_plan(a), B, H);
+        at.q = n->qbuf.as<double2>();
+        at.ldq = d;
+        at.items = at.o.nsplit * H * B;
+        ops.push_back(at);
+        // chunk combine + residual, then the Norm (self_attention_layer.rs:101-124)
+        // in the next product's prologue
+        ROp cb;
+        cb.kind = ROP_COMBINE;
+        cb.M = B;
+        cb.a = a;
+        cb.o = at.o;
+        cb.ro.resid = x1;
+        cb.ro.ldr = d;
+        cb.out = mats[mat_next];
+        cb.ldo = d;
+        cb.items = B * H;
+        mat_next ^= 1;
+        ops.push_back(cb);
+        pro = rows_of(cb.out, d);
+        pro.err = err;
+        width = d;
+        pro.ln = 1;
+        pro.eps = A->eps;
+        pro.gamma = A->gamma.as<double2>();
+        pro.beta = A->beta.as<double2>();
+        break;
+      }
+      case K_FEED_FORWARD: {
+        auto* F = (FeedForwardLayer*)L;
+        fit_prologue(F->d_in);
+        Epi e1;  // Dense: + b1, GELU, pad rows 0 (layer.rs:132-166)
+        e1.mode = EPI_GELU;
+        e1.bias = F->b1.as<double2>();
+        e1.out = n->hbuf.as<double2>();
+        e1.ldo = F->hidden;
+        e1.row_mask = sp.mask;
+        e1.err = err;
+        gemv(pro, F->w1.as<double2>(), F->hidden, F->d_in, e1, nullptr);
+        double2* out = parts[part_next];
+        part_next ^= 1;
+        Epi e2;
+        e2.mode = EPI_PART;
+        e2.out = out;
+        e2.err = err;
+        RowOps h = rows_of(n->hbuf.as<double2>(), F->hidden);
+        h.err = err;
+        const int p2 = gemv(h, F->w2.as<double2>(), F->d_out, F->hidden, e2, nullptr).P;
+        pro = part_rows(out, p2, F->d_out);  // Linear: + b2; non-finite check (transformer_network.rs:408)
+        pro.bias = F->b2.as<double2>();
+        pro.finite_check = 1;
+        width = (int)F->d_out;
+        break;
+      }
+      case K_LINEAR: {
+        auto* Ln = (LinearLayer*)L;
+        fit_prologue(Ln->d_in);
+        if (is_vocab_linear(n, li)) {
+          Epi e;
+          e.bias = Ln->b.as<double2>();
+          e.ldo = Ln->d_out;
+          e.err = err;
+          e.mode = EPI_RE;
+          e.out_re = sp.out_re;
+          e.hist_re = sp.hist_re;
+          e.hist_cnt = sp.hist_cnt;
+          Argmax am = *sp.am;
+          am.part_v = n->am_v.as<double>();
+          am.part_i = n->am_i.as<int>();
+          const int ncb = gemv(pro, Ln->w.as<double2>(), Ln->d_out, Ln->d_in, e, &am).ncb;
+          if ((size_t)B * ncb > n->am_v.bytes / sizeof(double)) return fail(ERR_STATE, "argmax partials");
+          *tiles_out = ncb;
+        } else {
+          double2* out = parts[part_next];
+          part_next ^= 1;
+          Epi e;
+          e.mode = EPI_PART;
+          e.out = out;
+          e.err = err;
+          const int pl = gemv(pro, Ln->w.as<double2>(), Ln->d_out, Ln->d_in, e, nullptr).P;
+          pro = part_rows(out, pl, Ln->d_out);
+          pro.bias = Ln->b.as<double2>();
+          width = (int)Ln->d_out;
+        }
+        break;
+      }
+      case K_SOFTMAX: break;
+    }
+  }
+  size_t shm = 0;
+  for (const ROp& op : ops) shm = std::max(shm, resident_op_lds(op));
+  if (shm > RES_MAX_DYN_LDS) return fail(ERR_ARG, "resident decode: %zu bytes of LDS", shm);
+  if (*tiles_out <= 0) return fail(ERR_ARG, "resident decode: no vocab product");
+  *dh_out = dh_k < 0 ? 0 : dh_k;
+  *shm_out = shm;
+  return OK;
+}
+
+// nsteps decode steps of generate in one launch (the step is what
+// enqueue_decode_step enqueues per launch)
+static int run_resident(Net* n, const Spec& sp, uint32_t nsteps) {
+  hipDeviceProp_t prop;
+  HIP_TRY(hipGetDeviceProperties(&prop, n->device));
+  const int grid = prop.multiProcessorCount;
+  // argmax partials: one per row and column block of the vocab product
+  size_t am_elems = 0;
+  for (uint32_t li = 0; li < n->layers.size(); ++li)
+    if (n->layers[li]->kind == K_LINEAR && is_vocab_linear(n, li))
+      am_elems = (size_t)sp.B * resident_gemv_plan(sp.B, n->layers[li]->d_out, n->layers[li]->d_in, false, grid).ncb;
+  TRY(reserve(n, n->am_v, am_elems * sizeof(double)));
+  TRY(reserve(n, n->am_i, am_elems * sizeof(int)));
+  if (n->res_flags.bytes < (size_t)grid * sizeof(uint32_t)) {
+    TRY(reserve(n, n->res_flags, (size_t)grid * sizeof(uint32_t)));
+    HIP_TRY(hipMemsetAsync(n->res_flags.p, 0, n->res_flags.bytes, n->stream));
+    n->res_epoch = 0;
+  }
+  Argmax am = *sp.am;
+  am.part_v = n->am_v.as<double>();
+  am.part_i = n->am_i.as<int>();
+  Spec s2 = sp;
+  s2.am = &am;
+  int dh = 0, tiles = 0;
+  size_t shm = 0;
+  TRY(resident_build(n, s2, grid, &dh, &shm, &tiles));
+  int g2 = 0;
+  TRY(launch_rc(resident_grid(n->device, res_mr(sp.B), dh, shm, &g2), "resident decode (grid)"));
+  if (g2 != grid) return fail(ERR_STATE, "resident decode: grid %d != %d", g2, grid);
+  const size_t ob = n->res_ops_h.size() * sizeof(ROp);
+  TRY(reserve(n, n->res_ops, ob));
+  HIP_TRY(hipMemcpyAsync(n->res_ops.p, n->res_ops_h.data(), ob, hipMemcpyHostToDevice, n->stream));
+  const int nops = (int)n->res_ops_h.size();
+  uint64_t* stamps = nullptr;
+  if (n->res_profile) {
+    TRY(reserve(n, n->res_stamps, ((size_t)nops * nsteps + 1) * sizeof(uint64_t)));
+    stamps = n->res_stamps.as<uint64_t>();
+  }
+  n->res_steps = nsteps;
+  RStep rst;
+  rst.B = sp.B;
+  rst.part_v = am.part_v;
+  rst.part_i = am.part_i;
+  rst.tiles = tiles;
+  rst.ids = am.ids;
+  rst.hist = am.hist;
+  rst.hist_stride = am.hist_stride;
+  rst.hist_cnt = am.hist_cnt;
+  rst.kv_len = am.kv_len;
+  rst.err = n->err_d.as<uint32_t>();
+  TRY(launch_rc(resident_launch(n->stream, n->res_ops.as<ROp>(), nops, (int)nsteps, rst, res_mr(sp.B), dh, shm, grid,
+                                n->res_flags.as<uint32_t>(), n->res_epoch, n->err_d.as<uint32_t>(), stamps),
+                "resident decode"));
+  n->res_epoch += (uint32_t)nops * nsteps;
+  return OK;
+}
+
+// ---------------------------------------------------------------------------
 // session helpers
 // ---------------------------------------------------------------------------
 static int alloc_caches(Net* n, uint32_t B) {
@@ -1457,8 +1794,26 @@ int mitok_generate(mitok_network* n, const uint32_t* prompt, const uint32_t* len
   dec.lens = n->ones_d.as<uint32_t>();
   dec.pos = nullptr;  // RoPE position = kv_len (the fed token's index)
   dec.out_re = n->logits_re.as<double>();
-  bool used_graph = false;
-  if (n_new > 1) {
+  bool used_graph = false, used_resident = false;
+  if (n_new > 1 && n->timing.cls == 0) {
+    Spec rs = dec;
+    Argmax am;
+    am.ids = n->dec_ids_d.as<uint32_t>();
+    am.hist = n->hist_d.as<uint32_t>();
+    am.hist_stride = (int)n_new;
+    am.hist_cnt = n->cnt_d.as<int>();
+    am.kv_len = n->kv_len_d.as<int>();
+    am.advance_kv = 1;
+    am.err = n->err_d.as<uint32_t>();
+    rs.am = &am;
+    rs.hist_re = want_logits ? n->logit_hist_d.as<double>() : nullptr;
+    rs.hist_cnt = n->cnt_d.as<int>();
+    if (resident_ok(n, rs)) {
+      TRY(run_resident(n, rs, n_new - 1));
+      used_resident = true;
+    }
+  }
+  if (n_new > 1 && !used_resident) {
     const bool direct = n->direct_launch || n->timing.cls != 0;
     if (!direct) {
       if (!n->graph || n->graph_B != B || n->graph_nnew != n_new || n->graph_logits != want_logits ||
@@ -1498,8 +1853,16 @@ int mitok_generate(mitok_network* n, const uint32_t* prompt, const uint32_t* len
   for (auto& e : ev) (void)hipEventDestroy(e);
   n->last_t[0] = a;
   n->last_t[1] = b2;
-  n->last_t[2] = used_graph ? 1.0 : 0.0;
+  n->last_t[2] = used_resident ? 2.0 : used_graph ? 1.0 : 0.0;
   collect_timing(n);
+  if (used_resident) {
+    uint32_t e = 0;
+    HIP_TRY(hipMemcpy(&e, n->err_d.p, sizeof e, hipMemcpyDeviceToHost));
+    if (e & EB_BARRIER) {  // the flags no longer follow the epochs: start over
+      HIP_TRY(hipMemset(n->res_flags.p, 0, n->res_flags.bytes));
+      n->res_epoch = 0;
+    }
+  }
   TRY(check_err_word(n));
   for (uint32_t b = 0; b < B; ++b) n->kv_len_h[b] += n_new - 1;
   return OK;
@@ -1557,10 +1920,38 @@ int mitok_set_graph_mode(mitok_network* n, int direct_launch) {
   return OK;
 }
 
-int mitok_set_decode_plan(mitok_network* n, int fused) {
+int mitok_resident_profile(mitok_network* n, int enable, int max_ops, int* nops, int* kinds, double* us) {
   if (!n) return fail(ERR_ARG, "null network");
-  n->fused_decode = fused ? 1 : 0;
-  n->tiled_prefill = fused ? 1 : 0;
+  n->res_profile = enable;
+  if (!nops) return OK;
+  *nops = 0;
+  const int no = (int)n->res_ops_h.size();
+  if (!n->res_stamps.p || !n->res_steps || !no) return OK;
+  const size_t cnt = (size_t)no * n->res_steps + 1;
+  if (n->res_stamps.bytes < cnt * sizeof(uint64_t)) return OK;
+  std::vector<uint64_t> st(cnt);
+  HIP_TRY(hipMemcpy(st.data(), n->res_stamps.p, cnt * sizeof(uint64_t), hipMemcpyDeviceToHost));
+  const int m = std::min(no, max_ops);
+  for (int i = 0; i < m; ++i) {
+    double t = 0.0;
+    for (uint32_t s2 = 0; s2 < n->res_steps; ++s2) {
+      const size_t k = (size_t)s2 * no + i;
+      const uint64_t prev = k == 0 ? st[cnt - 1] : st[k - 1];
+      t += (double)(st[k] - prev) * 0.01;  // 100 MHz clock -> us
+    }
+    if (kinds) kinds[i] = n->res_ops_h[i].kind;
+    if (us) us[i] = t / n->res_steps;
+  }
+  *nops = m;
+  return OK;
+}
+
+int mitok_set_decode_plan(mitok_network* n, int plan) {
+  if (!n) return fail(ERR_ARG, "null network");
+  if (plan < 0 || plan > 3) return fail(ERR_ARG, "decode plan %d (0 to 3)", plan);
+  n->resident = plan == 3 ? 2 : plan == 2 ? 1 : 0;
+  n->fused_decode = plan >= 1 ? 1 : 0;
+  n->tiled_prefill = plan >= 1 ? 1 : 0;
   drop_graph(n);
   return OK;
 }

@@ -1,0 +1,90 @@
+// resident.hip — host side of the resident decode loop (device code in
+// resident.hpp, one kernel instantiation per row count in resident_k<MR>.hip).
+#include <algorithm>
+
+#include "resident.hpp"
+
+namespace mitok {
+
+// kernels of resident_k1/2/4/8.hip for a head dim (64 specialised, others generic)
+const void* resident_kernel_1(int dh);
+const void* resident_kernel_2(int dh);
+const void* resident_kernel_4(int dh);
+const void* resident_kernel_8(int dh);
+
+static const void* pick_kernel(int mr, int dh) {
+  switch (mr) {
+    case 1: return resident_kernel_1(dh);
+    case 2: return resident_kernel_2(dh);
+    case 4: return resident_kernel_4(dh);
+    default: return resident_kernel_8(dh);
+  }
+}
+
+ResGemvPlan resident_gemv_plan(int M, int N, int K, bool part, int grid) {
+  ResGemvPlan p;
+  p.mr = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
+  p.C = 64;
+  for (int c : {8, 16, 32, 64})
+    if (rcdiv(N, c) <= grid) {
+      p.C = c;
+      break;
+    }
+  p.ncb = rcdiv(N, p.C);
+  const int rpw = 64 / p.C;
+  const int P = part ? std::min(8, std::max(1, grid / p.ncb)) : 1;
+  if (p.ncb * P <= grid) {  // one item per block: the prefetched layout if it fits the registers
+    const int kw3 = rcdiv(rcdiv(K, P), 3 * rpw) * rpw;
+    if (kw3 / rpw <= RES_NPF) {
+      p.waves = 3;
+      p.kw = kw3;
+      p.P = rcdiv(K, 3 * kw3);
+      return p;
+    }
+  }
+  p.waves = 4;
+  const int unit = 4 * rpw;
+  p.kw = rcdiv(rcdiv(K, P), unit) * unit / 4;
+  p.P = rcdiv(K, 4 * p.kw);
+  return p;
+}
+
+size_t resident_op_lds(const ROp& op) {
+  const size_t att = op.ro.att.po ? (size_t)op.M * op.ro.att.H * (op.ro.att.nsplit + 1) * sizeof(double) : 0;
+  if (op.kind == ROP_GEMV) {
+    const int mr = op.M <= 1 ? 1 : op.M <= 2 ? 2 : op.M <= 4 ? 4 : 8;
+    const size_t rl = op.ro.ln ? (size_t)op.K : (size_t)op.waves * op.kw;
+    return (size_t)mr * rl * sizeof(double2) + att;
+  }
+  if (op.kind == ROP_ROWS) {
+    const size_t rl = op.ro.ln ? (size_t)op.K : (size_t)std::min(op.cw, op.K);
+    const size_t a1 = op.ro.att.po ? (size_t)op.ro.att.H * (op.ro.att.nsplit + 1) * sizeof(double) : 0;
+    return rl * sizeof(double2) + a1;
+  }
+  return 0;
+}
+
+int resident_grid(int device, int mr, int dh, size_t shm, int* grid) {
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) != hipSuccess) return ERR_HIP;
+  if (!prop.cooperativeLaunch) return ERR_STATE;
+  int occ = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, pick_kernel(mr, dh), 256, shm) != hipSuccess) return ERR_HIP;
+  if (occ < 1) return ERR_STATE;
+  *grid = prop.multiProcessorCount;
+  return OK;
+}
+
+int resident_launch(hipStream_t st, const ROp* ops_d, int nops, int nsteps, const RStep& step, int mr, int dh,
+                    size_t shm, int grid, uint32_t* flags, uint32_t epoch0, uint32_t* err, uint64_t* stamps) {
+  if (nops <= 0 || nsteps <= 0) return OK;
+  if (step.B < 1 || step.B > 8 || step.B > mr) return ERR_ARG;
+  RStep sa = step;
+  void* args[] = {(void*)&ops_d, (void*)&nops, (void*)&nsteps, (void*)&sa, (void*)&flags, (void*)&epoch0, (void*)&err,
+                  (void*)&stamps};
+  if (hipLaunchCooperativeKernel(pick_kernel(mr, dh), dim3(grid), dim3(256), args, (unsigned)shm, st) != hipSuccess)
+    return ERR_HIP;
+  return OK;
+}
+
+}  // namespace mitok

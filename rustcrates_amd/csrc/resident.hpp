@@ -1,0 +1,683 @@
+// resident.hpp — device code of the resident decode loop (resident.hip): the
+// decode loop of mitok_generate for up to 8 sequences as one cooperative
+// launch that stays resident for every step.  Each resident_k<MR>.hip
+// instantiates the kernel for one row count, so the variants compile in
+// parallel.
+//
+// At batch 1 the decode step is a chain of small dependent products (QKV ->
+// attention -> FFN Dense -> FFN Linear per layer, then the vocab product and
+// the greedy id): each moves a few MB of weights, so as separate launches
+// every link pays a launch and a ramp-up and the HBM stream stalls between
+// them.  Here one block per CU runs a program of operations (ROp) for all
+// steps: the blocks share each operation's work items and meet at a grid
+// barrier between operations.  The barrier is a flag per block, each written
+// with a device-coherent store and polled by every block in one load per
+// lane (about 1.2 us for 256 blocks on MI355X, below one kernel boundary).
+//
+// Coherence: the XCDs' L2 caches are not coherent with each other, and an
+// agent-scope fence (L2 write-back + invalidate) measured 18-40 us per
+// barrier.  So every value one block leaves for another inside the launch —
+// activations, split partials, the KV rows appended this step, ids, KV
+// lengths — is stored and loaded at device coherence (COH = true in
+// rowops.hpp / epilogue.hpp, ld_dev / st_dev).  Weights and tables, which
+// nothing writes during the launch, use ordinary cached loads.
+//
+// Operations (the reference operations each restates are cited where the
+// same code serves the launch-per-operation plans):
+//   ROP_GEMV    rowops(x)[M][K] * W[K][N] -> epilogue; a work item is C
+//               columns x one K split (gemm.hip k_gemv's layout)
+//   ROP_ATTN    one key chunk of one (sequence, head) (attention.hip
+//               k_attention_split's layout; the QKV epilogue appended k, v)
+//   ROP_ROWS    materialise rowops(x) for a row or a column chunk of one
+//   ROP_COMBINE the key chunks of one (sequence, head) rescaled to their
+//               common max and summed, plus the residual
+// The step state (KV lengths, the ids being fed, the step count) lives in
+// every block's LDS: each block finds the greedy ids itself from the vocab
+// product's per-tile partials at the start of the next step, so no operation
+// reads a KV length or an id from memory.  Every wave of every block reaches
+// every barrier; a barrier that waits longer than its spin limit sets
+// EB_BARRIER and lets the grid run out.
+#pragma once
+
+#include "epilogue.hpp"
+
+namespace mitok {
+
+__host__ __device__ static inline int rcdiv(long a, long b) { return (int)((a + b - 1) / b); }
+
+// ---- step state and access policy -----------------------------------------
+static __shared__ int res_kvl[8];       // KV length of each sequence before this step's token
+static __shared__ uint32_t res_ids[8];  // the ids fed to this step
+static __shared__ int res_cnt;          // ids generated so far (logits-history slot of this step)
+
+struct AccRes {
+  template <class T>
+  static __device__ __forceinline__ T ld(const T* p) { return ld_dev(p); }
+  template <class T>
+  static __device__ __forceinline__ void st(T* p, T v) { st_dev(p, v); }
+  static __device__ __forceinline__ int kv(const int*, int m) { return res_kvl[m]; }
+  static __device__ __forceinline__ uint32_t id(const uint32_t*, int m) { return res_ids[m]; }
+  static __device__ __forceinline__ int cnt(const int*) { return res_cnt; }
+};
+
+// ---- grid barrier ----------------------------------------------------------
+constexpr uint32_t RES_SPIN_LIMIT = 1u << 22;  // ~several seconds of polling
+
+// `pf` runs in waves 1-3 while wave 0 signals and polls: the weight loads it
+// issues stay in flight through the barrier.  Wave 0 alone polls (a wave's
+// loads complete in order, so a poll would wait for them).
+template <class F>
+__device__ __forceinline__ void grid_barrier(uint32_t* flags, uint32_t epoch, uint32_t* err, F&& pf) {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's coherent stores are acknowledged
+  __syncthreads();
+  if (threadIdx.x >= 64) pf();
+  if (threadIdx.x == 0) st_dev(&flags[blockIdx.x], epoch);
+  if (threadIdx.x < 64 && (ld_dev(err) & EB_BARRIER) == 0) {
+    const int lane = threadIdx.x, nb = gridDim.x;
+    for (uint32_t spin = 0;; ++spin) {
+      bool ok = true;
+      for (int b0 = 0; b0 < nb; b0 += 256) {  // four flags per lane in flight per round
+        uint32_t v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int b = b0 + lane + 64 * j;
+          v[j] = b < nb ? ld_dev(&flags[b]) : epoch;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ok &= (int)(v[j] - epoch) >= 0;
+      }
+      if (__all(ok)) break;
+      if (spin >= RES_SPIN_LIMIT) {
+        if (lane == 0) atomicOr(err, (uint32_t)EB_BARRIER);
+        break;
+      }
+      if ((spin & 255u) == 255u && (ld_dev(err) & EB_BARRIER)) break;  // another block gave up: run out
+    }
+  }
+  __syncthreads();
+}
+
+// ---- ROP_GEMV --------------------------------------------------------------
+// Two layouts.  Streaming (waves == 4): lane (r, c) = (lane / C, lane % C) of
+// wave w reads rows k0 + r + u*RPW of column n; 16 weight loads per lane are
+// in flight before the prologue and the loop keeps 8-16 in flight (outputs
+// wider than the grid, e.g. the vocab product).  Prefetched (waves == 3): an
+// item is at most RES_NPF loads per lane of waves 1-3, issued during the
+// previous operation's barrier (gemv_weights), so the weights are in
+// registers when the inputs become visible; wave 0 polls the barrier and owns
+// the epilogue.
+constexpr int RES_NPF = 24;
+
+template <int C>
+__device__ __forceinline__ void gemv_weights(const ROp& op, int item, double2 (&w)[RES_NPF]) {
+  constexpr int RPW = 64 / C;
+  const int lane = threadIdx.x & 63, cwv = (threadIdx.x >> 6) - 1;
+  const int r = lane / C, c = lane - (lane / C) * C;
+  const int bx = item % op.ncb, by = item / op.ncb;
+  const int k0 = by * 3 * op.kw + cwv * op.kw;
+  const int n = bx * C + c;
+  const int kmax = max(0, min(op.kw, op.K - k0));
+  const int nu = (n < op.N && kmax > r) ? (kmax - r + RPW - 1) / RPW : 0;
+  const double2* wp = op.W + (long)(k0 + r) * op.ldw + n;
+  const long wstep = (long)RPW * op.ldw;
+#pragma unroll
+  for (int u = 0; u < RES_NPF; ++u) w[u] = u < nu ? wp[u * wstep] : make_double2(0.0, 0.0);
+}
+
+template <int MR, int C>
+__device__ __forceinline__ void r_gemv3(const ROp& op, int item, double2* lds2, double2* red, double2* st_mean,
+                                        double2* st_sd, double2 (&w)[RES_NPF], bool have) {
+  constexpr int RPW = 64 / C;
+  const RowOps& ro = op.ro;
+  const int M = op.M, N = op.N, K = op.K, kw = op.kw;
+  const int bx = item % op.ncb, by = item / op.ncb;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane / C, c = lane - (lane / C) * C;
+  const int KB = 3 * kw;
+  const int kb0 = by * KB;
+  const int n = bx * C + c;
+  const bool col_ok = n < N;
+  if (!have && wave >= 1) gemv_weights<C>(op, item, w);
+  const int ka = ro.ln ? 0 : kb0, RL = ro.ln ? K : KB;
+  RoLds L;
+  L.wts = (double*)(lds2 + MR * RL);
+  L.lsum = L.wts + (ro.att.po ? (size_t)M * ro.att.H * ro.att.nsplit : 0);
+  L.m0 = 0;
+  ro_prepare<AccRes>(ro, M, L);
+  ro_build<MR, AccRes>(ro, M, K, ka, RL, kb0, min(K, kb0 + KB), lds2, L, st_mean, st_sd);
+  if (bx == 0 && by == 0 && tid < M) ro_check<AccRes>(ro, tid);
+  const double2* xs = lds2 + (kb0 - ka);
+  if (ro.save && bx == 0)
+    for (int i = tid; i < MR * KB; i += 256) {
+      const int m = i / KB, k = kb0 + (i - m * KB);
+      if (m < M && k < K) st_dev(ro.save + (long)m * ro.ldsave + k, xs[m * RL + (k - kb0)]);
+    }
+  double2 acc[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) acc[m] = make_double2(0.0, 0.0);
+  if (wave >= 1 && col_ok) {
+    const int k0 = kb0 + (wave - 1) * kw;
+    const int kmax = max(0, min(kw, K - k0));
+    const int nu = kmax > r ? (kmax - r + RPW - 1) / RPW : 0;
+    const double2* xw = xs + (wave - 1) * kw + r;
+#pragma unroll
+    for (int u = 0; u < RES_NPF; ++u)
+      if (u < nu)
+#pragma unroll
+        for (int m = 0; m < MR; ++m) acc[m] = cadd(acc[m], cmul(xw[m * RL + u * RPW], w[u]));
+  }
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    acc[m].x = col_sum<C>(acc[m].x);
+    acc[m].y = col_sum<C>(acc[m].y);
+  }
+  if (wave > 0 && lane < C)
+#pragma unroll
+    for (int m = 0; m < MR; ++m) red[((wave - 1) * MR + m) * C + lane] = acc[m];
+  __syncthreads();
+  const bool owner = wave == 0 && lane < C;
+  if (owner)
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+      acc[m] = cadd(cadd(red[(0 * MR + m) * C + lane], red[(1 * MR + m) * C + lane]), red[(2 * MR + m) * C + lane]);
+  const Epi& ep = op.ep;
+  if (ep.mode == EPI_PART) {
+    if (owner && col_ok)
+#pragma unroll
+      for (int m = 0; m < MR; ++m)
+        if (m < M) st_dev(ep.out + ((long)by * M + m) * N + n, acc[m]);
+  } else {
+    double re[MR];
+    if (owner && col_ok)
+#pragma unroll
+      for (int m = 0; m < MR; ++m)
+        if (m < M) re[m] = apply_epi<AccRes>(ep, M, N, m, n, acc[m]);
+    const Argmax& am = op.am;
+    if (am.part_v && wave == 0)
+#pragma unroll
+      for (int m = 0; m < MR; ++m)
+        if (m < M) {
+          double bv = -INFINITY;
+          int bi = -1;
+          if (lane < C && col_ok) {
+            if (isnan(re[m])) atomicOr(am.err, (uint32_t)EB_ARGMAX_NAN);
+            else bv = re[m], bi = n;
+          }
+          wave_argmax(bv, bi);
+          if (lane == 0) {
+            st_dev(am.part_v + (long)m * op.ncb + bx, bv);
+            st_dev(am.part_i + (long)m * op.ncb + bx, bi);
+          }
+        }
+  }
+  __syncthreads();
+}
+
+template <int MR, int C>
+__device__ __forceinline__ void r_gemv4(const ROp& op, int item, double2* lds2, double2* red, double2* st_mean, double2* st_sd) {
+  constexpr int RPW = 64 / C;
+  const RowOps& ro = op.ro;
+  const int M = op.M, N = op.N, K = op.K, kw = op.kw;
+  const int bx = item % op.ncb, by = item / op.ncb;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane / C, c = lane - (lane / C) * C;
+  const int KB = 4 * kw;
+  const int kb0 = by * KB;
+  const int n = bx * C + c;
+  const bool col_ok = n < N;
+  const int k0 = kb0 + wave * kw;
+  const int kmax = max(0, min(kw, K - k0));
+  const int nu = kmax > r ? (kmax - r + RPW - 1) / RPW : 0;
+  const double2* wp = op.W + (long)(k0 + r) * op.ldw + n;
+  const long wstep = (long)RPW * op.ldw;
+  const int ka = ro.ln ? 0 : kb0, RL = ro.ln ? K : KB;
+  RoLds L;
+  L.wts = (double*)(lds2 + MR * RL);
+  L.lsum = L.wts + (ro.att.po ? (size_t)M * ro.att.H * ro.att.nsplit : 0);
+  L.m0 = 0;
+
+  double2 w0[8], w1[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) w0[u] = (col_ok && u < nu) ? wp[u * wstep] : make_double2(0.0, 0.0);
+#pragma unroll
+  for (int u = 0; u < 8; ++u) w1[u] = (col_ok && 8 + u < nu) ? wp[(8 + u) * wstep] : make_double2(0.0, 0.0);
+
+  ro_prepare<AccRes>(ro, M, L);
+  ro_build<MR, AccRes>(ro, M, K, ka, RL, kb0, min(K, kb0 + KB), lds2, L, st_mean, st_sd);
+  if (bx == 0 && by == 0 && tid < M) ro_check<AccRes>(ro, tid);
+  const double2* xs = lds2 + (kb0 - ka);
+  if (ro.save && bx == 0)
+    for (int i = tid; i < MR * KB; i += 256) {
+      const int m = i / KB, k = kb0 + (i - m * KB);
+      if (m < M && k < K) st_dev(ro.save + (long)m * ro.ldsave + k, xs[m * RL + (k - kb0)]);
+    }
+
+  double2 acc[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) acc[m] = make_double2(0.0, 0.0);
+  if (col_ok) {
+    const double2* xw = xs + wave * kw + r;  // row u of this lane: xw[m * RL + u * RPW]
+    for (int u0 = 0; u0 < nu; u0 += 16) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (u0 + u < nu)
+#pragma unroll
+          for (int m = 0; m < MR; ++m) acc[m] = cadd(acc[m], cmul(xw[m * RL + (u0 + u) * RPW], w0[u]));
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (u0 + 16 + u < nu) w0[u] = wp[(u0 + 16 + u) * wstep];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (u0 + 8 + u < nu)
+#pragma unroll
+          for (int m = 0; m < MR; ++m) acc[m] = cadd(acc[m], cmul(xw[m * RL + (u0 + 8 + u) * RPW], w1[u]));
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (u0 + 24 + u < nu) w1[u] = wp[(u0 + 24 + u) * wstep];
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    acc[m].x = col_sum<C>(acc[m].x);
+    acc[m].y = col_sum<C>(acc[m].y);
+  }
+  if (wave > 0 && lane < C)
+#pragma unroll
+    for (int m = 0; m < MR; ++m) red[((wave - 1) * MR + m) * C + lane] = acc[m];
+  __syncthreads();
+  const bool owner = wave == 0 && lane < C;
+  if (owner)
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+      acc[m] = cadd(cadd(cadd(acc[m], red[(0 * MR + m) * C + lane]), red[(1 * MR + m) * C + lane]),
+                    red[(2 * MR + m) * C + lane]);
+  const Epi& ep = op.ep;
+  if (ep.mode == EPI_PART) {
+    if (owner && col_ok)
+#pragma unroll
+      for (int m = 0; m < MR; ++m)
+        if (m < M) st_dev(ep.out + ((long)by * M + m) * N + n, acc[m]);
+  } else {
+    double re[MR];
+    if (owner && col_ok)
+#pragma unroll
+      for (int m = 0; m < MR; ++m)
+        if (m < M) re[m] = apply_epi<AccRes>(ep, M, N, m, n, acc[m]);
+    const Argmax& am = op.am;
+    if (am.part_v && wave == 0)
+#pragma unroll
+      for (int m = 0; m < MR; ++m)
+        if (m < M) {
+          double bv = -INFINITY;
+          int bi = -1;
+          if (lane < C && col_ok) {
+            if (isnan(re[m])) atomicOr(am.err, (uint32_t)EB_ARGMAX_NAN);
+            else bv = re[m], bi = n;
+          }
+          wave_argmax(bv, bi);
+          if (lane == 0) {
+            st_dev(am.part_v + (long)m * op.ncb + bx, bv);
+            st_dev(am.part_i + (long)m * op.ncb + bx, bi);
+          }
+        }
+  }
+  __syncthreads();  // LDS (rows, red) is reused by the next item
+}
+
+// ---- ROP_ATTN --------------------------------------------------------------
+// One chunk of CH <= 32 keys of sequence b, head h (masked_attention_head.rs:
+// 184-208 with the cache, bias_pos row 0, no causal mask): scores, the
+// chunk's max m and sum l of exp(s - m), and o = sum exp(s - m) v.  The new
+// token's k and v were appended by the QKV epilogue of this step.  Keys,
+// values, bias and q are all requested before the first is used.
+template <int DH>
+__device__ __forceinline__ void r_attn(const ROp& op, int item) {
+  constexpr int MAXC = 32;
+  __shared__ double sc[MAXC];
+  __shared__ double2 pv[256];
+  __shared__ double2 qs[256];
+  __shared__ double stat[2];
+  const Attn& a = op.a;
+  const AttnSplit& o = op.o;
+  const int dh = DH > 0 ? DH : a.dh;
+  const int split = item % o.nsplit, h = (item / o.nsplit) % a.H, b = item / (o.nsplit * a.H);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int T = res_kvl[b] + 1;
+  const int CH = o.CH;
+  const int c0 = split * CH;
+  if (c0 >= T) return;  // uniform over the block
+  const int nc = min(CH, T - c0);
+  const long bh = (long)b * a.H + h;
+  const double2* K = a.kc + bh * a.ctx * dh;
+  const double2* V = a.vc + bh * a.ctx * dh;
+  const double* bias0 = a.bias_re + (long)h * a.mc * a.mc;
+  constexpr int LPK = 16;
+  const int sub = lane & (LPK - 1), kq = lane / LPK;
+  constexpr int NP = MAXC / 16;
+  constexpr int EPL = DH > 0 ? (DH + LPK - 1) / LPK : 1;
+  const int G = 256 / dh;
+  const int e = tid % dh, g = tid / dh;
+  constexpr int VG = 256 / (DH > 0 ? DH : 256);
+  constexpr int VU = DH > 0 ? (MAXC + VG - 1) / VG : 1;
+  double2 kv[NP][EPL];
+  double bj[NP];
+  double2 vv[VU];
+  if (DH > 0) {
+#pragma unroll
+    for (int pass = 0; pass < NP; ++pass) {
+      const int j = pass * 16 + wave * 4 + kq;
+      const double2* kr = K + (long)(c0 + j) * dh;
+#pragma unroll
+      for (int t = 0; t < EPL; ++t) {
+        const int ee = sub + t * LPK;
+        kv[pass][t] = (j < nc && ee < dh) ? ld_dev(kr + ee) : make_double2(0.0, 0.0);
+      }
+      bj[pass] = (j < nc && sub == 0) ? bias0[c0 + j] : 0.0;
+    }
+#pragma unroll
+    for (int u = 0; u < VU; ++u) {
+      const int j = g + u * G;
+      vv[u] = (g < G && j < nc) ? ld_dev(V + (long)(c0 + j) * dh + e) : make_double2(0.0, 0.0);
+    }
+  }
+  for (int ee = tid; ee < dh; ee += 256) qs[ee] = ld_dev(op.q + (long)b * op.ldq + (long)h * dh + ee);
+  __syncthreads();
+  if (DH > 0) {
+#pragma unroll
+    for (int pass = 0; pass < NP; ++pass) {
+      const int j = pass * 16 + wave * 4 + kq;
+      double acc = 0.0;
+#pragma unroll
+      for (int t = 0; t < EPL; ++t) {
+        const int ee = sub + t * LPK;
+        if (ee < dh) acc += qs[ee].x * kv[pass][t].x - qs[ee].y * kv[pass][t].y;
+      }
+      acc = row16_sum(acc);  // the 16 lanes of key j
+      if (j < nc && sub == 0) sc[j] = acc * a.scale + bj[pass];
+    }
+  } else {
+    for (int j0 = 0; j0 < nc; j0 += 16) {
+      const int j = j0 + wave * 4 + kq;
+      double acc = 0.0;
+      if (j < nc) {
+        const double2* kr = K + (long)(c0 + j) * dh;
+        for (int ee = sub; ee < dh; ee += LPK) {
+          const double2 k2 = ld_dev(kr + ee), qv = qs[ee];
+          acc += qv.x * k2.x - qv.y * k2.y;
+        }
+      }
+      acc = row16_sum(acc);  // the 16 lanes of key j
+      if (j < nc && sub == 0) sc[j] = acc * a.scale + bias0[c0 + j];
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const double s = lane < nc ? sc[lane] : -INFINITY;
+    const double m = wave_max(s);
+    const double p = lane < nc ? exp(s - m) : 0.0;
+    const double l = wave_sum(p);
+    if (lane < nc) sc[lane] = p;
+    if (lane == 0) stat[0] = m, stat[1] = l;
+  }
+  __syncthreads();
+  double2 acc = make_double2(0.0, 0.0);
+  if (DH > 0) {
+#pragma unroll
+    for (int u = 0; u < VU; ++u) {
+      const int j = g + u * G;
+      if (g < G && j < nc) {
+        const double p = sc[j];
+        acc.x += p * vv[u].x;
+        acc.y += p * vv[u].y;
+      }
+    }
+  } else if (g < G) {
+    for (int j = g; j < nc; j += G) {
+      const double p = sc[j];
+      const double2 v = ld_dev(V + (long)(c0 + j) * dh + e);
+      acc.x += p * v.x;
+      acc.y += p * v.y;
+    }
+  }
+  pv[tid] = acc;
+  __syncthreads();
+  const long pidx = bh * o.nsplit + split;
+  if (tid < dh) {
+    double2 s = pv[tid];
+    for (int gg = 1; gg < G; ++gg) s = cadd(s, pv[gg * dh + tid]);
+    st_dev((double2*)o.po + pidx * dh + tid, s);
+  }
+  if (tid == 0) {
+    st_dev((double*)o.pm + pidx, stat[0]);
+    st_dev((double*)o.pl + pidx, stat[1]);
+  }
+  __syncthreads();  // LDS reuse by the next item
+}
+
+// ---- ROP_COMBINE -------------------------------------------------------------
+// Item (b, h): out = Re(sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M) + resid)
+// over the ns chunks of the sequence (the split form of the softmax-weighted
+// sum, masked_attention_head.rs:201-208, then add_matrix_3d_c, utils/matrix.rs:
+// 600-613).  Thread (g, e) takes chunks g, g + G, ...; every load of the item
+// is requested before the first is used.
+__device__ __forceinline__ void r_combine(const ROp& op, int item) {
+  constexpr int UPT = 16;  // chunks per thread kept in flight (ns <= 256, G >= 1)
+  __shared__ double cw_s[256];
+  __shared__ double2 part_s[256];
+  __shared__ double red_s[8];
+  const Attn& a = op.a;
+  const AttnSplit& o = op.o;
+  const int dh = a.dh, H = a.H;
+  const int b = item / H, h = item - b * H;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int T = res_kvl[b] + 1;
+  const int ns = (T + o.CH - 1) / o.CH;
+  const long base = ((long)b * H + h) * o.nsplit;
+  const int G = 256 / dh;
+  const int e = tid % dh, g = tid / dh;
+  const bool act = g < G;
+  double2 po[UPT];
+#pragma unroll
+  for (int u = 0; u < UPT; ++u) {
+    const int sidx = g + u * G;
+    po[u] = (act && sidx < ns) ? ld_dev(o.po + (base + sidx) * dh + e) : make_double2(0.0, 0.0);
+  }
+  const double pm = tid < ns ? ld_dev(o.pm + base + tid) : -INFINITY;
+  const double pl = tid < ns ? ld_dev(o.pl + base + tid) : 0.0;
+  const long col = (long)h * dh + e;
+  const double rres = (g == 0 && op.ro.resid) ? ld_dev(op.ro.resid + (long)b * op.ro.ldr + col).x : 0.0;
+  // common max and chunk weights
+  double mx = wave_max(pm);
+  if (lane == 0) red_s[wave] = mx;
+  __syncthreads();
+  mx = fmax(fmax(red_s[0], red_s[1]), fmax(red_s[2], red_s[3]));
+  const double w = tid < ns ? exp(pm - mx) : 0.0;
+  cw_s[tid] = w;
+  double l = wave_sum(pl * w);
+  __syncthreads();  // red_s reuse, cw_s complete
+  if (lane == 0) red_s[4 + wave] = l;
+  double2 acc = make_double2(0.0, 0.0);
+#pragma unroll
+  for (int u = 0; u < UPT; ++u) {
+    const int sidx = g + u * G;
+    if (act && sidx < ns) {
+      const double ww = cw_s[sidx];
+      acc.x += po[u].x * ww;
+      acc.y += po[u].y * ww;
+    }
+  }
+  for (int sidx = g + UPT * G; act && sidx < ns; sidx += G) {  // beyond UPT chunks per thread
+    const double2 v = ld_dev(o.po + (base + sidx) * dh + e);
+    const double ww = cw_s[sidx];
+    acc.x += v.x * ww;
+    acc.y += v.y * ww;
+  }
+  part_s[tid] = acc;
+  __syncthreads();
+  if (tid < dh) {
+    const double lsum = (red_s[4] + red_s[5]) + (red_s[6] + red_s[7]);
+    double2 sum = part_s[tid];
+    for (int gg = 1; gg < G; ++gg) sum = cadd(sum, part_s[gg * dh + tid]);
+    st_dev(op.out + (long)b * op.ldo + col, make_double2(sum.x / lsum + rres, 0.0));
+  }
+  __syncthreads();
+}
+
+// ---- ROP_ROWS --------------------------------------------------------------
+__device__ __forceinline__ void r_rows(const ROp& op, int item, double2* lds2, double2* st_mean, double2* st_sd) {
+  const RowOps& ro = op.ro;
+  const int K = op.K;
+  const int nch = ro.ln ? 1 : rcdiv(K, op.cw);
+  const int m = item / nch, ch = item - m * nch;
+  const int k0 = ro.ln ? 0 : ch * op.cw, k1 = ro.ln ? K : min(K, k0 + op.cw);
+  const int RL = k1 - k0;
+  RoLds L;
+  L.wts = (double*)(lds2 + RL);
+  L.lsum = L.wts + (ro.att.po ? (size_t)ro.att.H * ro.att.nsplit : 0);
+  L.m0 = m;
+  ro_prepare<AccRes>(ro, 1, L);
+  ro_build<1, AccRes>(ro, 1, K, k0, RL, k0, k1, lds2, L, st_mean, st_sd);
+  if (ch == 0 && threadIdx.x == 0) ro_check<AccRes>(ro, m);
+  for (int k = k0 + threadIdx.x; k < k1; k += 256) {
+    const double2 v = lds2[k - k0];
+    st_dev(op.out + (long)m * op.ldo + k, v);
+    if (ro.save) st_dev(ro.save + (long)m * ro.ldsave + k, v);
+  }
+  __syncthreads();
+}
+
+// ---- greedy ids of the previous step (sampling_methods.rs:5-18) -------------
+// Every block reduces the vocab product's per-tile (max, last index) partials
+// of each row (ties to the larger index) and advances its step state; block 0
+// writes ids, history, counts and KV lengths back for the host.
+__device__ __forceinline__ void step_argmax(const RStep& st, bool write) {
+  constexpr int U = 16;
+  __shared__ double sv[4][8];
+  __shared__ int si[4][8];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int B = st.B, tiles = st.tiles, tot = B * tiles;
+  double bv[8];
+  int bi[8];
+#pragma unroll
+  for (int m = 0; m < 8; ++m) bv[m] = -INFINITY, bi[m] = -1;
+  for (int i0 = 0; i0 < tot; i0 += 256 * U) {
+    double v[U];
+    int ix[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = i0 + tid + 256 * u;
+      v[u] = i < tot ? ld_dev(st.part_v + i) : -INFINITY;
+      ix[u] = i < tot ? ld_dev(st.part_i + i) : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = i0 + tid + 256 * u;
+      const int row = i < tot ? i / tiles : 8;
+#pragma unroll
+      for (int m = 0; m < 8; ++m)
+        if (row == m) argmax_combine(bv[m], bi[m], v[u], ix[u]);
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    if (m >= B) break;
+    wave_argmax(bv[m], bi[m]);
+    if (lane == 0) sv[wave][m] = bv[m], si[wave][m] = bi[m];
+  }
+  __syncthreads();
+  if (tid < B) {
+    const int m = tid;
+    double v = sv[0][m];
+    int id = si[0][m];
+    for (int w = 1; w < 4; ++w) argmax_combine(v, id, sv[w][m], si[w][m]);
+    if (id < 0) {  // every logit was NaN (the reference panics)
+      atomicOr(st.err, (uint32_t)EB_ARGMAX_NAN);
+      id = 0;
+    }
+    const int t = res_cnt;
+    res_ids[m] = (uint32_t)id;
+    res_kvl[m] += 1;
+    if (write) {
+      st_dev(st.ids + m, (uint32_t)id);
+      st_dev(st.hist + (long)m * st.hist_stride + t, (uint32_t)id);
+      st_dev(st.hist_cnt + m, t + 1);
+      st_dev(st.kv_len + m, res_kvl[m]);
+    }
+  }
+  __syncthreads();
+  if (tid == 0) res_cnt += 1;
+  __syncthreads();
+}
+
+// ---- the resident kernel -----------------------------------------------------
+template <int MR>
+__device__ __forceinline__ void run_gemv(const ROp& op, int it, double2* lds2, double2* red, double2* st_mean,
+                                         double2* st_sd, double2 (&w)[RES_NPF], bool have) {
+  if (op.waves == 3) {
+    switch (op.C) {
+      case 8: r_gemv3<MR, 8>(op, it, lds2, red, st_mean, st_sd, w, have); break;
+      case 16: r_gemv3<MR, 16>(op, it, lds2, red, st_mean, st_sd, w, have); break;
+      case 32: r_gemv3<MR, 32>(op, it, lds2, red, st_mean, st_sd, w, have); break;
+      default: r_gemv3<MR, 64>(op, it, lds2, red, st_mean, st_sd, w, have); break;
+    }
+    return;
+  }
+  switch (op.C) {
+    case 8: r_gemv4<MR, 8>(op, it, lds2, red, st_mean, st_sd); break;
+    case 16: r_gemv4<MR, 16>(op, it, lds2, red, st_mean, st_sd); break;
+    case 32: r_gemv4<MR, 32>(op, it, lds2, red, st_mean, st_sd); break;
+    default: r_gemv4<MR, 64>(op, it, lds2, red, st_mean, st_sd); break;
+  }
+}
+
+template <int MR, int DH>
+__global__ __launch_bounds__(256) void k_resident(const ROp* __restrict__ ops, int nops, int nsteps, RStep step,
+                                                  uint32_t* flags, uint32_t epoch0, uint32_t* err,
+                                                  uint64_t* stamps) {
+  extern __shared__ double2 lds2[];
+  __shared__ double2 red[3 * MR * 64];
+  __shared__ double2 st_mean[MR], st_sd[MR];
+  if (stamps && blockIdx.x == 0 && threadIdx.x == 0) stamps[(long)nsteps * nops] = wall_clock64();
+  if (threadIdx.x < step.B) {
+    res_kvl[threadIdx.x] = ld_dev(step.kv_len + threadIdx.x);
+    res_ids[threadIdx.x] = ld_dev(step.ids + threadIdx.x);
+  }
+  if (threadIdx.x == 0) res_cnt = ld_dev(step.hist_cnt);
+  __syncthreads();
+  double2 wpf[RES_NPF];  // the next product's weights (waves 1-3)
+  bool have = false;
+  uint32_t epoch = epoch0;
+  for (int s = 0; s < nsteps; ++s) {
+    if (s > 0) step_argmax(step, blockIdx.x == 0);
+    for (int i = 0; i < nops; ++i) {
+      const ROp& op = ops[i];
+      for (int it = blockIdx.x; it < op.items; it += gridDim.x) {
+        switch (op.kind) {
+          case ROP_GEMV: run_gemv<MR>(op, it, lds2, red, st_mean, st_sd, wpf, have && it == (int)blockIdx.x); break;
+          case ROP_ATTN: r_attn<DH>(op, it); break;
+          case ROP_COMBINE: r_combine(op, it); break;
+          default: r_rows(op, it, lds2, st_mean, st_sd); break;
+        }
+      }
+      // the next operation (the next step's first after the last); a
+      // prefetched product has at most one item per block
+      const bool last = s + 1 == nsteps && i + 1 == nops;
+      const ROp& nx = ops[i + 1 < nops ? i + 1 : 0];
+      const bool pf = !last && nx.kind == ROP_GEMV && nx.waves == 3 && (int)blockIdx.x < nx.items;
+      grid_barrier(flags, ++epoch, err, [&]() {
+        if (!pf) return;
+        switch (nx.C) {
+          case 8: gemv_weights<8>(nx, blockIdx.x, wpf); break;
+          case 16: gemv_weights<16>(nx, blockIdx.x, wpf); break;
+          case 32: gemv_weights<32>(nx, blockIdx.x, wpf); break;
+          default: gemv_weights<64>(nx, blockIdx.x, wpf); break;
+        }
+      });
+      have = pf;
+      if (stamps && blockIdx.x == 0 && threadIdx.x == 0) stamps[(long)s * nops + i] = wall_clock64();
+    }
+  }
+  if (blockIdx.x == 0) step_argmax(step, true);
+}
+
+}  // namespace mitok

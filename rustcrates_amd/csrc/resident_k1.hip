@@ -1,0 +1,11 @@
+// resident_k1.hip — the resident decode kernel for up to 1 sequence(s)
+// (resident.hpp); head dim 64 specialised, others generic.
+#include "resident.hpp"
+
+namespace mitok {
+
+const void* resident_kernel_1(int dh) {
+  return dh == 64 ? (const void*)k_resident<1, 64> : (const void*)k_resident<1, 0>;
+}
+
+}  // namespace mitok

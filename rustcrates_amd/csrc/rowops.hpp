@@ -29,23 +29,24 @@ __device__ __forceinline__ size_t ro_lds_doubles(const RowOps& r, int M) {
 }
 
 // Block-wide; all threads call it.  One wave per (row, head).
+template <class Acc = AccPlain>
 __device__ inline void ro_prepare(const RowOps& r, int M, const RoLds& L) {
   if (!r.att.po) return;
   const AttnSplit& a = r.att;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   for (int mh = wave; mh < M * a.H; mh += 4) {
     const int lm = mh / a.H, h = mh - lm * a.H;
-    const int T = a.kv_len[L.m0 + lm] + 1;
+    const int T = Acc::kv(a.kv_len, L.m0 + lm) + 1;
     const int ns = (T + a.CH - 1) / a.CH;
     const long base = ((long)(L.m0 + lm) * a.H + h) * a.nsplit;
     double mx = -INFINITY;
-    for (int s = lane; s < ns; s += 64) mx = fmax(mx, a.pm[base + s]);
+    for (int s = lane; s < ns; s += 64) mx = fmax(mx, Acc::ld(a.pm + base + s));
     mx = wave_max(mx);
     double l = 0.0;
     for (int s = lane; s < ns; s += 64) {
-      const double w = exp(a.pm[base + s] - mx);
+      const double w = exp(Acc::ld(a.pm + base + s) - mx);
       L.wts[(long)mh * a.nsplit + s] = w;
-      l += a.pl[base + s] * w;
+      l += Acc::ld(a.pl + base + s) * w;
     }
     l = wave_sum(l);
     if (lane == 0) L.lsum[mh] = l;
@@ -55,17 +56,18 @@ __device__ inline void ro_prepare(const RowOps& r, int M, const RoLds& L) {
 
 // source element (m global row) + bias -> finite check -> GELU.  Loads of
 // partials and attention chunks are unrolled by 8 so they are in flight together.
+template <class Acc = AccPlain>
 __device__ __forceinline__ double2 ro_base(const RowOps& r, int m, int k, int K, const RoLds& L) {
   double2 v;
   if (r.table) {
-    const uint32_t id = r.ids[m];
+    const uint32_t id = Acc::id(r.ids, m);
     if (id == 1u || id >= (uint32_t)r.vocab) v = make_double2(0.0, 0.0);  // PAD; bad ids flagged by ro_check
     else v = r.table[(long)id * K + k];
   } else if (r.att.po) {
     const AttnSplit& a = r.att;
     const int h = k / a.dh, e = k - h * a.dh;
     const int lm = m - L.m0;
-    const int T = a.kv_len[m] + 1;
+    const int T = Acc::kv(a.kv_len, m) + 1;
     const int ns = (T + a.CH - 1) / a.CH;
     const long base = ((long)m * a.H + h) * a.nsplit;
     const double* w = L.wts + ((long)lm * a.H + h) * a.nsplit;
@@ -73,7 +75,7 @@ __device__ __forceinline__ double2 ro_base(const RowOps& r, int m, int k, int K,
     for (int s0 = 0; s0 < ns; s0 += 8) {
       double2 t[8];
 #pragma unroll
-      for (int q = 0; q < 8; ++q) t[q] = s0 + q < ns ? a.po[(base + s0 + q) * a.dh + e] : make_double2(0.0, 0.0);
+      for (int q = 0; q < 8; ++q) t[q] = s0 + q < ns ? Acc::ld(a.po + (base + s0 + q) * a.dh + e) : make_double2(0.0, 0.0);
 #pragma unroll
       for (int q = 0; q < 8; ++q)
         if (s0 + q < ns) {
@@ -86,11 +88,11 @@ __device__ __forceinline__ double2 ro_base(const RowOps& r, int m, int k, int K,
   } else {
     const double2* p = r.x + (long)m * r.ldx + k;
     if (r.npart <= 1) {
-      v = p[0];
+      v = Acc::ld(p);
     } else {
       double2 t[8];  // npart <= 8 (the GEMV splits at most 8 ways)
 #pragma unroll
-      for (int q = 0; q < 8; ++q) t[q] = q < r.npart ? p[q * r.part_stride] : make_double2(0.0, 0.0);
+      for (int q = 0; q < 8; ++q) t[q] = q < r.npart ? Acc::ld(p + q * r.part_stride) : make_double2(0.0, 0.0);
       v = t[0];
 #pragma unroll
       for (int q = 1; q < 8; ++q)
@@ -112,25 +114,31 @@ __device__ __forceinline__ double2 ro_base(const RowOps& r, int m, int k, int K,
 }
 
 // with RoPE: pairs (2i, 2i+1) rotate by the tabulated angle of the row's position
+template <class Acc = AccPlain>
 __device__ __forceinline__ double2 ro_source(const RowOps& r, int m, int k, int K, const RoLds& L) {
-  if (!r.rope_cs) return ro_base(r, m, k, K, L);
-  const int p = min(r.rope_pos[m], r.rope_max - 1);  // overflow flagged by ro_check
+  if (!r.rope_cs) return ro_base<Acc>(r, m, k, K, L);
+  const int p = min(Acc::kv(r.rope_pos, m), r.rope_max - 1);  // overflow flagged by ro_check
   const int i = k >> 1;
   const double2 t = r.rope_cs[(long)p * (K >> 1) + i];
-  const double2 e = ro_base(r, m, 2 * i, K, L), o = ro_base(r, m, 2 * i + 1, K, L);
+  const double2 e = ro_base<Acc>(r, m, 2 * i, K, L), o = ro_base<Acc>(r, m, 2 * i + 1, K, L);
   return (k & 1) ? make_double2(e.x * t.y + o.x * t.x, e.y * t.y + o.y * t.x)
                  : make_double2(e.x * t.x - o.x * t.y, e.y * t.x - o.y * t.y);
 }
 
+template <class Acc = AccPlain>
 __device__ __forceinline__ double2 ro_value(const RowOps& r, int m, int k, int K, const RoLds& L) {
-  double2 v = ro_source(r, m, k, K, L);
-  if (r.resid) v = make_double2(v.x + r.resid[(long)m * r.ldr + k].x, 0.0);
+  double2 v = ro_source<Acc>(r, m, k, K, L);
+  if (r.resid) v = make_double2(v.x + Acc::ld(r.resid + (long)m * r.ldr + k).x, 0.0);
   return v;
 }
 
+template <class Acc = AccPlain>
 __device__ __forceinline__ void ro_check(const RowOps& r, int m) {
-  if (r.table && r.ids[m] != 1u && r.ids[m] >= (uint32_t)r.vocab) atomicOr(r.err, (uint32_t)EB_BAD_TOKEN);
-  if (r.rope_cs && r.rope_pos[m] >= r.rope_max) atomicOr(r.err, (uint32_t)EB_CTX_OVERFLOW);
+  if (r.table) {
+    const uint32_t id = Acc::id(r.ids, m);
+    if (id != 1u && id >= (uint32_t)r.vocab) atomicOr(r.err, (uint32_t)EB_BAD_TOKEN);
+  }
+  if (r.rope_cs && Acc::kv(r.rope_pos, m) >= r.rope_max) atomicOr(r.err, (uint32_t)EB_CTX_OVERFLOW);
 }
 
 // normalize (norm_layer.rs:77): Re(((x - mean) / sd) * gamma + beta) + 0i
@@ -142,7 +150,7 @@ __device__ __forceinline__ double2 ln_apply(double2 v, double2 mean, double2 sd,
 // LayerNorm statistics of rows L.m0 .. L.m0+M-1 (M <= MR) over K elements:
 // mean = sum(x) / K, var = sum((x - mean)^2) / K (complex square),
 // sd = csqrt(var + eps) (norm_layer.rs:64-80).  Block-wide; all threads call it.
-template <int MR>
+template <int MR, class Acc = AccPlain>
 __device__ void ro_stats(const RowOps& r, int M, int K, const RoLds& L, double2* mean_s, double2* sd_s) {
   __shared__ double red_s[4][2 * MR];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -154,7 +162,7 @@ __device__ void ro_stats(const RowOps& r, int M, int K, const RoLds& L, double2*
 #pragma unroll
     for (int m = 0; m < MR; ++m)
       if (m < M) {
-        const double2 v = ro_value(r, L.m0 + m, k, K, L);
+        const double2 v = ro_value<Acc>(r, L.m0 + m, k, K, L);
         a[2 * m] += v.x;
         a[2 * m + 1] += v.y;
       }
@@ -176,7 +184,7 @@ __device__ void ro_stats(const RowOps& r, int M, int K, const RoLds& L, double2*
 #pragma unroll
     for (int m = 0; m < MR; ++m)
       if (m < M) {
-        const double2 t = csub(ro_value(r, L.m0 + m, k, K, L), mean_s[m]);
+        const double2 t = csub(ro_value<Acc>(r, L.m0 + m, k, K, L), mean_s[m]);
         const double2 tt = cmul(t, t);
         a[2 * m] += tt.x;
         a[2 * m + 1] += tt.y;
@@ -203,17 +211,31 @@ __device__ void ro_stats(const RowOps& r, int M, int K, const RoLds& L, double2*
 // [n0, n1) is normalised; RoPE pairs must not straddle the range (ka even).
 // Every source element is loaded once; statistics are taken from LDS.
 // Block-wide; all threads call it; ends with a barrier.
-template <int MR>
+template <int MR, class Acc = AccPlain>
 __device__ void ro_build(const RowOps& r, int M, int K, int ka, int RL, int n0, int n1, double2* buf, const RoLds& L,
                          double2* st_mean, double2* st_sd) {
   __shared__ double red_s[4][2 * MR];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  for (int i = tid; i < MR * RL; i += 256) {
-    const int m = i / RL, k = ka + (i - m * RL);
-    buf[i] = (m < M && k < K) ? ro_base(r, L.m0 + m, k, K, L) : make_double2(0.0, 0.0);
+  // pass 1: every source element once, four per thread with their loads in
+  // flight together; without RoPE the residual joins here
+  const bool res1 = r.resid && !r.rope_cs;
+  const int tot = MR * RL;
+  for (int i0 = tid; i0 < tot; i0 += 4 * 256) {
+    double2 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = i0 + u * 256;
+      const int m = i / RL, k = ka + (i - m * RL);
+      const bool ok = i < tot && m < M && k < K;
+      v[u] = ok ? ro_base<Acc>(r, L.m0 + m, k, K, L) : make_double2(0.0, 0.0);
+      if (res1 && ok) v[u] = make_double2(v[u].x + Acc::ld(r.resid + (long)(L.m0 + m) * r.ldr + k).x, 0.0);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (i0 + u * 256 < tot) buf[i0 + u * 256] = v[u];
   }
   __syncthreads();
-  if (r.rope_cs || r.resid) {
+  if (r.rope_cs) {
     const int half = (RL + 1) / 2;
     for (int i = tid; i < MR * half; i += 256) {
       const int m = i / half, j = i - m * half, k = ka + 2 * j;
@@ -222,7 +244,7 @@ __device__ void ro_build(const RowOps& r, int M, int K, int ka, int RL, int n0, 
       const bool pair = 2 * j + 1 < RL && k + 1 < K;  // always true with RoPE (even K, even range)
       double2 e = buf[m * RL + 2 * j], o = pair ? buf[m * RL + 2 * j + 1] : make_double2(0.0, 0.0);
       if (r.rope_cs) {
-        const int p = min(r.rope_pos[gm], r.rope_max - 1);  // overflow flagged by ro_check
+        const int p = min(Acc::kv(r.rope_pos, gm), r.rope_max - 1);  // overflow flagged by ro_check
         const double2 t = r.rope_cs[(long)p * (K >> 1) + (k >> 1)];
         const double2 e2 = make_double2(e.x * t.x - o.x * t.y, e.y * t.x - o.y * t.y);
         const double2 o2 = make_double2(e.x * t.y + o.x * t.x, e.y * t.y + o.y * t.x);
@@ -230,8 +252,8 @@ __device__ void ro_build(const RowOps& r, int M, int K, int ka, int RL, int n0, 
         o = o2;
       }
       if (r.resid) {
-        e = make_double2(e.x + r.resid[(long)gm * r.ldr + k].x, 0.0);
-        if (pair) o = make_double2(o.x + r.resid[(long)gm * r.ldr + k + 1].x, 0.0);
+        e = make_double2(e.x + Acc::ld(r.resid + (long)gm * r.ldr + k).x, 0.0);
+        if (pair) o = make_double2(o.x + Acc::ld(r.resid + (long)gm * r.ldr + k + 1).x, 0.0);
       }
       buf[m * RL + 2 * j] = e;
       if (pair) buf[m * RL + 2 * j + 1] = o;

@@ -1,6 +1,7 @@
-"""GPU parity of the decode-step plans: the fused GEMV plan (row transforms in
-the product prologues, split-K and greedy argmax finished in-kernel) and the
-one-launch-per-operation plan, against the CPU oracle.
+"""GPU parity of the decode-step plans against the CPU oracle: the resident
+loop (one cooperative launch for every decode step, plan 3), the fused GEMV
+plan (row transforms in the product prologues, split-K and greedy argmax
+finished in-kernel, plan 1) and the one-launch-per-operation plan (plan 0).
 
 Bar: ids bit-exact, Re-logits within REL_TOL (conftest.max_rel_err).
 """
@@ -26,6 +27,7 @@ def log(msg):
 
 SMALL = configs.ModelConfig("small", layers=2, d=32, heads=4, ffn=64, vocab=211, max_ctx=64, seed=9)
 MID = configs.ModelConfig("mid", layers=2, d=64, heads=4, ffn=128, vocab=1000, max_ctx=96, seed=21)
+PLANS = (3, 1, 0)
 
 
 def _generate_both_plans(cfg, lens, n_new, prompt_seed):
@@ -34,9 +36,12 @@ def _generate_both_plans(cfg, lens, n_new, prompt_seed):
     prompt = seeded.prompts(prompt_seed, lens, cfg.vocab)
     io, lo = o.generate(prompt, lens=lens, n_new=n_new, want_logits=True)
     out = {}
-    for fused in (True, False):
-        g.set_decode_plan(fused)
-        out[fused] = g.generate(prompt, lens=lens, n_new=n_new, want_logits=True)
+    for plan in PLANS:
+        g.set_decode_plan(plan)
+        out[plan] = g.generate(prompt, lens=lens, n_new=n_new, want_logits=True)
+        want = "resident" if plan == 3 and len(lens) <= 8 else None
+        if want:
+            assert g.last_timings()["decode_loop"] == want
     return out, (io, lo)
 
 
@@ -44,27 +49,28 @@ def _generate_both_plans(cfg, lens, n_new, prompt_seed):
 def test_decode_plans_match_oracle(lens):
     log(f"decode plans, lens {lens}")
     out, (io, lo) = _generate_both_plans(MID, lens, 16, len(lens))
-    for fused, (ig, lg) in out.items():
-        assert np.array_equal(ig, io), f"fused={fused}"
-        assert max_rel_err(lg, lo) < REL_TOL, f"fused={fused}"
+    for plan, (ig, lg) in out.items():
+        assert np.array_equal(ig, io), f"plan={plan}"
+        assert max_rel_err(lg, lo) < REL_TOL, f"plan={plan}"
 
 
 def test_decode_batch_above_gemv_limit_uses_mfma_with_fused_argmax():
     lens = [10 + (3 * b) % 17 for b in range(12)]
     log("decode B=12 (MFMA + fused argmax)")
     out, (io, lo) = _generate_both_plans(MID, lens, 10, 77)
-    ig, lg = out[True]
-    assert np.array_equal(ig, io)
-    assert max_rel_err(lg, lo) < REL_TOL
+    for plan in (3, 1):
+        ig, lg = out[plan]
+        assert np.array_equal(ig, io), f"plan={plan}"
+        assert max_rel_err(lg, lo) < REL_TOL, f"plan={plan}"
 
 
 def test_fused_decode_rope_model():
     cfg = configs.ModelConfig("rope", layers=2, d=64, heads=4, ffn=128, vocab=500, max_ctx=96, seed=12, rope=True)
     log("fused decode with RoPE")
     out, (io, lo) = _generate_both_plans(cfg, [20, 6], 24, 3)
-    for fused, (ig, lg) in out.items():
-        assert np.array_equal(ig, io), f"fused={fused}"
-        assert max_rel_err(lg, lo) < REL_TOL, f"fused={fused}"
+    for plan, (ig, lg) in out.items():
+        assert np.array_equal(ig, io), f"plan={plan}"
+        assert max_rel_err(lg, lo) < REL_TOL, f"plan={plan}"
 
 
 def _odd_stack(net, cfg):
@@ -92,11 +98,11 @@ def test_fused_decode_odd_layer_stack():
     lens = [9, 4, 13]
     prompt = seeded.prompts(31, lens, cfg.vocab)
     io, lo = o.generate(prompt, lens=lens, n_new=12, want_logits=True)
-    for fused in (True, False):
-        g.set_decode_plan(fused)
+    for plan in PLANS:
+        g.set_decode_plan(plan)
         ig, lg = g.generate(prompt, lens=lens, n_new=12, want_logits=True)
-        assert np.array_equal(ig, io), f"fused={fused}"
-        assert max_rel_err(lg, lo) < REL_TOL, f"fused={fused}"
+        assert np.array_equal(ig, io), f"plan={plan}"
+        assert max_rel_err(lg, lo) < REL_TOL, f"plan={plan}"
 
 
 def test_cached_predict_single_row_uses_fused_plan():
@@ -115,9 +121,33 @@ def test_cached_predict_single_row_uses_fused_plan():
         assert max_rel_err(b_g, b_o) < REL_TOL
 
 
+def test_resident_loop_repeats_bit_identically():
+    """Every partial is summed in a fixed order, so repeated resident launches
+    (their barrier epochs carried over from call to call) are bit-identical."""
+    g = configs.build_network(ra.Network(0), MID)
+    g.set_decode_plan(3)
+    prompt = seeded.prompts(6, [13, 3, 40], MID.vocab)
+    runs = [g.generate(prompt, n_new=25, lens=[13, 3, 40], want_logits=True) for _ in range(4)]
+    assert g.last_timings()["decode_loop"] == "resident"
+    for ids, lg in runs[1:]:
+        assert np.array_equal(ids, runs[0][0])
+        assert np.array_equal(lg, runs[0][1])
+
+
+def test_default_plan_runs_batch1_resident():
+    g = configs.build_network(ra.Network(0), MID)
+    prompt = seeded.prompts(8, [17], MID.vocab)
+    g.generate(prompt, n_new=8)
+    assert g.last_timings()["decode_loop"] == "resident"
+    prompt2 = seeded.prompts(8, [17, 9], MID.vocab)
+    g.generate(prompt2, lens=[17, 9], n_new=8)
+    assert g.last_timings()["decode_loop"] == "graph"
+
+
 def test_graph_replay_fused_plan_is_deterministic():
     """Split-K partials are summed in split order, so replays are bit-identical."""
     g = configs.build_network(ra.Network(0), MID)
+    g.set_decode_plan(1)
     prompt = seeded.prompts(5, [11, 29], MID.vocab)
     runs = [g.generate(prompt, n_new=20, lens=[11, 29], want_logits=True) for _ in range(3)]
     g.set_graph_mode(True)

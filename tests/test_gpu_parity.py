@@ -189,6 +189,7 @@ def test_c1_generate_parity():
 
 def test_graph_replay_equals_direct_launch():
     g = configs.build_network(ra.Network(0), SMALL)
+    g.set_decode_plan(1)
     prompt = seeded.prompts(2, [10], SMALL.vocab)
     i1, l1 = g.generate(prompt, n_new=12, want_logits=True)
     assert g.last_timings()["graph"]

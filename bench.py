@@ -70,6 +70,46 @@ def kernel_class(net, prompt, lens, n_new, cls, reps=2):
     return r
 
 
+def prefill_flops(w, lens):
+    """Algorithmic flops of the prompt pass: 8 per complex multiply-add of the
+    Q/K/V and FFN products over every prompt row, the causal half of Re(q.k)
+    (8 per key) and of P.V (4, real x complex), and the vocab product of each
+    sequence's last row only."""
+    c = w.model
+    rows = float(sum(lens))
+    proj = 8.0 * c.layers * rows * (3 * c.d * c.d + 2 * c.d * c.ffn)
+    attn = c.layers * sum(12.0 * c.d * s * (s + 1) / 2 for s in lens)
+    vocab = 8.0 * len(lens) * c.d * c.vocab
+    return proj + attn + vocab
+
+
+def decode_step_bytes(c, lens, n_new):
+    """HBM bytes of one decode step averaged over the generation: every weight
+    once (plus the vocab bias), and per sequence and layer the K and V rows of
+    the cache, the new token's K, V and the Re(bias_pos) row 0 entries."""
+    weights = 16.0 * c.weight_elems() + 16.0 * c.vocab
+    kv = 0.0
+    for t0 in lens:
+        for step in range(1, n_new):
+            t = t0 + step  # keys of this step
+            kv += c.layers * (16.0 * (2 * t * c.d + 2 * c.d) + 8.0 * c.heads * t)
+    return weights + kv / (n_new - 1)
+
+
+def load_traffic(kernel_class, workload):
+    """HBM bytes per launch measured by rocprofv3 counters for this class and
+    workload (profiles/<class>_<workload>_traffic.json, python -m
+    rustcrates_amd.traffic), or None."""
+    path = os.path.join(ROOT, "profiles", f"{kernel_class}_{workload}_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as fh:
+        t = json.load(fh)
+    if t.get("kernel_class") != kernel_class or t.get("workload") != workload:
+        return None
+    return round(t["traffic_bytes_per_launch"], 1)
+
+
 def roofline_entry(r, bound):
     n = max(r["launches"], 1)
     avg_s = r["total_ms"] / n / 1e3
@@ -143,21 +183,24 @@ def main():
     decode_tok_s = B * (n_new - 1) / (dec_ms / 1e3) if dec_ms > 0 else None
 
     # roofline of the dominant kernel classes, HIP events on the library stream
-    roof, class_ms = None, None
+    roof, class_ms, prefill_gemm_roof = None, None, None
     if not args.no_classes:
         log("kernel-class timing")
         classes = {}
         for name, cls in (("vocab", ra.TIME_VOCAB), ("layer_gemm", ra.TIME_LAYER_GEMM),
-                          ("attention", ra.TIME_ATTENTION)):
+                          ("attention", ra.TIME_ATTENTION), ("prefill_gemm", ra.TIME_PREFILL_GEMM)):
             classes[name] = kernel_class(net, prompt, lens, n_new, cls)
+        # the decode products dominate the step; a GEMM class is MFMA-bound
+        # when its arithmetic intensity exceeds the ridge point
         dominant = max(("vocab", "layer_gemm"), key=lambda k: classes[k]["total_ms"])
         r = classes[dominant]
-        # a GEMM class is MFMA-bound when its arithmetic intensity exceeds the ridge point
         intensity = r["alg_flops"] / max(r["alg_bytes"], 1.0)
         bound = "mfma" if intensity > FP64_MFMA_PEAK_TFS * 1e12 / (HBM_PEAK_GBS * 1e9) else "hbm"
         roof = roofline_entry(r, bound)
         roof["kernel_class"] = dominant
+        roof["traffic"] = load_traffic(dominant, args.workload)
         class_ms = {k: round(v["total_ms"] / 2, 3) for k, v in classes.items()}
+        prefill_gemm_roof = roofline_entry(classes["prefill_gemm"], "mfma") if classes["prefill_gemm"]["launches"] else None
 
     out = {
         "metric": "generated tokens/s",
@@ -181,6 +224,17 @@ def main():
         "kernel_class_ms_per_step": class_ms,
         "roofline": roof,
     }
+    # the prompt pass against the FP64 MFMA peak (north_star's prefill target)
+    pf = prefill_flops(w, [int(x) for x in lens])
+    out["prefill"] = {
+        "alg_gflop": round(pf / 1e9, 2),
+        "tflops": round(pf / (pre_ms / 1e3) / 1e12, 3),
+        "mfma_frac": round(pf / (pre_ms / 1e3) / 1e12 / FP64_MFMA_PEAK_TFS, 4),
+        "gemm_roofline": prefill_gemm_roof,
+    }
+    if B <= 8:
+        sb = decode_step_bytes(cfg, [int(x) for x in lens], n_new)
+        out["decode_step_hbm_frac"] = round(sb / (dec_ms / (n_new - 1) / 1e3) / 1e9 / HBM_PEAK_GBS, 4)
 
     if not args.no_b1 and B > 1 and args.workload.startswith("c3"):
         log("batch-1 companion")
@@ -196,7 +250,8 @@ def main():
             "vocab_roofline": roofline_entry(rv, "hbm"),
         }
         # whole decode step against the HBM roofline: weights + KV + bias rows per token
-        step_bytes = 16.0 * cfg.weight_elems() + 16.0 * cfg.vocab  # weights + bias vector
+        step_bytes = decode_step_bytes(cfg, [int(x) for x in l1], w1.n_new)
+        out["batch1"]["decode_step_bytes"] = round(step_bytes)
         out["batch1"]["decode_step_hbm_frac"] = round(step_bytes / (dec1 / (w1.n_new - 1) / 1e3) / 1e9 / HBM_PEAK_GBS, 4)
 
     if not args.no_cpu:

@@ -47,9 +47,10 @@ extern "C" {
 
 /* kernel classes for mitok_timing_enable */
 #define MITOK_TIME_VOCAB 1       /* the vocab Linear (the Linear before Softmax) */
-#define MITOK_TIME_LAYER_GEMM 2  /* Q/K/V and FFN projections */
+#define MITOK_TIME_LAYER_GEMM 2  /* Q/K/V and FFN projections of one-row (decode) calls */
 #define MITOK_TIME_ATTENTION 3   /* attention kernels */
 #define MITOK_TIME_STEP 4        /* one whole decode step (one token for every sequence) */
+#define MITOK_TIME_PREFILL_GEMM 5 /* Q/K/V and FFN projections of calls with several rows per sequence */
 
 typedef struct mitok_network mitok_network; /* NeuralNetwork (neural_network_generic.rs:23-31) */
 

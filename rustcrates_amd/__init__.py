@@ -24,7 +24,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libmitok.so")
 
 TRAINING, PRODUCTION = 0, 1
-TIME_VOCAB, TIME_LAYER_GEMM, TIME_ATTENTION, TIME_STEP = 1, 2, 3, 4
+TIME_VOCAB, TIME_LAYER_GEMM, TIME_ATTENTION, TIME_STEP, TIME_PREFILL_GEMM = 1, 2, 3, 4, 5
 
 ERRORS = {1: "ERR_ARG", 2: "ERR_HIP", 3: "ERR_STATE", 4: "ERR_NAN", 5: "ERR_NOMEM"}
 

@@ -517,7 +517,8 @@ static int enqueue_forward(Net* n, const Spec& sp) {
           }
         }
         {
-          TimeScope ts(n, MITOK_TIME_LAYER_GEMM, gemm_bytes(rows, 3 * d, d, false), gemm_flops(rows, 3 * d, d));
+          TimeScope ts(n, S > 1 ? MITOK_TIME_PREFILL_GEMM : MITOK_TIME_LAYER_GEMM, gemm_bytes(rows, 3 * d, d, false),
+                       gemm_flops(rows, 3 * d, d));
           TRY(launch_rc(gemm(st, rows, 3 * d, d, rows_of(cur, d), A->wqkv.as<double2>(), 3 * d, e, nullptr, sy), "qkv"));
         }
         a.kc = e.kc;
@@ -578,13 +579,13 @@ static int enqueue_forward(Net* n, const Spec& sp) {
         e2.check_finite = 1;
         e2.err = err;
         {
-          TimeScope ts(n, MITOK_TIME_LAYER_GEMM, gemm_bytes(rows, F->hidden, F->d_in, false),
+          TimeScope ts(n, S > 1 ? MITOK_TIME_PREFILL_GEMM : MITOK_TIME_LAYER_GEMM, gemm_bytes(rows, F->hidden, F->d_in, false),
                        gemm_flops(rows, F->hidden, F->d_in));
           TRY(launch_rc(gemm(st, rows, F->hidden, F->d_in, rows_of(cur, F->d_in), F->w1.as<double2>(), F->hidden, e1,
                              nullptr, sy), "ffn1"));
         }
         {
-          TimeScope ts(n, MITOK_TIME_LAYER_GEMM, gemm_bytes(rows, F->d_out, F->hidden, false),
+          TimeScope ts(n, S > 1 ? MITOK_TIME_PREFILL_GEMM : MITOK_TIME_LAYER_GEMM, gemm_bytes(rows, F->d_out, F->hidden, false),
                        gemm_flops(rows, F->d_out, F->hidden));
           TRY(launch_rc(gemm(st, rows, F->d_out, F->hidden, rows_of(n->hbuf.as<double2>(), F->hidden),
                              F->w2.as<double2>(), F->d_out, e2, nullptr, sy), "ffn2"));

@@ -111,6 +111,8 @@ def load_traffic(kernel_class, workload):
 
 
 def roofline_entry(r, bound):
+    """Achieved rate of a kernel class from its HIP-event totals (each launch's
+    start and stop stamped by its dispatch on the library's stream)."""
     n = max(r["launches"], 1)
     avg_s = r["total_ms"] / n / 1e3
     if bound == "hbm":
@@ -200,7 +202,8 @@ def main():
         roof["kernel_class"] = dominant
         roof["traffic"] = load_traffic(dominant, args.workload)
         class_ms = {k: round(v["total_ms"] / 2, 3) for k, v in classes.items()}
-        prefill_gemm_roof = roofline_entry(classes["prefill_gemm"], "mfma") if classes["prefill_gemm"]["launches"] else None
+        prefill_gemm_roof = (roofline_entry(classes["prefill_gemm"], "mfma")
+                             if classes["prefill_gemm"]["launches"] else None)
 
     out = {
         "metric": "generated tokens/s",

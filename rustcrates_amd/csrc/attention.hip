@@ -89,7 +89,7 @@ __global__ __launch_bounds__(256) void k_attention_rows(Attn a) {
 
 void attention_rows(hipStream_t st, const Attn& a) {
   const size_t shm = (size_t)a.T_max * sizeof(double) + (size_t)(a.dh + 256) * sizeof(double2) + 8 * sizeof(double);
-  hipLaunchKernelGGL(k_attention_rows, dim3(a.S, a.H, a.B), dim3(256), shm, st, a);
+  MITOK_LAUNCH(k_attention_rows, dim3(a.S, a.H, a.B), dim3(256), shm, st, a);
 }
 
 // ===========================================================================
@@ -321,11 +321,11 @@ int attention_decode_split(hipStream_t st, const Attn& a, const double2* q, long
   const dim3 grid(o.nsplit, a.H, a.B);
   const int ap = append ? 1 : 0;
   switch (a.dh) {
-    case 16: hipLaunchKernelGGL(k_attention_split<16>, grid, dim3(256), 0, st, a, q, ldq, npart, part_stride, ap, o); break;
-    case 32: hipLaunchKernelGGL(k_attention_split<32>, grid, dim3(256), 0, st, a, q, ldq, npart, part_stride, ap, o); break;
-    case 64: hipLaunchKernelGGL(k_attention_split<64>, grid, dim3(256), 0, st, a, q, ldq, npart, part_stride, ap, o); break;
-    case 128: hipLaunchKernelGGL(k_attention_split<128>, grid, dim3(256), 0, st, a, q, ldq, npart, part_stride, ap, o); break;
-    default: hipLaunchKernelGGL(k_attention_split<0>, grid, dim3(256), 0, st, a, q, ldq, npart, part_stride, ap, o); break;
+    case 16: MITOK_LAUNCH(k_attention_split<16>, grid, dim3(256), 0, st, a, q, ldq, npart, part_stride, ap, o); break;
+    case 32: MITOK_LAUNCH(k_attention_split<32>, grid, dim3(256), 0, st, a, q, ldq, npart, part_stride, ap, o); break;
+    case 64: MITOK_LAUNCH(k_attention_split<64>, grid, dim3(256), 0, st, a, q, ldq, npart, part_stride, ap, o); break;
+    case 128: MITOK_LAUNCH(k_attention_split<128>, grid, dim3(256), 0, st, a, q, ldq, npart, part_stride, ap, o); break;
+    default: MITOK_LAUNCH(k_attention_split<0>, grid, dim3(256), 0, st, a, q, ldq, npart, part_stride, ap, o); break;
   }
   return OK;
 }
@@ -461,7 +461,7 @@ __global__ __launch_bounds__(64 * NW) void k_attention_prefill(Attn a) {
 bool attention_prefill(hipStream_t st, const Attn& a) {
   if (a.kv_len || a.T_const != a.S || a.S <= 0) return false;
   const auto launch = [&](auto kern, int nw) {
-    hipLaunchKernelGGL(kern, dim3(cdiv_i(a.S, 16 * nw), a.H, a.B), dim3(64 * nw), 0, st, a);
+    MITOK_LAUNCH(kern, dim3(cdiv_i(a.S, 16 * nw), a.H, a.B), dim3(64 * nw), 0, st, a);
   };
   switch (a.dh) {
     case 16: launch(k_attention_prefill<16, 8>, 8); return true;

@@ -5,10 +5,35 @@
 // reference cross the C ABI without conversion.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 namespace mitok {
+
+// ---- launch timing ----
+// When a timing scope is armed (mitok_timing_enable), the next product or
+// attention launch stamps these events at its own start and end through the
+// dispatch (hipExtLaunchKernelGGL): the kernel's execution time, as a profiler
+// reports it, without the cost of separate event records.  Other launches are
+// plain.
+struct LaunchTiming {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+inline LaunchTiming& launch_timing() {
+  static thread_local LaunchTiming t;
+  return t;
+}
+#define MITOK_LAUNCH(kern, grid, block, shm, st, ...)                                         \
+  do {                                                                                       \
+    ::mitok::LaunchTiming& lt_ = ::mitok::launch_timing();                                    \
+    if (lt_.start) {                                                                         \
+      hipExtLaunchKernelGGL(kern, grid, block, shm, st, lt_.start, lt_.stop, 0, __VA_ARGS__); \
+      lt_.start = lt_.stop = nullptr;                                                        \
+    } else {                                                                                 \
+      hipLaunchKernelGGL(kern, grid, block, shm, st, __VA_ARGS__);                           \
+    }                                                                                        \
+  } while (0)
 
 // accumulator of v_mfma_f64_16x16x4f64 (4 doubles per lane)
 typedef double v4d __attribute__((ext_vector_type(4)));

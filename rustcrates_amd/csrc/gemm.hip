@@ -218,7 +218,7 @@ __global__ __launch_bounds__(256) void k_rowops(RowOps ro, int K, double2* __res
 
 void rowops_apply(hipStream_t st, int M, int K, const RowOps& ro, double2* out, long ldo) {
   const size_t shm = (size_t)K * sizeof(double2) + (ro.att.po ? (size_t)ro.att.H * (ro.att.nsplit + 1) * sizeof(double) : 0);
-  if (M > 0) hipLaunchKernelGGL(k_rowops, dim3(M), dim3(256), shm, st, ro, K, out, ldo);
+  if (M > 0) MITOK_LAUNCH(k_rowops, dim3(M), dim3(256), shm, st, ro, K, out, ldo);
 }
 
 // ===========================================================================
@@ -741,7 +741,7 @@ static void launch_gemv(hipStream_t st, const GemvPlan& p, const RowOps& ro, int
                         int K, const Epi& ep, const Argmax& am, const Sync& sy) {
   dim3 grid(p.ncb, p.P);
   const size_t shm = gemv_lds_bytes(p, ro, M, K);
-  hipLaunchKernelGGL((k_gemv<MR, C>), grid, dim3(256), shm, st, ro, M, W, ldw, N, K, p.kw, ep, am, (double2*)sy.ws,
+  MITOK_LAUNCH((k_gemv<MR, C>), grid, dim3(256), shm, st, ro, M, W, ldw, N, K, p.kw, ep, am, (double2*)sy.ws,
                      sy.counters);
 }
 template <int MR>
@@ -759,18 +759,18 @@ static void launch_skinny(hipStream_t st, const SkinnyPlan& p, const RowOps& ro,
   double2* ws = (double2*)sy.ws;
   if (p.cw == 4) {
     switch (p.rt) {
-      case 1: hipLaunchKernelGGL((k_zgemm_skinny_cols<1, RE, 4>), grid, blk, 0, st, ro.x, ro.ldx, M, W, ldw, N, K, p.kc, ep, am, ws, sy.counters); break;
-      case 2: hipLaunchKernelGGL((k_zgemm_skinny_cols<2, RE, 4>), grid, blk, 0, st, ro.x, ro.ldx, M, W, ldw, N, K, p.kc, ep, am, ws, sy.counters); break;
-      case 3: hipLaunchKernelGGL((k_zgemm_skinny_cols<3, RE, 4>), grid, blk, 0, st, ro.x, ro.ldx, M, W, ldw, N, K, p.kc, ep, am, ws, sy.counters); break;
-      default: hipLaunchKernelGGL((k_zgemm_skinny_cols<4, RE, 4>), grid, blk, 0, st, ro.x, ro.ldx, M, W, ldw, N, K, p.kc, ep, am, ws, sy.counters); break;
+      case 1: MITOK_LAUNCH((k_zgemm_skinny_cols<1, RE, 4>), grid, blk, 0, st, ro.x, ro.ldx, M, W, ldw, N, K, p.kc, ep, am, ws, sy.counters); break;
+      case 2: MITOK_LAUNCH((k_zgemm_skinny_cols<2, RE, 4>), grid, blk, 0, st, ro.x, ro.ldx, M, W, ldw, N, K, p.kc, ep, am, ws, sy.counters); break;
+      case 3: MITOK_LAUNCH((k_zgemm_skinny_cols<3, RE, 4>), grid, blk, 0, st, ro.x, ro.ldx, M, W, ldw, N, K, p.kc, ep, am, ws, sy.counters); break;
+      default: MITOK_LAUNCH((k_zgemm_skinny_cols<4, RE, 4>), grid, blk, 0, st, ro.x, ro.ldx, M, W, ldw, N, K, p.kc, ep, am, ws, sy.counters); break;
     }
     return;
   }
   switch (p.rt) {
-    case 1: hipLaunchKernelGGL((k_zgemm_skinny<1, RE>), grid, blk, 0, st, ro.x, ro.ldx, M, W, ldw, N, K, p.kc, ep, am, ws, sy.counters); break;
-    case 2: hipLaunchKernelGGL((k_zgemm_skinny<2, RE>), grid, blk, 0, st, ro.x, ro.ldx, M, W, ldw, N, K, p.kc, ep, am, ws, sy.counters); break;
-    case 3: hipLaunchKernelGGL((k_zgemm_skinny<3, RE>), grid, blk, 0, st, ro.x, ro.ldx, M, W, ldw, N, K, p.kc, ep, am, ws, sy.counters); break;
-    default: hipLaunchKernelGGL((k_zgemm_skinny<4, RE>), grid, blk, 0, st, ro.x, ro.ldx, M, W, ldw, N, K, p.kc, ep, am, ws, sy.counters); break;
+    case 1: MITOK_LAUNCH((k_zgemm_skinny<1, RE>), grid, blk, 0, st, ro.x, ro.ldx, M, W, ldw, N, K, p.kc, ep, am, ws, sy.counters); break;
+    case 2: MITOK_LAUNCH((k_zgemm_skinny<2, RE>), grid, blk, 0, st, ro.x, ro.ldx, M, W, ldw, N, K, p.kc, ep, am, ws, sy.counters); break;
+    case 3: MITOK_LAUNCH((k_zgemm_skinny<3, RE>), grid, blk, 0, st, ro.x, ro.ldx, M, W, ldw, N, K, p.kc, ep, am, ws, sy.counters); break;
+    default: MITOK_LAUNCH((k_zgemm_skinny<4, RE>), grid, blk, 0, st, ro.x, ro.ldx, M, W, ldw, N, K, p.kc, ep, am, ws, sy.counters); break;
   }
 }
 
@@ -804,12 +804,12 @@ int gemm(hipStream_t st, int M, int N, int K, const RowOps& ro, const double2* W
       const MfmaPlan p = plan_mfma(M, N, K);
       if (p.P > 1 && (long)p.mt * p.nt >= SYNC_COUNTERS) return ERR_ARG;
       dim3 grid(p.nt, p.mt, p.P);
-      hipLaunchKernelGGL(k_zgemm_mfma, grid, dim3(256), 0, st, ro.x, ro.ldx, W, ldw, M, N, K, p.kchunk, ep, am,
+      MITOK_LAUNCH(k_zgemm_mfma, grid, dim3(256), 0, st, ro.x, ro.ldx, W, ldw, M, N, K, p.kchunk, ep, am,
                          (double2*)sy.ws, sy.counters);
       tiles = p.nt;
     }
   }
-  if (am.part_v) hipLaunchKernelGGL(k_argmax_finalize, dim3(M), dim3(256), 0, st, am, tiles);
+  if (am.part_v) MITOK_LAUNCH(k_argmax_finalize, dim3(M), dim3(256), 0, st, am, tiles);
   return OK;
 }
 

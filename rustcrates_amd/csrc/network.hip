@@ -270,22 +270,33 @@ static hipEvent_t take_event(Timing& t) {
   return e;
 }
 
+// Times the first kernel launched inside the scope when `cls` is the enabled
+// class (its start and stop stamped by the dispatch, see MITOK_LAUNCH); the
+// step class records events around the whole scope instead.
 struct TimeScope {
   Net* n;
-  bool on;
-  hipEvent_t a = nullptr;
+  bool on, whole;
+  hipEvent_t a = nullptr, b = nullptr;
   double bytes, flops;
   TimeScope(Net* net, int cls, double alg_bytes, double alg_flops = 0.0)
-      : n(net), on(net->timing.cls == cls), bytes(alg_bytes), flops(alg_flops) {
-    if (on) {
-      a = take_event(n->timing);
-      (void)hipEventRecord(a, n->stream);
-    }
+      : n(net), on(net->timing.cls == cls), whole(cls == MITOK_TIME_STEP), bytes(alg_bytes), flops(alg_flops) {
+    if (!on) return;
+    a = take_event(n->timing);
+    b = take_event(n->timing);
+    if (whole) (void)hipEventRecord(a, n->stream);
+    else launch_timing() = {a, b};
   }
   ~TimeScope() {
     if (!on) return;
-    hipEvent_t b = take_event(n->timing);
-    (void)hipEventRecord(b, n->stream);
+    LaunchTiming& lt = launch_timing();
+    if (whole) {
+      (void)hipEventRecord(b, n->stream);
+    } else if (lt.start) {  // nothing was launched
+      lt = LaunchTiming();
+      n->timing.pool.push_back(a);
+      n->timing.pool.push_back(b);
+      return;
+    }
     n->timing.pending.push_back({a, b});
     n->timing.pending_bytes.push_back(bytes);
     n->timing.pending_flops.push_back(flops);

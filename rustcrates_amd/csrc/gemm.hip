@@ -447,6 +447,14 @@ __global__ __launch_bounds__(256) void k_zgemm_skinny(const double2* __restrict_
     const int row = (tid >> 4) + 16 * j;
     v[j] = cadd(cadd(cadd(red[0][row][col], red[1][row][col]), red[2][row][col]), red[3][row][col]);
   }
+  if (ep.mode == EPI_PART) {  // the next launch sums the partials and applies what follows
+#pragma unroll
+    for (int j = 0; j < RT; ++j) {
+      const int m = (tid >> 4) + 16 * j;
+      if (m < M && n1 < N) ep.out[((long)blockIdx.y * M + m) * N + n1] = v[j];
+    }
+    return;
+  }
   const int P = gridDim.y;
   if (P > 1) {
 #pragma unroll
@@ -717,7 +725,14 @@ static MfmaPlan plan_mfma(int M, int N, int K) {
 
 constexpr int SKINNY_MAX_M = 64;
 
-int gemm_parts(int M, int N, int K) { return M <= 8 ? plan_gemv(M, N, K, true).P : 0; }
+int gemm_parts(int M, int N, int K) {
+  if (M <= 8) return plan_gemv(M, N, K, true).P;
+  if (M <= SKINNY_MAX_M) {
+    const SkinnyPlan p = plan_skinny(M, N, K);
+    return p.cw == 4 ? 0 : p.P;  // the wide-column variant takes no EPI_PART
+  }
+  return 0;
+}
 
 size_t gemm_ws_bytes(int M, int N, int K) {
   int P;
@@ -793,14 +808,16 @@ int gemm(hipStream_t st, int M, int N, int K, const RowOps& ro, const double2* W
     }
     tiles = p.ncb;
   } else {
-    if (!ro.plain() || ep.mode == EPI_PART) return ERR_ARG;  // the MFMA paths read plain rows
+    if (!ro.plain()) return ERR_ARG;  // the MFMA paths read plain rows
     if (M <= SKINNY_MAX_M) {
       const SkinnyPlan p = plan_skinny(M, N, K);
       if (p.ncb >= SYNC_COUNTERS) return ERR_ARG;
+      if (ep.mode == EPI_PART && (p.cw == 4 || am.part_v)) return ERR_ARG;
       if (ep.mode == EPI_RE) launch_skinny<true>(st, p, ro, M, W, ldw, N, K, ep, am, sy);
       else launch_skinny<false>(st, p, ro, M, W, ldw, N, K, ep, am, sy);
       tiles = cdiv_i(N, 16);  // argmax partials per 16 columns
     } else {
+      if (ep.mode == EPI_PART) return ERR_ARG;
       const MfmaPlan p = plan_mfma(M, N, K);
       if (p.P > 1 && (long)p.mt * p.nt >= SYNC_COUNTERS) return ERR_ARG;
       dim3 grid(p.nt, p.mt, p.P);

@@ -71,7 +71,7 @@ enum EpiMode : int {
   EPI_GELU = 1,   // out[m][n] = mask[m] ? gelu(v + bias) : 0 (layer.rs:132-166)
   EPI_RE = 2,     // out_re[m][n] = Re(v + bias) (logits, data_converter.rs:244-256)
   EPI_QKV = 3,    // columns [q | k | v] of all heads: q -> out, k/v -> KV cache
-  EPI_PART = 4,   // GEMV only: split partial p of C to out + p * M * N (ld N); the consumer sums them
+  EPI_PART = 4,   // split partial p of C to out + p * M * N (ld N); the consumer sums them (M <= 64)
 };
 
 struct Epi {
@@ -117,9 +117,10 @@ size_t gemm_ws_bytes(int M, int N, int K);
 size_t argmax_part_elems(int M, int N);
 int gemm(hipStream_t st, int M, int N, int K, const RowOps& ro, const double2* W, long ldw, const Epi& ep,
          const Argmax* am, const Sync& sy);
-// EPI_PART products (M <= 8): the number of partials gemm() writes, and the
-// LDS the prologue needs for an attention-combine source
+// EPI_PART products (M <= 64, except outputs wide enough for the 64-column
+// MFMA variant): the number of partials gemm() writes (0: not available)
 int gemm_parts(int M, int N, int K);
+constexpr int GEMM_PART_MAX_M = 64;
 // The prologue alone: out[m][k] = rowops(x)[m][k]  (materialises a pending row transform)
 void rowops_apply(hipStream_t st, int M, int K, const RowOps& ro, double2* out, long ldo);
 

@@ -399,7 +399,7 @@ static int prepare(Net* n, const Spec& sp) {
     if (sp.mode == MODE_STATELESS) TRY(reserve(n, n->kv_scratch, 2 * rows * dm.dsa * c16));
   }
   TRY(reserve(n, n->sync_ws, ws));
-  if (sp.mode == MODE_CACHED && sp.S == 1 && sp.B <= 8) {
+  if (sp.mode == MODE_CACHED && sp.S == 1 && sp.B <= GEMM_PART_MAX_M) {
     const size_t B = sp.B;
     TRY(reserve(n, n->dq, 8 * B * 3 * std::max(1u, dm.dsa) * c16));
     TRY(reserve(n, n->df1, 8 * B * std::max(1u, dm.fmax) * c16));
@@ -668,13 +668,27 @@ static int enqueue_forward(Net* n, const Spec& sp) {
 // (+GELU), FFN Linear; the vocab Linear ends the step with the greedy id.
 // ---------------------------------------------------------------------------
 static bool fused_decode_ok(const Net* n, const Spec& sp) {
-  if (!n->fused_decode || sp.mode != MODE_CACHED || sp.S != 1 || sp.B > 8 || !sp.forward_only) return false;
+  if (!n->fused_decode || sp.mode != MODE_CACHED || sp.S != 1 || sp.B > GEMM_PART_MAX_M || !sp.forward_only)
+    return false;
   if (sp.first != 0 || sp.last != n->layers.size() || sp.kv_row || sp.out_hidden) return false;
-  // the GEMV prologue holds whole input rows of a LayerNorm in LDS
-  const size_t mr = sp.B <= 1 ? 1 : sp.B <= 2 ? 2 : sp.B <= 4 ? 4 : 8;
-  size_t row = 0;  // widest product input
-  for (auto& L : n->layers) row = std::max<size_t>(row, L->d_in);
-  if (mr * row * sizeof(double2) > 64 * 1024) return false;
+  if (sp.B <= 8) {
+    // the GEMV prologue holds whole input rows of a LayerNorm in LDS
+    const size_t mr = sp.B <= 1 ? 1 : sp.B <= 2 ? 2 : sp.B <= 4 ? 4 : 8;
+    size_t row = 0;  // widest product input
+    for (auto& L : n->layers) row = std::max<size_t>(row, L->d_in);
+    if (mr * row * sizeof(double2) > 64 * 1024) return false;
+  } else {
+    // the MFMA products leave the partials of QKV, FFN Linear and hidden Linears
+    for (uint32_t li = 0; li < n->layers.size(); ++li) {
+      const Layer* L = n->layers[li].get();
+      if (L->kind == K_SELF_ATTENTION && !gemm_parts(sp.B, 3 * L->d_in, L->d_in)) return false;
+      if (L->kind == K_FEED_FORWARD) {
+        const auto* F = (const FeedForwardLayer*)L;
+        if (!gemm_parts(sp.B, F->d_out, F->hidden)) return false;
+      }
+      if (L->kind == K_LINEAR && !is_vocab_linear(n, li) && !gemm_parts(sp.B, L->d_out, L->d_in)) return false;
+    }
+  }
   for (auto& L : n->layers)
     if (L->kind == K_SELF_ATTENTION) {
       // the row transform keeps the chunk weights of every head in LDS
@@ -695,7 +709,11 @@ static bool fused_decode_ok(const Net* n, const Spec& sp) {
 // so no launch waits on another's blocks.  A transformer block is QKV
 // (+ LayerNorm of its input), attention (+ KV append), FFN Dense (+ attention
 // combine, residual, LayerNorm) and FFN Linear (+ bias, GELU); the vocab
-// Linear and the greedy id end the step.
+// Linear and the greedy id end the step.  From 9 to 64 sequences the products
+// are MFMA kernels that read plain rows: a pending row transform is first
+// materialised (rowops_apply), and FFN Dense finishes its sums in-kernel
+// (GELU needs them); QKV and FFN Linear still leave partials for the
+// attention and the next row transform.
 static int enqueue_decode_fused(Net* n, const Spec& sp) {
   hipStream_t st = n->stream;
   uint32_t* err = n->err_d.as<uint32_t>();
@@ -709,6 +727,7 @@ static int enqueue_decode_fused(Net* n, const Spec& sp) {
   int mat_next = 0;
   double2* parts[2] = {n->dp0.as<double2>(), n->dp1.as<double2>()};
   int part_next = 0;
+  const bool mat = B > 8;  // the MFMA products read plain rows
   auto materialize = [&]() {
     double2* out = mats[mat_next];
     mat_next ^= 1;
@@ -716,6 +735,9 @@ static int enqueue_decode_fused(Net* n, const Spec& sp) {
     RowOps r = rows_of(out, width);
     r.err = err;
     pro = r;
+  };
+  auto need_plain = [&]() {
+    if (mat && !pro.plain()) materialize();
   };
   auto part_rows = [&](double2* buf, int npart, int cols) {
     RowOps r = rows_of(buf, cols);
@@ -759,8 +781,15 @@ static int enqueue_decode_fused(Net* n, const Spec& sp) {
         const int d = A->d_in, H = A->heads, dh = A->dh;
         if (pro.resid) materialize();           // its residual source is about to be overwritten
         double2* x1 = n->act0.as<double2>();  // the block input, kept for the residual
-        pro.save = x1;
-        pro.ldsave = d;
+        if (mat) {
+          if (!pro.plain()) rowops_apply(st, B, d, pro, x1, d);
+          else x1 = const_cast<double2*>(pro.x);  // a materialised row buffer (ld d), not reused before the combine
+          pro = rows_of(x1, d);
+          pro.err = err;
+        } else {
+          pro.save = x1;
+          pro.ldsave = d;
+        }
         const int pq = gemm_parts(B, 3 * d, d);
         Epi e;
         e.mode = EPI_PART;
@@ -808,20 +837,38 @@ static int enqueue_decode_fused(Net* n, const Spec& sp) {
       }
       case K_FEED_FORWARD: {
         auto* F = (FeedForwardLayer*)L;
-        const int p1 = gemm_parts(B, F->hidden, F->d_in);
-        Epi e1;
-        e1.mode = EPI_PART;
-        e1.out = n->df1.as<double2>();
-        e1.err = err;
-        {
+        RowOps h;
+        if (mat) {  // Dense: + b1, GELU in the epilogue (layer.rs:132-166)
+          need_plain();
+          Epi e1;
+          e1.mode = EPI_GELU;
+          e1.bias = F->b1.as<double2>();
+          e1.out = n->hbuf.as<double2>();
+          e1.ldo = F->hidden;
+          e1.row_mask = sp.mask;
+          e1.err = err;
           TimeScope ts(n, MITOK_TIME_LAYER_GEMM, gemm_bytes(B, F->hidden, F->d_in, false),
                        gemm_flops(B, F->hidden, F->d_in));
           TRY(launch_rc(gemm(st, B, F->hidden, F->d_in, pro, F->w1.as<double2>(), F->hidden, e1, nullptr, sy), "ffn1"));
+          h = rows_of(n->hbuf.as<double2>(), F->hidden);
+          h.err = err;
+        } else {
+          const int p1 = gemm_parts(B, F->hidden, F->d_in);
+          Epi e1;
+          e1.mode = EPI_PART;
+          e1.out = n->df1.as<double2>();
+          e1.err = err;
+          {
+            TimeScope ts(n, MITOK_TIME_LAYER_GEMM, gemm_bytes(B, F->hidden, F->d_in, false),
+                         gemm_flops(B, F->hidden, F->d_in));
+            TRY(launch_rc(gemm(st, B, F->hidden, F->d_in, pro, F->w1.as<double2>(), F->hidden, e1, nullptr, sy),
+                          "ffn1"));
+          }
+          h = part_rows(n->df1.as<double2>(), p1, F->hidden);  // Dense: + b1, GELU (layer.rs:132-166)
+          h.bias = F->b1.as<double2>();
+          h.gelu = 1;
+          h.row_mask = sp.mask;
         }
-        RowOps h = part_rows(n->df1.as<double2>(), p1, F->hidden);  // Dense: + b1, GELU (layer.rs:132-166)
-        h.bias = F->b1.as<double2>();
-        h.gelu = 1;
-        h.row_mask = sp.mask;
         double2* out = parts[part_next];
         part_next ^= 1;
         const int p2 = gemm_parts(B, F->d_out, F->hidden);
@@ -842,6 +889,7 @@ static int enqueue_decode_fused(Net* n, const Spec& sp) {
       }
       case K_LINEAR: {
         auto* Ln = (LinearLayer*)L;
+        need_plain();
         if (is_vocab_linear(n, li)) {
           Epi e;
           e.bias = Ln->b.as<double2>();

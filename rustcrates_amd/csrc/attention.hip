@@ -118,15 +118,14 @@ static int decode_chunk(int B, int H) { return B * H <= 16 ? 16 : 32; }
 // load of the chunk is issued at entry, before q is summed, so the chunk
 // costs one memory round trip.  DH == 0: any head dim up to 256.
 template <int DH>
-__global__ __launch_bounds__(256) void k_attention_split(Attn a, const double2* __restrict__ qkv, long ldq, int npart,
-                                                         long pstride, int append, AttnSplit o) {
+__device__ __forceinline__ void attn_chunk(const Attn& a, const double2* __restrict__ qkv, long ldq, int npart,
+                                           long pstride, int append, const AttnSplit& o, int split, int h, int b) {
   constexpr int NP = DEC_MAX_CHUNK / 16;  // score passes (16 keys each)
   __shared__ double sc[DEC_MAX_CHUNK];
   __shared__ double2 pv[256];
   __shared__ double2 qs[256], kn[256], vn[256];
   __shared__ double stat[2];
   const int dh = DH > 0 ? DH : a.dh;
-  const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int T = a.kv_len[b] + 1;
   const int CH = o.CH;
@@ -297,6 +296,51 @@ __global__ __launch_bounds__(256) void k_attention_split(Attn a, const double2* 
   }
 }
 
+// The grid covers at most DEC_MAX_BLOCKS blocks (about the blocks resident on
+// the chip at once) whatever the cache length the launch was sized for: the
+// blocks walk the chunks the sequences have now, item = (sequence, head,
+// chunk) in that order, so no block starts only to find its chunk empty (a
+// graph replays one grid while the caches grow).  Up to 256 sequences; with
+// more, one block per (chunk, head, sequence) of the launch's maximum.
+constexpr int DEC_MAX_BLOCKS = 1024;
+constexpr int DEC_COMPACT_MAX_B = 256;
+
+template <int DH>
+__global__ __launch_bounds__(256) void k_attention_split(Attn a, const double2* __restrict__ qkv, long ldq, int npart,
+                                                         long pstride, int append, AttnSplit o, int compact) {
+  if (!compact) {
+    attn_chunk<DH>(a, qkv, ldq, npart, pstride, append, o, blockIdx.x, blockIdx.y, blockIdx.z);
+    return;
+  }
+  __shared__ int s_off[DEC_COMPACT_MAX_B + 1];  // first item of sequence b
+  __shared__ int s_ns[DEC_COMPACT_MAX_B];
+  const int tid = threadIdx.x;
+  const int ns = tid < a.B ? (a.kv_len[tid] + 1 + o.CH - 1) / o.CH : 0;
+  if (tid < DEC_COMPACT_MAX_B) s_ns[tid] = ns;
+  // inclusive scan of H * ns over the 256 threads
+  s_off[tid + 1] = a.H * ns;
+  if (tid == 0) s_off[0] = 0;
+  __syncthreads();
+  for (int off = 1; off < 256; off <<= 1) {
+    const int v = tid + 1 > off ? s_off[tid + 1 - off] : 0;
+    __syncthreads();
+    s_off[tid + 1] += v;
+    __syncthreads();
+  }
+  const int total = s_off[a.B];
+  for (int item = blockIdx.x; item < total; item += gridDim.x) {
+    int lo = 0, hi = a.B - 1;  // the sequence whose range holds item
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_off[mid] <= item) lo = mid;
+      else hi = mid - 1;
+    }
+    const int r = item - s_off[lo], nsb = s_ns[lo];
+    attn_chunk<DH>(a, qkv, ldq, npart, pstride, append, o, r % nsb, r / nsb, lo);
+    __syncthreads();  // the chunk's LDS is reused by the next item
+  }
+}
+
 AttnSplit attention_split_plan(const Attn& a) {
   AttnSplit o;
   o.H = a.H;
@@ -318,14 +362,16 @@ int attention_decode_split(hipStream_t st, const Attn& a, const double2* q, long
       npart < 1)
     return ERR_ARG;
   if (append && (!a.kc_w || !a.vc_w)) return ERR_ARG;
-  const dim3 grid(o.nsplit, a.H, a.B);
+  const long items = (long)o.nsplit * a.H * a.B;
+  const int compact = a.B <= DEC_COMPACT_MAX_B ? 1 : 0;
+  const dim3 grid = compact ? dim3((unsigned)std::min<long>(items, DEC_MAX_BLOCKS)) : dim3(o.nsplit, a.H, a.B);
   const int ap = append ? 1 : 0;
   switch (a.dh) {
-    case 16: MITOK_LAUNCH(k_attention_split<16>, grid, dim3(256), 0, st, a, q, ldq, npart, part_stride, ap, o); break;
-    case 32: MITOK_LAUNCH(k_attention_split<32>, grid, dim3(256), 0, st, a, q, ldq, npart, part_stride, ap, o); break;
-    case 64: MITOK_LAUNCH(k_attention_split<64>, grid, dim3(256), 0, st, a, q, ldq, npart, part_stride, ap, o); break;
-    case 128: MITOK_LAUNCH(k_attention_split<128>, grid, dim3(256), 0, st, a, q, ldq, npart, part_stride, ap, o); break;
-    default: MITOK_LAUNCH(k_attention_split<0>, grid, dim3(256), 0, st, a, q, ldq, npart, part_stride, ap, o); break;
+    case 16: MITOK_LAUNCH(k_attention_split<16>, grid, dim3(256), 0, st, a, q, ldq, npart, part_stride, ap, o, compact); break;
+    case 32: MITOK_LAUNCH(k_attention_split<32>, grid, dim3(256), 0, st, a, q, ldq, npart, part_stride, ap, o, compact); break;
+    case 64: MITOK_LAUNCH(k_attention_split<64>, grid, dim3(256), 0, st, a, q, ldq, npart, part_stride, ap, o, compact); break;
+    case 128: MITOK_LAUNCH(k_attention_split<128>, grid, dim3(256), 0, st, a, q, ldq, npart, part_stride, ap, o, compact); break;
+    default: MITOK_LAUNCH(k_attention_split<0>, grid, dim3(256), 0, st, a, q, ldq, npart, part_stride, ap, o, compact); break;
   }
   return OK;
 }

@@ -28,28 +28,56 @@ __device__ __forceinline__ size_t ro_lds_doubles(const RowOps& r, int M) {
   return r.att.po ? (size_t)M * r.att.H * (r.att.nsplit + 1) : 0;
 }
 
-// Block-wide; all threads call it.  One wave per (row, head).
+// Block-wide; all threads call it.  One wave per two (row, head) pairs: the
+// KV lengths and every chunk's (max, sum) of both pairs are requested
+// together (chunks past the sequence's length are read and then masked; the
+// buffer holds nsplit of them), so the weights cost one memory round trip.
 template <class Acc = AccPlain>
 __device__ inline void ro_prepare(const RowOps& r, int M, const RoLds& L) {
   if (!r.att.po) return;
   const AttnSplit& a = r.att;
+  constexpr int SL = 4;  // chunk slots per lane: nsplit <= 256
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  for (int mh = wave; mh < M * a.H; mh += 4) {
-    const int lm = mh / a.H, h = mh - lm * a.H;
-    const int T = Acc::kv(a.kv_len, L.m0 + lm) + 1;
-    const int ns = (T + a.CH - 1) / a.CH;
-    const long base = ((long)(L.m0 + lm) * a.H + h) * a.nsplit;
-    double mx = -INFINITY;
-    for (int s = lane; s < ns; s += 64) mx = fmax(mx, Acc::ld(a.pm + base + s));
-    mx = wave_max(mx);
-    double l = 0.0;
-    for (int s = lane; s < ns; s += 64) {
-      const double w = exp(Acc::ld(a.pm + base + s) - mx);
-      L.wts[(long)mh * a.nsplit + s] = w;
-      l += Acc::ld(a.pl + base + s) * w;
+  for (int mh0 = wave; mh0 < M * a.H; mh0 += 8) {
+    double vm[2][SL], vl[2][SL];
+    int ns[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int mh = mh0 + 4 * q;
+      const bool valid = mh < M * a.H;
+      const int lm = valid ? mh / a.H : 0, h = valid ? mh - lm * a.H : 0;
+      ns[q] = valid ? (Acc::kv(a.kv_len, L.m0 + lm) + 1 + a.CH - 1) / a.CH : 0;
+      const long base = ((long)(L.m0 + lm) * a.H + h) * a.nsplit;
+#pragma unroll
+      for (int j = 0; j < SL; ++j) {
+        const int sidx = lane + 64 * j;
+        const bool in = valid && sidx < a.nsplit;
+        vm[q][j] = in ? Acc::ld(a.pm + base + sidx) : -INFINITY;
+        vl[q][j] = in ? Acc::ld(a.pl + base + sidx) : 0.0;
+      }
     }
-    l = wave_sum(l);
-    if (lane == 0) L.lsum[mh] = l;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int mh = mh0 + 4 * q;
+      if (mh >= M * a.H) continue;  // uniform over the wave
+      double mx = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < SL; ++j)
+        if (lane + 64 * j < ns[q]) mx = fmax(mx, vm[q][j]);
+      mx = wave_max(mx);
+      double l = 0.0;
+#pragma unroll
+      for (int j = 0; j < SL; ++j) {
+        const int sidx = lane + 64 * j;
+        if (sidx < ns[q]) {
+          const double w = exp(vm[q][j] - mx);
+          L.wts[(long)mh * a.nsplit + sidx] = w;
+          l += vl[q][j] * w;
+        }
+      }
+      l = wave_sum(l);
+      if (lane == 0) L.lsum[mh] = l;
+    }
   }
   __syncthreads();
 }

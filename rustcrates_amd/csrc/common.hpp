@@ -37,6 +37,9 @@ inline LaunchTiming& launch_timing() {
 
 // accumulator of v_mfma_f64_16x16x4f64 (4 doubles per lane)
 typedef double v4d __attribute__((ext_vector_type(4)));
+typedef double v2d __attribute__((ext_vector_type(2)));
+
+
 
 // ---- status codes (include/mitok.h) ----
 enum Status : int {
@@ -217,28 +220,53 @@ __device__ __forceinline__ double wave_max(double v) {
 // atomics: the sc1 stores/loads that reach past the XCD's L2).  An
 // agent-scope fence would instead write back and invalidate the whole L2,
 // which measured several times slower than the whole product.
+// Every pointer is cast to the global address space: a pointer the compiler
+// cannot trace to a kernel argument (one read from a table in memory, as the
+// resident loop's operations are) would otherwise become a FLAT access, which
+// also counts against lgkmcnt, so each later LDS or scalar wait would wait for
+// every load in flight.
+#define MITOK_GLOBAL __attribute__((address_space(1)))
 __device__ __forceinline__ void st_dev(double* p, double v) {
-  __hip_atomic_store((unsigned long long*)p, (unsigned long long)__double_as_longlong(v), __ATOMIC_RELAXED,
-                     __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store((MITOK_GLOBAL unsigned long long*)p, (unsigned long long)__double_as_longlong(v),
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ double ld_dev(const double* p) {
-  return __longlong_as_double(
-      (long long)__hip_atomic_load((unsigned long long*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  return __longlong_as_double((long long)__hip_atomic_load((MITOK_GLOBAL unsigned long long*)p, __ATOMIC_RELAXED,
+                                                           __HIP_MEMORY_SCOPE_AGENT));
 }
 __device__ __forceinline__ void st_dev(double2* p, double2 v) {
   st_dev(&p->x, v.x);
   st_dev(&p->y, v.y);
 }
 __device__ __forceinline__ double2 ld_dev(const double2* p) { return make_double2(ld_dev(&p->x), ld_dev(&p->y)); }
-__device__ __forceinline__ void st_dev(int* p, int v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ void st_dev(int* p, int v) {
+  __hip_atomic_store((MITOK_GLOBAL int*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 __device__ __forceinline__ int ld_dev(const int* p) {
-  return __hip_atomic_load((int*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __hip_atomic_load((MITOK_GLOBAL int*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void st_dev(uint32_t* p, uint32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store((MITOK_GLOBAL uint32_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ uint32_t ld_dev(const uint32_t* p) {
-  return __hip_atomic_load((uint32_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __hip_atomic_load((MITOK_GLOBAL uint32_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// an ordinary load of data nothing writes during the kernel (weights, tables)
+template <class T>
+__device__ __forceinline__ T ld_glb(const T* p) {
+  return *(const MITOK_GLOBAL T*)p;
+}
+// double2's copy constructor takes a generic reference, so it is loaded as a
+// plain vector
+__device__ __forceinline__ double2 ld_glb(const double2* p) {
+  const v2d v = *(const MITOK_GLOBAL v2d*)p;
+  return make_double2(v.x, v.y);
+}
+// a streamed weight: read once per pass, so the load is non-temporal and the
+// caches keep the activations, flags and code instead
+__device__ __forceinline__ double2 ld_stream(const double2* p) {
+  const v2d v = __builtin_nontemporal_load((const MITOK_GLOBAL v2d*)p);
+  return make_double2(v.x, v.y);
 }
 
 // Access policy of the shared device code (rowops.hpp, epilogue.hpp) for
@@ -248,6 +276,7 @@ __device__ __forceinline__ uint32_t ld_dev(const uint32_t* p) {
 // step, supplies a policy with device-coherent activations and the per-step
 // state (KV lengths, ids, history count) kept in each block's LDS.
 //   ld / st    activations and partial results
+//   c          weights and tables (nothing writes them during a launch)
 //   kv(p, m)   KV length of sequence m (also the RoPE position of its new token)
 //   id(p, m)   token id of row m
 //   cnt(p)     decode-step count (the logits-history slot)
@@ -256,6 +285,8 @@ struct AccPlain {
   static __device__ __forceinline__ T ld(const T* p) { return *p; }
   template <class T>
   static __device__ __forceinline__ void st(T* p, T v) { *p = v; }
+  template <class T>
+  static __device__ __forceinline__ T c(const T* p) { return *p; }
   static __device__ __forceinline__ int kv(const int* p, int m) { return p[m]; }
   static __device__ __forceinline__ uint32_t id(const uint32_t* p, int m) { return p[m]; }
   static __device__ __forceinline__ int cnt(const int* p) { return p[0]; }

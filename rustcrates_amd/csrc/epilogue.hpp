@@ -15,7 +15,7 @@ namespace mitok {
 // ===========================================================================
 template <class Acc = AccPlain>
 __device__ __forceinline__ double apply_epi(const Epi& ep, int M, int N, int m, int n, double2 v) {
-  if (ep.bias) v = cadd(v, ep.bias[n]);
+  if (ep.bias) v = cadd(v, Acc::c(ep.bias + n));
   switch (ep.mode) {
     case EPI_STORE:
       if (ep.check_finite && !(isfinite(v.x) && isfinite(v.y))) atomicOr(ep.err, (uint32_t)EB_FFN_NONFINITE);
@@ -23,7 +23,7 @@ __device__ __forceinline__ double apply_epi(const Epi& ep, int M, int N, int m, 
       break;
     case EPI_GELU: {
       bool nan = false;
-      if (ep.row_mask && ep.row_mask[m] == 0) v = make_double2(0.0, 0.0);  // activation.rs:268-284
+      if (ep.row_mask && Acc::c(ep.row_mask + m) == 0) v = make_double2(0.0, 0.0);  // activation.rs:268-284
       else v = gelu_nc(v, &nan);
       if (nan) atomicOr(ep.err, (uint32_t)EB_GELU_NAN);
       Acc::st(ep.out + (long)m * ep.ldo + n, v);

@@ -55,6 +55,8 @@ struct AccRes {
   static __device__ __forceinline__ T ld(const T* p) { return ld_dev(p); }
   template <class T>
   static __device__ __forceinline__ void st(T* p, T v) { st_dev(p, v); }
+  template <class T>
+  static __device__ __forceinline__ T c(const T* p) { return ld_glb(p); }
   static __device__ __forceinline__ int kv(const int*, int m) { return res_kvl[m]; }
   static __device__ __forceinline__ uint32_t id(const uint32_t*, int m) { return res_ids[m]; }
   static __device__ __forceinline__ int cnt(const int*) { return res_cnt; }
@@ -108,6 +110,42 @@ __device__ __forceinline__ void grid_barrier(uint32_t* flags, uint32_t epoch, ui
 // the epilogue.
 constexpr int RES_NPF = 24;
 
+// acc[m] += x[m][row u] * w[u - u0] over rows u0 .. u0 + NU - 1 of this lane
+// (row u at xw[m * RL + u * RPW] in LDS); rows at or past nu count zero.  A
+// group of G rows has all its activations requested from LDS before its first
+// product and no branch per row, so the LDS latency is paid once per group.
+// ZW: the weights of rows past nu are zero and the activation a clamped row
+// reads is this lane's own first row (zero past K), so those rows add exact
+// zeros with no select.
+template <int MR, int NU, int G, bool ZW = false>
+__device__ __forceinline__ void fma_rows(double2 (&acc)[MR], const double2* xw, int RL, int RPW, int u0, int nu,
+                                         const double2 (&w)[NU]) {
+  static_assert(NU % G == 0, "row groups");
+#pragma unroll
+  for (int g0 = 0; g0 < NU; g0 += G) {
+    double2 xv[MR][G];
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      const int u = u0 + g0 + j;
+      const int iu = u < nu ? u : 0;
+#pragma unroll
+      for (int m = 0; m < MR; ++m) xv[m][j] = xw[m * RL + iu * RPW];
+    }
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      if (ZW) {
+#pragma unroll
+        for (int m = 0; m < MR; ++m) acc[m] = cadd(acc[m], cmul(xv[m][j], w[g0 + j]));
+      } else {
+        const bool ok = u0 + g0 + j < nu;
+        const double2 wv = ok ? w[g0 + j] : make_double2(0.0, 0.0);
+#pragma unroll
+        for (int m = 0; m < MR; ++m) acc[m] = cadd(acc[m], cmul(ok ? xv[m][j] : make_double2(0.0, 0.0), wv));
+      }
+    }
+  }
+}
+
 template <int C>
 __device__ __forceinline__ void gemv_weights(const ROp& op, int item, double2 (&w)[RES_NPF]) {
   constexpr int RPW = 64 / C;
@@ -121,7 +159,17 @@ __device__ __forceinline__ void gemv_weights(const ROp& op, int item, double2 (&
   const double2* wp = op.W + (long)(k0 + r) * op.ldw + n;
   const long wstep = (long)RPW * op.ldw;
 #pragma unroll
-  for (int u = 0; u < RES_NPF; ++u) w[u] = u < nu ? wp[u * wstep] : make_double2(0.0, 0.0);
+  for (int u = 0; u < RES_NPF; ++u) w[u] = u < nu ? ld_stream(wp + u * wstep) : make_double2(0.0, 0.0);
+}
+
+// this block's item of a prefetched product (item = blockIdx.x)
+__device__ __forceinline__ void prefetch_weights(const ROp& nx, double2 (&w)[RES_NPF]) {
+  switch (nx.C) {
+    case 8: gemv_weights<8>(nx, blockIdx.x, w); break;
+    case 16: gemv_weights<16>(nx, blockIdx.x, w); break;
+    case 32: gemv_weights<32>(nx, blockIdx.x, w); break;
+    default: gemv_weights<64>(nx, blockIdx.x, w); break;
+  }
 }
 
 template <int MR, int C>
@@ -160,12 +208,10 @@ __device__ __forceinline__ void r_gemv3(const ROp& op, int item, double2* lds2, 
     const int kmax = max(0, min(kw, K - k0));
     const int nu = kmax > r ? (kmax - r + RPW - 1) / RPW : 0;
     const double2* xw = xs + (wave - 1) * kw + r;
-#pragma unroll
-    for (int u = 0; u < RES_NPF; ++u)
-      if (u < nu)
-#pragma unroll
-        for (int m = 0; m < MR; ++m) acc[m] = cadd(acc[m], cmul(xw[m * RL + u * RPW], w[u]));
+    constexpr int G = MR <= 1 ? RES_NPF : MR <= 2 ? 12 : MR <= 4 ? 6 : 4;
+    fma_rows<MR, RES_NPF, G, true>(acc, xw, RL, RPW, 0, nu, w);  // gemv_weights zero-fills rows past nu
   }
+
 #pragma unroll
   for (int m = 0; m < MR; ++m) {
     acc[m].x = col_sum<C>(acc[m].x);
@@ -238,9 +284,9 @@ __device__ __forceinline__ void r_gemv4(const ROp& op, int item, double2* lds2, 
 
   double2 w0[8], w1[8];
 #pragma unroll
-  for (int u = 0; u < 8; ++u) w0[u] = (col_ok && u < nu) ? wp[u * wstep] : make_double2(0.0, 0.0);
+  for (int u = 0; u < 8; ++u) w0[u] = (col_ok && u < nu) ? ld_stream(wp + u * wstep) : make_double2(0.0, 0.0);
 #pragma unroll
-  for (int u = 0; u < 8; ++u) w1[u] = (col_ok && 8 + u < nu) ? wp[(8 + u) * wstep] : make_double2(0.0, 0.0);
+  for (int u = 0; u < 8; ++u) w1[u] = (col_ok && 8 + u < nu) ? ld_stream(wp + (8 + u) * wstep) : make_double2(0.0, 0.0);
 
   ro_prepare<AccRes>(ro, M, L);
   ro_build<MR, AccRes>(ro, M, K, ka, RL, kb0, min(K, kb0 + KB), lds2, L, st_mean, st_sd);
@@ -257,23 +303,16 @@ __device__ __forceinline__ void r_gemv4(const ROp& op, int item, double2* lds2, 
   for (int m = 0; m < MR; ++m) acc[m] = make_double2(0.0, 0.0);
   if (col_ok) {
     const double2* xw = xs + wave * kw + r;  // row u of this lane: xw[m * RL + u * RPW]
+    constexpr int G = MR <= 2 ? 8 : MR <= 4 ? 4 : 2;
     for (int u0 = 0; u0 < nu; u0 += 16) {
+      fma_rows<MR, 8, G>(acc, xw, RL, RPW, u0, nu, w0);
 #pragma unroll
       for (int u = 0; u < 8; ++u)
-        if (u0 + u < nu)
-#pragma unroll
-          for (int m = 0; m < MR; ++m) acc[m] = cadd(acc[m], cmul(xw[m * RL + (u0 + u) * RPW], w0[u]));
-#pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if (u0 + 16 + u < nu) w0[u] = wp[(u0 + 16 + u) * wstep];
+        if (u0 + 16 + u < nu) w0[u] = ld_stream(wp + (u0 + 16 + u) * wstep);
+      fma_rows<MR, 8, G>(acc, xw, RL, RPW, u0 + 8, nu, w1);
 #pragma unroll
       for (int u = 0; u < 8; ++u)
-        if (u0 + 8 + u < nu)
-#pragma unroll
-          for (int m = 0; m < MR; ++m) acc[m] = cadd(acc[m], cmul(xw[m * RL + (u0 + 8 + u) * RPW], w1[u]));
-#pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if (u0 + 24 + u < nu) w1[u] = wp[(u0 + 24 + u) * wstep];
+        if (u0 + 24 + u < nu) w1[u] = ld_stream(wp + (u0 + 24 + u) * wstep);
     }
   }
 #pragma unroll
@@ -372,7 +411,7 @@ __device__ __forceinline__ void r_attn(const ROp& op, int item) {
         const int ee = sub + t * LPK;
         kv[pass][t] = (j < nc && ee < dh) ? ld_dev(kr + ee) : make_double2(0.0, 0.0);
       }
-      bj[pass] = (j < nc && sub == 0) ? bias0[c0 + j] : 0.0;
+      bj[pass] = (j < nc && sub == 0) ? ld_glb(bias0 + c0 + j) : 0.0;
     }
 #pragma unroll
     for (int u = 0; u < VU; ++u) {
@@ -407,7 +446,7 @@ __device__ __forceinline__ void r_attn(const ROp& op, int item) {
         }
       }
       acc = row16_sum(acc);  // the 16 lanes of key j
-      if (j < nc && sub == 0) sc[j] = acc * a.scale + bias0[c0 + j];
+      if (j < nc && sub == 0) sc[j] = acc * a.scale + ld_glb(bias0 + c0 + j);
     }
   }
   __syncthreads();
@@ -660,18 +699,14 @@ __global__ __launch_bounds__(256) void k_resident(const ROp* __restrict__ ops, i
         }
       }
       // the next operation (the next step's first after the last); a
-      // prefetched product has at most one item per block
+      // prefetched product has at most one item per block.  Its weights are
+      // requested during the barrier: requested earlier, they delay this
+      // operation's own stores and so the barrier.
       const bool last = s + 1 == nsteps && i + 1 == nops;
       const ROp& nx = ops[i + 1 < nops ? i + 1 : 0];
       const bool pf = !last && nx.kind == ROP_GEMV && nx.waves == 3 && (int)blockIdx.x < nx.items;
       grid_barrier(flags, ++epoch, err, [&]() {
-        if (!pf) return;
-        switch (nx.C) {
-          case 8: gemv_weights<8>(nx, blockIdx.x, wpf); break;
-          case 16: gemv_weights<16>(nx, blockIdx.x, wpf); break;
-          case 32: gemv_weights<32>(nx, blockIdx.x, wpf); break;
-          default: gemv_weights<64>(nx, blockIdx.x, wpf); break;
-        }
+        if (pf) prefetch_weights(nx, wpf);
       });
       have = pf;
       if (stamps && blockIdx.x == 0 && threadIdx.x == 0) stamps[(long)s * nops + i] = wall_clock64();

@@ -90,7 +90,7 @@ __device__ __forceinline__ double2 ro_base(const RowOps& r, int m, int k, int K,
   if (r.table) {
     const uint32_t id = Acc::id(r.ids, m);
     if (id == 1u || id >= (uint32_t)r.vocab) v = make_double2(0.0, 0.0);  // PAD; bad ids flagged by ro_check
-    else v = r.table[(long)id * K + k];
+    else v = Acc::c(r.table + (long)id * K + k);
   } else if (r.att.po) {
     const AttnSplit& a = r.att;
     const int h = k / a.dh, e = k - h * a.dh;
@@ -127,10 +127,10 @@ __device__ __forceinline__ double2 ro_base(const RowOps& r, int m, int k, int K,
         if (q < r.npart) v = cadd(v, t[q]);
     }
   }
-  if (r.bias) v = cadd(v, r.bias[k]);
+  if (r.bias) v = cadd(v, Acc::c(r.bias + k));
   if (r.finite_check && !(isfinite(v.x) && isfinite(v.y))) atomicOr(r.err, (uint32_t)EB_FFN_NONFINITE);
   if (r.gelu) {
-    if (r.row_mask && r.row_mask[m] == 0) {
+    if (r.row_mask && Acc::c(r.row_mask + m) == 0) {
       v = make_double2(0.0, 0.0);
     } else {
       bool nan = false;
@@ -147,7 +147,7 @@ __device__ __forceinline__ double2 ro_source(const RowOps& r, int m, int k, int 
   if (!r.rope_cs) return ro_base<Acc>(r, m, k, K, L);
   const int p = min(Acc::kv(r.rope_pos, m), r.rope_max - 1);  // overflow flagged by ro_check
   const int i = k >> 1;
-  const double2 t = r.rope_cs[(long)p * (K >> 1) + i];
+  const double2 t = Acc::c(r.rope_cs + (long)p * (K >> 1) + i);
   const double2 e = ro_base<Acc>(r, m, 2 * i, K, L), o = ro_base<Acc>(r, m, 2 * i + 1, K, L);
   return (k & 1) ? make_double2(e.x * t.y + o.x * t.x, e.y * t.y + o.y * t.x)
                  : make_double2(e.x * t.x - o.x * t.y, e.y * t.x - o.y * t.y);
@@ -168,6 +168,8 @@ __device__ __forceinline__ void ro_check(const RowOps& r, int m) {
   }
   if (r.rope_cs && Acc::kv(r.rope_pos, m) >= r.rope_max) atomicOr(r.err, (uint32_t)EB_CTX_OVERFLOW);
 }
+
+constexpr int LN_PRE = 4;  // gamma/beta columns per thread requested up front (rows up to 1024 wide)
 
 // normalize (norm_layer.rs:77): Re(((x - mean) / sd) * gamma + beta) + 0i
 __device__ __forceinline__ double2 ln_apply(double2 v, double2 mean, double2 sd, double2 g, double2 b) {
@@ -242,8 +244,18 @@ __device__ void ro_stats(const RowOps& r, int M, int K, const RoLds& L, double2*
 template <int MR, class Acc = AccPlain>
 __device__ void ro_build(const RowOps& r, int M, int K, int ka, int RL, int n0, int n1, double2* buf, const RoLds& L,
                          double2* st_mean, double2* st_sd) {
-  __shared__ double red_s[4][2 * MR];
+  __shared__ double red_s[4][2 * MR], red_v[4][2 * MR];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // the LayerNorm's gamma and beta of this thread's first columns are
+  // requested with the source rows, not after the statistics
+  double2 gpre[LN_PRE], bpre[LN_PRE];
+#pragma unroll
+  for (int j = 0; j < LN_PRE; ++j) {
+    const int k = n0 + tid + 256 * j;
+    const bool ok = r.ln && k < n1;
+    gpre[j] = ok ? Acc::c(r.gamma + k) : make_double2(0.0, 0.0);
+    bpre[j] = ok ? Acc::c(r.beta + k) : make_double2(0.0, 0.0);
+  }
   // pass 1: every source element once, four per thread with their loads in
   // flight together; without RoPE the residual joins here
   const bool res1 = r.resid && !r.rope_cs;
@@ -273,7 +285,7 @@ __device__ void ro_build(const RowOps& r, int M, int K, int ka, int RL, int n0, 
       double2 e = buf[m * RL + 2 * j], o = pair ? buf[m * RL + 2 * j + 1] : make_double2(0.0, 0.0);
       if (r.rope_cs) {
         const int p = min(Acc::kv(r.rope_pos, gm), r.rope_max - 1);  // overflow flagged by ro_check
-        const double2 t = r.rope_cs[(long)p * (K >> 1) + (k >> 1)];
+        const double2 t = Acc::c(r.rope_cs + (long)p * (K >> 1) + (k >> 1));
         const double2 e2 = make_double2(e.x * t.x - o.x * t.y, e.y * t.x - o.y * t.y);
         const double2 o2 = make_double2(e.x * t.y + o.x * t.x, e.y * t.y + o.y * t.x);
         e = e2;
@@ -307,40 +319,64 @@ __device__ void ro_build(const RowOps& r, int M, int K, int ka, int RL, int n0, 
 #pragma unroll
     for (int j = 0; j < 2 * MR; ++j) red_s[wave][j] = a[j];
   __syncthreads();
-  if (tid < M) {
-    const double sre = (red_s[0][2 * tid] + red_s[1][2 * tid]) + (red_s[2][2 * tid] + red_s[3][2 * tid]);
-    const double sim = (red_s[0][2 * tid + 1] + red_s[1][2 * tid + 1]) + (red_s[2][2 * tid + 1] + red_s[3][2 * tid + 1]);
-    st_mean[tid] = make_double2(sre / len, sim / len);
+  // every thread forms the means (same operands, same order, same bits)
+  double2 mean[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    const double sre = (red_s[0][2 * m] + red_s[1][2 * m]) + (red_s[2][2 * m] + red_s[3][2 * m]);
+    const double sim = (red_s[0][2 * m + 1] + red_s[1][2 * m + 1]) + (red_s[2][2 * m + 1] + red_s[3][2 * m + 1]);
+    mean[m] = make_double2(sre / len, sim / len);
   }
-  __syncthreads();
 #pragma unroll
   for (int j = 0; j < 2 * MR; ++j) a[j] = 0.0;
   for (int k = tid; k < K; k += 256)
 #pragma unroll
     for (int m = 0; m < MR; ++m)
       if (m < M) {
-        const double2 t = csub(buf[m * RL + k], st_mean[m]);
+        const double2 t = csub(buf[m * RL + k], mean[m]);
         const double2 tt = cmul(t, t);
         a[2 * m] += tt.x;
         a[2 * m + 1] += tt.y;
       }
 #pragma unroll
   for (int j = 0; j < 2 * MR; ++j) a[j] = wave_sum(a[j]);
-  __syncthreads();  // red_s reuse
   if (lane == 0)
 #pragma unroll
-    for (int j = 0; j < 2 * MR; ++j) red_s[wave][j] = a[j];
-  __syncthreads();
-  if (tid < M) {
-    const double vre = (red_s[0][2 * tid] + red_s[1][2 * tid]) + (red_s[2][2 * tid] + red_s[3][2 * tid]);
-    const double vim = (red_s[0][2 * tid + 1] + red_s[1][2 * tid + 1]) + (red_s[2][2 * tid + 1] + red_s[3][2 * tid + 1]);
-    st_sd[tid] = csqrt_nc(make_double2(vre / len + r.eps, vim / len + 0.0));
-  }
+    for (int j = 0; j < 2 * MR; ++j) red_v[wave][j] = a[j];
   __syncthreads();
   const int w = n1 - n0;
-  for (int i = tid; i < MR * w; i += 256) {
-    const int m = i / w, k = n0 + (i - m * w);
-    if (m < M && k < K) buf[m * RL + k] = ln_apply(buf[m * RL + k], st_mean[m], st_sd[m], r.gamma[k], r.beta[k]);
+  if (MR == 1) {
+    // one row: every thread takes the square root itself rather than waiting
+    // at another barrier for one thread's
+    const double vre = (red_v[0][0] + red_v[1][0]) + (red_v[2][0] + red_v[3][0]);
+    const double vim = (red_v[0][1] + red_v[1][1]) + (red_v[2][1] + red_v[3][1]);
+    const double2 sd = csqrt_nc(make_double2(vre / len + r.eps, vim / len + 0.0));
+    if (tid == 0) st_mean[0] = mean[0], st_sd[0] = sd;
+#pragma unroll
+    for (int j = 0; j < LN_PRE; ++j) {
+      const int k = n0 + tid + 256 * j;
+      if (k < n1) buf[k] = ln_apply(buf[k], mean[0], sd, gpre[j], bpre[j]);
+    }
+    for (int k = n0 + tid + 256 * LN_PRE; k < n1; k += 256)
+      buf[k] = ln_apply(buf[k], mean[0], sd, Acc::c(r.gamma + k), Acc::c(r.beta + k));
+  } else {
+    if (tid < M) {
+      const double vre = (red_v[0][2 * tid] + red_v[1][2 * tid]) + (red_v[2][2 * tid] + red_v[3][2 * tid]);
+      const double vim = (red_v[0][2 * tid + 1] + red_v[1][2 * tid + 1]) + (red_v[2][2 * tid + 1] + red_v[3][2 * tid + 1]);
+      st_mean[tid] = mean[tid];
+      st_sd[tid] = csqrt_nc(make_double2(vre / len + r.eps, vim / len + 0.0));
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < LN_PRE; ++j) {
+      const int k = n0 + tid + 256 * j;
+      if (k < n1)
+        for (int m = 0; m < M; ++m) buf[m * RL + k] = ln_apply(buf[m * RL + k], st_mean[m], st_sd[m], gpre[j], bpre[j]);
+    }
+    for (int k = n0 + tid + 256 * LN_PRE; k < n1; k += 256) {
+      const double2 g = Acc::c(r.gamma + k), b = Acc::c(r.beta + k);
+      for (int m = 0; m < M; ++m) buf[m * RL + k] = ln_apply(buf[m * RL + k], st_mean[m], st_sd[m], g, b);
+    }
   }
   __syncthreads();
 }

@@ -242,7 +242,7 @@ class Network:
         kinds = (_i32 * mx)()
         us = (C.c_double * mx)()
         _check(self._lib.mitok_resident_profile(self._h, int(enable), mx, C.byref(n), kinds, us))
-        names = {0: "gemv", 1: "attn", 2: "rows", 3: "combine"}
+        names = {0: "gemv", 1: "attn", 2: "rows"}
         return [(names.get(kinds[i], "?"), us[i]) for i in range(n.value)]
 
     def set_decode_plan(self, plan: int):

@@ -167,7 +167,7 @@ int attention_decode_split(hipStream_t st, const Attn& a, const double2* q, long
 // (KV lengths, the ids being fed, the step count) in LDS and finds the greedy
 // ids itself from the vocab product's argmax partials at the start of the next
 // step; block 0 writes ids, history, counts and KV lengths back.
-enum ROpKind : int { ROP_GEMV = 0, ROP_ATTN = 1, ROP_ROWS = 2, ROP_COMBINE = 3 };
+enum ROpKind : int { ROP_GEMV = 0, ROP_ATTN = 1, ROP_ROWS = 2 };
 struct ROp {
   int kind = ROP_GEMV;
   int items = 0;
@@ -181,12 +181,14 @@ struct ROp {
   int N = 0, K = 0, C = 0, kw = 0, ncb = 0, P = 1, waves = 4;
   Epi ep;
   Argmax am;
-  // ATTN: chunks of attention_split_plan (items nsplit x H x B); q of sequence b at q + b * ldq
-  // COMBINE: out[b][h*dh + e] = Re(chunk combine + ro.resid) for item (b, h)
+  // ATTN: chunks of attention_split_plan (items nsplit x H x B); q of sequence b at q + b * ldq.
+  //   cnt != null: per (b, h) chunk counters [B][H]; the last chunk of (b, h) to finish
+  //   combines the chunks: out[b][h*dh + e] = Re(chunk combine + ro.resid)
   Attn a;
   AttnSplit o;
   const double2* q = nullptr;
   long ldq = 0;
+  uint32_t* cnt = nullptr;
   // ROWS: out[m][k] = rowops(ro)[m][k], k < K, in column chunks of cw (whole rows with a LayerNorm)
   double2* out = nullptr;
   long ldo = 0;

@@ -197,6 +197,7 @@ struct mitok_network {
   // one barrier flag per block (zeroed when allocated), the next barrier epoch
   std::vector<mitok::ROp> res_ops_h;
   mitok::DevBuf res_ops, res_flags, res_stamps;
+  mitok::DevBuf res_cnt;  // per (sequence, head) attention-chunk counters
   uint32_t res_epoch = 0;
   int res_profile = 0;  // record per-operation times of the next resident launches
   uint32_t res_steps = 0;
@@ -1104,22 +1105,18 @@ static int resident_build(Net* n, const Spec& sp, int grid, int* dh_out, size_t*
         at.q = n->qbuf.as<double2>();
         at.ldq = d;
         at.items = at.o.nsplit * H * B;
-        ops.push_back(at);
-        // chunk combine + residual, then the Norm (self_attention_layer.rs:101-124)
-        // in the next product's prologue
-        ROp cb;
-        cb.kind = ROP_COMBINE;
-        cb.M = B;
-        cb.a = a;
-        cb.o = at.o;
-        cb.ro.resid = x1;
-        cb.ro.ldr = d;
-        cb.out = mats[mat_next];
-        cb.ldo = d;
-        cb.items = B * H;
+        // chunk combine + residual by the last chunk of each (sequence, head),
+        // then the Norm (self_attention_layer.rs:101-124) in the next
+        // product's prologue
+        if ((size_t)B * H > n->res_cnt.bytes / sizeof(uint32_t)) return fail(ERR_STATE, "chunk counters");
+        at.cnt = n->res_cnt.as<uint32_t>();
+        at.ro.resid = x1;
+        at.ro.ldr = d;
+        at.out = mats[mat_next];
+        at.ldo = d;
         mat_next ^= 1;
-        ops.push_back(cb);
-        pro = rows_of(cb.out, d);
+        ops.push_back(at);
+        pro = rows_of(at.out, d);
         pro.err = err;
         width = d;
         pro.ln = 1;
@@ -1211,6 +1208,13 @@ static int run_resident(Net* n, const Spec& sp, uint32_t nsteps) {
       am_elems = (size_t)sp.B * resident_gemv_plan(sp.B, n->layers[li]->d_out, n->layers[li]->d_in, false, grid).ncb;
   TRY(reserve(n, n->am_v, am_elems * sizeof(double)));
   TRY(reserve(n, n->am_i, am_elems * sizeof(int)));
+  // attention-chunk counters, zeroed before every launch (a launch that ran
+  // out on a barrier time-out may leave counts behind)
+  size_t bh = 0;
+  for (auto& L : n->layers)
+    if (L->kind == K_SELF_ATTENTION) bh = std::max(bh, (size_t)sp.B * ((const SelfAttentionLayer*)L.get())->heads);
+  TRY(reserve(n, n->res_cnt, std::max<size_t>(bh, 1) * sizeof(uint32_t)));
+  HIP_TRY(hipMemsetAsync(n->res_cnt.p, 0, n->res_cnt.bytes, n->stream));
   if (n->res_flags.bytes < (size_t)grid * sizeof(uint32_t)) {
     TRY(reserve(n, n->res_flags, (size_t)grid * sizeof(uint32_t)));
     HIP_TRY(hipMemsetAsync(n->res_flags.p, 0, n->res_flags.bytes, n->stream));

@@ -27,10 +27,11 @@
 //   ROP_GEMV    rowops(x)[M][K] * W[K][N] -> epilogue; a work item is C
 //               columns x one K split (gemm.hip k_gemv's layout)
 //   ROP_ATTN    one key chunk of one (sequence, head) (attention.hip
-//               k_attention_split's layout; the QKV epilogue appended k, v)
+//               k_attention_split's layout; the QKV epilogue appended k, v);
+//               the last chunk of a (sequence, head) to finish rescales the
+//               chunks to their common max and sums them, plus the residual
+//               (a counter per pair, no grid barrier between the two)
 //   ROP_ROWS    materialise rowops(x) for a row or a column chunk of one
-//   ROP_COMBINE the key chunks of one (sequence, head) rescaled to their
-//               common max and summed, plus the residual
 // The step state (KV lengths, the ids being fed, the step count) lives in
 // every block's LDS: each block finds the greedy ids itself from the vocab
 // product's per-tile partials at the start of the next step, so no operation
@@ -117,10 +118,12 @@ constexpr int RES_NPF = 24;
 // ZW: the weights of rows past nu are zero and the activation a clamped row
 // reads is this lane's own first row (zero past K), so those rows add exact
 // zeros with no select.
-template <int MR, int NU, int G, bool ZW = false>
+// The weights of these rows are w[WO .. WO + NU - 1] (a compile-time offset:
+// the array stays in registers).
+template <int MR, int NU, int G, bool ZW = false, int WO = 0, int NW>
 __device__ __forceinline__ void fma_rows(double2 (&acc)[MR], const double2* xw, int RL, int RPW, int u0, int nu,
-                                         const double2 (&w)[NU]) {
-  static_assert(NU % G == 0, "row groups");
+                                         const double2 (&w)[NW]) {
+  static_assert(NU % G == 0 && WO + NU <= NW, "row groups");
 #pragma unroll
   for (int g0 = 0; g0 < NU; g0 += G) {
     double2 xv[MR][G];
@@ -135,10 +138,10 @@ __device__ __forceinline__ void fma_rows(double2 (&acc)[MR], const double2* xw, 
     for (int j = 0; j < G; ++j) {
       if (ZW) {
 #pragma unroll
-        for (int m = 0; m < MR; ++m) acc[m] = cadd(acc[m], cmul(xv[m][j], w[g0 + j]));
+        for (int m = 0; m < MR; ++m) acc[m] = cadd(acc[m], cmul(xv[m][j], w[WO + g0 + j]));
       } else {
         const bool ok = u0 + g0 + j < nu;
-        const double2 wv = ok ? w[g0 + j] : make_double2(0.0, 0.0);
+        const double2 wv = ok ? w[WO + g0 + j] : make_double2(0.0, 0.0);
 #pragma unroll
         for (int m = 0; m < MR; ++m) acc[m] = cadd(acc[m], cmul(ok ? xv[m][j] : make_double2(0.0, 0.0), wv));
       }
@@ -208,8 +211,15 @@ __device__ __forceinline__ void r_gemv3(const ROp& op, int item, double2* lds2, 
     const int kmax = max(0, min(kw, K - k0));
     const int nu = kmax > r ? (kmax - r + RPW - 1) / RPW : 0;
     const double2* xw = xs + (wave - 1) * kw + r;
-    constexpr int G = MR <= 1 ? RES_NPF : MR <= 2 ? 12 : MR <= 4 ? 6 : 4;
-    fma_rows<MR, RES_NPF, G, true>(acc, xw, RL, RPW, 0, nu, w);  // gemv_weights zero-fills rows past nu
+    if constexpr (MR == 1) {
+      fma_rows<MR, RES_NPF, RES_NPF, true>(acc, xw, RL, RPW, 0, nu, w);  // gemv_weights zero-fills rows past nu
+    } else {  // more rows: one row of weights at a time keeps the registers in bounds
+#pragma unroll
+      for (int u = 0; u < RES_NPF; ++u)
+        if (u < nu)
+#pragma unroll
+          for (int m = 0; m < MR; ++m) acc[m] = cadd(acc[m], cmul(xw[m * RL + u * RPW], w[u]));
+    }
   }
 
 #pragma unroll
@@ -259,8 +269,19 @@ __device__ __forceinline__ void r_gemv3(const ROp& op, int item, double2* lds2, 
   __syncthreads();
 }
 
+// w[WO .. WO + 7] <- rows un .. un + 7 of this lane's column (zero past nu)
+template <int WO, int NW>
+__device__ __forceinline__ void stream_rows(double2 (&w)[NW], const double2* wp, long wstep, int un, int nu) {
+#pragma unroll
+  for (int u = 0; u < 8; ++u) w[WO + u] = un + u < nu ? ld_stream(wp + (un + u) * wstep) : make_double2(0.0, 0.0);
+}
+
+// prev: this block's previous item of the operation (-1: none); when it
+// built the same rows (a LayerNorm's whole rows, or the same K split) they
+// are still in LDS and are not built again.
 template <int MR, int C>
-__device__ __forceinline__ void r_gemv4(const ROp& op, int item, double2* lds2, double2* red, double2* st_mean, double2* st_sd) {
+__device__ __forceinline__ void r_gemv4(const ROp& op, int item, int prev, double2* lds2, double2* red, double2* st_mean,
+                                        double2* st_sd) {
   constexpr int RPW = 64 / C;
   const RowOps& ro = op.ro;
   const int M = op.M, N = op.N, K = op.K, kw = op.kw;
@@ -282,14 +303,17 @@ __device__ __forceinline__ void r_gemv4(const ROp& op, int item, double2* lds2, 
   L.lsum = L.wts + (ro.att.po ? (size_t)M * ro.att.H * ro.att.nsplit : 0);
   L.m0 = 0;
 
+  // two buffers of 8 rows per lane keep 16 weight loads in flight; rows past
+  // nu load as zero
   double2 w0[8], w1[8];
-#pragma unroll
-  for (int u = 0; u < 8; ++u) w0[u] = (col_ok && u < nu) ? ld_stream(wp + u * wstep) : make_double2(0.0, 0.0);
-#pragma unroll
-  for (int u = 0; u < 8; ++u) w1[u] = (col_ok && 8 + u < nu) ? ld_stream(wp + (8 + u) * wstep) : make_double2(0.0, 0.0);
+  stream_rows<0>(w0, wp, wstep, col_ok ? 0 : nu, nu);
+  stream_rows<0>(w1, wp, wstep, col_ok ? 8 : nu, nu);
 
-  ro_prepare<AccRes>(ro, M, L);
-  ro_build<MR, AccRes>(ro, M, K, ka, RL, kb0, min(K, kb0 + KB), lds2, L, st_mean, st_sd);
+  const bool built = prev >= 0 && (ro.ln || prev / op.ncb == by);
+  if (!built) {
+    ro_prepare<AccRes>(ro, M, L);
+    ro_build<MR, AccRes>(ro, M, K, ka, RL, kb0, min(K, kb0 + KB), lds2, L, st_mean, st_sd);
+  }
   if (bx == 0 && by == 0 && tid < M) ro_check<AccRes>(ro, tid);
   const double2* xs = lds2 + (kb0 - ka);
   if (ro.save && bx == 0)
@@ -303,16 +327,27 @@ __device__ __forceinline__ void r_gemv4(const ROp& op, int item, double2* lds2, 
   for (int m = 0; m < MR; ++m) acc[m] = make_double2(0.0, 0.0);
   if (col_ok) {
     const double2* xw = xs + wave * kw + r;  // row u of this lane: xw[m * RL + u * RPW]
-    constexpr int G = MR <= 2 ? 8 : MR <= 4 ? 4 : 2;
     for (int u0 = 0; u0 < nu; u0 += 16) {
-      fma_rows<MR, 8, G>(acc, xw, RL, RPW, u0, nu, w0);
+      if constexpr (MR == 1) {
+        fma_rows<MR, 8, 8, true>(acc, xw, RL, RPW, u0, nu, w0);
+      } else {
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if (u0 + 16 + u < nu) w0[u] = ld_stream(wp + (u0 + 16 + u) * wstep);
-      fma_rows<MR, 8, G>(acc, xw, RL, RPW, u0 + 8, nu, w1);
+        for (int u = 0; u < 8; ++u)
+          if (u0 + u < nu)
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if (u0 + 24 + u < nu) w1[u] = ld_stream(wp + (u0 + 24 + u) * wstep);
+            for (int m = 0; m < MR; ++m) acc[m] = cadd(acc[m], cmul(xw[m * RL + (u0 + u) * RPW], w0[u]));
+      }
+      stream_rows<0>(w0, wp, wstep, u0 + 16, nu);
+      if constexpr (MR == 1) {
+        fma_rows<MR, 8, 8, true>(acc, xw, RL, RPW, u0 + 8, nu, w1);
+      } else {
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          if (u0 + 8 + u < nu)
+#pragma unroll
+            for (int m = 0; m < MR; ++m) acc[m] = cadd(acc[m], cmul(xw[m * RL + (u0 + 8 + u) * RPW], w1[u]));
+      }
+      stream_rows<0>(w1, wp, wstep, u0 + 24, nu);
     }
   }
 #pragma unroll
@@ -361,6 +396,75 @@ __device__ __forceinline__ void r_gemv4(const ROp& op, int item, double2* lds2, 
         }
   }
   __syncthreads();  // LDS (rows, red) is reused by the next item
+}
+
+// ---- attention combine (run by the last chunk of a pair) ----------------------
+// Item (b, h): out = Re(sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M) + resid)
+// over the ns chunks of the sequence (the split form of the softmax-weighted
+// sum, masked_attention_head.rs:201-208, then add_matrix_3d_c, utils/matrix.rs:
+// 600-613).  Thread (g, e) takes chunks g, g + G, ...; every load of the item
+// is requested before the first is used.
+__device__ __forceinline__ void r_combine(const ROp& op, int item) {
+  constexpr int UPT = 16;  // chunks per thread kept in flight (ns <= 256, G >= 1)
+  __shared__ double cw_s[256];
+  __shared__ double2 part_s[256];
+  __shared__ double red_s[8];
+  const Attn& a = op.a;
+  const AttnSplit& o = op.o;
+  const int dh = a.dh, H = a.H;
+  const int b = item / H, h = item - b * H;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int T = res_kvl[b] + 1;
+  const int ns = (T + o.CH - 1) / o.CH;
+  const long base = ((long)b * H + h) * o.nsplit;
+  const int G = 256 / dh;
+  const int e = tid % dh, g = tid / dh;
+  const bool act = g < G;
+  double2 po[UPT];
+#pragma unroll
+  for (int u = 0; u < UPT; ++u) {
+    const int sidx = g + u * G;
+    po[u] = (act && sidx < ns) ? ld_dev(o.po + (base + sidx) * dh + e) : make_double2(0.0, 0.0);
+  }
+  const double pm = tid < ns ? ld_dev(o.pm + base + tid) : -INFINITY;
+  const double pl = tid < ns ? ld_dev(o.pl + base + tid) : 0.0;
+  const long col = (long)h * dh + e;
+  const double rres = (g == 0 && op.ro.resid) ? ld_dev(op.ro.resid + (long)b * op.ro.ldr + col).x : 0.0;
+  // common max and chunk weights
+  double mx = wave_max(pm);
+  if (lane == 0) red_s[wave] = mx;
+  __syncthreads();
+  mx = fmax(fmax(red_s[0], red_s[1]), fmax(red_s[2], red_s[3]));
+  const double w = tid < ns ? exp(pm - mx) : 0.0;
+  cw_s[tid] = w;
+  double l = wave_sum(pl * w);
+  __syncthreads();  // red_s reuse, cw_s complete
+  if (lane == 0) red_s[4 + wave] = l;
+  double2 acc = make_double2(0.0, 0.0);
+#pragma unroll
+  for (int u = 0; u < UPT; ++u) {
+    const int sidx = g + u * G;
+    if (act && sidx < ns) {
+      const double ww = cw_s[sidx];
+      acc.x += po[u].x * ww;
+      acc.y += po[u].y * ww;
+    }
+  }
+  for (int sidx = g + UPT * G; act && sidx < ns; sidx += G) {  // beyond UPT chunks per thread
+    const double2 v = ld_dev(o.po + (base + sidx) * dh + e);
+    const double ww = cw_s[sidx];
+    acc.x += v.x * ww;
+    acc.y += v.y * ww;
+  }
+  part_s[tid] = acc;
+  __syncthreads();
+  if (tid < dh) {
+    const double lsum = (red_s[4] + red_s[5]) + (red_s[6] + red_s[7]);
+    double2 sum = part_s[tid];
+    for (int gg = 1; gg < G; ++gg) sum = cadd(sum, part_s[gg * dh + tid]);
+    st_dev(op.out + (long)b * op.ldo + col, make_double2(sum.x / lsum + rres, 0.0));
+  }
+  __syncthreads();
 }
 
 // ---- ROP_ATTN --------------------------------------------------------------
@@ -491,75 +595,9 @@ __device__ __forceinline__ void r_attn(const ROp& op, int item) {
     st_dev((double*)o.pl + pidx, stat[1]);
   }
   __syncthreads();  // LDS reuse by the next item
-}
-
-// ---- ROP_COMBINE -------------------------------------------------------------
-// Item (b, h): out = Re(sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M) + resid)
-// over the ns chunks of the sequence (the split form of the softmax-weighted
-// sum, masked_attention_head.rs:201-208, then add_matrix_3d_c, utils/matrix.rs:
-// 600-613).  Thread (g, e) takes chunks g, g + G, ...; every load of the item
-// is requested before the first is used.
-__device__ __forceinline__ void r_combine(const ROp& op, int item) {
-  constexpr int UPT = 16;  // chunks per thread kept in flight (ns <= 256, G >= 1)
-  __shared__ double cw_s[256];
-  __shared__ double2 part_s[256];
-  __shared__ double red_s[8];
-  const Attn& a = op.a;
-  const AttnSplit& o = op.o;
-  const int dh = a.dh, H = a.H;
-  const int b = item / H, h = item - b * H;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int T = res_kvl[b] + 1;
-  const int ns = (T + o.CH - 1) / o.CH;
-  const long base = ((long)b * H + h) * o.nsplit;
-  const int G = 256 / dh;
-  const int e = tid % dh, g = tid / dh;
-  const bool act = g < G;
-  double2 po[UPT];
-#pragma unroll
-  for (int u = 0; u < UPT; ++u) {
-    const int sidx = g + u * G;
-    po[u] = (act && sidx < ns) ? ld_dev(o.po + (base + sidx) * dh + e) : make_double2(0.0, 0.0);
-  }
-  const double pm = tid < ns ? ld_dev(o.pm + base + tid) : -INFINITY;
-  const double pl = tid < ns ? ld_dev(o.pl + base + tid) : 0.0;
-  const long col = (long)h * dh + e;
-  const double rres = (g == 0 && op.ro.resid) ? ld_dev(op.ro.resid + (long)b * op.ro.ldr + col).x : 0.0;
-  // common max and chunk weights
-  double mx = wave_max(pm);
-  if (lane == 0) red_s[wave] = mx;
-  __syncthreads();
-  mx = fmax(fmax(red_s[0], red_s[1]), fmax(red_s[2], red_s[3]));
-  const double w = tid < ns ? exp(pm - mx) : 0.0;
-  cw_s[tid] = w;
-  double l = wave_sum(pl * w);
-  __syncthreads();  // red_s reuse, cw_s complete
-  if (lane == 0) red_s[4 + wave] = l;
-  double2 acc = make_double2(0.0, 0.0);
-#pragma unroll
-  for (int u = 0; u < UPT; ++u) {
-    const int sidx = g + u * G;
-    if (act && sidx < ns) {
-      const double ww = cw_s[sidx];
-      acc.x += po[u].x * ww;
-      acc.y += po[u].y * ww;
-    }
-  }
-  for (int sidx = g + UPT * G; act && sidx < ns; sidx += G) {  // beyond UPT chunks per thread
-    const double2 v = ld_dev(o.po + (base + sidx) * dh + e);
-    const double ww = cw_s[sidx];
-    acc.x += v.x * ww;
-    acc.y += v.y * ww;
-  }
-  part_s[tid] = acc;
-  __syncthreads();
-  if (tid < dh) {
-    const double lsum = (red_s[4] + red_s[5]) + (red_s[6] + red_s[7]);
-    double2 sum = part_s[tid];
-    for (int gg = 1; gg < G; ++gg) sum = cadd(sum, part_s[gg * dh + tid]);
-    st_dev(op.out + (long)b * op.ldo + col, make_double2(sum.x / lsum + rres, 0.0));
-  }
-  __syncthreads();
+  // the last of the ceil(T / CH) chunks of (b, h) combines them: one grid
+  // barrier per layer fewer than a separate combine operation
+  if (op.cnt && arrive_last(op.cnt + bh, (uint32_t)((T + CH - 1) / CH))) r_combine(op, (int)bh);
 }
 
 // ---- ROP_ROWS --------------------------------------------------------------
@@ -650,7 +688,7 @@ __device__ __forceinline__ void step_argmax(const RStep& st, bool write) {
 
 // ---- the resident kernel -----------------------------------------------------
 template <int MR>
-__device__ __forceinline__ void run_gemv(const ROp& op, int it, double2* lds2, double2* red, double2* st_mean,
+__device__ __forceinline__ void run_gemv(const ROp& op, int it, int prev, double2* lds2, double2* red, double2* st_mean,
                                          double2* st_sd, double2 (&w)[RES_NPF], bool have) {
   if (op.waves == 3) {
     switch (op.C) {
@@ -662,10 +700,10 @@ __device__ __forceinline__ void run_gemv(const ROp& op, int it, double2* lds2, d
     return;
   }
   switch (op.C) {
-    case 8: r_gemv4<MR, 8>(op, it, lds2, red, st_mean, st_sd); break;
-    case 16: r_gemv4<MR, 16>(op, it, lds2, red, st_mean, st_sd); break;
-    case 32: r_gemv4<MR, 32>(op, it, lds2, red, st_mean, st_sd); break;
-    default: r_gemv4<MR, 64>(op, it, lds2, red, st_mean, st_sd); break;
+    case 8: r_gemv4<MR, 8>(op, it, prev, lds2, red, st_mean, st_sd); break;
+    case 16: r_gemv4<MR, 16>(op, it, prev, lds2, red, st_mean, st_sd); break;
+    case 32: r_gemv4<MR, 32>(op, it, prev, lds2, red, st_mean, st_sd); break;
+    default: r_gemv4<MR, 64>(op, it, prev, lds2, red, st_mean, st_sd); break;
   }
 }
 
@@ -692,9 +730,11 @@ __global__ __launch_bounds__(256) void k_resident(const ROp* __restrict__ ops, i
       const ROp& op = ops[i];
       for (int it = blockIdx.x; it < op.items; it += gridDim.x) {
         switch (op.kind) {
-          case ROP_GEMV: run_gemv<MR>(op, it, lds2, red, st_mean, st_sd, wpf, have && it == (int)blockIdx.x); break;
+          case ROP_GEMV:
+            run_gemv<MR>(op, it, it == (int)blockIdx.x ? -1 : it - (int)gridDim.x, lds2, red, st_mean, st_sd, wpf,
+                         have && it == (int)blockIdx.x);
+            break;
           case ROP_ATTN: r_attn<DH>(op, it); break;
-          case ROP_COMBINE: r_combine(op, it); break;
           default: r_rows(op, it, lds2, st_mean, st_sd); break;
         }
       }

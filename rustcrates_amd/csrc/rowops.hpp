@@ -319,13 +319,20 @@ __device__ void ro_build(const RowOps& r, int M, int K, int ka, int RL, int n0, 
 #pragma unroll
     for (int j = 0; j < 2 * MR; ++j) red_s[wave][j] = a[j];
   __syncthreads();
-  // every thread forms the means (same operands, same order, same bits)
-  double2 mean[MR];
-#pragma unroll
-  for (int m = 0; m < MR; ++m) {
-    const double sre = (red_s[0][2 * m] + red_s[1][2 * m]) + (red_s[2][2 * m] + red_s[3][2 * m]);
-    const double sim = (red_s[0][2 * m + 1] + red_s[1][2 * m + 1]) + (red_s[2][2 * m + 1] + red_s[3][2 * m + 1]);
-    mean[m] = make_double2(sre / len, sim / len);
+  // one row: every thread forms the mean (same operands, same order, same
+  // bits); more rows: one thread per row, through LDS
+  double2 mean0 = make_double2(0.0, 0.0);
+  if (MR == 1) {
+    const double sre = (red_s[0][0] + red_s[1][0]) + (red_s[2][0] + red_s[3][0]);
+    const double sim = (red_s[0][1] + red_s[1][1]) + (red_s[2][1] + red_s[3][1]);
+    mean0 = make_double2(sre / len, sim / len);
+  } else {
+    if (tid < M) {
+      const double sre = (red_s[0][2 * tid] + red_s[1][2 * tid]) + (red_s[2][2 * tid] + red_s[3][2 * tid]);
+      const double sim = (red_s[0][2 * tid + 1] + red_s[1][2 * tid + 1]) + (red_s[2][2 * tid + 1] + red_s[3][2 * tid + 1]);
+      st_mean[tid] = make_double2(sre / len, sim / len);
+    }
+    __syncthreads();
   }
 #pragma unroll
   for (int j = 0; j < 2 * MR; ++j) a[j] = 0.0;
@@ -333,7 +340,7 @@ __device__ void ro_build(const RowOps& r, int M, int K, int ka, int RL, int n0, 
 #pragma unroll
     for (int m = 0; m < MR; ++m)
       if (m < M) {
-        const double2 t = csub(buf[m * RL + k], mean[m]);
+        const double2 t = csub(buf[m * RL + k], MR == 1 ? mean0 : st_mean[m]);
         const double2 tt = cmul(t, t);
         a[2 * m] += tt.x;
         a[2 * m + 1] += tt.y;
@@ -351,19 +358,18 @@ __device__ void ro_build(const RowOps& r, int M, int K, int ka, int RL, int n0, 
     const double vre = (red_v[0][0] + red_v[1][0]) + (red_v[2][0] + red_v[3][0]);
     const double vim = (red_v[0][1] + red_v[1][1]) + (red_v[2][1] + red_v[3][1]);
     const double2 sd = csqrt_nc(make_double2(vre / len + r.eps, vim / len + 0.0));
-    if (tid == 0) st_mean[0] = mean[0], st_sd[0] = sd;
+    if (tid == 0) st_mean[0] = mean0, st_sd[0] = sd;
 #pragma unroll
     for (int j = 0; j < LN_PRE; ++j) {
       const int k = n0 + tid + 256 * j;
-      if (k < n1) buf[k] = ln_apply(buf[k], mean[0], sd, gpre[j], bpre[j]);
+      if (k < n1) buf[k] = ln_apply(buf[k], mean0, sd, gpre[j], bpre[j]);
     }
     for (int k = n0 + tid + 256 * LN_PRE; k < n1; k += 256)
-      buf[k] = ln_apply(buf[k], mean[0], sd, Acc::c(r.gamma + k), Acc::c(r.beta + k));
+      buf[k] = ln_apply(buf[k], mean0, sd, Acc::c(r.gamma + k), Acc::c(r.beta + k));
   } else {
     if (tid < M) {
       const double vre = (red_v[0][2 * tid] + red_v[1][2 * tid]) + (red_v[2][2 * tid] + red_v[3][2 * tid]);
       const double vim = (red_v[0][2 * tid + 1] + red_v[1][2 * tid + 1]) + (red_v[2][2 * tid + 1] + red_v[3][2 * tid + 1]);
-      st_mean[tid] = mean[tid];
       st_sd[tid] = csqrt_nc(make_double2(vre / len + r.eps, vim / len + 0.0));
     }
     __syncthreads();

@@ -303,8 +303,8 @@ __device__ __forceinline__ void r_gemv4(const ROp& op, int item, int prev, doubl
   L.lsum = L.wts + (ro.att.po ? (size_t)M * ro.att.H * ro.att.nsplit : 0);
   L.m0 = 0;
 
-  // two buffers of 8 rows per lane keep 16 weight loads in flight; rows past
-  // nu load as zero
+  // two buffers of 8 rows per lane keep 16 weight loads in flight (a third
+  // spills this kernel's registers); rows past nu load as zero
   double2 w0[8], w1[8];
   stream_rows<0>(w0, wp, wstep, col_ok ? 0 : nu, nu);
   stream_rows<0>(w1, wp, wstep, col_ok ? 8 : nu, nu);

@@ -127,8 +127,9 @@ int mitok_greedy_decoding(mitok_network* net, const double* logits, uint32_t row
 /* ---- measurement (no reference counterpart: the reference prints wall
  * clock only, transformer_network.rs:307-310) ---- */
 /* Wall time of the last mitok_generate on the device stream, in ms:
- * t[0] prefill (prompt forward + first id), t[1] all decode steps, t[2] 1 if
- * the decode steps ran as a replayed HIP graph. */
+ * t[0] prefill (prompt forward + first id), t[1] all decode steps, t[2] how
+ * the decode steps ran: 0 direct launches, 1 a replayed HIP graph, 2 the
+ * resident loop. */
 int mitok_last_timings(mitok_network* net, double* t3);
 /* HIP-event timing of one kernel class during the following calls (0 disables;
  * decode steps then run without graph replay so each launch is bracketed). */
@@ -142,9 +143,10 @@ int mitok_device_synchronize(int device);
 int mitok_set_graph_mode(mitok_network* net, int direct_launch);
 /* 3 = generate's decode loop for up to 8 sequences runs as one resident
  *     cooperative launch (one block per CU, grid barriers between operations);
- * 2 = the resident loop at batch 1, plan 1 for 2 to 8 sequences (default);
- * 1 = decode steps of up to 8 sequences run the fused plan (row transforms in
- *     the product prologues, one launch per product, replayed as a graph);
+ * 2 = the resident loop at batch 1, plan 1 for 2 to 64 sequences (default);
+ * 1 = decode steps of up to 64 sequences run the fused plan (up to 8: GEMV
+ *     products with the row transforms in their prologues; 9 to 64: skinny
+ *     MFMA products after a row-transform launch), replayed as a graph;
  * 0 = one launch per reference operation and one query row per attention block.
  * Plans 1 to 3 run prefill attention on the tiled kernel.
  * No counterpart in the reference (a scheduling choice; results agree to the
@@ -153,7 +155,7 @@ int mitok_set_decode_plan(mitok_network* net, int plan);
 /* Per-operation profile of the resident decode loop (plan 2).  enable = 1:
  * later launches record block 0's clock after every grid barrier.  Then, if
  * nops is not NULL, reports the last launch's operations (at most max_ops):
- * kinds[i] (0 product, 1 attention chunks, 2 row transform, 3 chunk combine) and
+ * kinds[i] (0 product, 1 attention chunks with their combine, 2 row transform) and
  * us[i], the microseconds from the previous barrier to the one after op i,
  * averaged over the steps.  No counterpart in the reference (instrumentation). */
 int mitok_resident_profile(mitok_network* net, int enable, int max_ops, int* nops, int* kinds, double* us);

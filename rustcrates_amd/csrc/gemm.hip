@@ -411,18 +411,22 @@ __global__ __launch_bounds__(256) void k_zgemm_skinny(const double2* __restrict_
       }
     }
   };
+  // the tiles' first products before their second ones: two MFMAs on one
+  // accumulator are never adjacent
   auto mma = [&](int buf) {
 #pragma unroll
-    for (int u = 0; u < U; ++u)
+    for (int u = 0; u < U; ++u) {
 #pragma unroll
       for (int t = 0; t < RT; ++t) {
         cr[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[buf][t][u].x, b[buf][u].x, cr[t], 0, 0, 0);
-        cr[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(-a[buf][t][u].y, b[buf][u].y, cr[t], 0, 0, 0);
-        if (!RE) {
-          ci[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[buf][t][u].x, b[buf][u].y, ci[t], 0, 0, 0);
-          ci[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[buf][t][u].y, b[buf][u].x, ci[t], 0, 0, 0);
-        }
+        if (!RE) ci[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[buf][t][u].x, b[buf][u].y, ci[t], 0, 0, 0);
       }
+#pragma unroll
+      for (int t = 0; t < RT; ++t) {
+        cr[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(-a[buf][t][u].y, b[buf][u].y, cr[t], 0, 0, 0);
+        if (!RE) ci[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[buf][t][u].y, b[buf][u].x, ci[t], 0, 0, 0);
+      }
+    }
   };
   constexpr int KS = 4 * U;  // unrolled by two: both buffer indices are constants
   if (ka < kz) load(0, ka);
@@ -520,7 +524,7 @@ __global__ __launch_bounds__(256) void k_zgemm_skinny(const double2* __restrict_
 // in L1, so wide outputs use CW = 4.  RE: only the real part is formed.
 // D[i][j] of row tile t sits at lane j + 16*(i%4), element i/4.
 // ===========================================================================
-template <int RT, bool RE, int CW>
+template <int RT, bool RE, int CW, int U = 4>
 __global__ __launch_bounds__(256) void k_zgemm_skinny_cols(const double2* __restrict__ X, long ldx, int M,
                                                         const double2* __restrict__ W, long ldw, int N, int K, int kc,
                                                         Epi ep, Argmax am, double2* __restrict__ ws,
@@ -539,7 +543,8 @@ __global__ __launch_bounds__(256) void k_zgemm_skinny_cols(const double2* __rest
 #pragma unroll
   for (int t = 0; t < RT; ++t) cr[t] = ci[t] = v4d{0.0, 0.0, 0.0, 0.0};
 
-  constexpr int U = 4;  // k-steps of 4 per batch
+  // U k-steps of 4 per batch: two batches (8U weight and 8U*RT activation
+  // loads per lane) in flight cover the load latency of the MFMAs of one
   double2 b[2][U], a[2][RT][U];
   auto load = [&](int buf, int k) {
 #pragma unroll
@@ -553,29 +558,102 @@ __global__ __launch_bounds__(256) void k_zgemm_skinny_cols(const double2* __rest
       }
     }
   };
+  // Cr += Ar*Br + (-Ai)*Bi; Ci += Ar*Bi + Ai*Br (only Cr when the real part is
+  // all that is used).  The tiles' first products go before their second ones,
+  // so two MFMAs on one accumulator are never adjacent (each would wait for
+  // the previous result).
   auto mma = [&](int buf) {
 #pragma unroll
-    for (int u = 0; u < U; ++u)
+    for (int u = 0; u < U; ++u) {
 #pragma unroll
       for (int t = 0; t < RT; ++t) {
-        // Cr += Ar*Br + (-Ai)*Bi; Ci += Ar*Bi + Ai*Br (only Cr when the real part is all that is used)
         cr[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[buf][t][u].x, b[buf][u].x, cr[t], 0, 0, 0);
+        if (!RE) ci[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[buf][t][u].x, b[buf][u].y, ci[t], 0, 0, 0);
+      }
+#pragma unroll
+      for (int t = 0; t < RT; ++t) {
         cr[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(-a[buf][t][u].y, b[buf][u].y, cr[t], 0, 0, 0);
-        if (!RE) {
-          ci[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[buf][t][u].x, b[buf][u].y, ci[t], 0, 0, 0);
-          ci[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[buf][t][u].y, b[buf][u].x, ci[t], 0, 0, 0);
+        if (!RE) ci[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[buf][t][u].y, b[buf][u].x, ci[t], 0, 0, 0);
+      }
+    }
+  };
+  constexpr int KS = 4 * U;
+  if constexpr (KG == 1) {
+    // All four waves walk the same K range, so the activation rows are staged
+    // through LDS once per block (coalesced loads of CK-wide chunks, the next
+    // chunk in registers while this one is used) instead of being read by
+    // every wave: that was 2 B of L2 traffic per weight byte and kept the
+    // texture path about 2/3 busy.  The weights stay a register stream.
+    constexpr int CK = RT <= 1 ? 128 : RT == 2 ? 64 : 32;  // k per chunk
+    constexpr int NR = 16 * RT;                            // rows staged
+    constexpr int PT = NR * CK / 256;                      // elements per thread per chunk
+    static_assert(CK % (2 * KS) == 0 && (NR * CK) % 256 == 0, "chunk shape");
+    __shared__ double2 As[2][NR][CK + 1];
+    const int tid = threadIdx.x;
+    double2 st[PT];
+    auto fetch = [&](int k0) {
+#pragma unroll
+      for (int j = 0; j < PT; ++j) {
+        const int e = tid + 256 * j, m = e / CK, kk = k0 + (e - m * CK);
+        st[j] = (m < M && kk < kz) ? X[(long)m * ldx + kk] : make_double2(0.0, 0.0);
+      }
+    };
+    auto stage = [&](int buf) {
+#pragma unroll
+      for (int j = 0; j < PT; ++j) {
+        const int e = tid + 256 * j, m = e / CK;
+        As[buf][m][e - m * CK] = st[j];
+      }
+    };
+    auto loadw = [&](int buf, int k) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int kk = k + 4 * u + kq;
+        b[buf][u] = (kk < kz && n < N) ? W[(long)kk * ldw + n] : make_double2(0.0, 0.0);
+      }
+    };
+    auto frag = [&](int abuf, int wbuf, int kl) {  // a[wbuf] <- the chunk's rows at local k kl
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int t = 0; t < RT; ++t) a[wbuf][t][u] = As[abuf][16 * t + i][kl + 4 * u + kq];
+    };
+    const int nch = (kz - ka + CK - 1) / CK;
+    if (nch > 0) {
+      fetch(ka);
+      stage(0);
+      loadw(0, ka);
+    }
+    __syncthreads();
+    for (int c = 0; c < nch; ++c) {
+      const int kc0 = ka + c * CK;
+      if (c + 1 < nch) fetch(kc0 + CK);
+      const int ab = c & 1;
+#pragma unroll
+      for (int bi = 0; bi < CK / KS; bi += 2) {  // two batches per pass: constant buffer indices
+        const int k = kc0 + bi * KS;
+        if (k < kz) {
+          loadw(1, k + KS);
+          frag(ab, 0, bi * KS);
+          mma(0);
+          loadw(0, k + 2 * KS);
+          frag(ab, 1, (bi + 1) * KS);
+          mma(1);
         }
       }
-  };
-  // double buffer unrolled by two so both buffer indices are constants (registers, not scratch)
-  constexpr int KS = 4 * U;
-  if (ka < kz) load(0, ka);
-  for (int k = ka; k < kz; k += 2 * KS) {
-    if (k + KS < kz) load(1, k + KS);
-    mma(0);
-    if (k + KS >= kz) break;
-    if (k + 2 * KS < kz) load(0, k + 2 * KS);
-    mma(1);
+      if (c + 1 < nch) stage(ab ^ 1);
+      __syncthreads();
+    }
+  } else {
+    // double buffer unrolled by two so both buffer indices are constants (registers, not scratch)
+    if (ka < kz) load(0, ka);
+    for (int k = ka; k < kz; k += 2 * KS) {
+      if (k + KS < kz) load(1, k + KS);
+      mma(0);
+      if (k + KS >= kz) break;
+      if (k + 2 * KS < kz) load(0, k + 2 * KS);
+      mma(1);
+    }
   }
 
   // K groups of a column group -> the kg == 0 wave, in group order

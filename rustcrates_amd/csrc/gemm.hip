@@ -514,14 +514,15 @@ __global__ __launch_bounds__(256) void k_zgemm_skinny(const double2* __restrict_
 }
 
 // ===========================================================================
-// Wide skinny variant (outputs of 16K+ columns, no K split): a block owns all M
-// rows (RT tiles of 16) and 16*CW columns; its 4 waves are CW column groups x
-// (4/CW) K groups.  Each wave accumulates its 16RT x 16 tile with
-// v_mfma_f64_16x16x4_f64 from operands loaded straight from global memory
+// Wide skinny variant (vocab-wide outputs): a block owns all M rows (RT
+// tiles of 16) and 16*CW columns; its 4 waves are CW column groups x (4/CW) K
+// groups.  Each wave accumulates its 16RT x 16 tile with v_mfma_f64_16x16x4_f64
 // (A: row i, k offset lane/16; B: column i, k offset lane/16), double-buffered.
-// Waves sharing columns are summed through LDS; blockIdx.y splits K at most 8
-// ways (last-arrival completion).  Waves of one column group share the A rows
-// in L1, so wide outputs use CW = 4.  RE: only the real part is formed.
+// With CW = 4 (the planned shape) the activation rows come from LDS, staged
+// once per block; otherwise both operands are loaded from global memory and
+// waves sharing columns are summed through LDS.  blockIdx.y splits K at most 8
+// ways: EPI_PART leaves the partials, other modes complete in the last block
+// to arrive.  RE: only the real part is formed.
 // D[i][j] of row tile t sits at lane j + 16*(i%4), element i/4.
 // ===========================================================================
 template <int RT, bool RE, int CW, int U = 4>
@@ -677,6 +678,17 @@ __global__ __launch_bounds__(256) void k_zgemm_skinny_cols(const double2* __rest
           }
   }
   const bool owner = kg == 0;
+  if (ep.mode == EPI_PART) {  // the next launch sums the partials and applies what follows
+    if (owner)
+#pragma unroll
+      for (int t = 0; t < RT; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int m = 16 * t + 4 * e + kq;
+          if (m < M && n < N) ep.out[((long)blockIdx.y * M + m) * N + n] = make_double2(cr[t][e], ci[t][e]);
+        }
+    return;
+  }
   const int P = gridDim.y;
   if (P > 1) {
     if (owner)
@@ -769,14 +781,22 @@ static GemvPlan plan_gemv(int M, int N, int K, bool part) {
 struct SkinnyPlan {
   int rt, cw, ncb, kc, P;  // cw 4: the wide variant
 };
+// outputs at least this wide take the wide variant (a grid of 256 blocks
+// without a K split); measured at config 3, batch 32, the layer products
+// (1536 and 2048 columns) were slower in it with 8-way K splits than in the
+// narrow variant, whose partials are fewer
+constexpr int SKINNY_WIDE_N = 64 * 256;
 static SkinnyPlan plan_skinny(int M, int N, int K) {
   SkinnyPlan p;
   p.rt = cdiv_i(M, 16);
-  if (cdiv_i(N, 64) >= 256) {
+  if (N >= SKINNY_WIDE_N) {
+    // 64 columns per block, activation rows shared through LDS; K split over
+    // blocks for a grid of about 256 (one split for outputs that fill it)
     p.cw = 4;
     p.ncb = cdiv_i(N, 64);
-    p.kc = cdiv_i(K, 64) * 64;
-    p.P = 1;
+    const int P = std::min(SKINNY_MAX_SPLIT, std::max(1, cdiv_i(256, p.ncb)));
+    p.kc = cdiv_i(cdiv_i(K, P), 64) * 64;
+    p.P = cdiv_i(K, p.kc);
     return p;
   }
   p.cw = 0;
@@ -807,7 +827,7 @@ int gemm_parts(int M, int N, int K) {
   if (M <= 8) return plan_gemv(M, N, K, true).P;
   if (M <= SKINNY_MAX_M) {
     const SkinnyPlan p = plan_skinny(M, N, K);
-    return p.cw == 4 ? 0 : p.P;  // the wide-column variant takes no EPI_PART
+    return p.P;
   }
   return 0;
 }
@@ -890,7 +910,7 @@ int gemm(hipStream_t st, int M, int N, int K, const RowOps& ro, const double2* W
     if (M <= SKINNY_MAX_M) {
       const SkinnyPlan p = plan_skinny(M, N, K);
       if (p.ncb >= SYNC_COUNTERS) return ERR_ARG;
-      if (ep.mode == EPI_PART && (p.cw == 4 || am.part_v)) return ERR_ARG;
+      if (ep.mode == EPI_PART && am.part_v) return ERR_ARG;
       if (ep.mode == EPI_RE) launch_skinny<true>(st, p, ro, M, W, ldw, N, K, ep, am, sy);
       else launch_skinny<false>(st, p, ro, M, W, ldw, N, K, ep, am, sy);
       tiles = cdiv_i(N, 16);  // argmax partials per 16 columns

@@ -296,8 +296,8 @@ __device__ __forceinline__ void attn_chunk(const Attn& a, const double2* __restr
   }
 }
 
-// The grid covers at most DEC_MAX_BLOCKS blocks (about the blocks resident on
-// the chip at once) whatever the cache length the launch was sized for: the
+// The grid covers at most the blocks resident on the chip at once (and at most
+// DEC_MAX_BLOCKS) whatever the cache length the launch was sized for: the
 // blocks walk the chunks the sequences have now, item = (sequence, head,
 // chunk) in that order, so no block starts only to find its chunk empty (a
 // graph replays one grid while the caches grow).  Up to 256 sequences; with
@@ -341,6 +341,27 @@ __global__ __launch_bounds__(256) void k_attention_split(Attn a, const double2* 
   }
 }
 
+// Blocks of k_attention_split<DH> resident on the device at once (occupancy x
+// CUs, at most DEC_MAX_BLOCKS): a compact grid no larger runs in one round.
+// Asked once per head-dim variant; the query enqueues nothing, so it is safe
+// while a graph is being captured.
+static int split_resident_blocks(int dh) {
+  static int cached[5] = {0, 0, 0, 0, 0};
+  const int slot = dh == 16 ? 0 : dh == 32 ? 1 : dh == 64 ? 2 : dh == 128 ? 3 : 4;
+  if (cached[slot] > 0) return cached[slot];
+  const void* k = slot == 0 ? (const void*)k_attention_split<16>
+                : slot == 1 ? (const void*)k_attention_split<32>
+                : slot == 2 ? (const void*)k_attention_split<64>
+                : slot == 3 ? (const void*)k_attention_split<128>
+                            : (const void*)k_attention_split<0>;
+  int dev = 0, cus = 0, occ = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k, 256, 0) != hipSuccess || cus <= 0 || occ <= 0)
+    return DEC_MAX_BLOCKS;
+  cached[slot] = std::min(DEC_MAX_BLOCKS, occ * cus);
+  return cached[slot];
+}
+
 AttnSplit attention_split_plan(const Attn& a) {
   AttnSplit o;
   o.H = a.H;
@@ -364,7 +385,7 @@ int attention_decode_split(hipStream_t st, const Attn& a, const double2* q, long
   if (append && (!a.kc_w || !a.vc_w)) return ERR_ARG;
   const long items = (long)o.nsplit * a.H * a.B;
   const int compact = a.B <= DEC_COMPACT_MAX_B ? 1 : 0;
-  const dim3 grid = compact ? dim3((unsigned)std::min<long>(items, DEC_MAX_BLOCKS)) : dim3(o.nsplit, a.H, a.B);
+  const dim3 grid = compact ? dim3((unsigned)std::min<long>(items, split_resident_blocks(a.dh))) : dim3(o.nsplit, a.H, a.B);
   const int ap = append ? 1 : 0;
   switch (a.dh) {
     case 16: MITOK_LAUNCH(k_attention_split<16>, grid, dim3(256), 0, st, a, q, ldq, npart, part_stride, ap, o, compact); break;

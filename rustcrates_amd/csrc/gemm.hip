@@ -514,6 +514,91 @@ __global__ __launch_bounds__(256) void k_zgemm_skinny(const double2* __restrict_
 }
 
 // ===========================================================================
+// Row-tile skinny variant (9 <= M <= 64, layer-wide outputs).  Block (bx, by,
+// bz) owns CT column tiles of 16 at bx, the 16-row tile by and K range bz of
+// 16*nkw; its 4 waves split that range, nkw k-steps of 4 each.  Per k-step a
+// wave loads one activation fragment and CT weight fragments and issues 4*CT
+// v_mfma_f64_16x16x4_f64 (A: row i, k offset lane/16; B: column i).  Three
+// batches of 4 k-steps are in flight ahead of the one being multiplied.  The
+// waves' tiles are summed through LDS in wave order.  One row tile per block
+// gives two or more blocks per column tile, so an output as wide as the FFN's
+// hidden layer fills the chip without a K split and its epilogue (GELU) runs
+// in the same block; EPI_PART leaves gridDim.z partials for the consumer.
+// D[i][j] sits at lane j + 16*(i%4), element i/4.
+// ===========================================================================
+template <int CT>
+__global__ __launch_bounds__(256) void k_zgemm_skinny_rows(const double2* __restrict__ X, long ldx, int M,
+                                                         const double2* __restrict__ W, long ldw, int N, int K,
+                                                         int nkw, Epi ep) {
+  constexpr int U = 4;  // k-steps per batch
+  __shared__ double2 red[4][16][16 * CT + 1];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int i = lane & 15, kq = lane >> 4;
+  const int n0 = blockIdx.x * 16 * CT, m = blockIdx.y * 16 + i;
+  const int ka = (blockIdx.z * 4 + wave) * 4 * nkw, kz = min(K, ka + 4 * nkw);
+  double2 a[3][U], b[3][U][CT];
+  auto load = [&](int s, int k) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int kk = k + 4 * u + kq;
+#pragma unroll
+      for (int c = 0; c < CT; ++c) {
+        const int n = n0 + 16 * c + i;
+        b[s][u][c] = (kk < kz && n < N) ? W[(long)kk * ldw + n] : make_double2(0.0, 0.0);
+      }
+      a[s][u] = (kk < kz && m < M) ? X[(long)m * ldx + kk] : make_double2(0.0, 0.0);
+    }
+  };
+  v4d cr[CT], ci[CT];
+#pragma unroll
+  for (int c = 0; c < CT; ++c) cr[c] = ci[c] = v4d{0.0, 0.0, 0.0, 0.0};
+  // the real-part products of the batch before its imaginary-part ones: two
+  // MFMAs on one accumulator are never adjacent
+  auto mma = [&](int s) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+#pragma unroll
+      for (int c = 0; c < CT; ++c) {
+        cr[c] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[s][u].x, b[s][u][c].x, cr[c], 0, 0, 0);
+        ci[c] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[s][u].x, b[s][u][c].y, ci[c], 0, 0, 0);
+      }
+#pragma unroll
+      for (int c = 0; c < CT; ++c) {
+        cr[c] = __builtin_amdgcn_mfma_f64_16x16x4f64(-a[s][u].y, b[s][u][c].y, cr[c], 0, 0, 0);
+        ci[c] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[s][u].y, b[s][u][c].x, ci[c], 0, 0, 0);
+      }
+    }
+  };
+  constexpr int KS = 4 * U;  // k per batch; the loop is unrolled by three so buffer indices are constants
+  load(0, ka);
+  load(1, ka + KS);
+  load(2, ka + 2 * KS);
+  for (int k = ka; k < kz; k += 3 * KS) {
+    mma(0);
+    if (k + 3 * KS < kz) load(0, k + 3 * KS);
+    if (k + KS >= kz) break;
+    mma(1);
+    if (k + 4 * KS < kz) load(1, k + 4 * KS);
+    if (k + 2 * KS >= kz) break;
+    mma(2);
+    if (k + 5 * KS < kz) load(2, k + 5 * KS);
+  }
+#pragma unroll
+  for (int c = 0; c < CT; ++c)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) red[wave][4 * e + kq][16 * c + i] = make_double2(cr[c][e], ci[c][e]);
+  __syncthreads();
+  for (int idx = tid; idx < 16 * 16 * CT; idx += 256) {
+    const int row = idx / (16 * CT), col = idx - row * 16 * CT;
+    const double2 v = cadd(cadd(cadd(red[0][row][col], red[1][row][col]), red[2][row][col]), red[3][row][col]);
+    const int n = n0 + col, mm = blockIdx.y * 16 + row;
+    if (mm >= M || n >= N) continue;
+    if (ep.mode == EPI_PART) ep.out[((long)blockIdx.z * M + mm) * N + n] = v;
+    else apply_epi(ep, M, N, mm, n, v);
+  }
+}
+
+// ===========================================================================
 // Wide skinny variant (vocab-wide outputs): a block owns all M rows (RT
 // tiles of 16) and 16*CW columns; its 4 waves are CW column groups x (4/CW) K
 // groups.  Each wave accumulates its 16RT x 16 tile with v_mfma_f64_16x16x4_f64
@@ -780,6 +865,7 @@ static GemvPlan plan_gemv(int M, int N, int K, bool part) {
 // SKINNY_MAX_SPLIT ways)
 struct SkinnyPlan {
   int rt, cw, ncb, kc, P;  // cw 4: the wide variant
+  int rows = 0, ct = 1, nkw = 0;  // rows: the row-tile variant, CT column tiles, nkw k-steps per wave
 };
 // outputs at least this wide take the wide variant (a grid of 256 blocks
 // without a K split); measured at config 3, batch 32, the layer products
@@ -790,7 +876,18 @@ constexpr int SKINNY_WIDE_N = 64 * 256;
 // config 3, batch 32 (layer products per generate call): 128 -> 39.4 ms,
 // 512 -> 32.7 ms, 1024 -> 34.9 ms (more partials for the consumers)
 constexpr int SKINNY_TARGET_BLOCKS = 512;
-static SkinnyPlan plan_skinny(int M, int N, int K) {
+// Row-tile variant: about this many MFMAs per wave.  Measured alone on MI355X
+// at config 3, batch 32 (weights streamed from HBM), against the narrow
+// variant: QKV (2 splits, CT 2) 10.4 -> 8.7 us; FFN Dense with no split
+// (GELU in the block) 10.3 -> 9.1 us before the narrow variant's split
+// completion; FFN Linear (4 splits) 10.2 -> 9.2 us with half the partials.
+// 64 and 256 MFMAs per wave measured slower.
+constexpr int SKINNY_ROWS_MFMA = 128;
+constexpr int SKINNY_ROWS_MAX_NKW = 64;     // k-steps per wave of a product that may not split K
+constexpr int SKINNY_ROWS_MIN_BLOCKS = 128;  // fewer: the chip is less than half busy
+// argmax: the fused greedy id needs per-tile partials, which only the narrow
+// and wide variants leave
+static SkinnyPlan plan_skinny(int M, int N, int K, bool part, bool argmax) {
   SkinnyPlan p;
   p.rt = cdiv_i(M, 16);
   if (N >= SKINNY_WIDE_N) {
@@ -804,6 +901,29 @@ static SkinnyPlan plan_skinny(int M, int N, int K) {
     return p;
   }
   p.cw = 0;
+  if (!argmax) {
+    SkinnyPlan r = p;
+    const int tiles = cdiv_i(N, 16) * p.rt;  // 16x16 output tiles
+    r.rows = 1;
+    r.ct = (part && tiles >= 128) ? 2 : 1;
+    r.ncb = cdiv_i(N, 16 * r.ct);
+    r.nkw = SKINNY_ROWS_MFMA / (4 * r.ct);
+    int P = cdiv_i(K, 16 * r.nkw);
+    if (part) {
+      // at most SKINNY_MAX_SPLIT partials; more splits (shorter waves) for a
+      // grid that would leave most of the chip idle
+      const int fill = std::min(SKINNY_MAX_SPLIT, cdiv_i(192, r.ncb * p.rt));
+      P = std::min(SKINNY_MAX_SPLIT, std::max(P, fill));
+      r.nkw = cdiv_i(cdiv_i(K, 16 * P), 4) * 4;
+      P = cdiv_i(K, 16 * r.nkw);
+    } else if (P > 1) {
+      r.nkw = cdiv_i(cdiv_i(K, 16), 4) * 4;
+      P = 1;
+    }
+    r.P = P;
+    r.kc = 16 * r.nkw;
+    if (r.nkw <= SKINNY_ROWS_MAX_NKW && (part || (long)r.ncb * p.rt >= SKINNY_ROWS_MIN_BLOCKS)) return r;
+  }
   p.ncb = cdiv_i(N, 16);
   const int P = std::min(SKINNY_MAX_SPLIT, std::max(1, cdiv_i(SKINNY_TARGET_BLOCKS, p.ncb)));
   p.kc = cdiv_i(cdiv_i(K, P), 64) * 64;
@@ -830,7 +950,7 @@ constexpr int SKINNY_MAX_M = 64;
 int gemm_parts(int M, int N, int K) {
   if (M <= 8) return plan_gemv(M, N, K, true).P;
   if (M <= SKINNY_MAX_M) {
-    const SkinnyPlan p = plan_skinny(M, N, K);
+    const SkinnyPlan p = plan_skinny(M, N, K, true, false);
     return p.P;
   }
   return 0;
@@ -839,7 +959,7 @@ int gemm_parts(int M, int N, int K) {
 size_t gemm_ws_bytes(int M, int N, int K) {
   int P;
   if (M <= 8) P = plan_gemv(M, N, K, false).P;
-  else if (M <= SKINNY_MAX_M) P = plan_skinny(M, N, K).P;
+  else if (M <= SKINNY_MAX_M) P = plan_skinny(M, N, K, false, true).P;  // the largest split workspace
   else P = plan_mfma(M, N, K).P;
   return P > 1 ? (size_t)P * M * N * sizeof(double2) : 0;
 }
@@ -874,6 +994,12 @@ static void launch_skinny(hipStream_t st, const SkinnyPlan& p, const RowOps& ro,
                           int N, int K, const Epi& ep, const Argmax& am, const Sync& sy) {
   const dim3 grid(p.ncb, p.P), blk(256);
   double2* ws = (double2*)sy.ws;
+  if (p.rows) {  // EPI_PART, or one K range per block (no argmax: not a vocab-wide output)
+    const dim3 g3(p.ncb, p.rt, p.P);
+    if (p.ct == 2) MITOK_LAUNCH(k_zgemm_skinny_rows<2>, g3, blk, 0, st, ro.x, ro.ldx, M, W, ldw, N, K, p.nkw, ep);
+    else MITOK_LAUNCH(k_zgemm_skinny_rows<1>, g3, blk, 0, st, ro.x, ro.ldx, M, W, ldw, N, K, p.nkw, ep);
+    return;
+  }
   if (p.cw == 4) {
     switch (p.rt) {
       case 1: MITOK_LAUNCH((k_zgemm_skinny_cols<1, RE, 4>), grid, blk, 0, st, ro.x, ro.ldx, M, W, ldw, N, K, p.kc, ep, am, ws, sy.counters); break;
@@ -912,7 +1038,7 @@ int gemm(hipStream_t st, int M, int N, int K, const RowOps& ro, const double2* W
   } else {
     if (!ro.plain()) return ERR_ARG;  // the MFMA paths read plain rows
     if (M <= SKINNY_MAX_M) {
-      const SkinnyPlan p = plan_skinny(M, N, K);
+      const SkinnyPlan p = plan_skinny(M, N, K, ep.mode == EPI_PART, am.part_v != nullptr);
       if (p.ncb >= SYNC_COUNTERS) return ERR_ARG;
       if (ep.mode == EPI_PART && am.part_v) return ERR_ARG;
       if (ep.mode == EPI_RE) launch_skinny<true>(st, p, ro, M, W, ldw, N, K, ep, am, sy);

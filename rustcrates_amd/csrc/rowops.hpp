@@ -351,7 +351,6 @@ __device__ void ro_build(const RowOps& r, int M, int K, int ka, int RL, int n0, 
 #pragma unroll
     for (int j = 0; j < 2 * MR; ++j) red_v[wave][j] = a[j];
   __syncthreads();
-  const int w = n1 - n0;
   if (MR == 1) {
     // one row: every thread takes the square root itself rather than waiting
     // at another barrier for one thread's

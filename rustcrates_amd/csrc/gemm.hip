@@ -32,7 +32,19 @@ __global__ __launch_bounds__(256) void k_argmax_finalize(Argmax am, int tiles) {
   const int m = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   double bv = -INFINITY;
   int bi = -1;
-  for (int t = tid; t < tiles; t += 256) argmax_combine(bv, bi, am.part_v[(long)m * tiles + t], am.part_i[(long)m * tiles + t]);
+  constexpr int U = 8;  // partials per thread requested together (one memory round trip up to 2048 tiles)
+  for (int t0 = tid; t0 < tiles; t0 += 256 * U) {
+    double v[U];
+    int ix[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int t = t0 + 256 * u;
+      v[u] = t < tiles ? am.part_v[(long)m * tiles + t] : -INFINITY;
+      ix[u] = t < tiles ? am.part_i[(long)m * tiles + t] : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) argmax_combine(bv, bi, v[u], ix[u]);
+  }
   wave_argmax(bv, bi);
   if (lane == 0) sv[wave] = bv, si[wave] = bi;
   __syncthreads();
@@ -197,6 +209,69 @@ __global__ __launch_bounds__(256) void k_gemv(RowOps ro, int M, const double2* _
     }
 }
 
+// The attention-combine row transform (chunk combine, residual, LayerNorm) of
+// row m with its two memory round trips overlapped: this thread's chunk
+// outputs (the first RO_ATT_CH chunks of each of its columns) and residuals
+// are requested before ro_prepare asks for the chunks' (max, sum).  The sums
+// run in ro_base's order and the LayerNorm is ro_build's (ro_ln), so the row
+// is the one ro_build would give.
+constexpr int RO_ATT_CH = 8, RO_ATT_EPT = 4;
+__device__ __forceinline__ bool rowops_att_ok(const RowOps& ro, int K) {
+  return ro.att.po && !ro.table && !ro.rope_cs && !ro.bias && !ro.gelu && !ro.finite_check && K <= 256 * RO_ATT_EPT;
+}
+__device__ void rowops_att(const RowOps& ro, int K, int m, double2* buf, const RoLds& L, double2* st_mean,
+                           double2* st_sd) {
+  const AttnSplit& a = ro.att;
+  const int tid = threadIdx.x;
+  const int ns = (a.kv_len[m] + 1 + a.CH - 1) / a.CH;
+  double2 gpre[LN_PRE], bpre[LN_PRE];
+#pragma unroll
+  for (int j = 0; j < LN_PRE; ++j) {
+    const int k = tid + 256 * j;
+    const bool ok = ro.ln && k < K;
+    gpre[j] = ok ? ro.gamma[k] : make_double2(0.0, 0.0);
+    bpre[j] = ok ? ro.beta[k] : make_double2(0.0, 0.0);
+  }
+  double2 t[RO_ATT_EPT][RO_ATT_CH], rs[RO_ATT_EPT];
+#pragma unroll
+  for (int j = 0; j < RO_ATT_EPT; ++j) {
+    const int k = tid + 256 * j;
+    const bool ok = k < K;
+    const int h = k / a.dh, e = k - h * a.dh;
+    const long base = ((long)m * a.H + h) * a.nsplit;
+#pragma unroll
+    for (int q = 0; q < RO_ATT_CH; ++q) t[j][q] = (ok && q < ns) ? a.po[(base + q) * a.dh + e] : make_double2(0.0, 0.0);
+    rs[j] = (ok && ro.resid) ? ro.resid[(long)m * ro.ldr + k] : make_double2(0.0, 0.0);
+  }
+  ro_prepare(ro, 1, L);
+#pragma unroll
+  for (int j = 0; j < RO_ATT_EPT; ++j) {
+    const int k = tid + 256 * j;
+    if (k >= K) continue;
+    const int h = k / a.dh, e = k - h * a.dh;
+    const long base = ((long)m * a.H + h) * a.nsplit;
+    const double* w = L.wts + (long)h * a.nsplit;
+    double2 o = make_double2(0.0, 0.0);
+#pragma unroll
+    for (int q = 0; q < RO_ATT_CH; ++q)
+      if (q < ns) {
+        o.x += t[j][q].x * w[q];
+        o.y += t[j][q].y * w[q];
+      }
+    for (int q = RO_ATT_CH; q < ns; ++q) {  // longer caches: the remaining chunks one by one
+      const double2 v = a.po[(base + q) * a.dh + e];
+      o.x += v.x * w[q];
+      o.y += v.y * w[q];
+    }
+    const double l = L.lsum[h];
+    double2 v = make_double2(o.x / l, o.y / l);
+    if (ro.resid) v = make_double2(v.x + rs[j].x, 0.0);
+    buf[k] = v;
+  }
+  __syncthreads();
+  if (ro.ln) ro_ln<1>(ro, 1, K, K, 0, K, buf, st_mean, st_sd, gpre, bpre);
+}
+
 // The prologue alone, one block per row.
 __global__ __launch_bounds__(256) void k_rowops(RowOps ro, int K, double2* __restrict__ out, long ldo) {
   extern __shared__ double2 lds2[];  // the row [K], then the attention-combine weights
@@ -206,8 +281,12 @@ __global__ __launch_bounds__(256) void k_rowops(RowOps ro, int K, double2* __res
   L.wts = (double*)(lds2 + K);
   L.lsum = L.wts + (ro.att.po ? (size_t)ro.att.H * ro.att.nsplit : 0);
   L.m0 = m;
-  ro_prepare(ro, 1, L);
-  ro_build<1>(ro, 1, K, 0, K, 0, K, lds2, L, st_mean, st_sd);
+  if (rowops_att_ok(ro, K)) {
+    rowops_att(ro, K, m, lds2, L, st_mean, st_sd);
+  } else {
+    ro_prepare(ro, 1, L);
+    ro_build<1>(ro, 1, K, 0, K, 0, K, lds2, L, st_mean, st_sd);
+  }
   if (threadIdx.x == 0) ro_check(ro, m);
   for (int k = threadIdx.x; k < K; k += 256) {
     const double2 v = lds2[k];

@@ -241,66 +241,15 @@ __device__ void ro_stats(const RowOps& r, int M, int K, const RoLds& L, double2*
 // [n0, n1) is normalised; RoPE pairs must not straddle the range (ka even).
 // Every source element is loaded once; statistics are taken from LDS.
 // Block-wide; all threads call it; ends with a barrier.
+// The LayerNorm of rows m < M (M <= MR) held in LDS at buf[m * RL + k]
+// (the whole row: ka = 0, RL = K), normalising columns [n0, n1) in place.
+// gpre/bpre: gamma and beta of this thread's first LN_PRE columns, requested
+// by the caller with the source rows.  Block-wide; ends with a barrier.
 template <int MR, class Acc = AccPlain>
-__device__ void ro_build(const RowOps& r, int M, int K, int ka, int RL, int n0, int n1, double2* buf, const RoLds& L,
-                         double2* st_mean, double2* st_sd) {
+__device__ void ro_ln(const RowOps& r, int M, int K, int RL, int n0, int n1, double2* buf, double2* st_mean,
+                      double2* st_sd, const double2 (&gpre)[LN_PRE], const double2 (&bpre)[LN_PRE]) {
   __shared__ double red_s[4][2 * MR], red_v[4][2 * MR];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  // the LayerNorm's gamma and beta of this thread's first columns are
-  // requested with the source rows, not after the statistics
-  double2 gpre[LN_PRE], bpre[LN_PRE];
-#pragma unroll
-  for (int j = 0; j < LN_PRE; ++j) {
-    const int k = n0 + tid + 256 * j;
-    const bool ok = r.ln && k < n1;
-    gpre[j] = ok ? Acc::c(r.gamma + k) : make_double2(0.0, 0.0);
-    bpre[j] = ok ? Acc::c(r.beta + k) : make_double2(0.0, 0.0);
-  }
-  // pass 1: every source element once, four per thread with their loads in
-  // flight together; without RoPE the residual joins here
-  const bool res1 = r.resid && !r.rope_cs;
-  const int tot = MR * RL;
-  for (int i0 = tid; i0 < tot; i0 += 4 * 256) {
-    double2 v[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int i = i0 + u * 256;
-      const int m = i / RL, k = ka + (i - m * RL);
-      const bool ok = i < tot && m < M && k < K;
-      v[u] = ok ? ro_base<Acc>(r, L.m0 + m, k, K, L) : make_double2(0.0, 0.0);
-      if (res1 && ok) v[u] = make_double2(v[u].x + Acc::ld(r.resid + (long)(L.m0 + m) * r.ldr + k).x, 0.0);
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u)
-      if (i0 + u * 256 < tot) buf[i0 + u * 256] = v[u];
-  }
-  __syncthreads();
-  if (r.rope_cs) {
-    const int half = (RL + 1) / 2;
-    for (int i = tid; i < MR * half; i += 256) {
-      const int m = i / half, j = i - m * half, k = ka + 2 * j;
-      if (m >= M || k >= K) continue;
-      const int gm = L.m0 + m;
-      const bool pair = 2 * j + 1 < RL && k + 1 < K;  // always true with RoPE (even K, even range)
-      double2 e = buf[m * RL + 2 * j], o = pair ? buf[m * RL + 2 * j + 1] : make_double2(0.0, 0.0);
-      if (r.rope_cs) {
-        const int p = min(Acc::kv(r.rope_pos, gm), r.rope_max - 1);  // overflow flagged by ro_check
-        const double2 t = Acc::c(r.rope_cs + (long)p * (K >> 1) + (k >> 1));
-        const double2 e2 = make_double2(e.x * t.x - o.x * t.y, e.y * t.x - o.y * t.y);
-        const double2 o2 = make_double2(e.x * t.y + o.x * t.x, e.y * t.y + o.y * t.x);
-        e = e2;
-        o = o2;
-      }
-      if (r.resid) {
-        e = make_double2(e.x + Acc::ld(r.resid + (long)gm * r.ldr + k).x, 0.0);
-        if (pair) o = make_double2(o.x + Acc::ld(r.resid + (long)gm * r.ldr + k + 1).x, 0.0);
-      }
-      buf[m * RL + 2 * j] = e;
-      if (pair) buf[m * RL + 2 * j + 1] = o;
-    }
-    __syncthreads();
-  }
-  if (!r.ln) return;
   const double len = (double)K;
   double a[2 * MR];
 #pragma unroll
@@ -384,6 +333,68 @@ __device__ void ro_build(const RowOps& r, int M, int K, int ka, int RL, int n0, 
     }
   }
   __syncthreads();
+}
+
+template <int MR, class Acc = AccPlain>
+__device__ void ro_build(const RowOps& r, int M, int K, int ka, int RL, int n0, int n1, double2* buf, const RoLds& L,
+                         double2* st_mean, double2* st_sd) {
+  const int tid = threadIdx.x;
+  // the LayerNorm's gamma and beta of this thread's first columns are
+  // requested with the source rows, not after the statistics
+  double2 gpre[LN_PRE], bpre[LN_PRE];
+#pragma unroll
+  for (int j = 0; j < LN_PRE; ++j) {
+    const int k = n0 + tid + 256 * j;
+    const bool ok = r.ln && k < n1;
+    gpre[j] = ok ? Acc::c(r.gamma + k) : make_double2(0.0, 0.0);
+    bpre[j] = ok ? Acc::c(r.beta + k) : make_double2(0.0, 0.0);
+  }
+  // pass 1: every source element once, four per thread with their loads in
+  // flight together; without RoPE the residual joins here
+  const bool res1 = r.resid && !r.rope_cs;
+  const int tot = MR * RL;
+  for (int i0 = tid; i0 < tot; i0 += 4 * 256) {
+    double2 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = i0 + u * 256;
+      const int m = i / RL, k = ka + (i - m * RL);
+      const bool ok = i < tot && m < M && k < K;
+      v[u] = ok ? ro_base<Acc>(r, L.m0 + m, k, K, L) : make_double2(0.0, 0.0);
+      if (res1 && ok) v[u] = make_double2(v[u].x + Acc::ld(r.resid + (long)(L.m0 + m) * r.ldr + k).x, 0.0);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (i0 + u * 256 < tot) buf[i0 + u * 256] = v[u];
+  }
+  __syncthreads();
+  if (r.rope_cs) {
+    const int half = (RL + 1) / 2;
+    for (int i = tid; i < MR * half; i += 256) {
+      const int m = i / half, j = i - m * half, k = ka + 2 * j;
+      if (m >= M || k >= K) continue;
+      const int gm = L.m0 + m;
+      const bool pair = 2 * j + 1 < RL && k + 1 < K;  // always true with RoPE (even K, even range)
+      double2 e = buf[m * RL + 2 * j], o = pair ? buf[m * RL + 2 * j + 1] : make_double2(0.0, 0.0);
+      if (r.rope_cs) {
+        const int p = min(Acc::kv(r.rope_pos, gm), r.rope_max - 1);  // overflow flagged by ro_check
+        const double2 t = Acc::c(r.rope_cs + (long)p * (K >> 1) + (k >> 1));
+        const double2 e2 = make_double2(e.x * t.x - o.x * t.y, e.y * t.x - o.y * t.y);
+        const double2 o2 = make_double2(e.x * t.y + o.x * t.x, e.y * t.y + o.y * t.x);
+        e = e2;
+        o = o2;
+      }
+      if (r.resid) {
+        e = make_double2(e.x + Acc::ld(r.resid + (long)gm * r.ldr + k).x, 0.0);
+        if (pair) o = make_double2(o.x + Acc::ld(r.resid + (long)gm * r.ldr + k + 1).x, 0.0);
+      }
+      buf[m * RL + 2 * j] = e;
+      if (pair) buf[m * RL + 2 * j + 1] = o;
+    }
+    __syncthreads();
+  }
+  if (!r.ln) return;
+  ro_ln<MR, Acc>(r, M, K, RL, n0, n1, buf, st_mean, st_sd, gpre, bpre);
 }
 
 }  // namespace mitok

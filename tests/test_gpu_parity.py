@@ -106,6 +106,9 @@ def test_linear_reference_known_answer():
 @pytest.mark.parametrize("M,K,N", [(1, 512, 1536), (2, 300, 77), (8, 2048, 512), (1, 512, 32000), (5, 768, 20000),
                                    (9, 64, 33), (16, 512, 1536), (32, 512, 2048), (40, 300, 77), (64, 2048, 512),
                                    (20, 96, 9000),
+                                   # row-tile MFMA products: a partial row tile, partial column
+                                   # tiles, K ranges that end inside a wave's batch
+                                   (33, 700, 4100), (64, 1000, 2050), (17, 1024, 3000),
                                    (100, 96, 130), (4096, 64, 64)])
 def test_gemm_random_vs_oracle(M, K, N):
     rng = np.random.default_rng(M * 7 + K)

@@ -17,7 +17,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 SRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libmitok.so")
-SOURCES = ["kernels.hip", "gemm.hip", "attention.hip", "resident.hip", "resident_k1.hip", "resident_k2.hip",
+SOURCES = ["kernels.hip", "gemm.hip", "gemm_mfma.hip", "attention.hip", "resident.hip", "resident_k1.hip", "resident_k2.hip",
            "resident_k4.hip", "resident_k8.hip", "network.hip"]
 ARCH = os.environ.get("MITOK_ARCH", "gfx950")
 
@@ -30,9 +30,14 @@ CFLAGS = [
 ]
 
 
+# per-file flags: the prompt-pass GEMM keeps its MFMA accumulators in VGPRs
+# (the reason is in gemm_mfma.hip's header)
+FILE_FLAGS = {"gemm_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
-    cmd = [HIPCC, *CFLAGS, "-c", os.path.join(SRC, src), "-o", obj]
+    cmd = [HIPCC, *CFLAGS, *FILE_FLAGS.get(src, []), "-c", os.path.join(SRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stderr}")

@@ -300,163 +300,6 @@ void rowops_apply(hipStream_t st, int M, int K, const RowOps& ro, double2* out, 
   if (M > 0) MITOK_LAUNCH(k_rowops, dim3(M), dim3(256), shm, st, ro, K, out, ldo);
 }
 
-// ===========================================================================
-// MFMA complex GEMM.  Block tile 64x64 (4 waves of 32x32), K step 16, operands
-// de-interleaved into re/im planes in LDS (double-buffered).  Per 16x16x4 step
-// a wave issues 4 v_mfma_f64_16x16x4_f64 per output tile:
-//     Cr += Ar*Br;  Cr += (-Ai)*Bi;  Ci += Ar*Bi;  Ci += Ai*Br
-// Lane layout of v_mfma_f64_16x16x4_f64 (wave64): A[i][k] at lane i+16k,
-// B[k][j] at lane j+16k, D[i][j] at lane j+16*(i%4), element i/4 (unlike the
-// f32 16x16x4 form, consecutive output rows sit in consecutive lane groups).
-// blockIdx.z splits K; the last block of a tile sums the partials.
-// ===========================================================================
-constexpr int GBM = 64, GBN = 64, GBK = 16, GPAD = 4;
-
-__global__ __launch_bounds__(256) void k_zgemm_mfma(const double2* __restrict__ A, long lda,
-                                                       const double2* __restrict__ Bm, long ldb, int M, int N, int K,
-                                                       int kchunk, Epi ep, Argmax am, double2* __restrict__ ws,
-                                                       uint32_t* __restrict__ cnt) {
-  __shared__ double As[2][2][GBK][GBM + GPAD];
-  __shared__ double Bs[2][2][GBK][GBN + GPAD];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int m0 = blockIdx.y * GBM, n0 = blockIdx.x * GBN;
-  const int kbeg = blockIdx.z * kchunk;
-  const int kend = min(K, kbeg + kchunk);
-  const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
-  const int a_row = tid >> 2, a_k = (tid & 3) * 4;
-  const int b_k = tid >> 4, b_n = (tid & 15) * 4;
-
-  double2 ra[4], rb[4];
-  auto gload = [&](int k0) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      int m = m0 + a_row, k = k0 + a_k + i;
-      ra[i] = (m < M && k < kend) ? A[(long)m * lda + k] : make_double2(0.0, 0.0);
-      int kb = k0 + b_k, n = n0 + b_n + i;
-      rb[i] = (kb < kend && n < N) ? Bm[(long)kb * ldb + n] : make_double2(0.0, 0.0);
-    }
-  };
-  auto sstore = [&](int st) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      As[st][0][a_k + i][a_row] = ra[i].x;
-      As[st][1][a_k + i][a_row] = ra[i].y;
-      Bs[st][0][b_k][b_n + i] = rb[i].x;
-      Bs[st][1][b_k][b_n + i] = rb[i].y;
-    }
-  };
-
-  v4d cr[2][2], ci[2][2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) cr[i][j] = ci[i][j] = v4d{0.0, 0.0, 0.0, 0.0};
-
-  const int nk = kend > kbeg ? (kend - kbeg + GBK - 1) / GBK : 0;
-  if (nk > 0) {
-    gload(kbeg);
-    sstore(0);
-  }
-  __syncthreads();
-  for (int it = 0; it < nk; ++it) {
-    const int st = it & 1;
-    if (it + 1 < nk) gload(kbeg + (it + 1) * GBK);
-#pragma unroll
-    for (int kk = 0; kk < GBK; kk += 4) {
-      const int kr = kk + (lane >> 4);
-      double ar[2], ai[2], br[2], bi[2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        ar[i] = As[st][0][kr][wm + 16 * i + (lane & 15)];
-        ai[i] = As[st][1][kr][wm + 16 * i + (lane & 15)];
-        br[i] = Bs[st][0][kr][wn + 16 * i + (lane & 15)];
-        bi[i] = Bs[st][1][kr][wn + 16 * i + (lane & 15)];
-      }
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          cr[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(ar[i], br[j], cr[i][j], 0, 0, 0);
-          ci[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(ar[i], bi[j], ci[i][j], 0, 0, 0);
-          cr[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(-ai[i], bi[j], cr[i][j], 0, 0, 0);
-          ci[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(ai[i], br[j], ci[i][j], 0, 0, 0);
-        }
-    }
-    if (it + 1 < nk) sstore(st ^ 1);
-    __syncthreads();
-  }
-
-  // Re values of the tile for the fused argmax, staged in the (now idle) As buffer
-  double* stage = &As[0][0][0][0];  // [64][65]
-  const bool argmax = am.part_v != nullptr;
-  if (gridDim.z == 1) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int ml = wm + 16 * i + (lane >> 4) + 4 * r, nl = wn + 16 * j + (lane & 15);
-          const int m = m0 + ml, n = n0 + nl;
-          if (m < M && n < N) {
-            const double re = apply_epi(ep, M, N, m, n, make_double2(cr[i][j][r], ci[i][j][r]));
-            if (argmax) stage[ml * 65 + nl] = re;
-          }
-        }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int m = m0 + wm + 16 * i + (lane >> 4) + 4 * r;
-          const int n = n0 + wn + 16 * j + (lane & 15);
-          if (m < M && n < N) st_dev(&ws[((long)blockIdx.z * M + m) * N + n], make_double2(cr[i][j][r], ci[i][j][r]));
-        }
-    if (!arrive_last(&cnt[blockIdx.y * gridDim.x + blockIdx.x], gridDim.z)) return;
-    // thread t owns tile elements t + 256 i (row t/64 + 4i, column t%64); the
-    // splits are summed in order, 16 independent loads in flight per split
-    const int P = gridDim.z;
-    const int nl = tid & 63, n = n0 + nl;
-    double2 v[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) v[i] = make_double2(0.0, 0.0);
-    for (int p = 0; p < P; ++p)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int m = m0 + (tid >> 6) + 4 * i;
-        if (m < M && n < N) v[i] = cadd(v[i], ld_dev(&ws[((long)p * M + m) * N + n]));
-      }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int ml = (tid >> 6) + 4 * i, m = m0 + ml;
-      if (m < M && n < N) {
-        const double re = apply_epi(ep, M, N, m, n, v[i]);
-        if (argmax) stage[ml * 65 + nl] = re;
-      }
-    }
-  }
-  if (!argmax) return;
-  __syncthreads();
-  // per-row (max, last index) over the tile's columns: wave w takes rows w, w+4, ...
-  for (int ml = wave; ml < GBM; ml += 4) {
-    const int m = m0 + ml, n = n0 + lane;
-    if (m >= M) break;
-    double bv = -INFINITY;
-    int bi = -1;
-    if (n < N) {
-      const double v = stage[ml * 65 + lane];
-      if (isnan(v)) atomicOr(am.err, (uint32_t)EB_ARGMAX_NAN);
-      else bv = v, bi = n;
-    }
-    wave_argmax(bv, bi);
-    if (lane == 0) {
-      am.part_v[(long)m * gridDim.x + blockIdx.x] = bv;
-      am.part_i[(long)m * gridDim.x + blockIdx.x] = bi;
-    }
-  }
-}
 
 template <int RT, bool RE>
 __global__ __launch_bounds__(256) void k_zgemm_skinny(const double2* __restrict__ X, long ldx, int M,
@@ -1128,8 +971,8 @@ int gemm(hipStream_t st, int M, int N, int K, const RowOps& ro, const double2* W
       const MfmaPlan p = plan_mfma(M, N, K);
       if (p.P > 1 && (long)p.mt * p.nt >= SYNC_COUNTERS) return ERR_ARG;
       dim3 grid(p.nt, p.mt, p.P);
-      MITOK_LAUNCH(k_zgemm_mfma, grid, dim3(256), 0, st, ro.x, ro.ldx, W, ldw, M, N, K, p.kchunk, ep, am,
-                         (double2*)sy.ws, sy.counters);
+      if (launch_zgemm_mfma(st, grid, ro.x, ro.ldx, W, ldw, M, N, K, p.kchunk, ep, am, (double2*)sy.ws, sy.counters) != OK)
+        return ERR_ARG;
       tiles = p.nt;
     }
   }

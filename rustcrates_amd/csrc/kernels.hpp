@@ -155,6 +155,12 @@ bool attention_prefill(hipStream_t st, const Attn& a);
 // npart partials (row b at q + b * ldq, partial stride part_stride); with
 // `append` the partials are [q | k | v] of the new token, whose k and v the
 // kernel appends to the cache (kc_w, vc_w).
+// MFMA-tiled GEMM (gemm_mfma.hip) for M > 64: block tile GBM x GBN, K step
+// GBK; grid (N tiles, M tiles, K splits of kchunk).  ERR_ARG for EPI_PART.
+constexpr int GBM = 64, GBN = 64, GBK = 16;
+int launch_zgemm_mfma(hipStream_t st, dim3 grid, const double2* A, long lda, const double2* W, long ldw, int M, int N,
+                      int K, int kchunk, const Epi& ep, const Argmax& am, double2* ws, uint32_t* cnt);
+
 AttnSplit attention_split_plan(const Attn& a);
 size_t attention_split_ws_bytes(int B, int H, int dh, int T_max);
 int attention_decode_split(hipStream_t st, const Attn& a, const double2* q, long ldq, int npart, long part_stride,

@@ -64,6 +64,23 @@ def test_decode_batch_above_gemv_limit_uses_mfma_with_fused_argmax():
         assert max_rel_err(lg, lo) < REL_TOL, f"plan={plan}"
 
 
+# FFN 1024 wide enough that FFN Dense takes the row-tile MFMA product with no K
+# split (GELU in the block); QKV and FFN Linear leave 2 and 8 partials; 20 and
+# 40 sequences end in a partial row tile
+WIDE = configs.ModelConfig("wide", layers=2, d=128, heads=4, ffn=1024, vocab=2000, max_ctx=64, seed=5)
+
+
+@pytest.mark.parametrize("B", [20, 40])
+def test_decode_row_tile_products(B):
+    lens = [4 + (7 * b) % 23 for b in range(B)]
+    log(f"decode B={B} (row-tile MFMA products)")
+    out, (io, lo) = _generate_both_plans(WIDE, lens, 8, 100 + B)
+    for plan in (1, 0):
+        ig, lg = out[plan]
+        assert np.array_equal(ig, io), f"plan={plan}"
+        assert max_rel_err(lg, lo) < REL_TOL, f"plan={plan}"
+
+
 def test_fused_decode_rope_model():
     cfg = configs.ModelConfig("rope", layers=2, d=64, heads=4, ffn=128, vocab=500, max_ctx=96, seed=12, rope=True)
     log("fused decode with RoPE")

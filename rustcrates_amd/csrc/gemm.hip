@@ -258,10 +258,16 @@ __device__ void rowops_att(const RowOps& ro, int K, int m, double2* buf, const R
         o.x += t[j][q].x * w[q];
         o.y += t[j][q].y * w[q];
       }
-    for (int q = RO_ATT_CH; q < ns; ++q) {  // longer caches: the remaining chunks one by one
-      const double2 v = a.po[(base + q) * a.dh + e];
-      o.x += v.x * w[q];
-      o.y += v.y * w[q];
+    for (int s0 = RO_ATT_CH; s0 < ns; s0 += 8) {  // longer caches: the rest, eight loads in flight
+      double2 u[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) u[q] = s0 + q < ns ? a.po[(base + s0 + q) * a.dh + e] : make_double2(0.0, 0.0);
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+        if (s0 + q < ns) {
+          o.x += u[q].x * w[s0 + q];
+          o.y += u[q].y * w[s0 + q];
+        }
     }
     const double l = L.lsum[h];
     double2 v = make_double2(o.x / l, o.y / l);

@@ -44,3 +44,14 @@ def test_library_is_gfx950_code():
 
     blob = open(rustcrates_amd.LIB_PATH, "rb").read()
     assert b"gfx950" in blob
+
+
+def test_bench_refuses_more_than_one_gpu():
+    # one GPU per box: --gpus N > 1 exits with a message before touching a device
+    import subprocess
+    import sys
+
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr

@@ -18,7 +18,9 @@ then
         --match 'k_zgemm_skinny<' --out profiles/layer_gemm_c3b32_traffic
 
 writes <out>.json (read by bench.py for the roofline's `traffic`) and <out>.md.
-`stats` writes the per-kernel table of a --kernel-trace database.
+`stats` writes the per-kernel table of a --kernel-trace database; `mfma` the
+MFMA utilisation of a class from a SQ_VALU_MFMA_BUSY_CYCLES /
+SQ_INSTS_VALU_MFMA_MOPS_F64 counter run and a kernel trace of the same workload.
 """
 from __future__ import annotations
 
@@ -160,6 +162,60 @@ def _stats(a) -> None:
     print(f"wrote {a.out}")
 
 
+def _mfma(a) -> None:
+    """MFMA utilisation per kernel of a class: SQ_VALU_MFMA_BUSY_CYCLES (summed
+    over the SIMDs) against SIMDs x clock x the kernel's traced duration, and
+    SQ_INSTS_VALU_MFMA_MOPS_F64 x 512 against the algorithmic flops."""
+    import sqlite3
+
+    busy = _per_dispatch(a.counters, "SQ_VALU_MFMA_BUSY_CYCLES")
+    mops = _per_dispatch(a.counters, "SQ_INSTS_VALU_MFMA_MOPS_F64")
+    pat = re.compile(re.escape(a.match))
+    dbs = glob.glob(os.path.join(a.trace, "**", "*.db"), recursive=True)
+    if not dbs:
+        raise SystemExit(f"no rocpd database under {a.trace}")
+    c = sqlite3.connect(dbs[0])
+    # the counter rows give only the total thread count, so launches of one
+    # kernel whose grids have the same total are averaged together
+    acc = {}
+    for name, gx, gy, gz, n, tot in c.execute("select name, grid_x, grid_y, grid_z, count(*), sum(duration) "
+                                              "from kernels group by name, grid_x, grid_y, grid_z"):
+        if pat.search(_short(name)):
+            e = acc.setdefault((_short(name), gx * gy * gz), [0, 0.0])
+            e[0] += n
+            e[1] += tot
+    dur = {k: tot / n * 1e-9 for k, (n, tot) in acc.items()}
+    cnt = {}
+    for r in csv.DictReader(open(glob.glob(os.path.join(a.counters, "**", "*counter_collection.csv"),
+                                           recursive=True)[0])):
+        cnt[(r["Kernel_Name"], r["Dispatch_Id"])] = int(r["Grid_Size"])
+    by = {}
+    for key, b in busy.items():
+        k = _short(key[0])
+        if not pat.search(k):
+            continue
+        g = cnt[key]
+        e = by.setdefault((k, g), [0, 0.0, 0.0])
+        e[0] += 1
+        e[1] += b
+        e[2] += mops.get(key, 0.0)
+    with open(a.out, "w") as fh:
+        fh.write(f"# {a.title}\n\n")
+        fh.write("Commands (from the repository root on the MI355X box, TMPDIR=/tmp):\n\n```\n" + a.command + "\n```\n\n")
+        fh.write(f"Summary: `python -m rustcrates_amd.traffic mfma`.  Utilisation = busy cycles / ({a.simds} SIMDs x "
+                 f"{a.clock_ghz} GHz x traced duration); flops = MOPS_F64 x 512.\n\n")
+        fh.write("| kernel | grid (threads) | dispatches | MFMA busy cycles | MOPS_F64 x 512 (GFLOP) | traced us | "
+                 "MFMA busy | TFLOP/s |\n|---|---:|---:|---:|---:|---:|---:|---:|\n")
+        for (k, g), (n, b, m) in sorted(by.items()):
+            d = dur.get((k, g))
+            bb, mm = b / n, m / n
+            util = bb / (a.simds * a.clock_ghz * 1e9 * d) if d else float("nan")
+            tf = mm * 512 / d / 1e12 if d else float("nan")
+            fh.write(f"| `{k}` | {g} | {n} | {bb:.4g} | {mm * 512 / 1e9:.2f} | {d * 1e6 if d else float('nan'):.1f} | "
+                     f"{100 * util:.1f}% | {tf:.1f} |\n")
+    print(f"wrote {a.out}")
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -176,7 +232,15 @@ def main() -> None:
     s.add_argument("--exclude", default="")
     s.add_argument("--run", default="bench.py --workload c3b32 --steps 1 --warmup 0 --no-cpu --no-b1 --no-classes --direct",
                    help="the profiled program (its arguments after python3)")
+    mf = sub.add_parser("mfma")
+    for k in ("counters", "trace", "match", "title", "command", "out"):
+        mf.add_argument("--" + k, required=True)
+    mf.add_argument("--simds", type=int, default=1024)
+    mf.add_argument("--clock-ghz", type=float, default=2.4)
     a = ap.parse_args()
+    if a.cmd == "mfma":
+        _mfma(a)
+        return
     if a.cmd == "copy":
         _copy()
     elif a.cmd == "stats":

@@ -842,10 +842,10 @@ static SkinnyPlan plan_skinny(int M, int N, int K, bool part, bool argmax) {
       // grid that would leave most of the chip idle
       const int fill = std::min(SKINNY_MAX_SPLIT, cdiv_i(192, r.ncb * p.rt));
       P = std::min(SKINNY_MAX_SPLIT, std::max(P, fill));
-      r.nkw = cdiv_i(cdiv_i(K, 16 * P), 4) * 4;
+      r.nkw = std::max(4, cdiv_i(cdiv_i(K, 16 * P), 4) * 4);
       P = cdiv_i(K, 16 * r.nkw);
     } else if (P > 1) {
-      r.nkw = cdiv_i(cdiv_i(K, 16), 4) * 4;
+      r.nkw = std::max(4, cdiv_i(cdiv_i(K, 16), 4) * 4);
       P = 1;
     }
     r.P = P;
@@ -952,6 +952,7 @@ static void launch_skinny(hipStream_t st, const SkinnyPlan& p, const RowOps& ro,
 int gemm(hipStream_t st, int M, int N, int K, const RowOps& ro, const double2* W, long ldw, const Epi& ep,
          const Argmax* amp, const Sync& sy) {
   if (M <= 0 || N <= 0) return OK;
+  if (K <= 0) return ERR_ARG;  // no product has an empty inner dimension
   const Argmax am = amp ? *amp : Argmax();
   if (ep.mode != EPI_PART && gemm_ws_bytes(M, N, K) > sy.ws_bytes) return ERR_STATE;
   int tiles = 0;  // column tiles of the argmax partials

@@ -98,16 +98,23 @@ def decode_step_bytes(c, lens, n_new):
 
 def load_traffic(kernel_class, workload):
     """HBM bytes per launch measured by rocprofv3 counters for this class and
-    workload (profiles/<class>_<workload>_traffic.json, python -m
-    rustcrates_amd.traffic), or None."""
+    workload (profiles/<class>_<workload>_traffic.json, written by python -m
+    rustcrates_amd.traffic), with where it came from.  A measurement whose
+    source hash differs from the current sources is stale: traffic is then
+    None and the note says so."""
+    from rustcrates_amd.build import source_hash
+
     path = os.path.join(ROOT, "profiles", f"{kernel_class}_{workload}_traffic.json")
     if not os.path.exists(path):
-        return None
+        return None, "no counter measurement for this class and workload"
     with open(path) as fh:
         t = json.load(fh)
     if t.get("kernel_class") != kernel_class or t.get("workload") != workload:
-        return None
-    return round(t["traffic_bytes_per_launch"], 1)
+        return None, f"{os.path.basename(path)} is for another class or workload"
+    sha = source_hash()
+    if t.get("csrc_sha") != sha:
+        return None, f"{os.path.basename(path)} measured on sources {t.get('csrc_sha')}, now {sha}: stale"
+    return round(t["traffic_bytes_per_launch"], 1), f"{os.path.basename(path)} (sources {sha})"
 
 
 def roofline_entry(r, bound):
@@ -127,12 +134,21 @@ def roofline_entry(r, bound):
             "alg_flops_per_launch": r["alg_flops"] / n}
 
 
+def host_threads():
+    """CPU threads this process may use: the OMP_NUM_THREADS the host sets for
+    it (the GPU box allots 16 per GPU), else every CPU in its affinity mask."""
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        return int(env)
+    return len(os.sched_getaffinity(0))
+
+
 def cpu_baseline(w, budget_s=20.0):
     """The CPU oracle (a port of the reference's forward, OpenMP over the
     reference's rayon axes) on the first sequences of the same workload."""
     import oracle
 
-    threads = min(16, os.cpu_count() or 1)
+    threads = host_threads()
     oracle.set_threads(threads)
     cfg = w.model
     o = configs.build_network(oracle.Network(), cfg)
@@ -148,7 +164,9 @@ def cpu_baseline(w, budget_s=20.0):
         t1 = time.perf_counter() - t0
     o.close()
     return {"value": round(nseq * n_new / t1, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"{nseq} of {w.batch} sequences, full prompt + {n_new} greedy tokens, {t1:.1f} s"}
+            "host_cpus": os.cpu_count(),
+            "sample": f"{nseq} of {w.batch} sequences, full prompt + {n_new} greedy tokens, {t1:.1f} s, "
+                      f"{threads} OpenMP threads"}
 
 
 def main():
@@ -170,9 +188,18 @@ def main():
         sys.exit(2)
 
     w = configs.WORKLOADS[args.workload]
-    cfg = w.model
     log(f"workload {args.workload}: building seeded network")
-    net = configs.build_network(ra.Network(0), cfg)
+    with ra.Network(0) as net:
+        out = run(args, w, configs.build_network(net, w.model))
+    # the network is released before the CPU baseline and before interpreter exit
+    if not args.no_cpu:
+        log("cpu baseline (oracle)")
+        out["cpu_baseline"] = cpu_baseline(w)
+    print(json.dumps(out), flush=True)
+
+
+def run(args, w, net):
+    cfg = w.model
     net.set_graph_mode(args.direct)
     prompt, lens = workload_prompt(w)
     B, n_new = w.batch, w.n_new
@@ -185,22 +212,29 @@ def main():
     decode_tok_s = B * (n_new - 1) / (dec_ms / 1e3) if dec_ms > 0 else None
 
     # roofline of the dominant kernel classes, HIP events on the library stream
-    roof, class_ms, prefill_gemm_roof = None, None, None
+    roof, class_ms, prefill_gemm_roof, class_roofs = None, None, None, None
     if not args.no_classes:
         log("kernel-class timing")
         classes = {}
         for name, cls in (("vocab", ra.TIME_VOCAB), ("layer_gemm", ra.TIME_LAYER_GEMM),
                           ("attention", ra.TIME_ATTENTION), ("prefill_gemm", ra.TIME_PREFILL_GEMM)):
             classes[name] = kernel_class(net, prompt, lens, n_new, cls)
-        # the decode products dominate the step; a GEMM class is MFMA-bound
-        # when its arithmetic intensity exceeds the ridge point
-        dominant = max(("vocab", "layer_gemm"), key=lambda k: classes[k]["total_ms"])
-        r = classes[dominant]
-        intensity = r["alg_flops"] / max(r["alg_bytes"], 1.0)
-        bound = "mfma" if intensity > FP64_MFMA_PEAK_TFS * 1e12 / (HBM_PEAK_GBS * 1e9) else "hbm"
-        roof = roofline_entry(r, bound)
-        roof["kernel_class"] = dominant
-        roof["traffic"] = load_traffic(dominant, args.workload)
+        # the dominant class of the decode step (the prompt pass has its own
+        # entry below); a class is MFMA-bound when its arithmetic intensity
+        # exceeds the ridge point, else HBM-bound
+        ridge = FP64_MFMA_PEAK_TFS * 1e12 / (HBM_PEAK_GBS * 1e9)
+        class_roofs = {}
+        for k in ("vocab", "layer_gemm", "attention"):
+            r = classes[k]
+            if not r["launches"]:
+                continue
+            intensity = r["alg_flops"] / max(r["alg_bytes"], 1.0)
+            e = roofline_entry(r, "mfma" if intensity > ridge else "hbm")
+            e["kernel_class"] = k
+            class_roofs[k] = e
+        dominant = max(class_roofs, key=lambda k: classes[k]["total_ms"])
+        roof = dict(class_roofs[dominant])
+        roof["traffic"], roof["traffic_source"] = load_traffic(dominant, args.workload)
         class_ms = {k: round(v["total_ms"] / 2, 3) for k, v in classes.items()}
         prefill_gemm_roof = (roofline_entry(classes["prefill_gemm"], "mfma")
                              if classes["prefill_gemm"]["launches"] else None)
@@ -226,6 +260,9 @@ def main():
         "decode_tokens_per_s": round(decode_tok_s, 2) if decode_tok_s else None,
         "kernel_class_ms_per_step": class_ms,
         "roofline": roof,
+        "class_rooflines": ({k: {"bound": v["bound"], "achieved": v["achieved"], "unit": v["unit"],
+                                 "frac": v["frac"], "avg_launch_us": v["avg_launch_us"]}
+                             for k, v in class_roofs.items()} if class_roofs else None),
     }
     # the prompt pass against the FP64 MFMA peak (north_star's prefill target)
     pf = prefill_flops(w, [int(x) for x in lens])
@@ -235,9 +272,11 @@ def main():
         "mfma_frac": round(pf / (pre_ms / 1e3) / 1e12 / FP64_MFMA_PEAK_TFS, 4),
         "gemm_roofline": prefill_gemm_roof,
     }
-    if B <= 8:
-        sb = decode_step_bytes(cfg, [int(x) for x in lens], n_new)
-        out["decode_step_hbm_frac"] = round(sb / (dec_ms / (n_new - 1) / 1e3) / 1e9 / HBM_PEAK_GBS, 4)
+    # the whole decode step against the HBM roofline: every weight once plus
+    # each sequence's KV rows and bias row 0 (the step's algorithmic bytes)
+    sb = decode_step_bytes(cfg, [int(x) for x in lens], n_new)
+    out["decode_step_bytes"] = round(sb)
+    out["decode_step_hbm_frac"] = round(sb / (dec_ms / (n_new - 1) / 1e3) / 1e9 / HBM_PEAK_GBS, 4)
 
     if not args.no_b1 and B > 1 and args.workload.startswith("c3"):
         log("batch-1 companion")
@@ -257,10 +296,7 @@ def main():
         out["batch1"]["decode_step_bytes"] = round(step_bytes)
         out["batch1"]["decode_step_hbm_frac"] = round(step_bytes / (dec1 / (w1.n_new - 1) / 1e3) / 1e9 / HBM_PEAK_GBS, 4)
 
-    if not args.no_cpu:
-        log("cpu baseline (oracle)")
-        out["cpu_baseline"] = cpu_baseline(w)
-    print(json.dumps(out), flush=True)
+    return out
 
 
 if __name__ == "__main__":

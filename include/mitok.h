@@ -120,6 +120,23 @@ int mitok_forward_layers(mitok_network* net, uint32_t first, uint32_t last, cons
 int mitok_generate(mitok_network* net, const uint32_t* prompt, const uint32_t* lens, uint32_t batch, uint32_t seq,
                    uint32_t n_new, uint32_t* out_ids, double* out_logits);
 
+/* The token loop one step at a time, for a host loop that inspects every id
+ * (predict_token_by_token, transformer_network.rs:225-304: the prompt at t = 0,
+ * then one fed token per step, the "<eos>" check and the print per token on the
+ * host).  Only ids cross PCIe: 4 B per sequence per step.
+ * mitok_prefill: resets the caches (k_cache = None) and runs the prompt
+ *   (ids [batch][seq] right-padded as for mitok_predict); out_ids [batch] = the
+ *   greedy id of each sequence's last prompt row; out_logits [batch][vocab]
+ *   Re-logits of that row, or NULL.
+ * mitok_decode_step: feeds ids [batch] (NULL: the ids the previous prefill or
+ *   step returned, already on the device) at position = each sequence's KV
+ *   length, appends to the caches; out_ids [batch] = the next greedy ids;
+ *   out_logits [batch][vocab] or NULL.  batch must equal the prefill's.
+ * On error the caches are dropped (prefill again). */
+int mitok_prefill(mitok_network* net, const uint32_t* prompt, const uint32_t* lens, uint32_t batch, uint32_t seq,
+                  uint32_t* out_ids, double* out_logits);
+int mitok_decode_step(mitok_network* net, const uint32_t* ids, uint32_t batch, uint32_t* out_ids, double* out_logits);
+
 /* greedy_decoding (src/utils/sampling_methods.rs:5-18) on the device for host
  * logits [rows][vocab]: last index among equal maxima; NaN -> MITOK_ERR_NAN. */
 int mitok_greedy_decoding(mitok_network* net, const double* logits, uint32_t rows, uint32_t vocab, uint32_t* out_ids);

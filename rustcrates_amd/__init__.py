@@ -13,8 +13,10 @@ to a CPU path: if libmitok.so is missing or no GPU is present, the calls raise.
 """
 from __future__ import annotations
 
+import atexit
 import ctypes as C
 import os
+import weakref
 
 import numpy as np
 
@@ -51,6 +53,8 @@ SIGNATURES = {
     "mitok_predict": (_i32, [_P, _P, _P, _u32, _u32, _P, _i32, _i32, _P, _P]),
     "mitok_forward_layers": (_i32, [_P, _u32, _u32, _P, _P, _u32, _u32, _P, _i32, _P]),
     "mitok_generate": (_i32, [_P, _P, _P, _u32, _u32, _u32, _P, _P]),
+    "mitok_prefill": (_i32, [_P, _P, _P, _u32, _u32, _P, _P]),
+    "mitok_decode_step": (_i32, [_P, _P, _u32, _P, _P]),
     "mitok_greedy_decoding": (_i32, [_P, _P, _u32, _u32, _P]),
     "mitok_last_timings": (_i32, [_P, _P]),
     "mitok_timing_enable": (_i32, [_P, _i32]),
@@ -95,8 +99,36 @@ def _ptr(a):
     return None if a is None else a.ctypes.data_as(C.c_void_p)
 
 
-def _c128(a):
-    return None if a is None else np.ascontiguousarray(a, dtype=np.complex128)
+def _c128(a, n=None, what="tensor"):
+    """A contiguous complex128 copy of `a` (None stays None); with n, its size
+    must be n elements, so the library never reads past a short host buffer."""
+    if a is None:
+        return None
+    a = np.ascontiguousarray(a, dtype=np.complex128)
+    if n is not None and a.size != n:
+        raise ValueError(f"{what}: {a.size} elements, expected {n}")
+    return a
+
+
+def _u32_vec(a, n, what):
+    a = np.ascontiguousarray(a, dtype=np.uint32)
+    if a.shape != (n,):
+        raise ValueError(f"{what}: shape {a.shape}, expected ({n},)")
+    return a
+
+
+# every open network, closed at interpreter exit before the HIP runtime's own
+# teardown (atexit handlers run before module globals are cleared)
+_live = weakref.WeakSet()
+
+
+@atexit.register
+def _close_all():
+    for net in list(_live):
+        try:
+            net.close()
+        except Exception:
+            pass
 
 
 def device_synchronize(device: int = 0) -> None:
@@ -111,7 +143,10 @@ def device_count() -> int:
 
 
 class Network:
-    """NeuralNetwork on one GPU (neural_network_generic.rs:23-31)."""
+    """NeuralNetwork on one GPU (neural_network_generic.rs:23-31).
+
+    Release it with close() or a `with` block; networks still open at exit are
+    closed by an atexit hook, while the HIP runtime is still up."""
 
     def __init__(self, device: int = 0):
         lib = load_library()
@@ -120,11 +155,20 @@ class Network:
         self._h = h
         self._lib = lib
         self.vocab = None
+        self.dim = None
+        _live.add(self)
 
     def close(self):
         if getattr(self, "_h", None):
             self._lib.mitok_network_destroy(self._h)
             self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+        return False
 
     def __del__(self):
         try:
@@ -138,27 +182,33 @@ class Network:
 
     # ---- LayerEnum variants ----
     def add_embedding(self, vocab, dim, table=None):
-        _check(self._lib.mitok_add_embedding(self._h, vocab, dim, _ptr(_c128(table))))
+        self.dim = dim
+        _check(self._lib.mitok_add_embedding(self._h, vocab, dim, _ptr(_c128(table, vocab * dim, "table"))))
 
     def add_positional_encoding(self, dim, base=1250.0):
         _check(self._lib.mitok_add_positional_encoding(self._h, dim, base))
 
     def add_norm(self, dim, eps, gamma=None, beta=None):
-        _check(self._lib.mitok_add_norm(self._h, dim, eps, _ptr(_c128(gamma)), _ptr(_c128(beta))))
+        _check(self._lib.mitok_add_norm(self._h, dim, eps, _ptr(_c128(gamma, dim, "gamma")),
+                                        _ptr(_c128(beta, dim, "beta"))))
 
     def add_self_attention(self, heads, dim, max_ctx, eps=1e-12, wq=None, wk=None, wv=None, bias_pos=None,
                            gamma=None, beta=None):
-        _check(self._lib.mitok_add_self_attention(self._h, heads, dim, max_ctx, eps, _ptr(_c128(wq)),
-                                                  _ptr(_c128(wk)), _ptr(_c128(wv)), _ptr(_c128(bias_pos)),
-                                                  _ptr(_c128(gamma)), _ptr(_c128(beta))))
+        nw = dim * dim  # [heads][dim][dim / heads]
+        _check(self._lib.mitok_add_self_attention(self._h, heads, dim, max_ctx, eps, _ptr(_c128(wq, nw, "wq")),
+                                                  _ptr(_c128(wk, nw, "wk")), _ptr(_c128(wv, nw, "wv")),
+                                                  _ptr(_c128(bias_pos, heads * max_ctx * max_ctx, "bias_pos")),
+                                                  _ptr(_c128(gamma, dim, "gamma")), _ptr(_c128(beta, dim, "beta"))))
 
     def add_feed_forward(self, dim, hidden, w1=None, b1=None, w2=None, b2=None):
-        _check(self._lib.mitok_add_feed_forward(self._h, dim, hidden, _ptr(_c128(w1)), _ptr(_c128(b1)),
-                                                _ptr(_c128(w2)), _ptr(_c128(b2))))
+        _check(self._lib.mitok_add_feed_forward(self._h, dim, hidden, _ptr(_c128(w1, dim * hidden, "w1")),
+                                                _ptr(_c128(b1, hidden, "b1")), _ptr(_c128(w2, hidden * dim, "w2")),
+                                                _ptr(_c128(b2, dim, "b2"))))
 
     def add_linear(self, d_in, d_out, w=None, b=None):
         self.vocab = d_out
-        _check(self._lib.mitok_add_linear(self._h, d_in, d_out, _ptr(_c128(w)), _ptr(_c128(b))))
+        _check(self._lib.mitok_add_linear(self._h, d_in, d_out, _ptr(_c128(w, d_in * d_out, "w")),
+                                          _ptr(_c128(b, d_out, "b"))))
 
     def add_softmax(self, mode=PRODUCTION):
         _check(self._lib.mitok_add_softmax(self._h, mode))
@@ -181,8 +231,8 @@ class Network:
     def predict(self, ids, lens=None, time_steps=None, forward_only=True, last_row_only=False):
         ids = np.ascontiguousarray(ids, dtype=np.uint32)
         B, S = ids.shape
-        lens = np.full(B, S, np.uint32) if lens is None else np.ascontiguousarray(lens, dtype=np.uint32)
-        ts = None if time_steps is None else np.ascontiguousarray(time_steps, dtype=np.uint32)
+        lens = np.full(B, S, np.uint32) if lens is None else _u32_vec(lens, B, "lens")
+        ts = None if time_steps is None else _u32_vec(time_steps, B, "time_steps")
         V = self.vocab
         out = np.empty((B, V) if last_row_only else (B, S, V), np.float64)
         mask = np.empty((B, S), np.uint32)
@@ -192,9 +242,15 @@ class Network:
 
     def forward_layers(self, first, last, x, mask=None, time_steps=None, forward_only=True, d_out=None):
         x = _c128(x)
+        if x.ndim != 3:
+            raise ValueError(f"hidden states: shape {x.shape}, expected (batch, seq, dim)")
         B, S, _ = x.shape
-        m = None if mask is None else np.ascontiguousarray(mask, dtype=np.uint32)
-        ts = None if time_steps is None else np.ascontiguousarray(time_steps, dtype=np.uint32)
+        m = None
+        if mask is not None:
+            m = np.ascontiguousarray(mask, dtype=np.uint32)
+            if m.shape != (B, S):
+                raise ValueError(f"padding mask: shape {m.shape}, expected ({B}, {S})")
+        ts = None if time_steps is None else _u32_vec(time_steps, B, "time_steps")
         out = np.empty((B, S, d_out if d_out else x.shape[2]), np.complex128)
         _check(self._lib.mitok_forward_layers(self._h, first, last, _ptr(x), _ptr(m), B, S, _ptr(ts),
                                               int(forward_only), _ptr(out)))
@@ -203,14 +259,38 @@ class Network:
     def generate(self, prompt, lens=None, n_new=1, want_logits=False):
         prompt = np.ascontiguousarray(prompt, dtype=np.uint32)
         B, S = prompt.shape
-        lens = np.full(B, S, np.uint32) if lens is None else np.ascontiguousarray(lens, dtype=np.uint32)
+        lens = np.full(B, S, np.uint32) if lens is None else _u32_vec(lens, B, "lens")
         ids = np.empty((B, n_new), np.uint32)
         logits = np.empty((n_new, B, self.vocab), np.float64) if want_logits else None
         _check(self._lib.mitok_generate(self._h, _ptr(prompt), _ptr(lens), B, S, n_new, _ptr(ids), _ptr(logits)))
         return (ids, logits) if want_logits else ids
 
+    def prefill(self, prompt, lens=None, want_logits=False):
+        """The prompt pass of the token loop: returns each sequence's first
+        greedy id [B] (and its Re-logits row [B][V])."""
+        prompt = np.ascontiguousarray(prompt, dtype=np.uint32)
+        B, S = prompt.shape
+        lens = np.full(B, S, np.uint32) if lens is None else _u32_vec(lens, B, "lens")
+        ids = np.empty(B, np.uint32)
+        logits = np.empty((B, self.vocab), np.float64) if want_logits else None
+        _check(self._lib.mitok_prefill(self._h, _ptr(prompt), _ptr(lens), B, S, _ptr(ids), _ptr(logits)))
+        self._batch = B
+        return (ids, logits) if want_logits else ids
+
+    def decode_step(self, ids=None, want_logits=False, batch=None):
+        """One decode step: feeds `ids` [B] (None: the ids the previous call
+        returned, still on the device) and returns the next greedy ids [B]."""
+        B = batch if batch is not None else (len(ids) if ids is not None else getattr(self, "_batch", 0))
+        fed = None if ids is None else _u32_vec(ids, B, "ids")
+        out = np.empty(B, np.uint32)
+        logits = np.empty((B, self.vocab), np.float64) if want_logits else None
+        _check(self._lib.mitok_decode_step(self._h, _ptr(fed), B, _ptr(out), _ptr(logits)))
+        return (out, logits) if want_logits else out
+
     def greedy_decoding(self, logits):
         logits = np.ascontiguousarray(logits, dtype=np.float64)
+        if logits.ndim != 2:
+            raise ValueError(f"logits: shape {logits.shape}, expected (rows, vocab)")
         rows, V = logits.shape
         out = np.empty(rows, np.uint32)
         _check(self._lib.mitok_greedy_decoding(self._h, _ptr(logits), rows, V, _ptr(out)))

@@ -35,6 +35,20 @@ CFLAGS = [
 FILE_FLAGS = {"gemm_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 
 
+def source_hash() -> str:
+    """SHA-256 (16 hex digits) of every device/host source file in csrc/: counter
+    measurements are stamped with it, so a stale one is recognised."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for name in sorted(os.listdir(SRC)):
+        if name.endswith((".hip", ".hpp", ".h")):
+            h.update(name.encode())
+            with open(os.path.join(SRC, name), "rb") as fh:
+                h.update(fh.read())
+    return h.hexdigest()[:16]
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
     cmd = [HIPCC, *CFLAGS, *FILE_FLAGS.get(src, []), "-c", os.path.join(SRC, src), "-o", obj]

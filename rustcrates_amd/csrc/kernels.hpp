@@ -221,8 +221,9 @@ struct ResGemvPlan {
 // prefetch registers of waves 1-3 (kw rows each), else 4 streaming waves
 ResGemvPlan resident_gemv_plan(int M, int N, int K, bool part, int grid);
 size_t resident_op_lds(const ROp& op);  // dynamic LDS of one operation
-// blocks of the launch (one per CU) if the kernel for (mr, dh) fits with `shm`
-int resident_grid(int device, int mr, int dh, size_t shm, int* grid);
+// blocks of the launch (one per CU: `cus` compute units, cooperative launch
+// supported) if the kernel for (mr, dh) fits with `shm`
+int resident_grid(int cus, bool cooperative, int mr, int dh, size_t shm, int* grid);
 // flags: one word per block, epochs below epoch0 + 1 (zeroed at set-up); the
 // launch performs nsteps * nops barriers.  stamps (optional, nsteps * nops + 1
 // words): block 0's wall clock (100 MHz) after each barrier, then at the start.

@@ -176,6 +176,8 @@ struct Timing {
 
 struct mitok_network {
   int device = 0;
+  int cus = 0;               // compute units (the resident loop runs one block per CU)
+  bool cooperative = false;  // cooperative launches supported
   hipStream_t stream = nullptr;
   std::vector<std::unique_ptr<mitok::Layer>> layers;
   // session (KV cache) state
@@ -201,14 +203,19 @@ struct mitok_network {
   uint32_t res_epoch = 0;
   int res_profile = 0;  // record per-operation times of the next resident launches
   uint32_t res_steps = 0;
-  // decode-step graph
+  // decode-step graph: generate's step (graph_step 0, ids history of n_new per
+  // sequence) or mitok_decode_step's (graph_step 1, one id per sequence)
   hipGraphExec_t graph = nullptr;
   uint32_t graph_B = 0, graph_nnew = 0;
+  int graph_step = 0;
   bool graph_logits = false;
   uint64_t ws_generation = 0, graph_generation = 0;
   int direct_launch = 0;
   double last_t[3] = {0, 0, 0};
   mitok::Timing timing;
+  // sum over sequences of the keys the next decode step attends over (the host
+  // loop sets it before each timed step): the attention class's algorithmic bytes
+  double dec_tsum = 0.0;
 };
 
 namespace mitok {
@@ -328,6 +335,13 @@ static double gemm_bytes(long M, long N, long K, bool re_out) {
 }
 // real flops of a complex product: 4 multiplies + 4 adds per complex MAC
 static double gemm_flops(long M, long N, long K) { return 8.0 * (double)M * N * K; }
+
+// algorithmic HBM bytes of one decode attention launch of a layer (width d,
+// H heads): per key of every sequence its K and V rows (16 B per element) and
+// the Re(bias_pos) row-0 entry of each head (8 B)
+static double attention_decode_bytes(const Net* n, long d, long H) {
+  return n->dec_tsum * (2.0 * 16.0 * (double)d + 8.0 * (double)H);
+}
 
 // ---------------------------------------------------------------------------
 // workspace sizing for one forward shape
@@ -550,7 +564,7 @@ static int enqueue_forward(Net* n, const Spec& sp) {
           // key chunks, then one row transform: chunk combine + residual + Norm (self_attention_layer.rs:101-124)
           AttnSplit o = split_buffers(n, attention_split_plan(a), B, H);
           {
-            TimeScope ts(n, MITOK_TIME_ATTENTION, 0.0);
+            TimeScope ts(n, MITOK_TIME_ATTENTION, attention_decode_bytes(n, d, H));
             TRY(launch_rc(attention_decode_split(st, a, n->qbuf.as<double2>(), d, 1, 0, false, o), "attention"));
           }
           RowOps r;
@@ -819,7 +833,7 @@ static int enqueue_decode_fused(Net* n, const Spec& sp) {
         a.err = err;
         const AttnSplit o = split_buffers(n, attention_split_plan(a), B, H);
         {
-          TimeScope ts(n, MITOK_TIME_ATTENTION, 0.0);
+          TimeScope ts(n, MITOK_TIME_ATTENTION, attention_decode_bytes(n, d, H));
           TRY(launch_rc(attention_decode_split(st, a, n->dq.as<double2>(), 3 * d, pq, (long)B * 3 * d, true, o),
                         "attention"));
         }
@@ -1198,9 +1212,7 @@ static int resident_build(Net* n, const Spec& sp, int grid, int* dh_out, size_t*
 // nsteps decode steps of generate in one launch (the step is what
 // enqueue_decode_step enqueues per launch)
 static int run_resident(Net* n, const Spec& sp, uint32_t nsteps) {
-  hipDeviceProp_t prop;
-  HIP_TRY(hipGetDeviceProperties(&prop, n->device));
-  const int grid = prop.multiProcessorCount;
+  const int grid = n->cus;
   // argmax partials: one per row and column block of the vocab product
   size_t am_elems = 0;
   for (uint32_t li = 0; li < n->layers.size(); ++li)
@@ -1229,7 +1241,7 @@ static int run_resident(Net* n, const Spec& sp, uint32_t nsteps) {
   size_t shm = 0;
   TRY(resident_build(n, s2, grid, &dh, &shm, &tiles));
   int g2 = 0;
-  TRY(launch_rc(resident_grid(n->device, res_mr(sp.B), dh, shm, &g2), "resident decode (grid)"));
+  TRY(launch_rc(resident_grid(n->cus, n->cooperative, res_mr(sp.B), dh, shm, &g2), "resident decode (grid)"));
   if (g2 != grid) return fail(ERR_STATE, "resident decode: grid %d != %d", g2, grid);
   const size_t ob = n->res_ops_h.size() * sizeof(ROp);
   TRY(reserve(n, n->res_ops, ob));
@@ -1330,6 +1342,15 @@ int mitok_network_create(int device, mitok_network** out) {
   if (!n) return fail(ERR_NOMEM, "out of host memory");
   n->device = device;
   int rc = set_device(n);
+  if (!rc) {
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess) {
+      rc = fail(ERR_HIP, "hipGetDeviceProperties failed");
+    } else {
+      n->cus = prop.multiProcessorCount;
+      n->cooperative = prop.cooperativeLaunch != 0;
+    }
+  }
   if (!rc && hipStreamCreateWithFlags(&n->stream, hipStreamNonBlocking) != hipSuccess)
     rc = fail(ERR_HIP, "hipStreamCreate failed");
   if (!rc) rc = n->err_d.reserve(sizeof(uint32_t));
@@ -1653,6 +1674,8 @@ static int begin_call(Net* n, const uint32_t* lens, uint32_t B, uint32_t S, cons
   sp.lens = n->lens_d.as<uint32_t>();
   sp.pos = n->pos_d.as<int>();
   if (sp.mode == MODE_CACHED) {
+    n->dec_tsum = 0.0;
+    for (uint32_t b = 0; b < B; ++b) n->dec_tsum += (double)n->kv_len_h[b] + 1;
     std::vector<int> kv(n->kv_len_h.begin(), n->kv_len_h.end());
     TRY(upload(n, n->kv_len_d, kv.data(), B * sizeof(int)));
     if (S > 1) {
@@ -1765,13 +1788,13 @@ int mitok_forward_layers(mitok_network* n, uint32_t first, uint32_t last, const 
 // stack with the cache, vocab Re-logits (+history) and the greedy ids fused
 // into the vocab product, which also appends to the id history and advances
 // every sequence's KV length.
-static int enqueue_decode_step(Net* n, Spec sp, bool want_logits, uint32_t n_new) {
+static int enqueue_decode_step(Net* n, Spec sp, bool want_logits, uint32_t hist_stride) {
   Argmax am;
   am.part_v = n->am_v.as<double>();
   am.part_i = n->am_i.as<int>();
   am.ids = n->dec_ids_d.as<uint32_t>();
   am.hist = n->hist_d.as<uint32_t>();
-  am.hist_stride = (int)n_new;
+  am.hist_stride = (int)hist_stride;
   am.hist_cnt = n->cnt_d.as<int>();
   am.kv_len = n->kv_len_d.as<int>();
   am.advance_kv = 1;
@@ -1782,33 +1805,61 @@ static int enqueue_decode_step(Net* n, Spec sp, bool want_logits, uint32_t n_new
   return enqueue_step(n, sp);
 }
 
-int mitok_generate(mitok_network* n, const uint32_t* prompt, const uint32_t* lens, uint32_t B, uint32_t S,
-                   uint32_t n_new, uint32_t* out_ids, double* out_logits) {
-  if (!n || !prompt || !lens || !out_ids) return fail(ERR_ARG, "null argument");
-  TRY(validate_batch(lens, B, S));
-  TRY(check_stack(n));
-  TRY(set_device(n));
-  if (n_new == 0) return OK;
-  const uint32_t mc = min_ctx(n);
-  for (uint32_t b = 0; b < B; ++b)
-    if (mc != UINT32_MAX && (uint64_t)lens[b] + n_new - 1 > mc)
-      return fail(ERR_ARG, "prompt %u + %u new tokens exceed max context %u", lens[b], n_new, mc);
-  TRY(mitok_reset(n));
-  hipStream_t st = n->stream;
-  const uint32_t V = n->layers[n->layers.size() - 2]->d_out;
-  const bool want_logits = out_logits != nullptr;
+// The three events of a token-loop call (start, prompt done, decode done),
+// destroyed on every return path.
+struct CallEvents {
+  hipEvent_t e[3] = {nullptr, nullptr, nullptr};
+  CallEvents() = default;
+  CallEvents(const CallEvents&) = delete;
+  CallEvents& operator=(const CallEvents&) = delete;
+  ~CallEvents() {
+    for (hipEvent_t x : e)
+      if (x) (void)hipEventDestroy(x);
+  }
+  int create() {
+    for (hipEvent_t& x : e) HIP_TRY(hipEventCreate(&x));
+    return OK;
+  }
+};
 
-  // workspaces for both shapes first, so nothing moves once the graph exists
+// The decode-step shape of a token-loop call on B sequences.
+static Spec decode_spec(Net* n, uint32_t B) {
   Spec dec;
-  dec.B = B;
+  dec.B = (int)B;
   dec.S = 1;
   dec.mode = MODE_CACHED;
   dec.first = 0;
   dec.last = (uint32_t)n->layers.size();
+  return dec;
+}
+
+// Decode-step inputs: the ids the previous step left on the device, RoPE
+// position = KV length (the fed token's index).
+static void bind_decode_inputs(Net* n, Spec& dec) {
+  dec.ids = n->dec_ids_d.as<uint32_t>();
+  dec.mask = n->ones_d.as<uint32_t>();
+  dec.lens = n->ones_d.as<uint32_t>();
+  dec.pos = nullptr;
+  dec.out_re = n->logits_re.as<double>();
+}
+
+// The prompt pass of the token loop (transformer_network.rs:225-248 at t = 0):
+// drops the caches, runs every prompt row, and leaves each sequence's first
+// greedy id at hist[b * hist_stride] and in dec_ids_d, its Re-logits row at
+// logit_hist[0][b] (want_logits), and the KV lengths on the device.  `ctx`
+// is the context the later steps will reach (RoPE table size).  The decode
+// shape's workspaces are reserved first, so nothing moves once a decode-step
+// graph exists.  The host cache state is left valid on success.
+static int run_prompt(Net* n, const uint32_t* prompt, const uint32_t* lens, uint32_t B, uint32_t S,
+                      uint32_t hist_stride, uint32_t ctx, bool want_logits) {
+  TRY(mitok_reset(n));
+  hipStream_t st = n->stream;
+  const uint32_t V = n->layers[n->layers.size() - 2]->d_out;
+  Spec dec = decode_spec(n, B);
   TRY(prepare(n, dec));
-  TRY(reserve(n, n->hist_d, (size_t)B * n_new * sizeof(uint32_t)));
+  TRY(reserve(n, n->hist_d, (size_t)B * hist_stride * sizeof(uint32_t)));
   TRY(reserve(n, n->cnt_d, (size_t)B * sizeof(int)));
-  if (want_logits) TRY(reserve(n, n->logit_hist_d, (size_t)n_new * B * V * sizeof(double)));
+  if (want_logits) TRY(reserve(n, n->logit_hist_d, (size_t)hist_stride * B * V * sizeof(double)));
 
   Spec pre;
   pre.first = 0;
@@ -1816,7 +1867,7 @@ int mitok_generate(mitok_network* n, const uint32_t* prompt, const uint32_t* len
   pre.last_row = true;
   std::vector<uint32_t> mask_h;
   TRY(begin_call(n, lens, B, S, nullptr, true, false, pre, mask_h));
-  TRY(ensure_rope_for(n, 0, pre.last, (int)std::max<uint32_t>(rope_positions_needed(n), S + n_new)));
+  TRY(ensure_rope_for(n, 0, pre.last, (int)std::max<uint32_t>(rope_positions_needed(n), ctx)));
   std::vector<uint32_t> padded((size_t)B * S);
   for (uint32_t b = 0; b < B; ++b)
     for (uint32_t s = 0; s < S; ++s) padded[(size_t)b * S + s] = s < lens[b] ? prompt[(size_t)b * S + s] : 1u;
@@ -1828,36 +1879,73 @@ int mitok_generate(mitok_network* n, const uint32_t* prompt, const uint32_t* len
   fill_int(st, n->cnt_d.as<int>(), B, 0);
   fill_u32(st, n->ones_d.as<uint32_t>(), B, 1);
 
-  hipEvent_t ev[3];
-  for (auto& e : ev) HIP_TRY(hipEventCreate(&e));
-  HIP_TRY(hipEventRecord(ev[0], st));
-  // ---- prompt: full forward, vocab on each sequence's last row, first ids ----
   Argmax am0;
   am0.part_v = n->am_v.as<double>();
   am0.part_i = n->am_i.as<int>();
   am0.ids = n->dec_ids_d.as<uint32_t>();
   am0.hist = n->hist_d.as<uint32_t>();
-  am0.hist_stride = (int)n_new;
+  am0.hist_stride = (int)hist_stride;
   am0.hist_cnt = n->cnt_d.as<int>();
   am0.err = n->err_d.as<uint32_t>();
   pre.am = &am0;
   pre.hist_re = want_logits ? n->logit_hist_d.as<double>() : nullptr;
   pre.hist_cnt = n->cnt_d.as<int>();
   TRY(enqueue_forward(n, pre));
-  {
-    std::vector<int> kv(lens, lens + B);
-    HIP_TRY(hipMemcpyAsync(n->kv_len_d.p, kv.data(), B * sizeof(int), hipMemcpyHostToDevice, st));
-    HIP_TRY(hipStreamSynchronize(st));  // kv is a stack vector
-  }
-  HIP_TRY(hipEventRecord(ev[1], st));
+  // KV lengths = prompt lengths (lens_d holds them since begin_call; same bits as int)
+  HIP_TRY(hipMemcpyAsync(n->kv_len_d.p, n->lens_d.p, B * sizeof(int), hipMemcpyDeviceToDevice, st));
   end_call(n, pre, lens);
+  return OK;
+}
+
+// (Re)captures the decode-step graph for its key: batch, history length,
+// logits history and kind (0: generate's step, 1: mitok_decode_step's step,
+// which first zeroes the per-sequence id counters with a fill kernel).  The
+// captured graph is destroyed on every return path.
+static int ensure_step_graph(Net* n, const Spec& dec, bool want_logits, uint32_t hist_stride, int kind) {
+  const uint32_t B = (uint32_t)dec.B;
+  if (n->graph && n->graph_B == B && n->graph_nnew == hist_stride && n->graph_logits == want_logits &&
+      n->graph_step == kind && n->graph_generation == n->ws_generation)
+    return OK;
+  drop_graph(n);
+  hipStream_t st = n->stream;
+  hipGraph_t g = nullptr;
+  HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+  if (kind == 1) fill_int(st, n->cnt_d.as<int>(), B, 0);
+  const int rc = enqueue_decode_step(n, dec, want_logits, hist_stride);
+  const hipError_t ce = hipStreamEndCapture(st, &g);
+  int out = rc;
+  if (!out && ce != hipSuccess) out = fail(ERR_HIP, "hipStreamEndCapture: %s", hipGetErrorString(ce));
+  if (!out) {
+    const hipError_t ie = hipGraphInstantiate(&n->graph, g, nullptr, nullptr, 0);
+    if (ie != hipSuccess) {
+      n->graph = nullptr;
+      out = fail(ERR_HIP, "hipGraphInstantiate: %s", hipGetErrorString(ie));
+    }
+  }
+  if (g) (void)hipGraphDestroy(g);
+  if (out) return out;
+  n->graph_B = B;
+  n->graph_nnew = hist_stride;
+  n->graph_logits = want_logits;
+  n->graph_step = kind;
+  n->graph_generation = n->ws_generation;
+  return OK;
+}
+
+static int generate_impl(Net* n, const uint32_t* prompt, const uint32_t* lens, uint32_t B, uint32_t S, uint32_t n_new,
+                         uint32_t* out_ids, double* out_logits) {
+  hipStream_t st = n->stream;
+  const uint32_t V = n->layers[n->layers.size() - 2]->d_out;
+  const bool want_logits = out_logits != nullptr;
+  CallEvents ev;
+  TRY(ev.create());
+  HIP_TRY(hipEventRecord(ev.e[0], st));
+  TRY(run_prompt(n, prompt, lens, B, S, n_new, S + n_new, want_logits));
+  HIP_TRY(hipEventRecord(ev.e[1], st));
 
   // ---- decode steps ----
-  dec.ids = n->dec_ids_d.as<uint32_t>();
-  dec.mask = n->ones_d.as<uint32_t>();
-  dec.lens = n->ones_d.as<uint32_t>();
-  dec.pos = nullptr;  // RoPE position = kv_len (the fed token's index)
-  dec.out_re = n->logits_re.as<double>();
+  Spec dec = decode_spec(n, B);
+  bind_decode_inputs(n, dec);
   bool used_graph = false, used_resident = false;
   if (n_new > 1 && n->timing.cls == 0) {
     Spec rs = dec;
@@ -1880,41 +1968,26 @@ int mitok_generate(mitok_network* n, const uint32_t* prompt, const uint32_t* len
   if (n_new > 1 && !used_resident) {
     const bool direct = n->direct_launch || n->timing.cls != 0;
     if (!direct) {
-      if (!n->graph || n->graph_B != B || n->graph_nnew != n_new || n->graph_logits != want_logits ||
-          n->graph_generation != n->ws_generation) {
-        drop_graph(n);
-        hipGraph_t g = nullptr;
-        HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
-        int rc = enqueue_decode_step(n, dec, want_logits, n_new);
-        hipError_t ce = hipStreamEndCapture(st, &g);
-        if (rc) return rc;
-        if (ce != hipSuccess) return fail(ERR_HIP, "hipStreamEndCapture: %s", hipGetErrorString(ce));
-        hipError_t ie = hipGraphInstantiate(&n->graph, g, nullptr, nullptr, 0);
-        (void)hipGraphDestroy(g);
-        if (ie != hipSuccess) return fail(ERR_HIP, "hipGraphInstantiate: %s", hipGetErrorString(ie));
-        n->graph_B = B;
-        n->graph_nnew = n_new;
-        n->graph_logits = want_logits;
-        n->graph_generation = n->ws_generation;
-      }
+      TRY(ensure_step_graph(n, dec, want_logits, n_new, 0));
       for (uint32_t t = 1; t < n_new; ++t) HIP_TRY(hipGraphLaunch(n->graph, st));
       used_graph = true;
     } else {
       for (uint32_t t = 1; t < n_new; ++t) {
+        n->dec_tsum = 0.0;
+        for (uint32_t b = 0; b < B; ++b) n->dec_tsum += (double)n->kv_len_h[b] + t;
         TimeScope ts(n, MITOK_TIME_STEP, 0.0);
         TRY(enqueue_decode_step(n, dec, want_logits, n_new));
       }
     }
   }
-  HIP_TRY(hipEventRecord(ev[2], st));
+  HIP_TRY(hipEventRecord(ev.e[2], st));
   HIP_TRY(hipMemcpyAsync(out_ids, n->hist_d.p, (size_t)B * n_new * sizeof(uint32_t), hipMemcpyDeviceToHost, st));
   if (want_logits)
     HIP_TRY(hipMemcpyAsync(out_logits, n->logit_hist_d.p, (size_t)n_new * B * V * sizeof(double), hipMemcpyDeviceToHost, st));
   HIP_TRY(hipStreamSynchronize(st));
   float a = 0.f, b2 = 0.f;
-  (void)hipEventElapsedTime(&a, ev[0], ev[1]);
-  (void)hipEventElapsedTime(&b2, ev[1], ev[2]);
-  for (auto& e : ev) (void)hipEventDestroy(e);
+  (void)hipEventElapsedTime(&a, ev.e[0], ev.e[1]);
+  (void)hipEventElapsedTime(&b2, ev.e[1], ev.e[2]);
   n->last_t[0] = a;
   n->last_t[1] = b2;
   n->last_t[2] = used_resident ? 2.0 : used_graph ? 1.0 : 0.0;
@@ -1930,6 +2003,106 @@ int mitok_generate(mitok_network* n, const uint32_t* prompt, const uint32_t* len
   TRY(check_err_word(n));
   for (uint32_t b = 0; b < B; ++b) n->kv_len_h[b] += n_new - 1;
   return OK;
+}
+
+// common argument checks of the token-loop entry points
+static int check_loop_args(Net* n, const uint32_t* prompt, const uint32_t* lens, uint32_t B, uint32_t S, uint32_t ctx_extra,
+                           const uint32_t* out_ids) {
+  if (!n || !prompt || !lens || !out_ids) return fail(ERR_ARG, "null argument");
+  TRY(validate_batch(lens, B, S));
+  TRY(check_stack(n));
+  TRY(set_device(n));
+  const uint32_t mc = min_ctx(n);
+  for (uint32_t b = 0; b < B; ++b)
+    if (mc != UINT32_MAX && (uint64_t)lens[b] + ctx_extra > mc)
+      return fail(ERR_ARG, "prompt %u + %u new tokens exceed max context %u", lens[b], ctx_extra, mc);
+  return OK;
+}
+
+int mitok_generate(mitok_network* n, const uint32_t* prompt, const uint32_t* lens, uint32_t B, uint32_t S,
+                   uint32_t n_new, uint32_t* out_ids, double* out_logits) {
+  TRY(check_loop_args(n, prompt, lens, B, S, n_new ? n_new - 1 : 0, out_ids));
+  if (n_new == 0) return OK;
+  const int rc = generate_impl(n, prompt, lens, B, S, n_new, out_ids, out_logits);
+  if (rc) (void)mitok_reset(n);  // caches and device lengths may be part-way through a step
+  return rc;
+}
+
+int mitok_prefill(mitok_network* n, const uint32_t* prompt, const uint32_t* lens, uint32_t B, uint32_t S,
+                  uint32_t* out_ids, double* out_logits) {
+  TRY(check_loop_args(n, prompt, lens, B, S, 0, out_ids));
+  hipStream_t st = n->stream;
+  const uint32_t V = n->layers[n->layers.size() - 2]->d_out;
+  int rc = run_prompt(n, prompt, lens, B, S, 1, S + 1, out_logits != nullptr);
+  if (!rc && hipMemcpyAsync(out_ids, n->hist_d.p, B * sizeof(uint32_t), hipMemcpyDeviceToHost, st) != hipSuccess)
+    rc = fail(ERR_HIP, "prefill: id copy failed");
+  if (!rc && out_logits &&
+      hipMemcpyAsync(out_logits, n->logit_hist_d.p, (size_t)B * V * sizeof(double), hipMemcpyDeviceToHost, st) != hipSuccess)
+    rc = fail(ERR_HIP, "prefill: logits copy failed");
+  if (!rc && hipStreamSynchronize(st) != hipSuccess) rc = fail(ERR_HIP, "prefill: stream sync failed");
+  if (!rc) rc = check_err_word(n);
+  if (rc) (void)mitok_reset(n);
+  return rc;
+}
+
+static int decode_step_impl(Net* n, const uint32_t* ids, uint32_t B, uint32_t* out_ids, double* out_logits) {
+  hipStream_t st = n->stream;
+  const uint32_t V = n->layers[n->layers.size() - 2]->d_out;
+  const bool want_logits = out_logits != nullptr;
+  uint32_t kv_max = 0;
+  for (uint32_t b = 0; b < B; ++b) kv_max = std::max(kv_max, n->kv_len_h[b]);
+  Spec dec = decode_spec(n, B);
+  TRY(prepare(n, dec));
+  TRY(reserve(n, n->hist_d, (size_t)B * sizeof(uint32_t)));
+  TRY(reserve(n, n->cnt_d, (size_t)B * sizeof(int)));
+  if (want_logits) TRY(reserve(n, n->logit_hist_d, (size_t)B * V * sizeof(double)));
+  TRY(ensure_rope_for(n, 0, dec.last, (int)std::max<uint32_t>(rope_positions_needed(n), kv_max + 1)));
+  bind_decode_inputs(n, dec);
+  if (ids) {
+    // the caller's ids are staged in ids_d (a stream-ordered copy of a host buffer
+    // that the call holds until its synchronisation below), then moved into place
+    TRY(reserve(n, n->ids_d, (size_t)B * sizeof(uint32_t)));
+    HIP_TRY(hipMemcpyAsync(n->ids_d.p, ids, B * sizeof(uint32_t), hipMemcpyHostToDevice, st));
+    HIP_TRY(hipMemcpyAsync(n->dec_ids_d.p, n->ids_d.p, B * sizeof(uint32_t), hipMemcpyDeviceToDevice, st));
+  }
+  fill_u32(st, n->ones_d.as<uint32_t>(), B, 1);
+  const bool direct = n->direct_launch || n->timing.cls != 0;
+  if (!direct) {
+    TRY(ensure_step_graph(n, dec, want_logits, 1, 1));
+    HIP_TRY(hipGraphLaunch(n->graph, st));
+  } else {
+    fill_int(st, n->cnt_d.as<int>(), B, 0);
+    n->dec_tsum = 0.0;
+    for (uint32_t b = 0; b < B; ++b) n->dec_tsum += (double)n->kv_len_h[b] + 1;
+    TimeScope ts(n, MITOK_TIME_STEP, 0.0);
+    TRY(enqueue_decode_step(n, dec, want_logits, 1));
+  }
+  HIP_TRY(hipMemcpyAsync(out_ids, n->hist_d.p, B * sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+  if (want_logits) HIP_TRY(hipMemcpyAsync(out_logits, n->logit_hist_d.p, (size_t)B * V * sizeof(double), hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  collect_timing(n);
+  TRY(check_err_word(n));
+  for (uint32_t b = 0; b < B; ++b) n->kv_len_h[b] += 1;
+  return OK;
+}
+
+int mitok_decode_step(mitok_network* n, const uint32_t* ids, uint32_t B, uint32_t* out_ids, double* out_logits) {
+  if (!n || !out_ids) return fail(ERR_ARG, "null argument");
+  if (!n->cache_valid) return fail(ERR_STATE, "decode_step before prefill (no KV cache)");
+  if (B != n->cache_B) return fail(ERR_STATE, "cached batch %u != %u; prefill first", n->cache_B, B);
+  TRY(set_device(n));
+  const uint32_t mc = min_ctx(n);
+  for (uint32_t b = 0; b < B; ++b)
+    if (mc != UINT32_MAX && n->kv_len_h[b] + 1 > mc)
+      return fail(ERR_ARG, "context %u exceeds max context %u", n->kv_len_h[b] + 1, mc);
+  if (ids) {
+    const uint32_t V0 = ((const EmbeddingLayer*)n->layers[0].get())->vocab;
+    for (uint32_t b = 0; b < B; ++b)
+      if (ids[b] >= V0) return fail(ERR_ARG, "No token embedding found: token id %u >= vocab %u (embedding_layer.rs:305)", ids[b], V0);
+  }
+  const int rc = decode_step_impl(n, ids, B, out_ids, out_logits);
+  if (rc) (void)mitok_reset(n);
+  return rc;
 }
 
 int mitok_greedy_decoding(mitok_network* n, const double* logits, uint32_t rows, uint32_t V, uint32_t* out_ids) {

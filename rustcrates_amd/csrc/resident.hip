@@ -64,14 +64,12 @@ size_t resident_op_lds(const ROp& op) {
   return 0;
 }
 
-int resident_grid(int device, int mr, int dh, size_t shm, int* grid) {
-  hipDeviceProp_t prop;
-  if (hipGetDeviceProperties(&prop, device) != hipSuccess) return ERR_HIP;
-  if (!prop.cooperativeLaunch) return ERR_STATE;
+int resident_grid(int cus, bool cooperative, int mr, int dh, size_t shm, int* grid) {
+  if (!cooperative) return ERR_STATE;
   int occ = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, pick_kernel(mr, dh), 256, shm) != hipSuccess) return ERR_HIP;
   if (occ < 1) return ERR_STATE;
-  *grid = prop.multiProcessorCount;
+  *grid = cus;
   return OK;
 }
 

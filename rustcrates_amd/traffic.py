@@ -92,9 +92,12 @@ def _summarize(a) -> None:
     fb = sum(fetch.values()) / len(fetch) * 1024.0 * factor_f
     wb = sum(write.values()) / len(write) * 1024.0 * factor_w
     kernels = sorted({_short(k[0]) for k in fetch})
+    from .build import source_hash
+
     res = {
         "workload": a.workload,
         "kernel_class": a.kernel_class,
+        "csrc_sha": source_hash(),
         "kernels": kernels,
         "dispatches": len(fetch),
         "fetch_bytes_per_launch": fb,
@@ -131,7 +134,9 @@ def _summarize(a) -> None:
         fh.write(f"| fetched per launch (scaled) | {fb / 1e6:.3f} MB |\n")
         fh.write(f"| written per launch (scaled) | {wb / 1e6:.3f} MB |\n")
         fh.write(f"| traffic per launch | {(fb + wb) / 1e6:.3f} MB |\n\n")
-        fh.write("Kernels: " + ", ".join(f"`{k}`" for k in kernels) + "\n")
+        fh.write("Kernels: " + ", ".join(f"`{k}`" for k in kernels) + "\n\n")
+        fh.write(f"Sources: `csrc` SHA-256 prefix `{res['csrc_sha']}` (bench.py reports this traffic only while "
+                 "the sources hash the same).\n")
     print(json.dumps(res))
 
 

@@ -89,3 +89,45 @@ def oracle_mod():
 
     oracle.lib()
     return oracle
+
+
+def seeded_tensors(cfg):
+    """Every tensor of cfg's seeded stack (configs.build_network), read back
+    from the CPU checker, as a list of per-layer dicts in LayerEnum order."""
+    import oracle
+    from rustcrates_amd import configs
+
+    o = configs.build_network(oracle.Network(), cfg)
+    d, F, V, h, mc = cfg.d, cfg.ffn, cfg.vocab, cfg.heads, cfg.max_ctx
+    out = [{"table": o.get_tensor(0, 0, V * d)}]
+    li = 1
+    for _ in range(cfg.layers):
+        nw = h * d * cfg.dh
+        out.append({"gamma": o.get_tensor(li, 6, d), "beta": o.get_tensor(li, 7, d)})
+        out.append({"wq": o.get_tensor(li + 1, 0, nw), "wk": o.get_tensor(li + 1, 1, nw),
+                    "wv": o.get_tensor(li + 1, 2, nw), "bias_pos": o.get_tensor(li + 1, 3, h * mc * mc),
+                    "gamma": o.get_tensor(li + 1, 6, d), "beta": o.get_tensor(li + 1, 7, d)})
+        out.append({"w1": o.get_tensor(li + 2, 0, d * F), "b1": o.get_tensor(li + 2, 4, F),
+                    "w2": o.get_tensor(li + 2, 1, F * d), "b2": o.get_tensor(li + 2, 5, d)})
+        li += 3
+    out.append({"w": o.get_tensor(li, 0, d * V), "b": o.get_tensor(li, 4, V)})
+    o.close()
+    return out
+
+
+def build_explicit(net, cfg, t):
+    """cfg's stack on `net` (HIP or checker) from explicit tensors `t`
+    (seeded_tensors layout, possibly edited)."""
+    net.add_embedding(cfg.vocab, cfg.d, t[0]["table"])
+    k = 1
+    for _ in range(cfg.layers):
+        net.add_norm(cfg.d, cfg.norm_eps, t[k]["gamma"], t[k]["beta"])
+        a = t[k + 1]
+        net.add_self_attention(cfg.heads, cfg.d, cfg.max_ctx, cfg.attn_eps, a["wq"], a["wk"], a["wv"], a["bias_pos"],
+                               a["gamma"], a["beta"])
+        f = t[k + 2]
+        net.add_feed_forward(cfg.d, cfg.ffn, f["w1"], f["b1"], f["w2"], f["b2"])
+        k += 3
+    net.add_linear(cfg.d, cfg.vocab, t[k]["w"], t[k]["b"])
+    net.add_softmax(1)
+    return net

@@ -162,3 +162,71 @@ def test_config5_full_decode_plans_agree():
             f"elementwise {e:.3e}, normwise {nw:.3e}")
         assert np.array_equal(out[1][0], out[3][0])
         assert nw < DECODE_SPREAD
+
+
+def test_config4_batch1_decoded_to_cache_end():
+    """Full config 4 at batch 1 (the resident loop): a 64-token prompt decoded
+    for 449 tokens, so the last step attends over all 512 cache rows
+    (max_ctx).  Ids bit-exact against the oracle over every step; the logits
+    normwise error is logged beside the bound (the oracle's own summation
+    orders differ by about 1e-5 normwise on this model, see above)."""
+    cfg = configs.C4
+    lens = [64]
+    n_new = cfg.max_ctx - lens[0] + 1
+    prompt = seeded.prompts(44, lens, cfg.vocab)
+    g = configs.build_network(ra.Network(0), cfg)
+    o = configs.build_network(oracle.Network(), cfg)
+    log(f"config 4 full, batch 1, prompt 64 + {n_new} tokens (oracle ~1 min)")
+    ig, lg = g.generate(prompt, lens=lens, n_new=n_new, want_logits=True)
+    assert g.last_timings()["decode_loop"] == "resident"
+    io, lo = o.generate(prompt, lens=lens, n_new=n_new, want_logits=True)
+    first_diff = int(np.argmax(ig[0] != io[0])) if not np.array_equal(ig, io) else -1
+    nw = normwise_rel_err(lg, lo)
+    log(f"  ids match {np.array_equal(ig, io)} (first difference {first_diff}); normwise {nw:.3e}; "
+        f"last step normwise {normwise_rel_err(lg[-1:], lo[-1:]):.3e}")
+    assert np.array_equal(ig, io)
+    assert nw < 1e-3
+    g.close()
+
+
+def test_config5_batch1_decoded_to_2047_keys():
+    """Full config 5 at batch 1: prompt 1920 + 128 tokens, so the last step
+    attends over 2047 keys.  The resident loop and the fused launches decode
+    from the same prefill and agree on every id (as in the batch-4 test)."""
+    w = configs.WORKLOADS["c5"]
+    lens = configs.prompt_lengths(w)[:1]
+    prompt = seeded.prompts(w.prompt_seed, lens, w.model.vocab, max_len=w.prompt_len)
+    n_new = w.model.max_ctx - lens[0]  # 1920 + 127 = 2047 keys at the last step
+    g = configs.build_network(ra.Network(0), w.model)
+    out = {}
+    for plan in (3, 1):
+        g.set_decode_plan(plan)
+        out[plan] = g.generate(prompt, lens=lens, n_new=n_new, want_logits=True)
+    nw = normwise_rel_err(out[1][1], out[3][1])
+    log(f"config 5 full, batch 1 to {lens[0] + n_new - 1} keys: ids match "
+        f"{np.array_equal(out[1][0], out[3][0])}, normwise {nw:.3e}")
+    assert np.array_equal(out[1][0], out[3][0])
+    assert nw < DECODE_SPREAD
+    g.close()
+
+
+def test_config5_layer_decoded_to_full_context_vs_oracle():
+    """The config-5 layer shape (d 768, 12 heads, FFN 3072, max_ctx 2048): a
+    1920-token prompt decoded for 129 tokens, so the last step attends over all
+    2048 cache rows, on every plan against the oracle."""
+    cfg = configs.ModelConfig("c5l1", layers=1, d=768, heads=12, ffn=3072, vocab=300, max_ctx=2048, seed=3)
+    lens = [1920]
+    n_new = cfg.max_ctx - lens[0] + 1
+    prompt = seeded.prompts(12, lens, cfg.vocab)
+    g = configs.build_network(ra.Network(0), cfg)
+    o = configs.build_network(oracle.Network(), cfg)
+    io, lo = o.generate(prompt, lens=lens, n_new=n_new, want_logits=True)
+    for plan in (3, 1, 0):
+        g.set_decode_plan(plan)
+        ig, lg = g.generate(prompt, lens=lens, n_new=n_new, want_logits=True)
+        e = max_rel_err(lg, lo)
+        log(f"c5 layer to 2048 keys, plan {plan}: ids {np.array_equal(ig, io)}, elementwise {e:.3e}, "
+            f"normwise {normwise_rel_err(lg, lo):.3e}")
+        assert np.array_equal(ig, io), f"plan {plan}"
+        assert e < REL_TOL, f"plan {plan}"
+    g.close()

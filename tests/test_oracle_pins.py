@@ -381,3 +381,171 @@ def test_pad_token_embeds_to_zero():
     out, _ = net.predict(np.array([[0, 1, 2]], np.uint32), forward_only=True)
     # identity Linear + bias 1: Re(embedding) + 1, id 1 gives the zero vector
     np.testing.assert_array_equal(out[0], np.array([[1, 2, 3], [1, 1, 1], [7, 8, 9]], float))
+
+
+# --------------------------------------------------------------------------
+# whole model, brute force (numpy, written from the reference text)
+# --------------------------------------------------------------------------
+def _np_layernorm(x, eps, gamma, beta):
+    """NormalNormLayer::normalize (norm_layer.rs:64-80): complex mean and
+    variance, principal csqrt, Re of ((x - mean) / s) * gamma + beta."""
+    mean = x.mean(axis=-1, keepdims=True)
+    var = ((x - mean) ** 2).mean(axis=-1, keepdims=True)
+    s = np.sqrt(var + eps)
+    return (((x - mean) / s) * gamma + beta).real.astype(complex)
+
+
+def _np_gelu(z):
+    """gelu_complex (activation.rs:195-212): clamp re and im of f(z) to [-30, 30]."""
+    f = math.sqrt(2.0 / math.pi) * (z + 0.044715 * z**3)
+    f = np.clip(f.real, -30, 30) + 1j * np.clip(f.imag, -30, 30)
+    return 0.5 * z * (1.0 + np.tanh(f))
+
+
+def _np_softmax_re(row):
+    e = np.exp(row.real - row.real.max())
+    return e / e.sum()
+
+
+def _np_model(W, ids, lens, mode):
+    """predict (transformer_network.rs:315-504) over Embedding -> [Norm ->
+    SelfAttention -> FeedForward] x L -> Linear -> Softmax, one sequence at a
+    time.  mode: 'logits' (forward_only: Re(logits) of every row),
+    'production' (softmax_last_row), 'training' (Re-softmax, pad rows 0)."""
+    B, S = ids.shape
+    out = np.zeros((B, S, W["V"]))
+    for b in range(B):
+        mask = (np.arange(S) < lens[b]).astype(np.uint32)
+        padded = np.where(mask == 1, ids[b], 1)  # apply_padding_to_batch: PAD = 1
+        x = W["table"][padded].copy()
+        x[padded == 1] = 0  # id 1 embeds to zeros (embedding_layer.rs:183-184)
+        for L in W["layers"]:
+            x = _np_layernorm(x, L["norm_eps"], L["n_gamma"], L["n_beta"])  # standalone Norm: no residual
+            h, d, dh = L["wq"].shape
+            cat = np.zeros((S, d), complex)
+            for hh in range(h):
+                q, k, v = x @ L["wq"][hh], x @ L["wk"][hh], x @ L["wv"][hh]
+                sc = (q @ k.T) * (1.0 / (1e-8 + math.sqrt(dh))) + L["bias_pos"][hh, :S, :S]
+                sc = np.where(np.tril(np.ones((S, S))) > 0, sc, -1e12 - 1e12j)
+                p = np.array([_np_softmax_re(r) for r in sc])
+                p[mask == 0] = 0  # softmax_complex_padding_real: pad query rows 0
+                cat[:, hh * dh:(hh + 1) * dh] = p @ v
+            x = _np_layernorm((cat + x).real.astype(complex), L["attn_eps"], L["a_gamma"], L["a_beta"])
+            hid = _np_gelu(x @ L["w1"] + L["b1"])  # Dense: bias before GELU (layer.rs:132-166)
+            hid[mask == 0] = 0  # activate_output_complex_padding (activation.rs:268-284)
+            x = hid @ L["w2"] + L["b2"]  # Linear, no residual, no norm (feedforward_layer.rs:44)
+        logits = x @ W["wv"] + W["bv"]  # vocab Linear (linear_layer.rs:55-75)
+        if mode == "logits":
+            out[b] = logits.real  # convert_c_to_f64_3d
+        elif mode == "production":
+            out[b, S - 1] = _np_softmax_re(logits[S - 1])  # softmax_last_row (activation.rs:409-419)
+        else:
+            for s in range(S):
+                out[b, s] = _np_softmax_re(logits[s]) if mask[s] else 0.0
+    return out
+
+
+def _rand_c(rng, *shape, scale=1.0):
+    return scale * (rng.standard_normal(shape) + 1j * rng.standard_normal(shape))
+
+
+def _brute_force_fixture(mode_const, seed=11):
+    """A 2-layer model with every tensor random and complex (gamma, beta and
+    all biases too, so no term can vanish) and a non-square, non-symmetric
+    vocab Linear."""
+    rng = np.random.default_rng(seed)
+    V, d, h, F, mc, nl = 23, 8, 2, 12, 16, 2
+    dh = d // h
+    W = {"V": V, "table": _rand_c(rng, V, d), "layers": []}
+    net = oracle.Network()
+    net.add_embedding(V, d, W["table"])
+    for _ in range(nl):
+        L = {"norm_eps": 1e-5, "attn_eps": 1e-12,
+             "n_gamma": _rand_c(rng, d), "n_beta": _rand_c(rng, d, scale=0.1),
+             "wq": _rand_c(rng, h, d, dh, scale=0.4), "wk": _rand_c(rng, h, d, dh, scale=0.4),
+             "wv": _rand_c(rng, h, d, dh, scale=0.4), "bias_pos": _rand_c(rng, h, mc, mc),
+             "a_gamma": _rand_c(rng, d), "a_beta": _rand_c(rng, d, scale=0.1),
+             "w1": _rand_c(rng, d, F, scale=0.3), "b1": _rand_c(rng, F, scale=0.2),
+             "w2": _rand_c(rng, F, d, scale=0.3), "b2": _rand_c(rng, d, scale=0.2)}
+        W["layers"].append(L)
+        net.add_norm(d, L["norm_eps"], L["n_gamma"], L["n_beta"])
+        net.add_self_attention(h, d, mc, L["attn_eps"], L["wq"], L["wk"], L["wv"], L["bias_pos"],
+                               L["a_gamma"], L["a_beta"])
+        net.add_feed_forward(d, F, L["w1"], L["b1"], L["w2"], L["b2"])
+    W["wv"] = _rand_c(rng, d, V, scale=0.5)
+    W["bv"] = _rand_c(rng, V, scale=0.5)
+    net.add_linear(d, V, W["wv"], W["bv"])
+    net.add_softmax(mode_const)
+    # two sequences, right-padded; PAD (id 1) also sits mid-prompt in sequence 0
+    ids = np.array([[5, 1, 17, 3, 22, 9, 0], [7, 4, 12, 2, 1, 1, 1]], np.uint32)
+    lens = np.array([7, 4], np.uint32)
+    return net, W, ids, lens
+
+
+@pytest.mark.parametrize("mode", ["logits", "production", "training"])
+def test_whole_model_matches_numpy_brute_force(mode):
+    const = oracle.TRAINING if mode == "training" else oracle.PRODUCTION
+    net, W, ids, lens = _brute_force_fixture(const)
+    got, mask = net.predict(ids, lens=lens, forward_only=(mode == "logits"))
+    want = _np_model(W, ids, lens, mode)
+    assert np.array_equal(mask, (np.arange(7)[None, :] < lens[:, None]).astype(np.uint32))
+    np.testing.assert_allclose(got, want, rtol=1e-10, atol=1e-12)
+    if mode == "training":
+        assert np.all(got[1, 4:] == 0.0)  # pad rows of the TRAINING arm are exactly 0
+        np.testing.assert_allclose(got[1, :4].sum(axis=1), 1.0, rtol=1e-14)
+    if mode == "production":
+        assert np.all(got[:, :-1] == 0.0)
+
+
+def test_brute_force_model_catches_a_transposed_linear():
+    """The vocab Linear is [in][out] (linear_layer.rs:38): the brute force with
+    the weight transposed into [out][in] order must disagree, so the pin above
+    distinguishes the two orientations."""
+    net, W, ids, lens = _brute_force_fixture(oracle.PRODUCTION)
+    got, _ = net.predict(ids, lens=lens, forward_only=True)
+    wrong = dict(W)
+    d, V = W["wv"].shape
+    wrong["wv"] = W["wv"].reshape(-1)[: d * V].reshape(V, d).T.copy()  # same memory read as [out][in]
+    assert not np.allclose(got, _np_model(wrong, ids, lens, "logits"), rtol=1e-6)
+
+
+def test_ffn_layer_matches_numpy_with_pad_rows():
+    """FeedForward alone through forward_layers: x W1 + b1 -> GELU -> pad rows
+    0 -> W2 + b2 (no residual), so pad rows come out as exactly b2."""
+    rng = np.random.default_rng(12)
+    d, F = 6, 10
+    w1, b1, w2, b2 = _rand_c(rng, d, F, scale=0.5), _rand_c(rng, F), _rand_c(rng, F, d, scale=0.5), _rand_c(rng, d)
+    net = oracle.Network()
+    net.add_feed_forward(d, F, w1, b1, w2, b2)
+    x = _rand_c(rng, 1, 5, d)
+    mask = np.array([[1, 1, 1, 0, 0]], np.uint32)
+    got = net.forward_layers(0, 1, x, mask=mask, forward_only=True)
+    hid = _np_gelu(x[0] @ w1 + b1)
+    hid[mask[0] == 0] = 0
+    np.testing.assert_allclose(got[0], hid @ w2 + b2, rtol=1e-12, atol=1e-13)
+    assert np.array_equal(got[0, 3:], np.broadcast_to(b2, (2, d)))
+
+
+def test_linear_layer_orientation_non_square():
+    """LinearLayer [in][out] with a non-square integer weight: exact."""
+    w = np.arange(12, dtype=float).reshape(3, 4) + 1j * np.arange(12, dtype=float).reshape(3, 4)[::-1]
+    b = np.array([1, 2, 3, 4], complex)
+    net = oracle.Network()
+    net.add_linear(3, 4, w, b)
+    x = np.array([[[1 + 2j, -1 + 0j, 3 - 1j]]])
+    got = net.forward_layers(0, 1, x, forward_only=True, d_out=4)
+    assert np.array_equal(got[0, 0], x[0, 0] @ w + b)
+
+
+def test_explicit_tensor_stack_equals_seeded_stack():
+    """The tests' explicit-tensor builder (conftest.build_explicit) reproduces
+    the seeded stack bit for bit, so edited copies differ only where edited."""
+    from conftest import build_explicit, seeded_tensors
+
+    cfg = configs.ModelConfig("t", layers=2, d=16, heads=2, ffn=24, vocab=50, max_ctx=24, seed=8)
+    a = configs.build_network(oracle.Network(), cfg)
+    b = build_explicit(oracle.Network(), cfg, seeded_tensors(cfg))
+    p = seeded.prompts(4, [6, 3], cfg.vocab)
+    ia, la = a.generate(p, lens=[6, 3], n_new=5, want_logits=True)
+    ib, lb = b.generate(p, lens=[6, 3], n_new=5, want_logits=True)
+    assert np.array_equal(ia, ib) and np.array_equal(la, lb)

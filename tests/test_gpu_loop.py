@@ -16,7 +16,7 @@ import pytest
 
 import oracle
 import rustcrates_amd as ra
-from conftest import REL_TOL, build_explicit, max_rel_err, seeded_tensors
+from conftest import NOISE_FACTOR, REL_TOL, build_explicit, max_rel_err, oracle_noise_floor, seeded_tensors
 from rustcrates_amd import configs, seeded
 
 pytestmark = pytest.mark.gpu
@@ -112,12 +112,16 @@ def test_prefill_and_decode_steps_equal_generate(lens):
         ids.append(nxt)
         lgs.append(ln)
     steps, steps_lg = np.stack(ids, axis=1), np.stack(lgs)
+    # the batched products sum in another order than the oracle; at the edge of
+    # the bar the oracle's own valid orders set it (conftest.oracle_noise_floor)
+    floor = oracle_noise_floor(o, prompt, lens, n_new, lo)[0]
+    tol = max(REL_TOL, NOISE_FACTOR * floor)
     log(f"per-step B={B}: equals generate {np.array_equal(steps, ig)}, logits identical "
-        f"{np.array_equal(steps_lg, lg)}, vs oracle {max_rel_err(steps_lg, lo):.2e}")
+        f"{np.array_equal(steps_lg, lg)}, vs oracle {max_rel_err(steps_lg, lo):.2e} (tol {tol:.2e})")
     assert np.array_equal(steps, ig)
     assert np.array_equal(steps_lg, lg)
     assert np.array_equal(steps, io)
-    assert max_rel_err(steps_lg, lo) < REL_TOL
+    assert max_rel_err(steps_lg, lo) < tol
     # logits-free steps give the same ids
     first2 = g.prefill(prompt, lens=lens)
     seq = [first2] + [g.decode_step() for _ in range(n_new - 1)]

@@ -141,6 +141,17 @@ int mitok_decode_step(mitok_network* net, const uint32_t* ids, uint32_t batch, u
  * logits [rows][vocab]: last index among equal maxima; NaN -> MITOK_ERR_NAN. */
 int mitok_greedy_decoding(mitok_network* net, const double* logits, uint32_t rows, uint32_t vocab, uint32_t* out_ids);
 
+/* mitok_greedy_decoding without any device allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops).  The logits and ids are staged in a
+ * fixed per-GPU array of the library (8 MiB + 16 KiB, held by every GPU the
+ * library runs on until the process ends): rows * vocab <= 1048576 and
+ * rows <= 4096, else MITOK_ERR_ARG.  All calls on one GPU share that array, so
+ * calls that overlap on one GPU (two networks on one device used from two
+ * threads) race; calls through one network are serialised by its stream. */
+int mitok_greedy_decoding_noalloc(mitok_network* net, const double* logits, uint32_t rows, uint32_t vocab,
+                                  uint32_t* out_ids);
+
 /* ---- measurement (no reference counterpart: the reference prints wall
  * clock only, transformer_network.rs:307-310) ---- */
 /* Wall time of the last mitok_generate on the device stream, in ms:

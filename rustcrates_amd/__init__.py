@@ -56,6 +56,7 @@ SIGNATURES = {
     "mitok_prefill": (_i32, [_P, _P, _P, _u32, _u32, _P, _P]),
     "mitok_decode_step": (_i32, [_P, _P, _u32, _P, _P]),
     "mitok_greedy_decoding": (_i32, [_P, _P, _u32, _u32, _P]),
+    "mitok_greedy_decoding_noalloc": (_i32, [_P, _P, _u32, _u32, _P]),
     "mitok_last_timings": (_i32, [_P, _P]),
     "mitok_timing_enable": (_i32, [_P, _i32]),
     "mitok_timing_read": (_i32, [_P, _P, _P, _P, _P]),

@@ -14,6 +14,7 @@
 
 #include <algorithm>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -177,6 +178,7 @@ struct Timing {
 struct mitok_network {
   int device = 0;
   int cus = 0;               // compute units (the resident loop runs one block per CU)
+  void* scratch = nullptr;   // this device's copy of the no-allocation staging array
   bool cooperative = false;  // cooperative launches supported
   hipStream_t stream = nullptr;
   std::vector<std::unique_ptr<mitok::Layer>> layers;
@@ -1313,6 +1315,37 @@ static int rope_positions_needed(const Net* n) {
   return (int)std::max<uint32_t>(m == UINT32_MAX ? 512u : m, 512u);
 }
 
+// ---------------------------------------------------------------------------
+// staging of mitok_greedy_decoding_noalloc, for callers that cannot allocate
+// ---------------------------------------------------------------------------
+constexpr size_t NOALLOC_MAX_LOGITS = size_t(1) << 20;  // doubles (8 MiB): 32 rows of a 32000-id vocab
+constexpr size_t NOALLOC_MAX_ROWS = 4096;
+constexpr size_t NOALLOC_BYTES = NOALLOC_MAX_LOGITS * sizeof(double) + NOALLOC_MAX_ROWS * sizeof(uint32_t);
+constexpr int NOALLOC_MAX_DEVICES = 64;
+
+// Every GPU the library runs on holds its own copy for the life of the
+// process.  In host code this name is not a device address: kernels and
+// copies take the per-device address that noalloc_scratch() resolves.
+static __device__ __align__(256) unsigned char scratch[NOALLOC_BYTES];
+
+static std::mutex g_scratch_mu;
+static void* g_scratch[NOALLOC_MAX_DEVICES] = {};
+
+// The address of `scratch` on `device`, which must be the current device;
+// resolved once per device (at network creation) and kept.
+static int noalloc_scratch(int device, void** out) {
+  if (device < 0 || device >= NOALLOC_MAX_DEVICES) return fail(ERR_ARG, "device %d beyond the staging table", device);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[device]) {
+    void* p = nullptr;
+    HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) return fail(ERR_HIP, "hipGetSymbolAddress returned no address");
+    g_scratch[device] = p;
+  }
+  *out = g_scratch[device];
+  return OK;
+}
+
 }  // namespace mitok
 
 using namespace mitok;
@@ -1353,6 +1386,7 @@ int mitok_network_create(int device, mitok_network** out) {
   }
   if (!rc && hipStreamCreateWithFlags(&n->stream, hipStreamNonBlocking) != hipSuccess)
     rc = fail(ERR_HIP, "hipStreamCreate failed");
+  if (!rc) rc = noalloc_scratch(device, &n->scratch);
   if (!rc) rc = n->err_d.reserve(sizeof(uint32_t));
   if (!rc) rc = n->sync_cnt.reserve((size_t)SYNC_COUNTERS * sizeof(uint32_t));
   if (!rc) {
@@ -2114,6 +2148,22 @@ int mitok_greedy_decoding(mitok_network* n, const double* logits, uint32_t rows,
   HIP_TRY(hipMemcpyAsync(lg.p, logits, (size_t)rows * V * sizeof(double), hipMemcpyHostToDevice, n->stream));
   argmax_rows(n->stream, lg.as<double>(), rows, V, ids.as<uint32_t>(), n->err_d.as<uint32_t>());
   HIP_TRY(hipMemcpyAsync(out_ids, ids.p, rows * sizeof(uint32_t), hipMemcpyDeviceToHost, n->stream));
+  HIP_TRY(hipStreamSynchronize(n->stream));
+  return check_err_word(n);
+}
+
+int mitok_greedy_decoding_noalloc(mitok_network* n, const double* logits, uint32_t rows, uint32_t V, uint32_t* out_ids) {
+  if (!n || !logits || !out_ids || !rows || !V) return fail(ERR_ARG, "bad arguments");
+  if (rows > NOALLOC_MAX_ROWS || (uint64_t)rows * V > NOALLOC_MAX_LOGITS)
+    return fail(ERR_ARG, "%u x %u logits exceed the no-allocation staging (%zu logits, %zu rows)", rows, V,
+                NOALLOC_MAX_LOGITS, NOALLOC_MAX_ROWS);
+  if (!n->scratch) return fail(ERR_STATE, "no staging address for device %d", n->device);
+  TRY(set_device(n));
+  double* lg = (double*)n->scratch;
+  uint32_t* ids = (uint32_t*)((unsigned char*)n->scratch + NOALLOC_MAX_LOGITS * sizeof(double));
+  HIP_TRY(hipMemcpyAsync(lg, logits, (size_t)rows * V * sizeof(double), hipMemcpyHostToDevice, n->stream));
+  argmax_rows(n->stream, lg, rows, V, ids, n->err_d.as<uint32_t>());
+  HIP_TRY(hipMemcpyAsync(out_ids, ids, rows * sizeof(uint32_t), hipMemcpyDeviceToHost, n->stream));
   HIP_TRY(hipStreamSynchronize(n->stream));
   return check_err_word(n);
 }

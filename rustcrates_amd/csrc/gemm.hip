@@ -527,6 +527,76 @@ __global__ __launch_bounds__(256) void k_zgemm_skinny_rows(const double2* __rest
 }
 
 // ===========================================================================
+// Row-tile variant with 16 waves per block: as k_zgemm_skinny_rows (CT = 1),
+// but the block's K range of 64*nkw is split over 16 waves, four per SIMD, so
+// each SIMD interleaves four waves' loads and MFMAs.  With one wave per SIMD
+// a wave of ~128 MFMAs cannot hide its own load latency (the 4-wave kernel ran
+// at 22-28% MFMA busy); here each wave has a quarter of the work and the
+// SIMD's other waves compute while it waits.  Two batches of 4 k-steps per
+// wave are requested ahead of the one being multiplied (the register budget at
+// four waves per SIMD).  The 16 waves' tiles are summed through LDS in wave
+// order, so results repeat bit for bit.
+// ===========================================================================
+constexpr int ROWS16_WAVES = 16;
+constexpr size_t ROWS16_LDS = (size_t)ROWS16_WAVES * 16 * 16 * sizeof(double2);  // 64 KB
+
+__global__ __launch_bounds__(1024) void k_zgemm_rows16(const double2* __restrict__ X, long ldx, int M,
+                                                     const double2* __restrict__ W, long ldw, int N, int K, int nkw,
+                                                     Epi ep) {
+  constexpr int U = 4, NW = ROWS16_WAVES, LD = 16;
+  extern __shared__ double2 red16[];  // [NW][16][LD]: lanes write and read whole 1 KB rows, no bank conflicts
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int i = lane & 15, kq = lane >> 4;
+  const int n = blockIdx.x * 16 + i, m = blockIdx.y * 16 + i;
+  const int ka = (blockIdx.z * NW + wave) * 4 * nkw, kz = min(K, ka + 4 * nkw);
+  double2 a[2][U], b[2][U];
+  auto load = [&](int s, int k) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int kk = k + 4 * u + kq;
+      b[s][u] = (kk < kz && n < N) ? W[(long)kk * ldw + n] : make_double2(0.0, 0.0);
+      a[s][u] = (kk < kz && m < M) ? X[(long)m * ldx + kk] : make_double2(0.0, 0.0);
+    }
+  };
+  v4d cr = {0.0, 0.0, 0.0, 0.0}, ci = {0.0, 0.0, 0.0, 0.0};
+  // each batch's real-part products before its imaginary-part ones, so two
+  // MFMAs on one accumulator are never adjacent
+  auto mma = [&](int s) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      cr = __builtin_amdgcn_mfma_f64_16x16x4f64(a[s][u].x, b[s][u].x, cr, 0, 0, 0);
+      ci = __builtin_amdgcn_mfma_f64_16x16x4f64(a[s][u].x, b[s][u].y, ci, 0, 0, 0);
+      cr = __builtin_amdgcn_mfma_f64_16x16x4f64(-a[s][u].y, b[s][u].y, cr, 0, 0, 0);
+      ci = __builtin_amdgcn_mfma_f64_16x16x4f64(a[s][u].y, b[s][u].x, ci, 0, 0, 0);
+    }
+  };
+  constexpr int KS = 4 * U;  // k per batch; unrolled by two so buffer indices are constants
+  load(0, ka);
+  load(1, ka + KS);
+  for (int k = ka; k < kz; k += 2 * KS) {
+    mma(0);
+    if (k + 2 * KS < kz) load(0, k + 2 * KS);
+    if (k + KS >= kz) break;
+    mma(1);
+    if (k + 3 * KS < kz) load(1, k + 3 * KS);
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) red16[(wave * 16 + 4 * e + kq) * LD + i] = make_double2(cr[e], ci[e]);
+  __syncthreads();
+  if (tid < 256) {
+    const int row = tid >> 4, col = tid & 15;
+    double2 v = red16[row * LD + col];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) v = cadd(v, red16[(w * 16 + row) * LD + col]);
+    const int nn = blockIdx.x * 16 + col, mm = blockIdx.y * 16 + row;
+    if (mm < M && nn < N) {
+      if (ep.mode == EPI_PART) ep.out[((long)blockIdx.z * M + mm) * N + nn] = v;
+      else apply_epi(ep, M, N, mm, nn, v);
+    }
+  }
+}
+
+// ===========================================================================
 // Wide skinny variant (vocab-wide outputs): a block owns all M rows (RT
 // tiles of 16) and 16*CW columns; its 4 waves are CW column groups x (4/CW) K
 // groups.  Each wave accumulates its 16RT x 16 tile with v_mfma_f64_16x16x4_f64
@@ -794,6 +864,7 @@ static GemvPlan plan_gemv(int M, int N, int K, bool part) {
 struct SkinnyPlan {
   int rt, cw, ncb, kc, P;  // cw 4: the wide variant
   int rows = 0, ct = 1, nkw = 0;  // rows: the row-tile variant, CT column tiles, nkw k-steps per wave
+  int w16 = 0;                    // rows with 16 waves per block (k_zgemm_rows16)
 };
 // outputs at least this wide take the wide variant (a grid of 256 blocks
 // without a K split); measured at config 3, batch 32, the layer products
@@ -811,6 +882,9 @@ constexpr int SKINNY_TARGET_BLOCKS = 512;
 // completion; FFN Linear (4 splits) 10.2 -> 9.2 us with half the partials.
 // 64 and 256 MFMAs per wave measured slower.
 constexpr int SKINNY_ROWS_MFMA = 128;
+// the 16-wave row-tile kernel from this inner dimension up (a block's K range
+// covers 16 waves of 4-step batches)
+constexpr int ROWS16_MIN_K = 256;
 constexpr int SKINNY_ROWS_MAX_NKW = 64;     // k-steps per wave of a product that may not split K
 constexpr int SKINNY_ROWS_MIN_BLOCKS = 128;  // fewer: the chip is less than half busy
 // argmax: the fused greedy id needs per-tile partials, which only the narrow
@@ -829,6 +903,28 @@ static SkinnyPlan plan_skinny(int M, int N, int K, bool part, bool argmax) {
     return p;
   }
   p.cw = 0;
+  if (!argmax && K >= ROWS16_MIN_K) {
+    // 16 waves per block, 512 of K per block (32 per wave): the layer products
+    // of config 3 and up fill the chip with one K range per block (FFN Dense,
+    // QKV) or four (FFN Linear, K 2048)
+    SkinnyPlan r = p;
+    r.rows = 1;
+    r.w16 = 1;
+    r.ct = 1;
+    r.ncb = cdiv_i(N, 16);
+    r.nkw = 8;
+    int P = cdiv_i(K, 64 * r.nkw);
+    if (!part) {
+      r.nkw = cdiv_i(K, 64);
+      P = 1;
+    } else if (P > SKINNY_MAX_SPLIT) {
+      r.nkw = cdiv_i(K, 64 * SKINNY_MAX_SPLIT);
+      P = cdiv_i(K, 64 * r.nkw);
+    }
+    r.P = P;
+    r.kc = 64 * r.nkw;
+    if (r.nkw <= SKINNY_ROWS_MAX_NKW) return r;
+  }
   if (!argmax) {
     SkinnyPlan r = p;
     const int tiles = cdiv_i(N, 16) * p.rt;  // 16x16 output tiles
@@ -928,6 +1024,10 @@ static void launch_skinny(hipStream_t st, const SkinnyPlan& p, const RowOps& ro,
   double2* ws = (double2*)sy.ws;
   if (p.rows) {  // EPI_PART, or one K range per block (no argmax: not a vocab-wide output)
     const dim3 g3(p.ncb, p.rt, p.P);
+    if (p.w16) {
+      MITOK_LAUNCH(k_zgemm_rows16, g3, dim3(64 * ROWS16_WAVES), ROWS16_LDS, st, ro.x, ro.ldx, M, W, ldw, N, K, p.nkw, ep);
+      return;
+    }
     if (p.ct == 2) MITOK_LAUNCH(k_zgemm_skinny_rows<2>, g3, blk, 0, st, ro.x, ro.ldx, M, W, ldw, N, K, p.nkw, ep);
     else MITOK_LAUNCH(k_zgemm_skinny_rows<1>, g3, blk, 0, st, ro.x, ro.ldx, M, W, ldw, N, K, p.nkw, ep);
     return;

@@ -189,3 +189,49 @@ def test_generate_to_max_context_exactly():
         assert np.array_equal(ig, io), f"plan {plan}"
         assert max_rel_err(lg, lo) < REL_TOL, f"plan {plan}"
     g.close()
+
+
+def test_imported_reference_model_file_runs_on_gpu():
+    """The committed model file in the reference's layout (bincode
+    NeuralNetwork + sled embedding pairs, tests/golden/make_model_fixture.py)
+    imported onto the HIP network: ids equal the stored checker ids, logits
+    within REL_TOL, on every decode plan."""
+    import os
+
+    from conftest import ROOT
+    from rustcrates_amd import model_io
+
+    gold = os.path.join(ROOT, "tests", "golden")
+    m = model_io.read_network(os.path.join(gold, "tiny_model.bincode"))
+    pairs = model_io.read_embedding_pairs(open(os.path.join(gold, "tiny_embeddings.pairs"), "rb").read())
+    exp = np.load(os.path.join(gold, "tiny_expected.npz"))
+    g = model_io.to_device(m, ra.Network(0), pairs)
+    for plan in (3, 1, 0):
+        g.set_decode_plan(plan)
+        ig, lg = g.generate(exp["prompt"], n_new=exp["ids"].shape[1], want_logits=True)
+        log(f"imported model plan {plan}: ids {ig[0].tolist()}, logits {max_rel_err(lg, exp['logits']):.2e}")
+        assert np.array_equal(ig, exp["ids"]), f"plan {plan}"
+        assert max_rel_err(lg, exp["logits"]) < REL_TOL, f"plan {plan}"
+    g.close()
+
+
+def test_import_of_a_config3_shaped_file_equals_the_seeded_network():
+    """A config-3-shaped model written in the reference's file layout and read
+    back uploads the same tensors: the imported and the seeded HIP networks
+    give bit-identical ids and logits."""
+    from rustcrates_amd import model_io
+
+    cfg = configs.ModelConfig("c3f", layers=2, d=512, heads=8, ffn=2048, vocab=3000, max_ctx=160, seed=4)
+    t = seeded_tensors(cfg)
+    blob = model_io.write_network(model_io.from_tensors(cfg, t))
+    table = t[0]["table"].reshape(cfg.vocab, cfg.d)
+    pairs = model_io.read_embedding_pairs(model_io.write_embedding_pairs({i: table[i] for i in range(cfg.vocab)}))
+    a = model_io.to_device(model_io.read_network(blob), ra.Network(0), pairs)
+    b = configs.build_network(ra.Network(0), cfg)
+    prompt = seeded.prompts(15, [40, 23], cfg.vocab)
+    ia, la = a.generate(prompt, lens=[40, 23], n_new=10, want_logits=True)
+    ib, lb = b.generate(prompt, lens=[40, 23], n_new=10, want_logits=True)
+    log(f"c3-shaped import: {len(blob) / 1e6:.1f} MB file, ids equal {np.array_equal(ia, ib)}")
+    assert np.array_equal(ia, ib) and np.array_equal(la, lb)
+    a.close()
+    b.close()

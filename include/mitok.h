@@ -84,6 +84,22 @@ int mitok_add_feed_forward(mitok_network* net, uint32_t dim, uint32_t hidden, co
 int mitok_add_linear(mitok_network* net, uint32_t in, uint32_t out, const double* w, const double* b);
 /* SoftmaxLayer (softmax_output_layer.rs:30-65) */
 int mitok_add_softmax(mitok_network* net, int operation_mode);
+/* DiscreteWaveletLayer (network_types/wavelet_discrete_layer.rs:46-161), partial
+ * mode, over rows of `dim` features.  At a prompt pass (and a stateless one)
+ * it replaces each sequence's S rows by the low half of dwt_1d along the
+ * sequence of every feature (wavelet_transform/dwt.rs:36-90), and the padding
+ * mask by its thresholded low half (:297-313); later layers and the KV cache
+ * see S' = mitok_seq_out_len rows.  A cached step's row passes through, and
+ * its RoPE position still counts the uncompressed prompt (time_step,
+ * transformer_network.rs:300-304).  wavelet: DiscreteWaletetType index (0 DB1,
+ * 1 DB2); mode: WaveletMode index (0 ZERO, 1 CONSTANT, 2 SYMMETRIC,
+ * 3 ANTISYMMETRIC, 4 REFLECT, 6 PERIODIC); is_full_mode must be 0.  Others
+ * are MITOK_ERR_ARG. */
+int mitok_add_discrete_wavelet(mitok_network* net, uint32_t dim, uint32_t wavelet, uint32_t mode, int is_full_mode);
+/* Rows per sequence that layers [first, last) leave of a prompt pass of `seq`
+ * rows (the wavelet layers compress them): the row count of mitok_predict's
+ * and mitok_forward_layers' outputs. */
+int mitok_seq_out_len(const mitok_network* net, uint32_t first, uint32_t last, uint32_t seq, uint32_t* out);
 
 /* Seeded Xavier-uniform weights (initialize_weights_complex, utils/weights_initializer.rs:73-89),
  * computed on the device from a counter generator: the CPU checker holds the same values. */
@@ -99,7 +115,8 @@ int mitok_reset(mitok_network* net);
  * forward_only: KV-cache semantics (masked_attention_head.rs:135-178) and
  *   out = Re(logits) (convert_c_to_f64_3d); otherwise stateless and out = the
  *   SoftmaxLayer output for its OperationMode.
- * last_row_only: out is [batch][vocab] from row lens[b]-1, else [batch][seq][vocab].
+ * last_row_only: out is [batch][vocab] from each sequence's last row, else
+ *   [batch][seq'][vocab] with seq' = mitok_seq_out_len (seq without wavelet layers).
  * out_padding_mask [batch][seq] or NULL. */
 int mitok_predict(mitok_network* net, const uint32_t* ids, const uint32_t* lens, uint32_t batch, uint32_t seq,
                   const uint32_t* time_steps, int forward_only, int last_row_only, double* out,

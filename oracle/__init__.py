@@ -66,6 +66,9 @@ def _load():
         "orc_add_feed_forward": (i32, [P, u32, u32, P, P, P, P]),
         "orc_add_linear": (i32, [P, u32, u32, P, P]),
         "orc_add_softmax": (i32, [P, i32]),
+        "orc_add_discrete_wavelet": (i32, [P, u32, u32, u32, i32]),
+        "orc_dwt_1d": (i32, [P, u32, u32, u32, P, P]),
+        "orc_seq_out_len": (u32, [P, u32]),
         "orc_init_seeded": (i32, [P, u64]),
         "orc_get_tensor": (i32, [P, u32, u32, P, u64]),
         "orc_reset": (i32, [P]),
@@ -143,6 +146,21 @@ def gelu(z: complex) -> tuple[complex, bool]:
     return complex(r.re, r.im), bool(flag.value)
 
 
+def dwt_rows(S: int, wavelet: int) -> int:
+    """Rows a wavelet layer leaves of S (the low half of dwt_1d, dwt.rs:36-60)."""
+    n = S + (2 if wavelet == 0 else 4) - 2 + (S % 2)
+    return n >> 1
+
+
+def dwt_1d(x, wavelet: int, mode: int) -> np.ndarray:
+    """dwt_1d (wavelet_transform/dwt.rs:36-90) of a real sequence: [low | high]."""
+    x = np.ascontiguousarray(x, dtype=np.float64)
+    out = np.empty(x.shape[0] + 8, np.float64)
+    n = C.c_uint32(0)
+    _check(lib().orc_dwt_1d(_ptr(x), x.shape[0], wavelet, mode, _ptr(out), C.byref(n)))
+    return out[:n.value].copy()
+
+
 def zgemm(A: np.ndarray, B: np.ndarray) -> np.ndarray:
     A, B = _c128(A), _c128(B)
     m, k = A.shape
@@ -217,6 +235,7 @@ class Network:
         if not self._h:
             raise OracleError("orc_net_create failed")
         self.vocab = None
+        self._wavelets = {}  # layer index -> wavelet type of each DiscreteWaveletLayer
 
     def close(self):
         if self._h:
@@ -259,6 +278,16 @@ class Network:
     def add_softmax(self, mode=PRODUCTION):
         _check(lib().orc_add_softmax(self._h, mode))
 
+    def add_discrete_wavelet(self, dim, wavelet=1, mode=2, is_full_mode=False):
+        """DiscreteWaveletLayer over rows of `dim` features; defaults DB2 /
+        SYMMETRIC (wavelet_discrete_layer.rs:46-70)."""
+        _check(lib().orc_add_discrete_wavelet(self._h, dim, wavelet, mode, int(is_full_mode)))
+        self._wavelets[self.num_layers - 1] = wavelet
+
+    def seq_out_len(self, S: int) -> int:
+        """Rows per sequence after the wavelet layers of a prompt pass."""
+        return int(lib().orc_seq_out_len(self._h, S))
+
     def init_seeded(self, seed):
         _check(lib().orc_init_seeded(self._h, seed))
 
@@ -276,8 +305,10 @@ class Network:
         lens = np.full(B, S, np.uint32) if lens is None else np.ascontiguousarray(lens, dtype=np.uint32)
         ts = None if time_steps is None else np.ascontiguousarray(time_steps, dtype=np.uint32)
         V = self.vocab
-        out = np.empty((B, V) if last_row_only else (B, S, V), np.float64)
-        mask = np.empty((B, S), np.uint32)
+        prompt_pass = not forward_only or ts is None or ts[0] == 0
+        So = self.seq_out_len(S) if prompt_pass else S
+        out = np.empty((B, V) if last_row_only else (B, So, V), np.float64)
+        mask = np.empty((B, So), np.uint32)
         _check(lib().orc_predict(self._h, _ptr(ids), _ptr(lens), B, S, _ptr(ts), int(forward_only),
                                  int(last_row_only), _ptr(out), _ptr(mask)))
         return out, mask
@@ -287,7 +318,13 @@ class Network:
         B, S, _ = x.shape
         m = None if mask is None else np.ascontiguousarray(mask, dtype=np.uint32)
         ts = None if time_steps is None else np.ascontiguousarray(time_steps, dtype=np.uint32)
-        out = np.empty((B, S, d_out if d_out else x.shape[2]), np.complex128)
+        prompt_pass = not forward_only or ts is None or ts[0] == 0
+        So = S
+        if prompt_pass:
+            for li in range(first, last):
+                if self._wavelets.get(li) is not None:  # a wavelet layer in the range
+                    So = dwt_rows(So, self._wavelets[li])
+        out = np.empty((B, So, d_out if d_out else x.shape[2]), np.complex128)
         _check(lib().orc_forward_layers(self._h, first, last, _ptr(x), _ptr(m), B, S, _ptr(ts), int(forward_only),
                                         _ptr(out)))
         return out

@@ -381,6 +381,8 @@ static oc64* fill_const(const oc64* src, size_t n, oc64 v) {
   return p;
 }
 
+static int dwt_low_pass(uint32_t wavelet, double* lo, uint32_t* L);
+
 int orc_add_embedding(orc_net* net, uint32_t vocab, uint32_t dim, const oc64* table) {
   if (!net || !vocab || !dim) return fail(ORC_ERR_ARG, "embedding: bad dims");
   orc_layer* L = push_layer(net, ORC_EMBEDDING);
@@ -452,6 +454,22 @@ int orc_add_linear(orc_net* net, uint32_t in, uint32_t out, const oc64* w, const
   L->w1 = dup_or_zero(w, (size_t)in * out);
   L->b1 = fill_const(b, out, (oc64){1.0, 0.0});
   if (!L->w1 || !L->b1) return fail(ORC_ERR_NOMEM, "linear: out of memory");
+  return ORC_OK;
+}
+
+int orc_add_discrete_wavelet(orc_net* net, uint32_t dim, uint32_t wavelet, uint32_t mode, int is_full_mode) {
+  if (!net) return fail(ORC_ERR_ARG, "null network");
+  if (is_full_mode) return fail(ORC_ERR_ARG, "DiscreteWaveletLayer in full mode is not supported");
+  double lo[4];
+  uint32_t L;
+  int rc = dwt_low_pass(wavelet, lo, &L);
+  if (rc) return rc;
+  if (!(mode <= 4 || mode == 6)) return fail(ORC_ERR_ARG, "wavelet mode %u is not supported", mode);
+  orc_layer* Lr = push_layer(net, ORC_DISCRETE_WAVELET);
+  if (!Lr) return fail(ORC_ERR_NOMEM, "out of memory");
+  Lr->vocab = wavelet; /* the wavelet type */
+  Lr->mode = (int)mode;
+  Lr->d_in = Lr->d_out = dim;
   return ORC_OK;
 }
 
@@ -557,6 +575,186 @@ int orc_reset(orc_net* net) {
   for (int i = 0; i < net->n; ++i)
     if (net->layers[i].kind == ORC_SELF_ATTENTION) free_cache(&net->layers[i]);
   return ORC_OK;
+}
+
+
+/* ------------------------------------------------------------------------ */
+/* DiscreteWaveletLayer (network_types/wavelet_discrete_layer.rs:46-161)     */
+/* ------------------------------------------------------------------------ */
+
+/* Low-pass filters of DiscreteWaletetType DB1 and DB2 (wavelet_transform/
+ * dwt_coeffients.rs DB_1, DB_2; dwt_type_resolver.rs:6-9): 1/sqrt(2) twice, and
+ * Daubechies' closed form (1+sqrt3, 3+sqrt3, 3-sqrt3, 1-sqrt3) / (4 sqrt2),
+ * evaluated in long double and rounded once to double. */
+static int dwt_low_pass(uint32_t wavelet, double* lo, uint32_t* L) {
+  if (wavelet == 0) {
+    lo[0] = lo[1] = (double)(1.0L / sqrtl(2.0L));
+    *L = 2;
+    return ORC_OK;
+  }
+  if (wavelet == 1) {
+    const long double s3 = sqrtl(3.0L), den = 4.0L * sqrtl(2.0L);
+    lo[0] = (double)((1.0L + s3) / den);
+    lo[1] = (double)((3.0L + s3) / den);
+    lo[2] = (double)((3.0L - s3) / den);
+    lo[3] = (double)((1.0L - s3) / den);
+    *L = 4;
+    return ORC_OK;
+  }
+  return fail(ORC_ERR_ARG, "wavelet type %u: only DB1 and DB2 are supported", wavelet);
+}
+
+/* get_high_pass_filter (dwt_type_resolver.rs:107-123): the low-pass filter
+ * reversed, odd entries negated */
+static void dwt_high_pass(const double* lo, uint32_t L, double* hi) {
+  for (uint32_t i = 0; i < L; ++i) hi[i] = (i % 2 == 1) ? -lo[L - 1 - i] : lo[L - 1 - i];
+}
+
+/* one element of the padded array: source index (-1: a zero) and sign */
+typedef struct {
+  int32_t idx;
+  double sign;
+} dwt_src;
+
+/* insert_padding_before / insert_padding_after (wavelet_transform/dwt.rs:149-293)
+ * applied to the indices of n elements; *before = L - 2 elements in front */
+static int dwt_padded(uint32_t n, uint32_t L, uint32_t mode, dwt_src** out, uint32_t* plen, uint32_t* before) {
+  if (!(mode <= 4 || mode == 6)) return fail(ORC_ERR_ARG, "wavelet mode %u is not supported", mode);
+  if (n == 0) return fail(ORC_ERR_ARG, "empty sequence");
+  const uint32_t nb = L - 2;
+  const uint32_t len0 = n + nb;
+  const uint32_t na = (len0 % L != 0) ? L - len0 % L + 2 : L - len0 % L + 1; /* dwt.rs:50-54 */
+  dwt_src* a = (dwt_src*)malloc((size_t)(n + nb + na) * sizeof(dwt_src));
+  dwt_src* orig = (dwt_src*)malloc((size_t)(n + nb) * sizeof(dwt_src));
+  if (!a || !orig) {
+    free(a), free(orig);
+    return fail(ORC_ERR_NOMEM, "dwt: out of memory");
+  }
+  uint32_t cur = n;
+  for (uint32_t i = 0; i < n; ++i) a[i] = (dwt_src){(int32_t)i, 1.0};
+  uint32_t rtmp = 0;
+  for (uint32_t i = 0; i < nb; ++i) {
+    dwt_src v = {-1, 1.0};
+    switch (mode) {
+      case 0: break;                                 /* ZERO */
+      case 1: v = a[i]; break;                       /* CONSTANT: data_trans[i] */
+      case 2: v = a[cur % n + i % n]; break;         /* SYMMETRIC */
+      case 3: v = a[cur % n + i % n]; v.sign = -v.sign; break; /* ANTISYMMETRIC */
+      case 4:                                        /* REFLECT */
+        if (i > 0) rtmp = (rtmp + 2) % cur;
+        if (rtmp == 0) rtmp = 1;
+        v = a[rtmp];
+        break;
+      default: v = (dwt_src){(int32_t)(n - 1 - (i % n)), 1.0}; break; /* PERIODIC: origin_data */
+    }
+    memmove(a + 1, a, (size_t)cur * sizeof(dwt_src));
+    a[0] = v;
+    ++cur;
+  }
+  const uint32_t olen = cur;
+  memcpy(orig, a, (size_t)olen * sizeof(dwt_src));
+  for (uint32_t i = 0; i < na; ++i) {
+    dwt_src v = {-1, 1.0};
+    switch (mode) {
+      case 0: break;
+      case 1: v = a[cur - 1]; break;
+      case 2: v = a[cur - (cur % olen + i % olen) - 1]; break;
+      case 3: v = a[cur - (cur % olen + i % olen) - 1]; v.sign = -v.sign; break;
+      case 4: v = orig[olen - ((i + 1) % olen) - 1]; break;
+      default: v = orig[i % (olen - nb) + nb]; break;
+    }
+    a[cur++] = v;
+  }
+  free(orig);
+  *out = a;
+  *plen = cur;
+  *before = nb;
+  return ORC_OK;
+}
+
+/* geometry of dwt_1d (dwt.rs:36-90) on n elements: the transform length N and
+ * its midpoint (the low half is [0, N/2)) */
+static uint32_t dwt_len(uint32_t n, uint32_t L) {
+  uint32_t N = n + (L - 2);
+  if (n % 2 != 0) N += 1;
+  return N;
+}
+
+int orc_dwt_1d(const double* x, uint32_t n, uint32_t wavelet, uint32_t mode, double* out, uint32_t* out_len) {
+  double lo[4] = {0.0, 0.0, 0.0, 0.0}, hi[4];
+  uint32_t L = 0, plen = 0, nb = 0;
+  int rc = dwt_low_pass(wavelet, lo, &L);
+  if (rc) return rc;
+  dwt_high_pass(lo, L, hi);
+  dwt_src* a;
+  if ((rc = dwt_padded(n, L, mode, &a, &plen, &nb))) return rc;
+  const uint32_t N = dwt_len(n, L), middle = N >> 1;
+  for (uint32_t i = 0; i < N; ++i) out[i] = 0.0;
+  uint32_t ind = 0;
+  for (uint32_t i = 0; i < N; i += 2) {
+    double vl = 0.0, vh = 0.0;
+    for (uint32_t l = 0; l < L; ++l) {
+      const dwt_src e = a[(i + l) % plen];
+      const double v = e.idx < 0 ? 0.0 : e.sign * x[e.idx];
+      vl = vl + v * lo[l];
+      vh = vh + v * hi[l];
+    }
+    out[ind] = vl;
+    out[ind + middle] = vh;
+    ++ind;
+  }
+  free(a);
+  *out_len = N;
+  return ORC_OK;
+}
+
+/* compress_partial + compress_padding_mask (wavelet_discrete_layer.rs:260-281,
+ * 297-313): every feature's sequence of the B x S rows becomes the low half
+ * of its dwt_1d; the mask becomes the low half of dwt_1d of its 0/1 values
+ * thresholded at 0.99.  Rows per sequence: *S2; lens2[b] = ones of its mask. */
+static int dwt_compress(uint32_t wavelet, uint32_t mode, const oc64* x, const uint32_t* mask, uint32_t B, uint32_t S,
+                        uint32_t d, oc64* out, uint32_t* mask2, uint32_t* lens2, uint32_t* S2) {
+  double lo[4] = {0.0, 0.0, 0.0, 0.0};
+  uint32_t L = 0, plen = 0, nb = 0;
+  int rc = dwt_low_pass(wavelet, lo, &L);
+  if (rc) return rc;
+  dwt_src* a;
+  if ((rc = dwt_padded(S, L, mode, &a, &plen, &nb))) return rc;
+  const uint32_t M = dwt_len(S, L) >> 1;
+  for (uint32_t b = 0; b < B; ++b) {
+    const oc64* xb = x + (size_t)b * S * d;
+    for (uint32_t j = 0; j < M; ++j)
+      for (uint32_t c = 0; c < d; ++c) {
+        oc64 v = {0.0, 0.0};
+        for (uint32_t l = 0; l < L; ++l) {
+          const dwt_src e = a[(2 * j + l) % plen];
+          const oc64 t = e.idx < 0 ? (oc64){0.0, 0.0} : c_scale(xb[(size_t)e.idx * d + c], e.sign);
+          v = c_add(v, c_scale(t, lo[l])); /* value_low + data * low_pass (dwt.rs:74-79) */
+        }
+        out[((size_t)b * M + j) * d + c] = v;
+      }
+    uint32_t ones = 0;
+    for (uint32_t j = 0; j < M; ++j) {
+      double v = 0.0;
+      for (uint32_t l = 0; l < L; ++l) {
+        const dwt_src e = a[(2 * j + l) % plen];
+        const double t = e.idx < 0 ? 0.0 : e.sign * (double)mask[(size_t)b * S + e.idx];
+        v = v + t * lo[l];
+      }
+      mask2[(size_t)b * M + j] = v > 0.99 ? 1u : 0u;
+      ones += mask2[(size_t)b * M + j];
+    }
+    lens2[b] = ones ? ones : 1;
+  }
+  free(a);
+  *S2 = M;
+  return ORC_OK;
+}
+
+uint32_t orc_seq_out_len(const orc_net* net, uint32_t S) {
+  for (int i = 0; net && i < net->n; ++i)
+    if (net->layers[i].kind == ORC_DISCRETE_WAVELET) S = dwt_len(S, net->layers[i].vocab == 0 ? 2 : 4) >> 1;
+  return S;
 }
 
 /* ------------------------------------------------------------------------ */
@@ -826,31 +1024,71 @@ static int check_lens(const uint32_t* lens, uint32_t B, uint32_t S) {
   return ORC_OK;
 }
 
-int orc_predict(orc_net* net, const uint32_t* ids, const uint32_t* lens, uint32_t B, uint32_t S,
+/* A wavelet layer at a prompt or stateless pass (wavelet_discrete_layer.rs:
+ * 102-128): *cur [B][*S][d] becomes [B][S'][d], mask and lens follow. */
+static int run_wavelet(const orc_layer* L, oc64** cur, oc64** nxt, uint64_t* cap, uint32_t** mask, uint32_t* lens,
+                       uint32_t B, uint32_t* S, uint32_t d) {
+  const uint32_t M = dwt_len(*S, L->vocab == 0 ? 2 : 4) >> 1;
+  const uint64_t need = (uint64_t)B * (M > *S ? M : *S) * d;
+  if (need > *cap) {
+    oc64* c2 = (oc64*)realloc(*cur, need * sizeof(oc64));
+    if (c2) *cur = c2;
+    free(*nxt);
+    *nxt = (oc64*)malloc(need * sizeof(oc64));
+    if (!c2 || !*nxt) return fail(ORC_ERR_NOMEM, "wavelet: out of memory");
+    *cap = need;
+  }
+  uint32_t* m2 = (uint32_t*)malloc((size_t)B * M * sizeof(uint32_t));
+  if (!m2) return fail(ORC_ERR_NOMEM, "wavelet: out of memory");
+  uint32_t S2 = 0;
+  int rc = dwt_compress(L->vocab, (uint32_t)L->mode, *cur, *mask, B, *S, d, *nxt, m2, lens, &S2);
+  if (rc) {
+    free(m2);
+    return rc;
+  }
+  free(*mask);
+  *mask = m2;
+  *S = S2;
+  oc64* t = *cur;
+  *cur = *nxt;
+  *nxt = t;
+  return ORC_OK;
+}
+
+int orc_predict(orc_net* net, const uint32_t* ids, const uint32_t* lens_in, uint32_t B, uint32_t S_in,
                 const uint32_t* time_steps, int forward_only, int out_rows, double* out, uint32_t* out_mask) {
-  if (!net || !ids || !lens || !out) return fail(ORC_ERR_ARG, "null argument");
-  int rc = check_lens(lens, B, S);
+  if (!net || !ids || !lens_in || !out) return fail(ORC_ERR_ARG, "null argument");
+  int rc = check_lens(lens_in, B, S_in);
   if (rc) return rc;
   if (net->n < 2 || net->layers[0].kind != ORC_EMBEDDING || net->layers[net->n - 1].kind != ORC_SOFTMAX)
     return fail(ORC_ERR_STATE, "network must start with Embedding and end with Softmax");
-  const uint64_t rows = (uint64_t)B * S;
+  uint32_t S = S_in; /* rows per sequence: a wavelet layer compresses them */
+  const uint64_t rows0 = (uint64_t)B * S;
   uint32_t dmax = 0;
   for (int i = 0; i < net->n; ++i) {
     if (net->layers[i].d_in > dmax) dmax = net->layers[i].d_in;
     if (net->layers[i].d_out > dmax) dmax = net->layers[i].d_out;
   }
-  uint64_t cap = rows * dmax;
+  uint64_t cap = rows0 * dmax;
   oc64* cur = (oc64*)malloc(cap * sizeof(oc64));
   oc64* nxt = (oc64*)malloc(cap * sizeof(oc64));
-  uint32_t* mask = (uint32_t*)malloc(rows * sizeof(uint32_t));
-  if (!cur || !nxt || !mask) {
-    free(cur), free(nxt), free(mask);
+  uint32_t* mask = (uint32_t*)malloc(rows0 * sizeof(uint32_t));
+  uint32_t* lens = (uint32_t*)malloc(B * sizeof(uint32_t));
+  if (!cur || !nxt || !mask || !lens) {
+    free(cur), free(nxt), free(mask), free(lens);
     return fail(ORC_ERR_NOMEM, "activation: out of memory");
   }
+  memcpy(lens, lens_in, B * sizeof(uint32_t));
   rc = embedding_forward(&net->layers[0], ids, lens, B, S, cur, mask);
+  uint32_t d = net->layers[0].d_out;
+  const int prompt_pass = !forward_only || !time_steps || time_steps[0] == 0;
   int gathered = 0; /* rows reduced to one per sequence before the vocab Linear */
   for (int li = 1; rc == ORC_OK && li < net->n - 1; ++li) {
     orc_layer* L = &net->layers[li];
+    if (L->kind == ORC_DISCRETE_WAVELET) {
+      if (prompt_pass) rc = run_wavelet(L, &cur, &nxt, &cap, &mask, lens, B, &S, d);
+      continue; /* a cached step's row passes through (:112-128) */
+    }
     if (out_rows == 1 && forward_only && L->kind == ORC_LINEAR && li == net->n - 2) {
       for (uint32_t b = 0; b < B; ++b)
         memmove(cur + (size_t)b * L->d_in, cur + ((size_t)b * S + lens[b] - 1) * L->d_in, L->d_in * sizeof(oc64));
@@ -878,6 +1116,7 @@ int orc_predict(orc_net* net, const uint32_t* ids, const uint32_t* lens, uint32_
       break;
     }
     rc = run_layer(L, &cur, &nxt, &cap, mask, lens, B, S, time_steps, forward_only);
+    if (L->d_out) d = L->d_out;
   }
   if (rc == ORC_OK) {
     const orc_layer* SM = &net->layers[net->n - 1];
@@ -905,16 +1144,18 @@ int orc_predict(orc_net* net, const uint32_t* ids, const uint32_t* lens, uint32_
         }
       }
     }
-    if (out_mask) memcpy(out_mask, mask, rows * sizeof(uint32_t));
+    if (out_mask) memcpy(out_mask, mask, (size_t)B * S * sizeof(uint32_t));
   }
   free(cur);
   free(nxt);
   free(mask);
+  free(lens);
   return rc;
 }
 
 int orc_forward_layers(orc_net* net, uint32_t first, uint32_t last, const oc64* in, const uint32_t* mask_in,
                        uint32_t B, uint32_t S, const uint32_t* time_steps, int forward_only, oc64* out) {
+  /* S: rows per sequence in; a wavelet layer in the range compresses them (out [B][S'][d]) */
   if (!net || !in || !out || first >= last || last > (uint32_t)net->n) return fail(ORC_ERR_ARG, "bad layer range");
   if (!B || !S) return fail(ORC_ERR_ARG, "empty batch");
   const uint64_t rows = (uint64_t)B * S;
@@ -941,9 +1182,18 @@ int orc_forward_layers(orc_net* net, uint32_t first, uint32_t last, const oc64* 
       if (!lens[b]) lens[b] = 1;
     }
   }
-  for (uint32_t li = first; rc == ORC_OK && li < last; ++li)
-    rc = run_layer(&net->layers[li], &cur, &nxt, &cap, mask, lens, B, S, time_steps, forward_only);
-  if (rc == ORC_OK) memcpy(out, cur, rows * net->layers[last - 1].d_out * sizeof(oc64));
+  const int prompt_pass = !forward_only || !time_steps || time_steps[0] == 0;
+  uint32_t d = net->layers[first].d_in;
+  for (uint32_t li = first; rc == ORC_OK && li < last; ++li) {
+    orc_layer* L = &net->layers[li];
+    if (L->kind == ORC_DISCRETE_WAVELET) {
+      if (prompt_pass) rc = run_wavelet(L, &cur, &nxt, &cap, &mask, lens, B, &S, d);
+      continue;
+    }
+    rc = run_layer(L, &cur, &nxt, &cap, mask, lens, B, S, time_steps, forward_only);
+    if (L->d_out) d = L->d_out;
+  }
+  if (rc == ORC_OK) memcpy(out, cur, (size_t)B * S * d * sizeof(oc64));
   free(cur);
   free(nxt);
   free(mask);

@@ -32,7 +32,8 @@ enum {
   ORC_SELF_ATTENTION = 3,
   ORC_FEED_FORWARD = 4,
   ORC_LINEAR = 5,
-  ORC_SOFTMAX = 6
+  ORC_SOFTMAX = 6,
+  ORC_DISCRETE_WAVELET = 7
 };
 
 /* OperationMode (network_types/neural_network_generic.rs:17-20) */
@@ -86,6 +87,19 @@ int orc_add_feed_forward(orc_net* net, uint32_t dim, uint32_t hidden, const oc64
                          const oc64* w2, const oc64* b2);
 int orc_add_linear(orc_net* net, uint32_t in, uint32_t out, const oc64* w, const oc64* b);
 int orc_add_softmax(orc_net* net, int operation_mode);
+/* DiscreteWaveletLayer (network_types/wavelet_discrete_layer.rs:46-161), partial
+ * mode: at the prompt pass (time_step 0) or a stateless pass it replaces the
+ * rows by the low-pass half of dwt_1d along the sequence of every feature and
+ * the padding mask by its thresholded low-pass half; at cached steps it
+ * passes the row through.  dim: features per row.  wavelet: DiscreteWaletetType index (0 DB1, 1 DB2);
+ * mode: WaveletMode index (0 ZERO, 1 CONSTANT, 2 SYMMETRIC, 3 ANTISYMMETRIC,
+ * 4 REFLECT, 6 PERIODIC); is_full_mode must be 0. */
+int orc_add_discrete_wavelet(orc_net* net, uint32_t dim, uint32_t wavelet, uint32_t mode, int is_full_mode);
+/* dwt_1d (wavelet_transform/dwt.rs:36-90) of n reals: out (at least n + 4
+ * doubles) = [low half | high half], *out_len its length. */
+int orc_dwt_1d(const double* x, uint32_t n, uint32_t wavelet, uint32_t mode, double* out, uint32_t* out_len);
+/* rows per sequence after every wavelet layer of a prompt pass of S rows */
+uint32_t orc_seq_out_len(const orc_net* net, uint32_t S);
 int orc_init_seeded(orc_net* net, uint64_t seed);
 /* reads back a weight tensor (slot: 0 table/w/w1/wq, 1 wk/w2, 2 wv, 3 bias_pos, 4 b/b1, 5 b2, 6 gamma, 7 beta) */
 int orc_get_tensor(const orc_net* net, uint32_t layer, uint32_t slot, oc64* out, uint64_t n);

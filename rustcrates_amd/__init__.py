@@ -47,6 +47,8 @@ SIGNATURES = {
     "mitok_add_feed_forward": (_i32, [_P, _u32, _u32, _P, _P, _P, _P]),
     "mitok_add_linear": (_i32, [_P, _u32, _u32, _P, _P]),
     "mitok_add_softmax": (_i32, [_P, _i32]),
+    "mitok_add_discrete_wavelet": (_i32, [_P, _u32, _u32, _u32, _i32]),
+    "mitok_seq_out_len": (_i32, [_P, _u32, _u32, _u32, _P]),
     "mitok_init_seeded": (_i32, [_P, _u64]),
     "mitok_get_tensor": (_i32, [_P, _u32, _u32, _P, _u64]),
     "mitok_reset": (_i32, [_P]),
@@ -214,6 +216,18 @@ class Network:
     def add_softmax(self, mode=PRODUCTION):
         _check(self._lib.mitok_add_softmax(self._h, mode))
 
+    def add_discrete_wavelet(self, dim, wavelet=1, mode=2, is_full_mode=False):
+        """DiscreteWaveletLayer over rows of `dim` features; defaults DB2 /
+        SYMMETRIC (wavelet_discrete_layer.rs:46-70)."""
+        _check(self._lib.mitok_add_discrete_wavelet(self._h, dim, wavelet, mode, int(is_full_mode)))
+
+    def seq_out_len(self, S, first=0, last=None):
+        """Rows per sequence that layers [first, last) leave of a prompt pass of S rows."""
+        out = C.c_uint32(0)
+        _check(self._lib.mitok_seq_out_len(self._h, first, self.num_layers if last is None else last, S,
+                                           C.byref(out)))
+        return out.value
+
     def init_seeded(self, seed):
         _check(self._lib.mitok_init_seeded(self._h, seed))
 
@@ -235,8 +249,10 @@ class Network:
         lens = np.full(B, S, np.uint32) if lens is None else _u32_vec(lens, B, "lens")
         ts = None if time_steps is None else _u32_vec(time_steps, B, "time_steps")
         V = self.vocab
-        out = np.empty((B, V) if last_row_only else (B, S, V), np.float64)
-        mask = np.empty((B, S), np.uint32)
+        prompt_pass = not forward_only or ts is None or ts[0] == 0
+        So = self.seq_out_len(S) if prompt_pass else S
+        out = np.empty((B, V) if last_row_only else (B, So, V), np.float64)
+        mask = np.empty((B, So), np.uint32)
         _check(self._lib.mitok_predict(self._h, _ptr(ids), _ptr(lens), B, S, _ptr(ts), int(forward_only),
                                        int(last_row_only), _ptr(out), _ptr(mask)))
         return out, mask
@@ -252,7 +268,9 @@ class Network:
             if m.shape != (B, S):
                 raise ValueError(f"padding mask: shape {m.shape}, expected ({B}, {S})")
         ts = None if time_steps is None else _u32_vec(time_steps, B, "time_steps")
-        out = np.empty((B, S, d_out if d_out else x.shape[2]), np.complex128)
+        prompt_pass = not forward_only or ts is None or ts[0] == 0
+        So = self.seq_out_len(S, first, last) if prompt_pass else S
+        out = np.empty((B, So, d_out if d_out else x.shape[2]), np.complex128)
         _check(self._lib.mitok_forward_layers(self._h, first, last, _ptr(x), _ptr(m), B, S, _ptr(ts),
                                               int(forward_only), _ptr(out)))
         return out

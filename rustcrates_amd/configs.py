@@ -87,6 +87,35 @@ def build_network(net, cfg: ModelConfig, seed: int | None = None):
     return net
 
 
+# create_transformer's default stack (network_types/transformer/transformer_builder.rs:10-72)
+REFERENCE_VOCAB = 50280
+REFERENCE_DIM = 16  # 512 / 2^DECOMPOSITION_LEVELS (wavelet_network.rs:13)
+WAVELET_DB2, WAVELET_MODE_SYMMETRIC = 1, 2  # DiscreteWaveletLayer::new (wavelet_discrete_layer.rs:46-70)
+
+
+def build_reference_default(net, vocab: int = REFERENCE_VOCAB, seed: int = 0, max_ctx: int = 512,
+                            mode: int = PRODUCTION):
+    """The layer stack create_transformer builds, in its order, with seeded
+    Xavier weights (the reference draws them unseeded):
+
+        Embedding(V, 16) -> DiscreteWavelet(DB2, SYMMETRIC) -> Norm(16, 1e-8)
+        -> PositionalEncoding(16) -> SelfAttention(2 heads) -> FeedForward(16, 512)
+        -> SelfAttention(4 heads) -> FeedForward(16, 1024) -> Linear(16, V) -> Softmax
+    """
+    d = REFERENCE_DIM
+    net.add_embedding(vocab, d)
+    net.add_discrete_wavelet(d, WAVELET_DB2, WAVELET_MODE_SYMMETRIC)
+    net.add_norm(d, 1e-8)
+    net.add_positional_encoding(d, 1250.0)
+    for i in range(2):
+        net.add_self_attention(2 if i == 0 else 4, d, max_ctx, 1e-12)
+        net.add_feed_forward(d, 512 if i == 0 else 1024)
+    net.add_linear(d, vocab)
+    net.add_softmax(mode)
+    net.init_seeded(seed)
+    return net
+
+
 def prompt_lengths(w: Workload):
     """Per-sequence prompt lengths: fixed, or uniform in [lo, hi] from the counter generator."""
     if not w.ragged:

@@ -40,14 +40,16 @@ void embed(hipStream_t st, const double2* table, int V, int d, const uint32_t* i
 }
 
 // apply_rotary_positional_encoding (positional_encoding_layer.rs:181-209) with
-// (cos, sin) of the clamped angle tabulated on the host with libm.
+// (cos, sin) of the clamped angle tabulated on the host with libm.  Without
+// explicit positions, row r (one per sequence) sits at kv_len[r] + off[r].
 __global__ void k_rope(double2* __restrict__ x, int rows, int d, const double2* __restrict__ cs, int max_pos,
-                       const int* __restrict__ pos, const int* __restrict__ kv_len, uint32_t* err) {
+                       const int* __restrict__ pos, const int* __restrict__ kv_len, const int* __restrict__ off,
+                       uint32_t* err) {
   const int half = d / 2;
   long i = (long)blockIdx.x * 256 + threadIdx.x;
   if (i >= (long)rows * half) return;
   int r = (int)(i / half), k = (int)(i - (long)r * half);
-  int p = pos ? pos[r] : kv_len[r];
+  int p = pos ? pos[r] : kv_len[r] + (off ? off[r] : 0);
   if (p >= max_pos) {
     atomicOr(err, (uint32_t)EB_CTX_OVERFLOW);
     return;
@@ -60,9 +62,45 @@ __global__ void k_rope(double2* __restrict__ x, int rows, int d, const double2* 
 }
 
 void rope(hipStream_t st, double2* x, int rows, int d, const double2* cs_table, int max_pos, const int* pos,
-          const int* kv_len, uint32_t* err) {
+          const int* kv_len, const int* off, uint32_t* err) {
   long n = (long)rows * (d / 2);
-  hipLaunchKernelGGL(k_rope, dim3(cdiv_i(n, 256)), dim3(256), 0, st, x, rows, d, cs_table, max_pos, pos, kv_len, err);
+  hipLaunchKernelGGL(k_rope, dim3(cdiv_i(n, 256)), dim3(256), 0, st, x, rows, d, cs_table, max_pos, pos, kv_len, off,
+                     err);
+}
+
+// DiscreteWaveletLayer at a prompt pass (wavelet_discrete_layer.rs:102-128,
+// compress_partial :260-266): feature c of output row j of sequence b is the
+// low half of dwt_1d (wavelet_transform/dwt.rs:36-90) along the sequence,
+//   v = 0 + t_0 lo[0] + ... + t_(L-1) lo[L-1],   t_l = sgn_l x[b][src_l][c],
+// summed in that order (src -1: a padding zero).  The tap table [S2][L]
+// restates the reference's sequence padding on the host.
+__global__ void k_dwt_rows(const double2* __restrict__ x, int B, int S, int d, const int* __restrict__ src,
+                           const double* __restrict__ sgn, const double* __restrict__ lo, int L, int S2,
+                           double2* __restrict__ out) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (long)B * S2 * d) return;
+  const int c = (int)(i % d);
+  const long bj = i / d;
+  const int j = (int)(bj % S2), b = (int)(bj / S2);
+  double2 v = make_double2(0.0, 0.0);
+  for (int l = 0; l < L; ++l) {
+    const int s = src[j * L + l];
+    const double g = sgn[j * L + l];
+    double2 t = make_double2(0.0, 0.0);
+    if (s >= 0) {
+      const double2 xv = x[((long)b * S + s) * d + c];
+      t = make_double2(xv.x * g, xv.y * g);
+    }
+    v.x = v.x + t.x * lo[l];
+    v.y = v.y + t.y * lo[l];
+  }
+  out[i] = v;
+}
+
+void dwt_rows(hipStream_t st, const double2* x, int B, int S, int d, const int* src, const double* sgn,
+              const double* lo, int L, int S2, double2* out) {
+  const long n = (long)B * S2 * d;
+  if (n) hipLaunchKernelGGL(k_dwt_rows, dim3(cdiv_i(n, 256)), dim3(256), 0, st, x, B, S, d, src, sgn, lo, L, S2, out);
 }
 
 // NormalNormLayer::forward/normalize (norm_layer.rs:64-130): one wave per row,

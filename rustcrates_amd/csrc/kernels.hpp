@@ -47,8 +47,9 @@ struct RowOps {
   int finite_check = 0;              // flag non-finite values (FFN output, transformer_network.rs:408)
   int gelu = 0;                      // gelu_complex, rows with mask 0 -> 0 (activation.rs:195-212,268-284)
   const uint32_t* row_mask = nullptr;
-  const double2* rope_cs = nullptr;  // [rope_max][K/2] (cos, sin); position of row m = rope_pos[m]
+  const double2* rope_cs = nullptr;  // [rope_max][K/2] (cos, sin); position of row m = rope_pos[m] (+ rope_off[m])
   const int* rope_pos = nullptr;
+  const int* rope_off = nullptr;  // per-row position offsets, or null
   int rope_max = 0;
   const double2* resid = nullptr;  // x = Re(x + resid) + 0i  (add_matrix_3d_c, utils/matrix.rs:600-613)
   long ldr = 0;
@@ -235,7 +236,11 @@ void embed(hipStream_t st, const double2* table, int V, int d, const uint32_t* i
            uint32_t* err);
 // positions per row (pos != null) or per sequence from kv_len (S == 1 decode)
 void rope(hipStream_t st, double2* x, int rows, int d, const double2* cs_table, int max_pos, const int* pos,
-          const int* kv_len, uint32_t* err);
+          const int* kv_len, const int* off, uint32_t* err);
+// DiscreteWaveletLayer compression of a prompt pass: [B][S][d] -> [B][S2][d]
+// through a tap table [S2][L] (source row or -1, sign) and low-pass filter lo[L]
+void dwt_rows(hipStream_t st, const double2* x, int B, int S, int d, const int* src, const double* sgn,
+              const double* lo, int L, int S2, double2* out);
 void layernorm(hipStream_t st, const double2* x, const double2* before, double2* out, int rows, int d, double eps,
                const double2* gamma, const double2* beta);
 void gather_rows(hipStream_t st, const double2* src, int S, int d, const uint32_t* lens, int B, double2* dst);

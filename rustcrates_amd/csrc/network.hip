@@ -87,7 +87,16 @@ struct DevBuf {
 // ---------------------------------------------------------------------------
 // layers (LayerEnum variants on the token-loop path)
 // ---------------------------------------------------------------------------
-enum Kind { K_EMBEDDING = 0, K_POSENC = 1, K_NORM = 2, K_SELF_ATTENTION = 3, K_FEED_FORWARD = 4, K_LINEAR = 5, K_SOFTMAX = 6 };
+enum Kind {
+  K_EMBEDDING = 0,
+  K_POSENC = 1,
+  K_NORM = 2,
+  K_SELF_ATTENTION = 3,
+  K_FEED_FORWARD = 4,
+  K_LINEAR = 5,
+  K_SOFTMAX = 6,
+  K_WAVELET = 7
+};
 
 struct Layer {
   int kind;
@@ -140,6 +149,108 @@ struct SoftmaxLayer : Layer {  // softmax_output_layer.rs:15-27
   int mode = 1;
   SoftmaxLayer() : Layer(K_SOFTMAX) {}
 };
+
+struct WaveletLayer : Layer {  // DiscreteWaveletLayer, network_types/wavelet_discrete_layer.rs:20-70
+  uint32_t wavelet = 1, mode = 2;  // DiscreteWaletetType DB2, WaveletMode SYMMETRIC by default
+  int L = 4;                       // filter length
+  double lo[4] = {0, 0, 0, 0};     // low-pass filter
+  WaveletLayer() : Layer(K_WAVELET) {}
+};
+
+// ---------------------------------------------------------------------------
+// DiscreteWaveletLayer geometry (host): the reference's dwt_1d padding
+// (wavelet_transform/dwt.rs:36-90, 149-293) restated on indices, so the
+// device applies it as a tap table
+// ---------------------------------------------------------------------------
+// Low-pass filters of DB1 and DB2 (dwt_coeffients.rs DB_1, DB_2): 1/sqrt(2)
+// twice, and Daubechies' closed form (1+sqrt3, 3+sqrt3, 3-sqrt3, 1-sqrt3) /
+// (4 sqrt2), each evaluated in long double and rounded once to double (the
+// same doubles as the reference's table).
+static bool wavelet_low_pass(uint32_t wavelet, double* lo, int* L) {
+  if (wavelet == 0) {
+    lo[0] = lo[1] = (double)(1.0L / sqrtl(2.0L));
+    *L = 2;
+    return true;
+  }
+  if (wavelet == 1) {
+    const long double s3 = sqrtl(3.0L), den = 4.0L * sqrtl(2.0L);
+    lo[0] = (double)((1.0L + s3) / den);
+    lo[1] = (double)((3.0L + s3) / den);
+    lo[2] = (double)((3.0L - s3) / den);
+    lo[3] = (double)((1.0L - s3) / den);
+    *L = 4;
+    return true;
+  }
+  return false;
+}
+
+static bool wavelet_mode_ok(uint32_t mode) { return mode <= 4 || mode == 6; }  // index-expressible paddings
+
+// rows a wavelet layer leaves of S: the low half of dwt_1d's n + L - 2 (+1 if odd) values
+static int wavelet_rows(int S, int L) { return (S + L - 2 + (S % 2)) >> 1; }
+
+// Tap table of one prompt-pass compression of S rows: output row j reads rows
+// src[j][l] (-1: a padding zero) with signs sgn[j][l], l < L.
+struct WaveletTaps {
+  int S2 = 0;
+  std::vector<int> src;
+  std::vector<double> sgn;
+};
+
+static WaveletTaps wavelet_taps(int S, int L, uint32_t mode) {
+  struct E {
+    int idx;
+    double sign;
+  };
+  const int nb = L - 2, len0 = S + nb;
+  const int na = (len0 % L != 0) ? L - len0 % L + 2 : L - len0 % L + 1;
+  std::vector<E> a;
+  a.reserve(S + nb + na);
+  for (int i = 0; i < S; ++i) a.push_back({i, 1.0});
+  int rtmp = 0;
+  for (int i = 0; i < nb; ++i) {  // insert_padding_before
+    const int cur = (int)a.size();
+    E v = {-1, 1.0};
+    switch (mode) {
+      case 0: break;
+      case 1: v = a[i]; break;
+      case 2: v = a[cur % S + i % S]; break;
+      case 3: v = a[cur % S + i % S]; v.sign = -v.sign; break;
+      case 4:
+        if (i > 0) rtmp = (rtmp + 2) % cur;
+        if (rtmp == 0) rtmp = 1;
+        v = a[rtmp];
+        break;
+      default: v = {S - 1 - (i % S), 1.0}; break;
+    }
+    a.insert(a.begin(), v);
+  }
+  const std::vector<E> orig = a;
+  const int olen = (int)orig.size();
+  for (int i = 0; i < na; ++i) {  // insert_padding_after
+    const int cur = (int)a.size();
+    E v = {-1, 1.0};
+    switch (mode) {
+      case 0: break;
+      case 1: v = a[cur - 1]; break;
+      case 2: v = a[cur - (cur % olen + i % olen) - 1]; break;
+      case 3: v = a[cur - (cur % olen + i % olen) - 1]; v.sign = -v.sign; break;
+      case 4: v = orig[olen - ((i + 1) % olen) - 1]; break;
+      default: v = orig[i % (olen - nb) + nb]; break;
+    }
+    a.push_back(v);
+  }
+  WaveletTaps t;
+  t.S2 = wavelet_rows(S, L);
+  const int plen = (int)a.size();
+  for (int j = 0; j < t.S2; ++j)
+    for (int l = 0; l < L; ++l) {
+      const E e = a[(2 * j + l) % plen];
+      t.src.push_back(e.idx);
+      t.sgn.push_back(e.sign);
+    }
+  return t;
+}
 
 enum RunMode { MODE_PREFILL = 0, MODE_CACHED = 1, MODE_STATELESS = 2 };
 
@@ -218,11 +329,29 @@ struct mitok_network {
   // sum over sequences of the keys the next decode step attends over (the host
   // loop sets it before each timed step): the attention class's algorithmic bytes
   double dec_tsum = 0.0;
+  // wavelet compression of the current prompt or stateless call: one stage per
+  // DiscreteWaveletLayer in the call's range (tap table, filter, and the
+  // compressed mask, lens and row positions on the device); the last stage's
+  // mask and lens on the host; rows per sequence after the stages
+  struct WaveletStage {
+    int S_in = 0, S2 = 0, L = 0;
+    mitok::DevBuf src, sgn, lo, mask, lens, pos;
+  };
+  std::vector<std::unique_ptr<WaveletStage>> wstages;
+  std::vector<uint32_t> wmask_h, wlens_h;
+  int wS = 0;
+  // decode-time RoPE offset per sequence after a compressed prompt: prompt
+  // length minus its cached rows (positions count the uncompressed prompt)
+  mitok::DevBuf pos_off_d;
+  bool pos_off = false;
 };
 
 namespace mitok {
 
 using Net = mitok_network;
+
+// the RoPE offsets of decode steps after a compressed prompt, or null
+static const int* rope_offsets(const Net* n) { return n->pos_off ? n->pos_off_d.as<int>() : nullptr; }
 
 static int set_device(Net* n) {
   HIP_TRY(hipSetDevice(n->device));
@@ -424,6 +553,7 @@ static int prepare(Net* n, const Spec& sp) {
     TRY(reserve(n, n->dp1, 8 * B * dm.dmax * c16));
   }
   TRY(reserve(n, n->kv_len_d, (size_t)sp.B * sizeof(int)));
+  if (n->pos_off) TRY(reserve(n, n->pos_off_d, (size_t)sp.B * sizeof(int)));
   TRY(reserve(n, n->ones_d, std::max<size_t>(rows, sp.B) * sizeof(uint32_t)));
   TRY(reserve(n, n->dec_ids_d, (size_t)sp.B * sizeof(uint32_t)));
   return OK;
@@ -483,7 +613,12 @@ static int enqueue_forward(Net* n, const Spec& sp) {
   hipStream_t st = n->stream;
   uint32_t* err = n->err_d.as<uint32_t>();
   const Sync sy = sync_of(n);
-  const int B = sp.B, S = sp.S, rows = B * S;
+  const int B = sp.B;
+  int S = sp.S, rows = B * S;  // a wavelet layer of a prompt pass compresses the rows
+  const uint32_t* mask = mask;
+  const uint32_t* lens = lens;
+  const int* pos = pos;
+  size_t wi = 0;  // next wavelet stage
   double2* cur = n->act0.as<double2>();
   double2* nxt = n->act1.as<double2>();
   if (sp.in) HIP_TRY(hipMemcpyAsync(cur, sp.in, (size_t)rows * n->layers[sp.first]->d_in * sizeof(double2),
@@ -498,8 +633,8 @@ static int enqueue_forward(Net* n, const Spec& sp) {
       }
       case K_POSENC: {
         auto* P = (PositionalEncodingLayer*)L;
-        rope(st, cur, rows, P->d_in, P->cs.as<double2>(), P->positions, sp.pos, sp.pos ? nullptr : n->kv_len_d.as<int>(),
-             err);
+        rope(st, cur, rows, P->d_in, P->cs.as<double2>(), P->positions, pos, pos ? nullptr : n->kv_len_d.as<int>(),
+             pos ? nullptr : rope_offsets(n), err);
         break;
       }
       case K_NORM: {
@@ -554,7 +689,7 @@ static int enqueue_forward(Net* n, const Spec& sp) {
         a.ctx = e.ctx;
         a.bias_re = A->bias_re.as<double>();
         a.mc = A->max_ctx;
-        a.row_mask = sp.mask;
+        a.row_mask = mask;
         a.out = n->concat.as<double2>();
         a.ldo = d;
         a.B = B;
@@ -597,7 +732,7 @@ static int enqueue_forward(Net* n, const Spec& sp) {
         e1.bias = F->b1.as<double2>();
         e1.out = n->hbuf.as<double2>();
         e1.ldo = F->hidden;
-        e1.row_mask = sp.mask;
+        e1.row_mask = mask;
         e1.err = err;
         Epi e2;
         e2.mode = EPI_STORE;
@@ -639,7 +774,7 @@ static int enqueue_forward(Net* n, const Spec& sp) {
         const double2* x = cur;
         int M = rows;
         if (sp.last_row) {
-          gather_rows(st, cur, S, Ln->d_in, sp.lens, B, n->gath.as<double2>());
+          gather_rows(st, cur, S, Ln->d_in, lens, B, n->gath.as<double2>());
           x = n->gath.as<double2>();
           M = B;
         }
@@ -661,12 +796,24 @@ static int enqueue_forward(Net* n, const Spec& sp) {
           TRY(launch_rc(gemm(st, M, Ln->d_out, Ln->d_in, rows_of(x, Ln->d_in), Ln->w.as<double2>(), Ln->d_out, e,
                              nullptr, sy), "vocab"));
           auto* SM = (SoftmaxLayer*)n->layers.back().get();
-          softmax_rows(st, n->logits_c.as<double2>(), M, S, Ln->d_out, sp.mask, SM->mode == MITOK_TRAINING ? 0 : 1,
+          softmax_rows(st, n->logits_c.as<double2>(), M, S, Ln->d_out, mask, SM->mode == MITOK_TRAINING ? 0 : 1,
                        sp.out_prob);
         }
         break;
       }
       case K_SOFTMAX: break;  // applied together with the vocab Linear
+      case K_WAVELET: {
+        if (wi >= n->wstages.size()) break;  // a cached step's row passes through (wavelet_discrete_layer.rs:102-128)
+        const auto& W = *n->wstages[wi++];
+        dwt_rows(st, cur, B, S, (int)L->d_in, W.src.as<int>(), W.sgn.as<double>(), W.lo.as<double>(), W.L, W.S2, nxt);
+        std::swap(cur, nxt);
+        S = W.S2;
+        rows = B * S;
+        mask = W.mask.as<uint32_t>();
+        lens = W.lens.as<uint32_t>();
+        pos = W.pos.as<int>();
+        break;
+      }
     }
   }
   if (sp.out_hidden && cur != sp.out_hidden) {
@@ -781,6 +928,7 @@ static int enqueue_decode_fused(Net* n, const Spec& sp) {
         if (pro.rope_cs || pro.resid || pro.ln) materialize();
         pro.rope_cs = P->cs.as<double2>();
         pro.rope_pos = sp.pos ? sp.pos : kv_len;
+        pro.rope_off = sp.pos ? nullptr : rope_offsets(n);
         pro.rope_max = P->positions;
         break;
       }
@@ -934,6 +1082,7 @@ static int enqueue_decode_fused(Net* n, const Spec& sp) {
         break;
       }
       case K_SOFTMAX: break;
+      case K_WAVELET: break;  // a decode step's row passes through (wavelet_discrete_layer.rs:102-128)
     }
   }
   HIP_TRY(hipGetLastError());
@@ -1063,6 +1212,7 @@ static int resident_build(Net* n, const Spec& sp, int grid, int* dh_out, size_t*
         if (pro.rope_cs || pro.resid || pro.ln || pro.att.po) materialize();
         pro.rope_cs = P->cs.as<double2>();
         pro.rope_pos = sp.pos ? sp.pos : kv_len;
+        pro.rope_off = sp.pos ? nullptr : rope_offsets(n);
         pro.rope_max = P->positions;
         break;
       }
@@ -1200,6 +1350,7 @@ static int resident_build(Net* n, const Spec& sp, int grid, int* dh_out, size_t*
         break;
       }
       case K_SOFTMAX: break;
+      case K_WAVELET: break;  // a decode step's row passes through (wavelet_discrete_layer.rs:102-128)
     }
   }
   size_t shm = 0;
@@ -1532,6 +1683,33 @@ int mitok_add_linear(mitok_network* n, uint32_t in, uint32_t out, const double* 
   return upload_c(n, L->b, b, out, make_double2(1.0, 0.0), true);
 }
 
+int mitok_add_discrete_wavelet(mitok_network* n, uint32_t dim, uint32_t wavelet, uint32_t mode, int is_full_mode) {
+  if (!n || !dim) return fail(ERR_ARG, "bad arguments");
+  if (is_full_mode) return fail(ERR_ARG, "DiscreteWaveletLayer in full mode (2-D) is not on the device path");
+  auto L = std::make_unique<WaveletLayer>();
+  if (!wavelet_low_pass(wavelet, L->lo, &L->L))
+    return fail(ERR_ARG, "wavelet type %u: only DB1 and DB2 are on the device path", wavelet);
+  if (!wavelet_mode_ok(mode)) return fail(ERR_ARG, "wavelet mode %u is not on the device path", mode);
+  L->wavelet = wavelet;
+  L->mode = mode;
+  L->d_in = L->d_out = dim;
+  n->pos_off = true;  // decode steps after a compressed prompt shift their RoPE positions
+  TRY(set_device(n));
+  TRY(reserve(n, n->pos_off_d, 64 * sizeof(int)));
+  fill_int(n->stream, n->pos_off_d.as<int>(), 64, 0);
+  HIP_TRY(hipStreamSynchronize(n->stream));
+  return add_layer(n, L.release());
+}
+
+int mitok_seq_out_len(const mitok_network* n, uint32_t first, uint32_t last, uint32_t seq, uint32_t* out) {
+  if (!n || !out || first > last || last > n->layers.size()) return fail(ERR_ARG, "bad layer range");
+  int S = (int)seq;
+  for (uint32_t li = first; li < last; ++li)
+    if (n->layers[li]->kind == K_WAVELET) S = wavelet_rows(S, ((const WaveletLayer*)n->layers[li].get())->L);
+  *out = (uint32_t)S;
+  return OK;
+}
+
 int mitok_add_softmax(mitok_network* n, int operation_mode) {
   if (!n) return fail(ERR_ARG, "null network");
   if (operation_mode != MITOK_TRAINING && operation_mode != MITOK_PRODUCTION) return fail(ERR_ARG, "bad operation mode");
@@ -1670,13 +1848,15 @@ static int validate_batch(const uint32_t* lens, uint32_t B, uint32_t S) {
 }
 
 // Host-side part of a predict/forward call: mode, bounds, uploads.
+// Host-side part of a predict/forward call: mode, bounds, uploads, and the
+// wavelet stages of a prompt or stateless pass.  mask_src: the caller's
+// padding mask [B][S] (forward_layers), or null for lens' prefixes.
 static int begin_call(Net* n, const uint32_t* lens, uint32_t B, uint32_t S, const uint32_t* ts, bool forward_only,
-                      bool hidden_path, Spec& sp, std::vector<uint32_t>& mask_h) {
+                      const uint32_t* mask_src, Spec& sp, std::vector<uint32_t>& mask_h) {
   sp.B = B;
   sp.S = S;
   sp.forward_only = forward_only;
   const uint32_t mc = min_ctx(n);
-  if (mc != UINT32_MAX && S > mc) return fail(ERR_ARG, "sequence %u exceeds max context %u", S, mc);
   if (forward_only && n->cache_valid) {
     if (B != n->cache_B) return fail(ERR_STATE, "cached batch %u != %u; reset first", n->cache_B, B);
     for (uint32_t b = 0; b < B; ++b)
@@ -1687,18 +1867,33 @@ static int begin_call(Net* n, const uint32_t* lens, uint32_t B, uint32_t S, cons
   } else {
     sp.mode = MODE_STATELESS;
   }
-  TRY(prepare(n, sp));
+  // wavelet layers compress the rows of a stateless pass or one at time step 0
+  // (wavelet_discrete_layer.rs:102-128: !forward_only || time_step == 0); a
+  // later cached step passes its row through
+  std::vector<const WaveletLayer*> wl;
+  if (!forward_only || !ts || ts[0] == 0)
+    for (uint32_t li = sp.first; li < sp.last; ++li)
+      if (n->layers[li]->kind == K_WAVELET) wl.push_back((const WaveletLayer*)n->layers[li].get());
+  int S_alloc = (int)S, Sc = (int)S;
+  for (const WaveletLayer* W : wl) {
+    Sc = wavelet_rows(Sc, W->L);
+    S_alloc = std::max(S_alloc, Sc);
+  }
+  if (mc != UINT32_MAX && (uint32_t)Sc > mc) return fail(ERR_ARG, "sequence %d exceeds max context %u", Sc, mc);
+  Spec sz = sp;
+  sz.S = S_alloc;
+  TRY(prepare(n, sz));
   if (sp.mode == MODE_PREFILL) TRY(alloc_caches(n, B));
   const size_t rows = (size_t)B * S;
   mask_h.assign(rows, 0);
   std::vector<int> pos(rows);
   for (uint32_t b = 0; b < B; ++b)
     for (uint32_t s = 0; s < S; ++s) {
-      mask_h[(size_t)b * S + s] = s < lens[b] ? 1 : 0;
+      mask_h[(size_t)b * S + s] = mask_src ? (mask_src[(size_t)b * S + s] ? 1u : 0u) : (s < lens[b] ? 1u : 0u);
       uint32_t t = ts ? ts[b] : 0;
       pos[(size_t)b * S + s] = (forward_only && t > 0) ? (int)t : (int)s;  // positional_encoding_layer.rs:61-65
     }
-  int maxpos = 0;
+  int maxpos = std::max(0, S_alloc - 1);
   for (int p : pos) maxpos = std::max(maxpos, p);
   TRY(ensure_rope_for(n, sp.first, sp.last, std::max(rope_positions_needed(n), maxpos + 1)));
   TRY(upload(n, n->mask_d, mask_h.data(), rows * sizeof(uint32_t)));
@@ -1707,28 +1902,96 @@ static int begin_call(Net* n, const uint32_t* lens, uint32_t B, uint32_t S, cons
   sp.mask = n->mask_d.as<uint32_t>();
   sp.lens = n->lens_d.as<uint32_t>();
   sp.pos = n->pos_d.as<int>();
+
+  // each stage: tap table, filter, compressed mask (the low half of dwt_1d of
+  // the 0/1 mask above 0.99, compress_padding_mask :297-313), the rows left
+  // to each sequence (the mask's ones) and row positions 0 .. S2-1
+  n->wstages.clear();
+  std::vector<std::vector<int>> keep_i;  // host staging kept alive until the synchronisation below
+  std::vector<std::vector<double>> keep_d;
+  std::vector<std::vector<uint32_t>> keep_u;
+  std::vector<uint32_t> m = mask_h, ln(lens, lens + B);
+  int Sin = (int)S;
+  for (const WaveletLayer* W : wl) {
+    const WaveletTaps t = wavelet_taps(Sin, W->L, W->mode);
+    const int S2 = t.S2, L = W->L;
+    std::vector<uint32_t> m2((size_t)B * S2), ln2(B);
+    std::vector<int> p2((size_t)B * S2);
+    for (uint32_t b = 0; b < B; ++b) {
+      uint32_t ones = 0;
+      for (int j = 0; j < S2; ++j) {
+        double v = 0.0;
+        for (int l = 0; l < L; ++l) {
+          const int sidx = t.src[(size_t)j * L + l];
+          const double x = sidx < 0 ? 0.0 : t.sgn[(size_t)j * L + l] * (double)m[(size_t)b * Sin + sidx];
+          v = v + x * W->lo[l];
+        }
+        m2[(size_t)b * S2 + j] = v > 0.99 ? 1u : 0u;
+        ones += m2[(size_t)b * S2 + j];
+        p2[(size_t)b * S2 + j] = j;
+      }
+      ln2[b] = ones ? ones : 1u;
+    }
+    auto st = std::make_unique<Net::WaveletStage>();
+    st->S_in = Sin;
+    st->S2 = S2;
+    st->L = L;
+    keep_i.push_back(t.src);
+    keep_d.push_back(t.sgn);
+    keep_d.push_back(std::vector<double>(W->lo, W->lo + L));
+    TRY(upload(n, st->src, keep_i.back().data(), keep_i.back().size() * sizeof(int)));
+    TRY(upload(n, st->sgn, keep_d[keep_d.size() - 2].data(), t.sgn.size() * sizeof(double)));
+    TRY(upload(n, st->lo, keep_d.back().data(), (size_t)L * sizeof(double)));
+    keep_u.push_back(m2);
+    TRY(upload(n, st->mask, keep_u.back().data(), m2.size() * sizeof(uint32_t)));
+    keep_u.push_back(ln2);
+    TRY(upload(n, st->lens, keep_u.back().data(), (size_t)B * sizeof(uint32_t)));
+    keep_i.push_back(p2);
+    TRY(upload(n, st->pos, keep_i.back().data(), p2.size() * sizeof(int)));
+    n->wstages.push_back(std::move(st));
+    m = std::move(m2);
+    ln = std::move(ln2);
+    Sin = S2;
+  }
+  n->wS = Sin;
+  n->wmask_h = m;
+  n->wlens_h = ln;
+  if (n->pos_off && sp.mode == MODE_PREFILL) {
+    // decode positions count the uncompressed prompt: offset = prompt length - cached rows
+    std::vector<int> off(B);
+    for (uint32_t b = 0; b < B; ++b) off[b] = (int)lens[b] - (int)ln[b];
+    keep_i.push_back(off);
+    TRY(upload(n, n->pos_off_d, keep_i.back().data(), (size_t)B * sizeof(int)));
+  }
   if (sp.mode == MODE_CACHED) {
     n->dec_tsum = 0.0;
     for (uint32_t b = 0; b < B; ++b) n->dec_tsum += (double)n->kv_len_h[b] + 1;
     std::vector<int> kv(n->kv_len_h.begin(), n->kv_len_h.end());
     TRY(upload(n, n->kv_len_d, kv.data(), B * sizeof(int)));
-    if (S > 1) {
+    if (n->wS > 1) {  // rows per sequence after any compression
       std::vector<int> kr(B);
-      for (uint32_t b = 0; b < B; ++b) kr[b] = (int)lens[b] - 1;  // the last token (masked_attention_head.rs:141-153)
+      for (uint32_t b = 0; b < B; ++b) kr[b] = (int)ln[b] - 1;  // the last token (masked_attention_head.rs:141-153)
       TRY(upload(n, n->kv_row_d, kr.data(), B * sizeof(int)));
       sp.kv_row = n->kv_row_d.as<int>();
     }
+    HIP_TRY(hipStreamSynchronize(n->stream));  // kv, kr go out of scope
   }
-  (void)hidden_path;
   HIP_TRY(hipStreamSynchronize(n->stream));  // the host staging vectors above go out of scope
   return OK;
+}
+
+// rows each sequence keeps in the cache after a prompt pass (compressed by
+// the wavelet stages, if any)
+static const uint32_t* cached_lens(const Net* n, const uint32_t* lens) {
+  return n->wstages.empty() ? lens : n->wlens_h.data();
 }
 
 static void end_call(Net* n, const Spec& sp, const uint32_t* lens) {
   if (sp.mode == MODE_PREFILL) {
     n->cache_valid = true;
     n->cache_B = sp.B;
-    n->kv_len_h.assign(lens, lens + sp.B);  // the cache keeps each sequence's own rows
+    const uint32_t* cl = cached_lens(n, lens);
+    n->kv_len_h.assign(cl, cl + sp.B);  // the cache keeps each sequence's own rows
   } else if (sp.mode == MODE_CACHED) {
     for (uint32_t b = 0; b < (uint32_t)sp.B; ++b) n->kv_len_h[b] += 1;
   }
@@ -1745,8 +2008,9 @@ int mitok_predict(mitok_network* n, const uint32_t* ids, const uint32_t* lens, u
   sp.last = (uint32_t)n->layers.size();
   sp.last_row = last_row_only && forward_only;
   std::vector<uint32_t> mask_h;
-  TRY(begin_call(n, lens, B, S, time_steps, forward_only != 0, false, sp, mask_h));
+  TRY(begin_call(n, lens, B, S, time_steps, forward_only != 0, nullptr, sp, mask_h));
   const size_t rows = (size_t)B * S;
+  const size_t orows = (size_t)B * n->wS;  // output rows (a wavelet layer compresses a prompt pass)
   std::vector<uint32_t> padded(rows);
   for (uint32_t b = 0; b < B; ++b)
     for (uint32_t s = 0; s < S; ++s) padded[(size_t)b * S + s] = s < lens[b] ? ids[(size_t)b * S + s] : 1u;
@@ -1757,22 +2021,23 @@ int mitok_predict(mitok_network* n, const uint32_t* ids, const uint32_t* lens, u
   sp.out_prob = n->probs.as<double>();
   TRY(enqueue_step(n, sp));
   if (forward_only) {
-    size_t cnt = (sp.last_row ? (size_t)B : rows) * V;
+    size_t cnt = (sp.last_row ? (size_t)B : orows) * V;
     HIP_TRY(hipMemcpyAsync(out, sp.out_re, cnt * sizeof(double), hipMemcpyDeviceToHost, n->stream));
     HIP_TRY(hipStreamSynchronize(n->stream));
   } else {
-    std::vector<double> all(rows * V);
+    std::vector<double> all(orows * V);
     HIP_TRY(hipMemcpyAsync(all.data(), sp.out_prob, all.size() * sizeof(double), hipMemcpyDeviceToHost, n->stream));
     HIP_TRY(hipStreamSynchronize(n->stream));
+    const uint32_t* ol = cached_lens(n, lens);
     if (last_row_only)
       for (uint32_t b = 0; b < B; ++b)
-        memcpy(out + (size_t)b * V, all.data() + ((size_t)b * S + lens[b] - 1) * V, V * sizeof(double));
+        memcpy(out + (size_t)b * V, all.data() + ((size_t)b * n->wS + ol[b] - 1) * V, V * sizeof(double));
     else memcpy(out, all.data(), all.size() * sizeof(double));
   }
   collect_timing(n);
   TRY(check_err_word(n));
   end_call(n, sp, lens);
-  if (out_mask) memcpy(out_mask, mask_h.data(), rows * sizeof(uint32_t));
+  if (out_mask) memcpy(out_mask, n->wstages.empty() ? mask_h.data() : n->wmask_h.data(), orows * sizeof(uint32_t));
   return OK;
 }
 
@@ -1795,22 +2060,17 @@ int mitok_forward_layers(mitok_network* n, uint32_t first, uint32_t last, const 
   sp.first = first;
   sp.last = last;
   std::vector<uint32_t> mask_h;
-  TRY(begin_call(n, lens.data(), B, S, time_steps, forward_only != 0, true, sp, mask_h));
-  const size_t rows = (size_t)B * S;
-  if (mask_in) {
-    TRY(upload(n, n->mask_d, mask_in, rows * sizeof(uint32_t)));
-  } else {
-    fill_u32(n->stream, n->mask_d.as<uint32_t>(), rows, 1);
-  }
+  TRY(begin_call(n, lens.data(), B, S, time_steps, forward_only != 0, mask_in, sp, mask_h));
+  const size_t rows = (size_t)B * S, orows = (size_t)B * n->wS;
   const uint32_t din = n->layers[first]->d_in, dout = n->layers[last - 1]->d_out;
   DevBuf xin, xout;
   TRY(xin.reserve(rows * din * sizeof(double2)));
-  TRY(xout.reserve(rows * dout * sizeof(double2)));
+  TRY(xout.reserve(orows * dout * sizeof(double2)));
   HIP_TRY(hipMemcpyAsync(xin.p, in, rows * din * sizeof(double2), hipMemcpyHostToDevice, n->stream));
   sp.in = xin.as<double2>();
   sp.out_hidden = xout.as<double2>();
   TRY(enqueue_forward(n, sp));
-  HIP_TRY(hipMemcpyAsync(out, xout.p, rows * dout * sizeof(double2), hipMemcpyDeviceToHost, n->stream));
+  HIP_TRY(hipMemcpyAsync(out, xout.p, orows * dout * sizeof(double2), hipMemcpyDeviceToHost, n->stream));
   HIP_TRY(hipStreamSynchronize(n->stream));
   collect_timing(n);
   TRY(check_err_word(n));
@@ -1900,7 +2160,7 @@ static int run_prompt(Net* n, const uint32_t* prompt, const uint32_t* lens, uint
   pre.last = (uint32_t)n->layers.size();
   pre.last_row = true;
   std::vector<uint32_t> mask_h;
-  TRY(begin_call(n, lens, B, S, nullptr, true, false, pre, mask_h));
+  TRY(begin_call(n, lens, B, S, nullptr, true, nullptr, pre, mask_h));
   TRY(ensure_rope_for(n, 0, pre.last, (int)std::max<uint32_t>(rope_positions_needed(n), ctx)));
   std::vector<uint32_t> padded((size_t)B * S);
   for (uint32_t b = 0; b < B; ++b)
@@ -1925,8 +2185,10 @@ static int run_prompt(Net* n, const uint32_t* prompt, const uint32_t* lens, uint
   pre.hist_re = want_logits ? n->logit_hist_d.as<double>() : nullptr;
   pre.hist_cnt = n->cnt_d.as<int>();
   TRY(enqueue_forward(n, pre));
-  // KV lengths = prompt lengths (lens_d holds them since begin_call; same bits as int)
-  HIP_TRY(hipMemcpyAsync(n->kv_len_d.p, n->lens_d.p, B * sizeof(int), hipMemcpyDeviceToDevice, st));
+  // KV lengths = the rows each prompt left in the cache (lens_d, or the last
+  // wavelet stage's compressed lens; same bits as int)
+  const void* kvsrc = n->wstages.empty() ? n->lens_d.p : n->wstages.back()->lens.p;
+  HIP_TRY(hipMemcpyAsync(n->kv_len_d.p, kvsrc, B * sizeof(int), hipMemcpyDeviceToDevice, st));
   end_call(n, pre, lens);
   return OK;
 }

@@ -141,11 +141,19 @@ __device__ __forceinline__ double2 ro_base(const RowOps& r, int m, int k, int K,
   return v;
 }
 
+// position of row m for RoPE: its table entry, plus the row's offset when the
+// prompt pass compressed the sequence (a wavelet layer: decode positions count
+// the uncompressed prompt, transformer_network.rs:300-304)
+template <class Acc = AccPlain>
+__device__ __forceinline__ int ro_pos(const RowOps& r, int m) {
+  return Acc::kv(r.rope_pos, m) + (r.rope_off ? Acc::c(r.rope_off + m) : 0);
+}
+
 // with RoPE: pairs (2i, 2i+1) rotate by the tabulated angle of the row's position
 template <class Acc = AccPlain>
 __device__ __forceinline__ double2 ro_source(const RowOps& r, int m, int k, int K, const RoLds& L) {
   if (!r.rope_cs) return ro_base<Acc>(r, m, k, K, L);
-  const int p = min(Acc::kv(r.rope_pos, m), r.rope_max - 1);  // overflow flagged by ro_check
+  const int p = min(ro_pos<Acc>(r, m), r.rope_max - 1);  // overflow flagged by ro_check
   const int i = k >> 1;
   const double2 t = Acc::c(r.rope_cs + (long)p * (K >> 1) + i);
   const double2 e = ro_base<Acc>(r, m, 2 * i, K, L), o = ro_base<Acc>(r, m, 2 * i + 1, K, L);
@@ -166,7 +174,7 @@ __device__ __forceinline__ void ro_check(const RowOps& r, int m) {
     const uint32_t id = Acc::id(r.ids, m);
     if (id != 1u && id >= (uint32_t)r.vocab) atomicOr(r.err, (uint32_t)EB_BAD_TOKEN);
   }
-  if (r.rope_cs && Acc::kv(r.rope_pos, m) >= r.rope_max) atomicOr(r.err, (uint32_t)EB_CTX_OVERFLOW);
+  if (r.rope_cs && ro_pos<Acc>(r, m) >= r.rope_max) atomicOr(r.err, (uint32_t)EB_CTX_OVERFLOW);
 }
 
 constexpr int LN_PRE = 4;  // gamma/beta columns per thread requested up front (rows up to 1024 wide)
@@ -377,7 +385,7 @@ __device__ void ro_build(const RowOps& r, int M, int K, int ka, int RL, int n0, 
       const bool pair = 2 * j + 1 < RL && k + 1 < K;  // always true with RoPE (even K, even range)
       double2 e = buf[m * RL + 2 * j], o = pair ? buf[m * RL + 2 * j + 1] : make_double2(0.0, 0.0);
       if (r.rope_cs) {
-        const int p = min(Acc::kv(r.rope_pos, gm), r.rope_max - 1);  // overflow flagged by ro_check
+        const int p = min(ro_pos<Acc>(r, gm), r.rope_max - 1);  // overflow flagged by ro_check
         const double2 t = Acc::c(r.rope_cs + (long)p * (K >> 1) + (k >> 1));
         const double2 e2 = make_double2(e.x * t.x - o.x * t.y, e.y * t.x - o.y * t.y);
         const double2 o2 = make_double2(e.x * t.y + o.x * t.x, e.y * t.y + o.y * t.x);

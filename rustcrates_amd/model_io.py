@@ -410,6 +410,7 @@ def to_device(model: Model, net, embeddings: dict | None = None, missing: str = 
     """Appends `model`'s layers to `net` (rustcrates_amd.Network, or the CPU
     checker's Network with the same methods) in LayerEnum order, with every
     weight uploaded as stored.  Returns net."""
+    width = 0  # features per row after the layers so far
     for L in model.layers:
         f = L.f
         if L.kind == "Embedding":
@@ -417,6 +418,9 @@ def to_device(model: Model, net, embeddings: dict | None = None, missing: str = 
             if embeddings is None:
                 raise ValueError("the model has an Embedding layer: pass the embedding pairs")
             net.add_embedding(V, d, embedding_table(embeddings, V, d, missing))
+            width = d
+        elif L.kind == "DiscreteWavelet":
+            net.add_discrete_wavelet(width, f["wavelet"], f["wavelet_mode"], f["is_full_mode"])
         elif L.kind == "PositionalEncoding":
             net.add_positional_encoding(f["embedding_dim"], f["base"])
         elif L.kind == "Norm":
@@ -447,6 +451,7 @@ def to_device(model: Model, net, embeddings: dict | None = None, missing: str = 
         elif L.kind == "Linear":
             w = f["weights"]
             net.add_linear(w.shape[0], w.shape[1], w, f["bias"])
+            width = w.shape[1]
         elif L.kind == "Softmax":
             net.add_softmax(f["operation_mode"])
         else:

@@ -184,3 +184,29 @@ def test_unsupported_layers_are_refused():
     assert m2.layers[1].kind == "RMSNorm"
     with pytest.raises(NotImplementedError, match="RMSNorm"):
         model_io.to_device(m2, oracle.Network(), {i: np.zeros(4) for i in range(10)})
+
+
+def test_default_stack_file_with_wavelet_layer_imports():
+    """A DiscreteWavelet layer (wavelet_discrete_layer.rs:20-52: time_step,
+    wavelet, wavelet_mode, is_full_mode) decodes from hand-assembled bytes and
+    imports as the device stack's wavelet layer."""
+    blob = (_u64(1) + _u32(9) + _u64(0) + _u32(1) + _u32(2) + b"\x00" + _f64(0.01) + _u64(0) * 5)
+    m = model_io.read_network(blob)
+    assert m.layers[0].kind == "DiscreteWavelet"
+    assert m.layers[0].f == {"time_step": 0, "wavelet": 1, "wavelet_mode": 2, "is_full_mode": False}
+    assert model_io.write_network(m) == blob
+    cfg = configs.ModelConfig("t", layers=1, d=8, heads=2, ffn=16, vocab=40, max_ctx=24, seed=3)
+    full = model_io.from_tensors(cfg, seeded_tensors(cfg))
+    full.layers.insert(1, m.layers[0])
+    t = seeded_tensors(cfg)[0]["table"].reshape(40, 8)
+    a = model_io.to_device(model_io.read_network(model_io.write_network(full)), oracle.Network(),
+                           {i: t[i] for i in range(40) if i != 1})
+    b = oracle.Network()
+    b.add_embedding(40, 8, t)
+    b.add_discrete_wavelet(8, 1, 2)
+    rest = model_io.Model(full.layers[2:])
+    model_io.to_device(rest, b)
+    ids = np.array([[3, 9, 27, 5, 11, 2, 30]], np.uint32)
+    la, _ = a.predict(ids, forward_only=True)
+    lb, _ = b.predict(ids, forward_only=True)
+    assert la.shape == (1, oracle.dwt_rows(7, 1), 40) and np.array_equal(la, lb)

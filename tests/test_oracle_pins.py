@@ -549,3 +549,97 @@ def test_explicit_tensor_stack_equals_seeded_stack():
     ia, la = a.generate(p, lens=[6, 3], n_new=5, want_logits=True)
     ib, lb = b.generate(p, lens=[6, 3], n_new=5, want_logits=True)
     assert np.array_equal(ia, ib) and np.array_equal(la, lb)
+
+
+# --------------------------------------------------------------------------
+# DiscreteWaveletLayer (network_types/wavelet_discrete_layer.rs:46-161,
+# wavelet_transform/dwt.rs)
+# --------------------------------------------------------------------------
+def _dwt_2d_full(data, wavelet, mode):
+    """dwt_2d_full (dwt.rs:22-34): rows, transpose, rows, transpose."""
+    rows = np.array([oracle.dwt_1d(r, wavelet, mode) for r in np.asarray(data, float)])
+    cols = np.array([oracle.dwt_1d(r, wavelet, mode) for r in rows.T])
+    return cols.T
+
+
+def _ll_hl_lh_hh(t):
+    """get_ll_hl_lh_hh (dwt.rs:378-402)"""
+    hr, hc = t.shape[0] >> 1, t.shape[1] >> 1
+    return [t[:hr, :hc], t[hr:, :hc], t[:hr, hc:], t[hr:, hc:]]
+
+
+def test_dwt_known_answers_from_reference_tests():
+    """wavelet_transform/tests.rs:531-560 (test_dwt): DB1 and DB2, CONSTANT mode,
+    compared exactly as the reference asserts them."""
+    t = _dwt_2d_full([[1.0, 2.0, 3.0, 4.0, 5.0], [6.0, 7.0, 8.0, 9.0, 10.0]], 0, 1)
+    assert t.tolist() == [[8.0, 12.000000000000004, 15.000000000000004, -0.9999999999999998, -1.0000000000000004, 0.0],
+                          [-5.0, -5.000000000000001, -5.000000000000001, -4.440892098500626e-16, 3.3306690738754696e-16,
+                           0.0]]
+    data = [[1.15, 2.22, 3.36, 4.45, 5.59], [6.61, 7.72, 8.83, 9.94, 10.17]]
+    parts = _ll_hl_lh_hh(_dwt_2d_full(data, 1, 1))
+    want = [[[1.1055969296248855, 2.659056465474454, 7.315913630276377, 10.341801825333636],
+             [9.290106548568122, 10.882806465474454, 15.449230777830874, 17.21180182533364]],
+            [[-3.7267493523315185, -3.744617138124092, -3.7034392801983413, -3.128198174666365],
+             [0.9985794793504406, 1.0033671381240925, 0.992333564346846, 0.838198174666366]],
+            [[-0.7283235910246749, 0.02329246824526906, 0.8107842982524609, 1.3710127121807463e-15],
+             [-0.7488139720814411, 0.0072876587736526175, 0.4722794887808437, 4.289572369704812e-16]],
+            [[0.009330127018921996, 0.007287658773652618, 0.15413538968048013, 4.2895723697048124e-16],
+             [-0.0025000000000000022, -0.0019527222831138048, -0.04130045318994102, -1.1493874523372615e-16]]]
+    for got, w in zip(parts, want):
+        np.testing.assert_array_equal(got, w)  # bit for bit, as assert_eq! checks them
+
+
+def test_dwt_symmetric_padding_and_filters_closed_forms():
+    """SYMMETRIC pads half-sample symmetrically (x1 x0 | x0 .. xn-1 | xn-1 xn-2 ..),
+    so a constant sequence has low-pass value sqrt(2) * c everywhere and a zero
+    high pass; DB2 is orthonormal (sum h = sqrt 2, sum h^2 = 1, sum h_k h_k+2 = 0)
+    and has two vanishing moments: a linear ramp's interior high pass is zero."""
+    for n in (5, 6, 9):
+        out = oracle.dwt_1d(np.full(n, 3.0), 1, 2)
+        half = out.shape[0] // 2
+        np.testing.assert_allclose(out[:half], 3.0 * np.sqrt(2.0), rtol=1e-15)
+        np.testing.assert_allclose(out[half:], 0.0, atol=1e-14)
+    # the taps, read out with unit impulses (ZERO mode, 2 zeros in front):
+    # output j of an impulse at p is h[p + 2 - 2j]
+    taps = [None] * 4
+    for p in range(4):
+        out = oracle.dwt_1d(np.eye(8)[p], 1, 0)
+        for j in range(5):
+            l = p + 2 - 2 * j
+            if 0 <= l < 4:
+                taps[l] = out[j]
+            else:
+                assert out[j] == 0.0
+    h = np.array(taps)
+    s3 = np.sqrt(3.0)
+    np.testing.assert_allclose(h, np.array([1 + s3, 3 + s3, 3 - s3, 1 - s3]) / (4 * np.sqrt(2.0)), rtol=4e-16)
+    assert abs(h.sum() - np.sqrt(2.0)) < 1e-15 and abs((h ** 2).sum() - 1.0) < 1e-15
+    assert abs(h[0] * h[2] + h[1] * h[3]) < 1e-16
+    # DB1 (Haar): FRAC_1_SQRT_2 twice
+    assert oracle.dwt_1d(np.array([1.0, 0.0]), 0, 0)[0] == math.sqrt(0.5)  # correctly rounded 1/sqrt(2)
+    ramp = oracle.dwt_1d(np.arange(12.0), 1, 2)
+    np.testing.assert_allclose(ramp[7 + 1:7 + 5], 0.0, atol=1e-13)  # interior high pass of a line
+
+
+def test_wavelet_layer_compresses_prompt_rows_and_mask():
+    """The layer at a prompt pass (wavelet_discrete_layer.rs:102-128): every
+    feature column becomes the low half of its dwt_1d along the sequence; the
+    padding mask the thresholded low half of its own dwt_1d (:297-313)."""
+    net = oracle.Network()
+    net.add_discrete_wavelet(3, 1, 2)
+    rng = np.random.default_rng(30)
+    x = rng.standard_normal((2, 9, 3)) + 1j * rng.standard_normal((2, 9, 3))
+    mask = np.array([[1] * 9, [1] * 6 + [0] * 3], np.uint32)
+    got = net.forward_layers(0, 1, x, mask=mask, forward_only=False)
+    M = oracle.dwt_rows(9, 1)
+    assert got.shape == (2, M, 3) and M == 6
+    for b in range(2):
+        for c in range(3):
+            re = oracle.dwt_1d(x[b, :, c].real, 1, 2)[:M]
+            im = oracle.dwt_1d(x[b, :, c].imag, 1, 2)[:M]
+            np.testing.assert_allclose(got[b, :, c], re + 1j * im, rtol=1e-14, atol=1e-15)
+    m1 = oracle.dwt_1d(mask[1].astype(float), 1, 2)[:M]
+    assert (m1 > 0.99).tolist() == [True, True, True, True, False, False]
+    # a cached step (time_step > 0) passes the row through
+    step = net.forward_layers(0, 1, x[:, :1], forward_only=True, time_steps=[9, 9])
+    np.testing.assert_array_equal(step, x[:, :1])

@@ -270,6 +270,7 @@ struct Spec {
   double* out_prob = nullptr;        // softmax output (not forward_only)
   double2* out_hidden = nullptr;     // result of a hidden-state range
   const Argmax* am = nullptr;        // greedy ids fused into the vocab GEMM (token loop)
+  bool compress = false;             // apply the wavelet stages begin_call planned for this call
   double* hist_re = nullptr;         // Re-logits history [step][B][V] at hist_cnt[0] (token loop)
   const int* hist_cnt = nullptr;
 };
@@ -615,9 +616,9 @@ static int enqueue_forward(Net* n, const Spec& sp) {
   const Sync sy = sync_of(n);
   const int B = sp.B;
   int S = sp.S, rows = B * S;  // a wavelet layer of a prompt pass compresses the rows
-  const uint32_t* mask = mask;
-  const uint32_t* lens = lens;
-  const int* pos = pos;
+  const uint32_t* mask = sp.mask;
+  const uint32_t* lens = sp.lens;
+  const int* pos = sp.pos;
   size_t wi = 0;  // next wavelet stage
   double2* cur = n->act0.as<double2>();
   double2* nxt = n->act1.as<double2>();
@@ -803,7 +804,10 @@ static int enqueue_forward(Net* n, const Spec& sp) {
       }
       case K_SOFTMAX: break;  // applied together with the vocab Linear
       case K_WAVELET: {
-        if (wi >= n->wstages.size()) break;  // a cached step's row passes through (wavelet_discrete_layer.rs:102-128)
+        // only the call begin_call planned compresses; a cached step's row
+        // passes through (wavelet_discrete_layer.rs:102-128)
+        if (!sp.compress) break;
+        if (wi >= n->wstages.size()) return fail(ERR_STATE, "wavelet stage %zu not planned", wi);
         const auto& W = *n->wstages[wi++];
         dwt_rows(st, cur, B, S, (int)L->d_in, W.src.as<int>(), W.sgn.as<double>(), W.lo.as<double>(), W.L, W.S2, nxt);
         std::swap(cur, nxt);
@@ -834,6 +838,7 @@ static int enqueue_forward(Net* n, const Spec& sp) {
 static bool fused_decode_ok(const Net* n, const Spec& sp) {
   if (!n->fused_decode || sp.mode != MODE_CACHED || sp.S != 1 || sp.B > GEMM_PART_MAX_M || !sp.forward_only)
     return false;
+  if (sp.compress) return false;  // a one-row call at time step 0 that a wavelet layer widens
   if (sp.first != 0 || sp.last != n->layers.size() || sp.kv_row || sp.out_hidden) return false;
   if (sp.B <= 8) {
     // the GEMV prologue holds whole input rows of a LayerNorm in LDS
@@ -1115,7 +1120,7 @@ constexpr int RES_AUTO_MAX_B = 1;
 
 static bool resident_ok(const Net* n, const Spec& sp) {
   const int max_b = n->resident == 2 ? 8 : n->resident == 1 ? RES_AUTO_MAX_B : 0;
-  if (sp.mode != MODE_CACHED || sp.S != 1 || sp.B > max_b || !sp.forward_only || !sp.am) return false;
+  if (sp.mode != MODE_CACHED || sp.S != 1 || sp.B > max_b || !sp.forward_only || !sp.am || sp.compress) return false;
   if (sp.first != 0 || sp.last != n->layers.size() || sp.kv_row || sp.out_hidden) return false;
   for (auto& L : n->layers)
     if (L->kind == K_SELF_ATTENTION) {
@@ -1690,6 +1695,11 @@ int mitok_add_discrete_wavelet(mitok_network* n, uint32_t dim, uint32_t wavelet,
   if (!wavelet_low_pass(wavelet, L->lo, &L->L))
     return fail(ERR_ARG, "wavelet type %u: only DB1 and DB2 are on the device path", wavelet);
   if (!wavelet_mode_ok(mode)) return fail(ERR_ARG, "wavelet mode %u is not on the device path", mode);
+  // one cached length per sequence: every attention layer's cache holds the
+  // compressed rows, so compression happens before the first attention layer
+  for (auto& P : n->layers)
+    if (P->kind == K_SELF_ATTENTION)
+      return fail(ERR_ARG, "DiscreteWaveletLayer after a SelfAttentionLayer is not on the device path");
   L->wavelet = wavelet;
   L->mode = mode;
   L->d_in = L->d_out = dim;
@@ -1956,6 +1966,7 @@ static int begin_call(Net* n, const uint32_t* lens, uint32_t B, uint32_t S, cons
   n->wS = Sin;
   n->wmask_h = m;
   n->wlens_h = ln;
+  sp.compress = !wl.empty();
   if (n->pos_off && sp.mode == MODE_PREFILL) {
     // decode positions count the uncompressed prompt: offset = prompt length - cached rows
     std::vector<int> off(B);

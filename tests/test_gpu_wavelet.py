@@ -99,3 +99,14 @@ def test_reference_default_stack_generate(lens):
     steps = [first] + [g.decode_step() for _ in range(n_new - 1)]
     assert np.array_equal(np.stack(steps, axis=1), io)
     g.close()
+
+
+def test_wavelet_after_attention_is_refused():
+    """Every attention layer's cache holds the rows of one cached length per
+    sequence, so a wavelet layer may only precede the attention layers."""
+    g = ra.Network(0)
+    g.add_embedding(40, 8)
+    g.add_self_attention(2, 8, 16, 1e-12)
+    with pytest.raises(ra.MitokError, match="after a SelfAttentionLayer"):
+        g.add_discrete_wavelet(8, 1, 2)
+    g.close()

@@ -1,0 +1,98 @@
+//! The device-backed text loop: `predict_token_by_token`
+//! (network_types/transformer/transformer_network.rs:165-313) with every
+//! forward pass on the GPU.
+//!
+//! The crate's own function keeps its signature and, when the network holds a
+//! device handle, returns `predict_token_by_token_device(handle, input_batch,
+//! &tokenizer)`.  What the loop does around the forward passes:
+//!   - each input gets the "<bos> " prefix (network_components/input.rs:70-72);
+//!   - sequence 0 is tokenized with special tokens and cut to its last
+//!     MAX_CONTEXT_WINDOW_SIZE ids (:32, 208-218);
+//!   - step 0 runs every prompt row and keeps the [S][V] Re-logits; each later
+//!     step feeds the last greedy id at time_step = its position (:225-248,
+//!     300-304) and keeps its [1][V] Re-logits (:257);
+//!   - the greedy id is the last index among equal maxima of the last row
+//!     (sampling_methods.rs:5-18), decoded on its own with special tokens kept;
+//!   - "<eos>" ends the loop without being appended (:285-288), any other token
+//!     is appended to sequence 0's text (:291), and 21 appended tokens end it
+//!     (:293-297).
+
+use crate::{MitokError, Network};
+
+pub const MAX_CONTEXT_WINDOW_SIZE: usize = 512;
+pub const MAX_NEW_TOKENS: usize = 21;
+
+/// The two tokenizer calls the loop makes (the crate's GPT-NeoX `Tokenizer`,
+/// utils/tokenizer.rs:9-50).
+pub trait TextTokenizer {
+    /// `encode(text, add_special_tokens = true)` ids.
+    fn encode_ids(&self, text: &str) -> Vec<u32>;
+    /// `decode(&[id], skip_special_tokens = false)`.
+    fn decode_id(&self, id: u32) -> String;
+}
+
+/// sampling_methods.rs:5-18: `max_by(partial_cmp)` keeps the last of equal
+/// maxima; a NaN is an error where the reference's `unwrap()` panics.
+pub fn greedy_id(row: &[f64]) -> Result<u32, MitokError> {
+    let mut best = 0usize;
+    for (i, &x) in row.iter().enumerate() {
+        if x.is_nan() {
+            return Err(MitokError { code: crate::MITOK_ERR_NAN, message: "greedy_decoding: NaN in logits".into() });
+        }
+        if x >= row[best] {
+            best = i;
+        }
+    }
+    Ok(best as u32)
+}
+
+pub fn predict_token_by_token_device<T: TextTokenizer>(net: &mut Network, input_batch: &[String], tokenizer: &T)
+                                                      -> Result<(Vec<Vec<Vec<f64>>>, Vec<String>), MitokError> {
+    let mut texts: Vec<String> = input_batch.iter().map(|t| format!("<bos> {}", t)).collect();
+    let mut predictions: Vec<Vec<Vec<f64>>> = Vec::new();
+    if texts.is_empty() {
+        return Ok((predictions, texts));
+    }
+    let all = tokenizer.encode_ids(&texts[0]);
+    let ids = all[all.len().saturating_sub(MAX_CONTEXT_WINDOW_SIZE)..].to_vec();
+    if ids.is_empty() {
+        return Ok((predictions, texts));
+    }
+    net.reset()?;
+    let (mut out, _) = net.predict(&[ids.clone()], None, true)?;
+    predictions.push(out.swap_remove(0));
+    let mut pos = ids.len() as u32;
+    for count in 0..MAX_NEW_TOKENS {
+        let last = predictions.last().and_then(|p| p.last()).expect("one row per step");
+        let next = greedy_id(last)?;
+        let token = tokenizer.decode_id(next);
+        if token == "<eos>" {
+            break;
+        }
+        texts[0].push_str(&token);
+        if count + 1 == MAX_NEW_TOKENS {
+            break;
+        }
+        let (mut out, _) = net.predict(&[vec![next]], Some(pos), true)?;
+        predictions.push(out.swap_remove(0));
+        pos += 1;
+    }
+    Ok((predictions, texts))
+}
+
+/// Ids only (no per-step logits): the prompt pass, then one decode step per
+/// token with the fed id staying on the device; 4 bytes per step cross PCIe.
+/// `eos` is the id whose text is "<eos>" (50279 in the GPT-NeoX vocabulary the
+/// crate extends, utils/tokenizer.rs:51-75).
+pub fn generate_ids_device(net: &mut Network, prompt: &[u32], eos: u32) -> Result<Vec<u32>, MitokError> {
+    let mut out = Vec::with_capacity(MAX_NEW_TOKENS);
+    let mut id = net.prefill(prompt, None)?;
+    while id != eos {
+        out.push(id);
+        if out.len() == MAX_NEW_TOKENS {
+            break;
+        }
+        id = net.decode_step(None, None)?;
+    }
+    Ok(out)
+}

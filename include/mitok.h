@@ -117,7 +117,7 @@ int mitok_reset(mitok_network* net);
  *   SoftmaxLayer output for its OperationMode.
  * last_row_only: out is [batch][vocab] from each sequence's last row, else
  *   [batch][seq'][vocab] with seq' = mitok_seq_out_len (seq without wavelet layers).
- * out_padding_mask [batch][seq] or NULL. */
+ * out_padding_mask [batch][seq'] or NULL (the mask the last layer saw). */
 int mitok_predict(mitok_network* net, const uint32_t* ids, const uint32_t* lens, uint32_t batch, uint32_t seq,
                   const uint32_t* time_steps, int forward_only, int last_row_only, double* out,
                   uint32_t* out_padding_mask);

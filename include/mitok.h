@@ -5,7 +5,7 @@
  * foreign-function boundary on this path except the OpenBLAS `zgemm_` it
  * calls (utils/matrix.rs:13-15).  This header is the boundary a Rust FFI crate
  * binds instead: each entry point names the Rust item it replaces.  The Rust
- * binding and the drop-in wiring are in INTEGRATION.md.
+ * declarations of this header are bindings/rust/mitok-sys/src/lib.rs.
  *
  * Conventions
  *  - Complex<f64> (num-complex 0.4.6, #[repr(C)] {re, im}) crosses the ABI as

@@ -20,8 +20,9 @@ decodes embedding values (`decode_embedding`, `read_embedding_pairs`), and
 builds the stack on a HIP `Network` (`to_device`).  The sled storage engine
 itself is not reimplemented: its `db` log file is absent from the reference
 snapshot and sled's on-disk format belongs to the storage engine, not to the
-token loop.  Embeddings come in as the (id, value bytes) pairs a sled tree
-iterates to (INTEGRATION.md shows the few lines of Rust that export them).
+token loop.  Embeddings come in as the (key, value bytes) pairs a sled tree
+iterates to, exported one after another as (u64 key length, key bytes, u64
+value length, value bytes): a loop of four writes over `db.iter()` in Rust.
 """
 from __future__ import annotations
 

@@ -78,6 +78,9 @@ extern "C" {
     pub fn mitok_forward_layers(net: *mut MitokNetwork, first: u32, last: u32, inp: *const c_double,
                                 padding_mask: *const u32, batch: u32, seq: u32, time_steps: *const u32,
                                 forward_only: c_int, out: *mut c_double) -> c_int;
+    pub fn mitok_forward_layers_device(net: *mut MitokNetwork, first: u32, last: u32, d_in: *const c_double,
+                                       padding_mask: *const u32, batch: u32, seq: u32, time_steps: *const u32,
+                                       forward_only: c_int, d_out: *mut c_double) -> c_int;
     pub fn mitok_generate(net: *mut MitokNetwork, prompt: *const u32, lens: *const u32, batch: u32, seq: u32,
                           n_new: u32, out_ids: *mut u32, out_logits: *mut c_double) -> c_int;
     pub fn mitok_prefill(net: *mut MitokNetwork, prompt: *const u32, lens: *const u32, batch: u32, seq: u32,
@@ -86,6 +89,8 @@ extern "C" {
                              out_logits: *mut c_double) -> c_int;
     pub fn mitok_greedy_decoding(net: *mut MitokNetwork, logits: *const c_double, rows: u32, vocab: u32,
                                  out_ids: *mut u32) -> c_int;
+    pub fn mitok_greedy_decoding_device(net: *mut MitokNetwork, d_logits: *const c_double, rows: u32, vocab: u32,
+                                        d_out_ids: *mut u32) -> c_int;
     // No counterpart in the reference: greedy_decoding for callers that cannot
     // allocate device memory.  Stages in a fixed per-GPU array (8 MiB + 16 KiB):
     // rows * vocab <= 1048576 and rows <= 4096; overlapping calls on one GPU race.

@@ -128,6 +128,15 @@ int mitok_predict(mitok_network* net, const uint32_t* ids, const uint32_t* lens,
 int mitok_forward_layers(mitok_network* net, uint32_t first, uint32_t last, const double* in,
                          const uint32_t* padding_mask, uint32_t batch, uint32_t seq, const uint32_t* time_steps,
                          int forward_only, double* out);
+/* mitok_forward_layers on device buffers (the per-layer drop-in for a caller
+ * whose hidden states stay on the GPU): d_in and d_out are device memory of the
+ * network's GPU (hipMalloc), d_out [batch][seq'][dim_out] with
+ * seq' = mitok_seq_out_len.  padding_mask and time_steps stay host arrays.  A
+ * pointer that is not device memory of that GPU, or an allocation too small
+ * for the shape, is MITOK_ERR_ARG. */
+int mitok_forward_layers_device(mitok_network* net, uint32_t first, uint32_t last, const double* d_in,
+                                const uint32_t* padding_mask, uint32_t batch, uint32_t seq,
+                                const uint32_t* time_steps, int forward_only, double* d_out);
 
 /* Greedy token loop on ids (predict_token_by_token, transformer_network.rs:165-313,
  * without the text tokenizer): resets the caches, runs the prompt, then feeds
@@ -157,6 +166,11 @@ int mitok_decode_step(mitok_network* net, const uint32_t* ids, uint32_t batch, u
 /* greedy_decoding (src/utils/sampling_methods.rs:5-18) on the device for host
  * logits [rows][vocab]: last index among equal maxima; NaN -> MITOK_ERR_NAN. */
 int mitok_greedy_decoding(mitok_network* net, const double* logits, uint32_t rows, uint32_t vocab, uint32_t* out_ids);
+/* greedy_decoding on device buffers: d_logits [rows][vocab] f64 and d_out_ids
+ * [rows] are device memory of the network's GPU, checked as for
+ * mitok_forward_layers_device. */
+int mitok_greedy_decoding_device(mitok_network* net, const double* d_logits, uint32_t rows, uint32_t vocab,
+                                 uint32_t* d_out_ids);
 
 /* mitok_greedy_decoding without any device allocation.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under

@@ -58,6 +58,8 @@ SIGNATURES = {
     "mitok_prefill": (_i32, [_P, _P, _P, _u32, _u32, _P, _P]),
     "mitok_decode_step": (_i32, [_P, _P, _u32, _P, _P]),
     "mitok_greedy_decoding": (_i32, [_P, _P, _u32, _u32, _P]),
+    "mitok_greedy_decoding_device": (_i32, [_P, _P, _u32, _u32, _P]),
+    "mitok_forward_layers_device": (_i32, [_P, _u32, _u32, _P, _P, _u32, _u32, _P, _i32, _P]),
     "mitok_greedy_decoding_noalloc": (_i32, [_P, _P, _u32, _u32, _P]),
     "mitok_last_timings": (_i32, [_P, _P]),
     "mitok_timing_enable": (_i32, [_P, _i32]),
@@ -100,6 +102,55 @@ def _check(rc: int):
 
 def _ptr(a):
     return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+def _dev(p):
+    return C.c_void_p(p.ptr if isinstance(p, DeviceBuffer) else int(p))
+
+
+class DeviceBuffer:
+    """Device memory for the *_device entry points, from the HIP runtime the
+    library links (hipMalloc / hipMemcpy / hipFree).  torch in this image
+    bundles a HIP runtime of its own, and one process holds the GPU through one
+    runtime, so a process using the library takes its device memory here."""
+
+    def __init__(self, nbytes: int, device: int = 0):
+        load_library()
+        self._hip = C.CDLL("libamdhip64.so.7")  # the copy the library loaded
+        self.nbytes, self.device = int(nbytes), device
+        self._p = C.c_void_p()
+        if self._hip.hipSetDevice(device) != 0 or self._hip.hipMalloc(C.byref(self._p), C.c_size_t(self.nbytes)) != 0:
+            raise MitokError(2, f"hipMalloc of {self.nbytes} bytes on device {device} failed")
+
+    @property
+    def ptr(self) -> int:
+        return self._p.value
+
+    def upload(self, a: np.ndarray):
+        a = np.ascontiguousarray(a)
+        if a.nbytes > self.nbytes:
+            raise ValueError(f"{a.nbytes} bytes do not fit a {self.nbytes}-byte buffer")
+        if self._hip.hipMemcpy(self._p, a.ctypes.data_as(C.c_void_p), C.c_size_t(a.nbytes), 1) != 0:  # H2D
+            raise MitokError(2, "hipMemcpy to the device failed")
+
+    def download(self, shape, dtype) -> np.ndarray:
+        out = np.empty(shape, dtype)
+        if out.nbytes > self.nbytes:
+            raise ValueError(f"{out.nbytes} bytes exceed a {self.nbytes}-byte buffer")
+        if self._hip.hipMemcpy(out.ctypes.data_as(C.c_void_p), self._p, C.c_size_t(out.nbytes), 2) != 0:  # D2H
+            raise MitokError(2, "hipMemcpy from the device failed")
+        return out
+
+    def free(self):
+        if self._p.value:
+            self._hip.hipFree(self._p)
+            self._p = C.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.free()
 
 
 def _c128(a, n=None, what="tensor"):
@@ -274,6 +325,26 @@ class Network:
         _check(self._lib.mitok_forward_layers(self._h, first, last, _ptr(x), _ptr(m), B, S, _ptr(ts),
                                               int(forward_only), _ptr(out)))
         return out
+
+    def forward_layers_device(self, first, last, d_in, B, S, d_out, mask=None, time_steps=None, forward_only=True):
+        """forward_layers on device memory: `d_in` holds [B][S][d_in] complex,
+        `d_out` receives [B][S'][d_out] (DeviceBuffer or a device address).
+        The mask and time steps stay host arrays.  Returns S'."""
+        m = None
+        if mask is not None:
+            m = np.ascontiguousarray(mask, dtype=np.uint32)
+            if m.shape != (B, S):
+                raise ValueError(f"padding mask: shape {m.shape}, expected ({B}, {S})")
+        ts = None if time_steps is None else _u32_vec(time_steps, B, "time_steps")
+        prompt_pass = not forward_only or ts is None or ts[0] == 0
+        _check(self._lib.mitok_forward_layers_device(self._h, first, last, _dev(d_in), _ptr(m), B, S, _ptr(ts),
+                                                     int(forward_only), _dev(d_out)))
+        return self.seq_out_len(S, first, last) if prompt_pass else S
+
+    def greedy_decoding_device(self, d_logits, rows, vocab, d_ids):
+        """greedy_decoding of [rows][vocab] f64 logits in device memory into
+        [rows] u32 ids in device memory."""
+        _check(self._lib.mitok_greedy_decoding_device(self._h, _dev(d_logits), rows, vocab, _dev(d_ids)))
 
     def generate(self, prompt, lens=None, n_new=1, want_logits=False):
         prompt = np.ascontiguousarray(prompt, dtype=np.uint32)

@@ -2052,8 +2052,31 @@ int mitok_predict(mitok_network* n, const uint32_t* ids, const uint32_t* lens, u
   return OK;
 }
 
-int mitok_forward_layers(mitok_network* n, uint32_t first, uint32_t last, const double* in, const uint32_t* mask_in,
-                         uint32_t B, uint32_t S, const uint32_t* time_steps, int forward_only, double* out) {
+// `bytes` of device memory at `p` inside one allocation of the network's
+// device: the check that turns a caller's wrong device pointer into an error
+// instead of a memory fault.
+static int check_device_range(const Net* n, const void* p, size_t bytes, const char* what) {
+  hipPointerAttribute_t at;
+  if (hipPointerGetAttributes(&at, p) != hipSuccess || at.type != hipMemoryTypeDevice) {
+    (void)hipGetLastError();
+    return fail(ERR_ARG, "%s is not device memory", what);
+  }
+  if (at.device != n->device) return fail(ERR_ARG, "%s is on device %d, the network on %d", what, at.device, n->device);
+  void* base = nullptr;
+  size_t size = 0;
+  if (hipMemGetAddressRange(&base, &size, const_cast<void*>(p)) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(ERR_ARG, "%s: no device allocation holds it", what);
+  }
+  const size_t off = (size_t)((const char*)p - (const char*)base);
+  if (off > size || bytes > size - off)
+    return fail(ERR_ARG, "%s: %zu bytes from offset %zu exceed its allocation of %zu", what, bytes, off, size);
+  return OK;
+}
+
+static int forward_layers_impl(Net* n, uint32_t first, uint32_t last, const double* in, const uint32_t* mask_in,
+                               uint32_t B, uint32_t S, const uint32_t* time_steps, int forward_only, double* out,
+                               bool on_device) {
   if (!n || !in || !out || first >= last || last > n->layers.size()) return fail(ERR_ARG, "bad layer range");
   if (!B || !S) return fail(ERR_ARG, "empty batch");
   for (uint32_t li = first; li < last; ++li) {
@@ -2067,26 +2090,50 @@ int mitok_forward_layers(mitok_network* n, uint32_t first, uint32_t last, const 
     for (uint32_t s = 0; s < S; ++s) c += (mask_in ? mask_in[(size_t)b * S + s] : 1) ? 1 : 0;
     lens[b] = c ? c : 1;
   }
+  const uint32_t din = n->layers[first]->d_in, dout = n->layers[last - 1]->d_out;
+  const size_t rows = (size_t)B * S;
+  if (on_device) {
+    uint32_t so = 0;
+    TRY(mitok_seq_out_len(n, first, last, S, &so));
+    TRY(check_device_range(n, in, rows * din * sizeof(double2), "in"));
+    TRY(check_device_range(n, out, (size_t)B * so * dout * sizeof(double2), "out"));
+  }
   Spec sp;
   sp.first = first;
   sp.last = last;
   std::vector<uint32_t> mask_h;
   TRY(begin_call(n, lens.data(), B, S, time_steps, forward_only != 0, mask_in, sp, mask_h));
-  const size_t rows = (size_t)B * S, orows = (size_t)B * n->wS;
-  const uint32_t din = n->layers[first]->d_in, dout = n->layers[last - 1]->d_out;
+  const size_t orows = (size_t)B * n->wS;
   DevBuf xin, xout;
-  TRY(xin.reserve(rows * din * sizeof(double2)));
-  TRY(xout.reserve(orows * dout * sizeof(double2)));
-  HIP_TRY(hipMemcpyAsync(xin.p, in, rows * din * sizeof(double2), hipMemcpyHostToDevice, n->stream));
-  sp.in = xin.as<double2>();
-  sp.out_hidden = xout.as<double2>();
+  if (on_device) {
+    sp.in = (const double2*)in;
+    sp.out_hidden = (double2*)out;
+  } else {
+    TRY(xin.reserve(rows * din * sizeof(double2)));
+    TRY(xout.reserve(orows * dout * sizeof(double2)));
+    HIP_TRY(hipMemcpyAsync(xin.p, in, rows * din * sizeof(double2), hipMemcpyHostToDevice, n->stream));
+    sp.in = xin.as<double2>();
+    sp.out_hidden = xout.as<double2>();
+  }
   TRY(enqueue_forward(n, sp));
-  HIP_TRY(hipMemcpyAsync(out, xout.p, orows * dout * sizeof(double2), hipMemcpyDeviceToHost, n->stream));
+  if (!on_device)
+    HIP_TRY(hipMemcpyAsync(out, xout.p, orows * dout * sizeof(double2), hipMemcpyDeviceToHost, n->stream));
   HIP_TRY(hipStreamSynchronize(n->stream));
   collect_timing(n);
   TRY(check_err_word(n));
   end_call(n, sp, lens.data());
   return OK;
+}
+
+int mitok_forward_layers(mitok_network* n, uint32_t first, uint32_t last, const double* in, const uint32_t* mask_in,
+                         uint32_t B, uint32_t S, const uint32_t* time_steps, int forward_only, double* out) {
+  return forward_layers_impl(n, first, last, in, mask_in, B, S, time_steps, forward_only, out, false);
+}
+
+int mitok_forward_layers_device(mitok_network* n, uint32_t first, uint32_t last, const double* d_in,
+                                const uint32_t* mask_in, uint32_t B, uint32_t S, const uint32_t* time_steps,
+                                int forward_only, double* d_out) {
+  return forward_layers_impl(n, first, last, d_in, mask_in, B, S, time_steps, forward_only, d_out, true);
 }
 
 // One decode step for every sequence: embed the previous greedy ids, run the
@@ -2421,6 +2468,17 @@ int mitok_greedy_decoding(mitok_network* n, const double* logits, uint32_t rows,
   HIP_TRY(hipMemcpyAsync(lg.p, logits, (size_t)rows * V * sizeof(double), hipMemcpyHostToDevice, n->stream));
   argmax_rows(n->stream, lg.as<double>(), rows, V, ids.as<uint32_t>(), n->err_d.as<uint32_t>());
   HIP_TRY(hipMemcpyAsync(out_ids, ids.p, rows * sizeof(uint32_t), hipMemcpyDeviceToHost, n->stream));
+  HIP_TRY(hipStreamSynchronize(n->stream));
+  return check_err_word(n);
+}
+
+int mitok_greedy_decoding_device(mitok_network* n, const double* d_logits, uint32_t rows, uint32_t V,
+                                 uint32_t* d_out_ids) {
+  if (!n || !d_logits || !d_out_ids || !rows || !V) return fail(ERR_ARG, "bad arguments");
+  TRY(set_device(n));
+  TRY(check_device_range(n, d_logits, (size_t)rows * V * sizeof(double), "logits"));
+  TRY(check_device_range(n, d_out_ids, (size_t)rows * sizeof(uint32_t), "out_ids"));
+  argmax_rows(n->stream, d_logits, rows, V, d_out_ids, n->err_d.as<uint32_t>());
   HIP_TRY(hipStreamSynchronize(n->stream));
   return check_err_word(n);
 }

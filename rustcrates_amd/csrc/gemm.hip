@@ -596,6 +596,65 @@ __global__ __launch_bounds__(1024) void k_zgemm_rows16(const double2* __restrict
   }
 }
 
+// The same product for the planned shape of 8 k-steps (32 of K) per wave,
+// as straight-line code: the loads of all four 8-k batches go out first, an
+// out-of-range operand lane reading a zero constant instead (no branch), so
+// the compiler waits for each batch's own loads (in-order vmcnt) and the
+// first batch's MFMAs run while the later batches are still in flight.  In
+// k_zgemm_rows16 the guarded loads are branches, and the loop waits for every
+// load before its first MFMA.  The MFMA sequence on each accumulator (k-steps
+// in ascending order) is the same as there, so the results are identical.
+__device__ const double2 rows16s_zero = {0.0, 0.0};  // what an out-of-range operand lane reads
+
+__global__ __launch_bounds__(1024) void k_zgemm_rows16s(const double2* __restrict__ X, long ldx, int M,
+                                                      const double2* __restrict__ W, long ldw, int N, int K, Epi ep) {
+  constexpr int NB = 4, U = 2, NW = ROWS16_WAVES, LD = 16;  // 4 batches x 2 k-steps of 4 = 32 of K per wave
+  extern __shared__ double2 red16[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int i = lane & 15, kq = lane >> 4;
+  const int n = blockIdx.x * 16 + i, m = blockIdx.y * 16 + i;
+  const int ka = (blockIdx.z * NW + wave) * 32;
+  const long nc = min(n, N - 1), mc = min(m, M - 1);
+  const bool nok = n < N, mok = m < M;
+  double2 a[NB][U], b[NB][U];
+#pragma unroll
+  for (int s = 0; s < NB; ++s)
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      // the address, not the value, is selected: every lane loads, so no
+      // load sits under a branch
+      const int kk = ka + 8 * s + 4 * u + kq;
+      const long kc = min(kk, K - 1);
+      const bool ok = kk < K;
+      b[s][u] = ld_glb((ok && nok) ? W + kc * ldw + nc : &rows16s_zero);
+      a[s][u] = ld_glb((ok && mok) ? X + mc * ldx + kc : &rows16s_zero);
+    }
+  v4d cr = {0.0, 0.0, 0.0, 0.0}, ci = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+  for (int s = 0; s < NB; ++s)
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      cr = __builtin_amdgcn_mfma_f64_16x16x4f64(a[s][u].x, b[s][u].x, cr, 0, 0, 0);
+      ci = __builtin_amdgcn_mfma_f64_16x16x4f64(a[s][u].x, b[s][u].y, ci, 0, 0, 0);
+      cr = __builtin_amdgcn_mfma_f64_16x16x4f64(-a[s][u].y, b[s][u].y, cr, 0, 0, 0);
+      ci = __builtin_amdgcn_mfma_f64_16x16x4f64(a[s][u].y, b[s][u].x, ci, 0, 0, 0);
+    }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) red16[(wave * 16 + 4 * e + kq) * LD + i] = make_double2(cr[e], ci[e]);
+  __syncthreads();
+  if (tid < 256) {
+    const int row = tid >> 4, col = tid & 15;
+    double2 v = red16[row * LD + col];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) v = cadd(v, red16[(w * 16 + row) * LD + col]);
+    const int nn = blockIdx.x * 16 + col, mm = blockIdx.y * 16 + row;
+    if (mm < M && nn < N) {
+      if (ep.mode == EPI_PART) ep.out[((long)blockIdx.z * M + mm) * N + nn] = v;
+      else apply_epi(ep, M, N, mm, nn, v);
+    }
+  }
+}
+
 // ===========================================================================
 // Wide skinny variant (vocab-wide outputs): a block owns all M rows (RT
 // tiles of 16) and 16*CW columns; its 4 waves are CW column groups x (4/CW) K
@@ -1025,7 +1084,8 @@ static void launch_skinny(hipStream_t st, const SkinnyPlan& p, const RowOps& ro,
   if (p.rows) {  // EPI_PART, or one K range per block (no argmax: not a vocab-wide output)
     const dim3 g3(p.ncb, p.rt, p.P);
     if (p.w16) {
-      MITOK_LAUNCH(k_zgemm_rows16, g3, dim3(64 * ROWS16_WAVES), ROWS16_LDS, st, ro.x, ro.ldx, M, W, ldw, N, K, p.nkw, ep);
+      if (p.nkw == 8) MITOK_LAUNCH(k_zgemm_rows16s, g3, dim3(64 * ROWS16_WAVES), ROWS16_LDS, st, ro.x, ro.ldx, M, W, ldw, N, K, ep);
+      else MITOK_LAUNCH(k_zgemm_rows16, g3, dim3(64 * ROWS16_WAVES), ROWS16_LDS, st, ro.x, ro.ldx, M, W, ldw, N, K, p.nkw, ep);
       return;
     }
     if (p.ct == 2) MITOK_LAUNCH(k_zgemm_skinny_rows<2>, g3, blk, 0, st, ro.x, ro.ldx, M, W, ldw, N, K, p.nkw, ep);

@@ -467,6 +467,8 @@ static double gemm_bytes(long M, long N, long K, bool re_out) {
 }
 // real flops of a complex product: 4 multiplies + 4 adds per complex MAC
 static double gemm_flops(long M, long N, long K) { return 8.0 * (double)M * N * K; }
+// of its real part alone (Re-logits): Re(a b) = ar br - ai bi, 2 + 2 per MAC
+static double gemm_flops_re(long M, long N, long K) { return 4.0 * (double)M * N * K; }
 
 // algorithmic HBM bytes of one decode attention launch of a layer (width d,
 // H heads): per key of every sequence its K and V rows (16 B per element) and
@@ -788,7 +790,7 @@ static int enqueue_forward(Net* n, const Spec& sp) {
           e.out_re = sp.out_re;
           e.hist_re = sp.hist_re;
           e.hist_cnt = sp.hist_cnt;
-          TimeScope ts(n, MITOK_TIME_VOCAB, gemm_bytes(M, Ln->d_out, Ln->d_in, true), gemm_flops(M, Ln->d_out, Ln->d_in));
+          TimeScope ts(n, MITOK_TIME_VOCAB, gemm_bytes(M, Ln->d_out, Ln->d_in, true), gemm_flops_re(M, Ln->d_out, Ln->d_in));
           TRY(launch_rc(gemm(st, M, Ln->d_out, Ln->d_in, rows_of(x, Ln->d_in), Ln->w.as<double2>(), Ln->d_out, e,
                              sp.am, sy), "vocab"));
         } else {
@@ -1069,7 +1071,7 @@ static int enqueue_decode_fused(Net* n, const Spec& sp) {
           e.out_re = sp.out_re;
           e.hist_re = sp.hist_re;
           e.hist_cnt = sp.hist_cnt;
-          TimeScope ts(n, MITOK_TIME_VOCAB, gemm_bytes(B, Ln->d_out, Ln->d_in, true), gemm_flops(B, Ln->d_out, Ln->d_in));
+          TimeScope ts(n, MITOK_TIME_VOCAB, gemm_bytes(B, Ln->d_out, Ln->d_in, true), gemm_flops_re(B, Ln->d_out, Ln->d_in));
           TRY(launch_rc(gemm(st, B, Ln->d_out, Ln->d_in, pro, Ln->w.as<double2>(), Ln->d_out, e, sp.am, sy), "vocab"));
         } else {
           double2* out = parts[part_next];

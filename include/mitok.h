@@ -163,6 +163,22 @@ int mitok_prefill(mitok_network* net, const uint32_t* prompt, const uint32_t* le
                   uint32_t* out_ids, double* out_logits);
 int mitok_decode_step(mitok_network* net, const uint32_t* ids, uint32_t batch, uint32_t* out_ids, double* out_logits);
 
+/* The output head's training step: backward (transformer_network.rs:506-636)
+ * through the Softmax and the vocab Linear of the last stateless predict
+ * (forward_only = 0; any other call in between is MITOK_ERR_STATE).
+ * SoftmaxLayer::backward (softmax_output_layer.rs:67-145): targets [batch][T],
+ * tlens[b] of them used; the cross-entropy gradient of the softmax output
+ * rows that predict them.  LinearLayer::backward (linear_layer.rs:77-128):
+ * dW = conj(X)^T G, db = column sums, and out_grad_input [batch][seq'][d_in]
+ * (complex) = G conj(W)^T, or NULL.  update_params: LinearLayer::
+ * update_parameters (linear_layer.rs:130-175) at learning_rate: the layer's
+ * first update descends by the clipped gradient / batch, later ones run
+ * AdamW (utils/adam_w.rs:9-103) at time_step.  The weights stay on the
+ * device (mitok_get_tensor reads them).  The layers below the vocab Linear
+ * are not differentiated. */
+int mitok_backward_head(mitok_network* net, const uint32_t* targets, const uint32_t* tlens, uint32_t batch, uint32_t T,
+                        int update_params, double learning_rate, uint32_t time_step, double* out_grad_input);
+
 /* greedy_decoding (src/utils/sampling_methods.rs:5-18) on the device for host
  * logits [rows][vocab]: last index among equal maxima; NaN -> MITOK_ERR_NAN. */
 int mitok_greedy_decoding(mitok_network* net, const double* logits, uint32_t rows, uint32_t vocab, uint32_t* out_ids);

@@ -77,6 +77,9 @@ def _load():
         "orc_predict": (i32, [P, P, P, u32, u32, P, i32, i32, P, P]),
         "orc_forward_layers": (i32, [P, u32, u32, P, P, u32, u32, P, i32, P]),
         "orc_generate": (i32, [P, P, P, u32, u32, u32, P, P]),
+        "orc_softmax_backward": (i32, [P, u32, u32, u32, P, P, u32, P]),
+        "orc_linear_backward": (i32, [P, P, P, u32, u32, u32, u32, P, P, P]),
+        "orc_linear_update": (i32, [P, P, u32, u32, P, P, u32, P, P, P, P, i32, f64, u32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -159,6 +162,46 @@ def dwt_1d(x, wavelet: int, mode: int) -> np.ndarray:
     n = C.c_uint32(0)
     _check(lib().orc_dwt_1d(_ptr(x), x.shape[0], wavelet, mode, _ptr(out), C.byref(n)))
     return out[:n.value].copy()
+
+
+def softmax_backward(P, targets, tlens=None) -> np.ndarray:
+    """SoftmaxLayer::backward (softmax_output_layer.rs:67-145): the
+    cross-entropy gradient [B][S][V] of the TRAINING softmax output P."""
+    P = np.ascontiguousarray(P, dtype=np.float64)
+    B, S, V = P.shape
+    t = np.ascontiguousarray(targets, dtype=np.uint32)
+    T = t.shape[1]
+    tl = np.full(B, T, np.uint32) if tlens is None else np.ascontiguousarray(tlens, dtype=np.uint32)
+    G = np.empty_like(P)
+    _check(lib().orc_softmax_backward(_ptr(P), B, S, V, _ptr(t), _ptr(tl), T, _ptr(G)))
+    return G
+
+
+def linear_backward(X, G, W):
+    """LinearLayer::backward (linear_layer.rs:77-128), grouped over the batch:
+    (dW [d][V], db [V], dX [B][S][d])."""
+    X, W = _c128(X), _c128(W)
+    G = np.ascontiguousarray(G, dtype=np.float64)
+    B, S, d = X.shape
+    V = W.shape[1]
+    dW = np.empty((d, V), np.complex128)
+    db = np.empty(V, np.complex128)
+    dX = np.empty((B, S, d), np.complex128)
+    _check(lib().orc_linear_backward(_ptr(X), _ptr(G), _ptr(W), B, S, d, V, _ptr(dW), _ptr(db), _ptr(dX)))
+    return dW, db, dX
+
+
+def linear_update(W, b, dW, db, batch, state, first, lr, time_step):
+    """LinearLayer::update_parameters (linear_layer.rs:130-175): returns the
+    new (W, b); `state` = [mW, vW, mb, vb] is updated in place."""
+    W, b = _c128(W).copy(), _c128(b).copy()
+    dW, db = _c128(dW), _c128(db)
+    d, V = W.shape
+    for a in state:
+        assert a.dtype == np.complex128 and a.flags.c_contiguous
+    _check(lib().orc_linear_update(_ptr(W), _ptr(b), d, V, _ptr(dW), _ptr(db), batch, *[_ptr(a) for a in state],
+                                   int(first), float(lr), int(time_step)))
+    return W, b
 
 
 def zgemm(A: np.ndarray, B: np.ndarray) -> np.ndarray:

@@ -1243,3 +1243,141 @@ int orc_generate(orc_net* net, const uint32_t* prompt, const uint32_t* lens, uin
   free(ts);
   return rc;
 }
+
+/* ======================================================================
+ * The output head's training step: SoftmaxLayer::backward, LinearLayer::
+ * backward and LinearLayer::update_parameters with the AdamW of
+ * utils/adam_w.rs.  Parity anchors: the closed forms in
+ * tests/test_oracle_pins.py (cross-entropy gradient rows summing to zero and
+ * matching finite differences of the loss, the first AdamW step, the clipped
+ * descent step, dW against an explicit sum of outer products).
+ * ====================================================================== */
+
+int orc_softmax_backward(const double* P, uint32_t B, uint32_t S, uint32_t V, const uint32_t* targets,
+                         const uint32_t* tlens, uint32_t T, double* G) {
+  if (!P || !targets || !tlens || !G || !B || !S || !V) return fail(ORC_ERR_ARG, "bad arguments");
+  memset(G, 0, (size_t)B * S * V * sizeof(double));
+  for (uint32_t b = 0; b < B; ++b) {
+    const uint32_t tl = tlens[b];
+    if (tl > T) return fail(ORC_ERR_ARG, "target length %u > %u", tl, T);
+    /* seq_ind_start = len - target_len - 1 in usize (softmax_output_layer.rs:95-96) */
+    if ((uint64_t)tl + 1 > S) return fail(ORC_ERR_ARG, "sequence %u: %u targets need more than %u rows", b, tl, S);
+    const uint32_t start = S - tl - 1, end = S - 1;
+    double unpadded = 0.0; /* targets that are not PAD (:98-103) */
+    for (uint32_t t = 0; t < tl; ++t)
+      if (targets[(size_t)b * T + t] != 1) unpadded += 1.0;
+    const double normalizer = (double)B * unpadded;
+    for (uint32_t t = 0; t < tl; ++t) {
+      const uint32_t tc = targets[(size_t)b * T + t];
+      if (tc >= V) return fail(ORC_ERR_ARG, "target token %u exceeds vocabulary %u", tc, V); /* :108-110 */
+      if (tc == 1) continue;                                                                  /* :112-114 */
+      const uint32_t s = start + t;
+      if (s >= end) break; /* :118-120 */
+      const double* p = P + ((size_t)b * S + s) * V;
+      double* g = G + ((size_t)b * S + s) * V;
+      for (uint32_t c = 0; c < V; ++c) g[c] += (c == tc ? p[c] - 1.0 : p[c]) / normalizer;
+    }
+  }
+  return ORC_OK;
+}
+
+int orc_linear_backward(const oc64* X, const double* G, const oc64* W, uint32_t B, uint32_t S, uint32_t d,
+                        uint32_t V, oc64* dW, oc64* db, oc64* dX) {
+  if (!X || !G || !W || !dW || !db || !dX || !B || !S || !d || !V) return fail(ORC_ERR_ARG, "bad arguments");
+  oc64* xh = (oc64*)malloc((size_t)d * S * sizeof(oc64));   /* conjugate_transpose(input_sample) */
+  oc64* gc = (oc64*)malloc((size_t)S * V * sizeof(oc64));   /* the gradient as Complex (im 0) */
+  oc64* wh = (oc64*)malloc((size_t)V * d * sizeof(oc64));   /* conjugate_transpose(weights) */
+  oc64* wg = (oc64*)malloc((size_t)d * V * sizeof(oc64));   /* one sequence's weight gradient */
+  if (!xh || !gc || !wh || !wg) {
+    free(xh), free(gc), free(wh), free(wg);
+    return fail(ORC_ERR_NOMEM, "linear backward: out of memory");
+  }
+  for (uint32_t k = 0; k < d; ++k)
+    for (uint32_t v = 0; v < V; ++v) {
+      const oc64 w = W[(size_t)k * V + v];
+      wh[(size_t)v * d + k] = (oc64){w.re, -w.im};
+    }
+  memset(dW, 0, (size_t)d * V * sizeof(oc64));
+  memset(db, 0, (size_t)V * sizeof(oc64));
+  for (uint32_t b = 0; b < B; ++b) {
+    const oc64* xb = X + (size_t)b * S * d;
+    for (uint32_t s = 0; s < S; ++s)
+      for (uint32_t k = 0; k < d; ++k) {
+        const oc64 x = xb[(size_t)s * d + k];
+        xh[(size_t)k * S + s] = (oc64){x.re, -x.im};
+      }
+    for (size_t i = 0; i < (size_t)S * V; ++i) gc[i] = (oc64){G[(size_t)b * S * V + i], 0.0};
+    orc_zgemm(d, V, S, xh, gc, wg);                                 /* linear_layer.rs:99 */
+    for (size_t i = 0; i < (size_t)d * V; ++i) dW[i] = c_add(dW[i], wg[i]); /* group_gradient_batch */
+    oc64 bsum; /* bias gradient of this sequence (:101-105), then grouped */
+    for (uint32_t v = 0; v < V; ++v) {
+      bsum = (oc64){0.0, 0.0};
+      for (uint32_t s = 0; s < S; ++s) bsum = c_add(bsum, gc[(size_t)s * V + v]);
+      db[v] = c_add(db[v], bsum);
+    }
+    orc_zgemm(S, d, V, gc, wh, dX + (size_t)b * S * d);           /* :107 */
+  }
+  free(xh), free(gc), free(wh), free(wg);
+  return ORC_OK;
+}
+
+/* f64::powi as compiler-rt's __powidf2: square-and-multiply over the bits */
+static double powi_f64(double a, int e) {
+  const int recip = e < 0;
+  double r = 1.0;
+  for (;;) {
+    if (e & 1) r *= a;
+    e /= 2;
+    if (e == 0) break;
+    a *= a;
+  }
+  return recip ? 1.0 / r : r;
+}
+
+/* clip_gradient_1d on one value (utils/matrix.rs:709-717) */
+static oc64 clip1(oc64 g, double threshold) {
+  const double n = hypot(g.re, g.im);
+  return n > threshold ? c_scale(g, threshold / n) : g;
+}
+
+static int finite_c(oc64 z) { return isfinite(z.re) && isfinite(z.im); }
+
+/* calculate_adam_w / calculate_adam_w_bias on one element (adam_w.rs:9-103);
+ * weights take v_hat's norm at least EPSILON, the bias does not */
+static oc64 adamw1(oc64 w, oc64 g, oc64* m, oc64* v, double lr, uint32_t ts, int weight) {
+  const double B1 = 0.9, B2 = 0.999, EPS = 1e-8, WD = 0.01, MAX_NORM = 1.0;
+  const int t = ts > 0 ? (int)ts : 1;
+  const double gn = hypot(g.re, g.im);
+  if (gn > MAX_NORM) g = c_scale(g, MAX_NORM / gn);
+  *m = c_add(c_scale(*m, B1), c_scale(g, 1.0 - B1));
+  *v = c_add(c_scale(*v, B2), c_mul(c_scale(g, 1.0 - B2), (oc64){g.re, -g.im}));
+  const oc64 mh = c_unscale(*m, 1.0 - powi_f64(B1, t));
+  const oc64 vh = c_unscale(*v, 1.0 - powi_f64(B2, t));
+  double vn = hypot(vh.re, vh.im);
+  if (weight) vn = fmax(vn, EPS);
+  const double alr = lr / (sqrt(vn) + EPS);
+  const oc64 decayed = c_scale(w, 1.0 - lr * WD);
+  return c_sub(decayed, c_mul((oc64){alr, 0.0}, mh));
+}
+
+int orc_linear_update(oc64* W, oc64* b, uint32_t d, uint32_t V, const oc64* dW, const oc64* db, uint32_t batch,
+                      oc64* mW, oc64* vW, oc64* mb, oc64* vb, int first, double lr, uint32_t time_step) {
+  if (!W || !b || !dW || !db || !mW || !vW || !mb || !vb || !d || !V || !batch) return fail(ORC_ERR_ARG, "bad arguments");
+  const size_t n = (size_t)d * V;
+  const double bs = (double)batch;
+  if (first) { /* linear_layer.rs:159-174: the clipped copies, gradient descent */
+    for (size_t i = 0; i < n; ++i) {
+      const oc64 g = clip1(dW[i], 1.0);
+      if (finite_c(g)) W[i] = c_sub(W[i], c_scale(c_unscale(g, bs), lr));
+    }
+    for (uint32_t j = 0; j < V; ++j) {
+      const oc64 g = clip1(db[j], 1.0);
+      if (finite_c(g)) b[j] = c_sub(b[j], c_scale(c_unscale(g, bs), lr));
+    }
+    return ORC_OK;
+  }
+  /* :150-158: AdamW on the grouped (unclipped) gradients */
+  for (size_t i = 0; i < n; ++i) W[i] = adamw1(W[i], dW[i], &mW[i], &vW[i], lr, time_step, 1);
+  for (uint32_t j = 0; j < V; ++j) b[j] = adamw1(b[j], db[j], &mb[j], &vb[j], lr, time_step, 0);
+  return ORC_OK;
+}

@@ -122,6 +122,28 @@ int orc_forward_layers(orc_net* net, uint32_t first, uint32_t last, const oc64* 
 int orc_generate(orc_net* net, const uint32_t* prompt, const uint32_t* lens, uint32_t B, uint32_t S,
                  uint32_t n_new, uint32_t* out_ids, double* out_logits);
 
+/* ---- the output head's training step (transformer_network.rs:506-636 for
+ * the Softmax and the vocab Linear) ---- */
+/* SoftmaxLayer::backward (softmax_output_layer.rs:67-145): P [B][S][V] the
+ * TRAINING softmax output, targets [B][T] (tlens[b] of them used); G [B][S][V]
+ * (real; the reference stores it as Complex with im 0). */
+int orc_softmax_backward(const double* P, uint32_t B, uint32_t S, uint32_t V, const uint32_t* targets,
+                         const uint32_t* tlens, uint32_t T, double* G);
+/* LinearLayer::backward (linear_layer.rs:77-128), complex arm, grouped over
+ * the batch (gradient_struct.rs:360-436): X [B][S][d] the layer's input,
+ * G [B][S][V], W [d][V]; dW [d][V] = sum_b conj(X_b)^T G_b, db [V] =
+ * sum_b sum_s G_b[s], dX [B][S][d] = G_b conj(W)^T. */
+int orc_linear_backward(const oc64* X, const double* G, const oc64* W, uint32_t B, uint32_t S, uint32_t d,
+                        uint32_t V, oc64* dW, oc64* db, oc64* dX);
+/* LinearLayer::update_parameters (linear_layer.rs:130-175) for `batch`
+ * sequences: first != 0 is the first update (no previous gradient): each
+ * element's clipped gradient (clip_gradients, utils/matrix.rs:703-717), if
+ * finite, descends by lr * g / batch.  Otherwise AdamW (utils/adam_w.rs:9-103)
+ * from the moments mW, vW, mb, vb at time_step.  The moments are updated in
+ * place. */
+int orc_linear_update(oc64* W, oc64* b, uint32_t d, uint32_t V, const oc64* dW, const oc64* db, uint32_t batch,
+                      oc64* mW, oc64* vW, oc64* mb, oc64* vb, int first, double lr, uint32_t time_step);
+
 #ifdef __cplusplus
 }
 #endif

@@ -58,6 +58,7 @@ SIGNATURES = {
     "mitok_prefill": (_i32, [_P, _P, _P, _u32, _u32, _P, _P]),
     "mitok_decode_step": (_i32, [_P, _P, _u32, _P, _P]),
     "mitok_greedy_decoding": (_i32, [_P, _P, _u32, _u32, _P]),
+    "mitok_backward_head": (_i32, [_P, _P, _P, _u32, _u32, _i32, C.c_double, _u32, _P]),
     "mitok_greedy_decoding_device": (_i32, [_P, _P, _u32, _u32, _P]),
     "mitok_forward_layers_device": (_i32, [_P, _u32, _u32, _P, _P, _u32, _u32, _P, _i32, _P]),
     "mitok_greedy_decoding_noalloc": (_i32, [_P, _P, _u32, _u32, _P]),
@@ -261,6 +262,7 @@ class Network:
 
     def add_linear(self, d_in, d_out, w=None, b=None):
         self.vocab = d_out
+        self._head_in = d_in
         _check(self._lib.mitok_add_linear(self._h, d_in, d_out, _ptr(_c128(w, d_in * d_out, "w")),
                                           _ptr(_c128(b, d_out, "b"))))
 
@@ -304,8 +306,11 @@ class Network:
         So = self.seq_out_len(S) if prompt_pass else S
         out = np.empty((B, V) if last_row_only else (B, So, V), np.float64)
         mask = np.empty((B, So), np.uint32)
+        self._head_rows = None
         _check(self._lib.mitok_predict(self._h, _ptr(ids), _ptr(lens), B, S, _ptr(ts), int(forward_only),
                                        int(last_row_only), _ptr(out), _ptr(mask)))
+        if not forward_only:
+            self._head_rows = (B, So)  # what backward_head differentiates
         return out, mask
 
     def forward_layers(self, first, last, x, mask=None, time_steps=None, forward_only=True, d_out=None):
@@ -376,6 +381,26 @@ class Network:
         logits = np.empty((B, self.vocab), np.float64) if want_logits else None
         _check(self._lib.mitok_decode_step(self._h, _ptr(fed), B, _ptr(out), _ptr(logits)))
         return (out, logits) if want_logits else out
+
+    def backward_head(self, targets, tlens=None, update=True, learning_rate=0.001, time_step=1, want_grad_input=True):
+        """backward through the Softmax and the vocab Linear of the last
+        stateless predict (transformer_network.rs:506-636 for those two
+        layers); with `update`, the Linear's update_parameters.  Returns the
+        gradient with respect to the Linear's input [B][S'][d_in] (complex)."""
+        t = np.ascontiguousarray(targets, dtype=np.uint32)
+        if t.ndim != 2:
+            raise ValueError(f"targets: shape {t.shape}, expected (batch, T)")
+        B, T = t.shape
+        tl = np.full(B, T, np.uint32) if tlens is None else _u32_vec(tlens, B, "tlens")
+        gx = None
+        if want_grad_input:
+            rows = getattr(self, "_head_rows", None)
+            if rows is None or rows[0] != B:
+                raise MitokError(3, "no stateless predict of this batch to differentiate")
+            gx = np.empty((B, rows[1], self._head_in), np.complex128)
+        _check(self._lib.mitok_backward_head(self._h, _ptr(t), _ptr(tl), B, T, int(bool(update)), float(learning_rate),
+                                             int(time_step), _ptr(gx)))
+        return gx
 
     def greedy_decoding(self, logits):
         logits = np.ascontiguousarray(logits, dtype=np.float64)

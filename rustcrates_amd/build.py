@@ -18,7 +18,7 @@ SRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libmitok.so")
 SOURCES = ["kernels.hip", "gemm.hip", "gemm_mfma.hip", "attention.hip", "resident.hip", "resident_k1.hip", "resident_k2.hip",
-           "resident_k4.hip", "resident_k8.hip", "network.hip"]
+           "resident_k4.hip", "resident_k8.hip", "train.hip", "network.hip"]
 ARCH = os.environ.get("MITOK_ARCH", "gfx950")
 
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
@@ -32,7 +32,9 @@ CFLAGS = [
 
 # per-file flags: the prompt-pass GEMM keeps its MFMA accumulators in VGPRs
 # (the reason is in gemm_mfma.hip's header)
-FILE_FLAGS = {"gemm_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+FILE_FLAGS = {"gemm_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+              # the optimizer's arithmetic rounds every multiply and add, as Rust does
+              "train.hip": ["-ffp-contract=off"]}
 
 
 def source_hash() -> str:

@@ -125,6 +125,24 @@ constexpr int GEMM_PART_MAX_M = 64;
 // The prologue alone: out[m][k] = rowops(x)[m][k]  (materialises a pending row transform)
 void rowops_apply(hipStream_t st, int M, int K, const RowOps& ro, double2* out, long ldo);
 
+// ---- the output head's training step (train.hip) ----
+struct TrainStep {
+  int first = 0;      // the first update: clipped gradient descent (linear_layer.rs:159-174)
+  double lr = 0.0;    // the layer's learning rate
+  double batch = 1;   // sequences in the batch (the descent divides by it)
+  int time_step = 0;  // AdamW's bias-correction step (at least 1)
+};
+// G[r][c] (complex, im 0) = tgt[r] < 0 ? 0 : (P[r][c] - [c == tgt[r]]) / norm[r / S]
+void softmax_grad(hipStream_t st, const double* P, int rows, int V, const int* tgt, const double* norm, int S,
+                  double2* G);
+// out [C][R] = conj(in)^T for in [R][C]
+void conj_transpose(hipStream_t st, const double2* in, long R, long C, double2* out);
+// db [V] = sum_b sum_s G[b][s][:] (per-sequence sums in row order, then in sequence order)
+void bias_grad(hipStream_t st, const double2* G, int B, int S, int V, double2* db);
+// W [n], b [V] updated in place from dW, db (moments mW, vW, mb, vb)
+void linear_update(hipStream_t st, double2* W, const double2* dW, double2* mW, double2* vW, long n, double2* b,
+                   const double2* db, double2* mb, double2* vb, int V, const TrainStep& ts);
+
 // ---- attention ----
 struct Attn {
   const double2* q = nullptr;  // [B*S][ldq]; head h at column h*dh

@@ -142,6 +142,11 @@ struct FeedForwardLayer : Layer {  // feedforward_layer.rs:14-26, layer.rs:91-11
 
 struct LinearLayer : Layer {  // linear_layer.rs:18-34
   DevBuf w, b;
+  // training state (linear_layer.rs:130-175): AdamW moments of the weights and
+  // the bias, allocated and zeroed at the first update; updates so far (the
+  // first one is plain clipped descent, as when previous_gradient is None)
+  DevBuf mw, vw, mb, vb;
+  uint32_t updates = 0;
   LinearLayer() : Layer(K_LINEAR) {}
 };
 
@@ -345,6 +350,13 @@ struct mitok_network {
   // length minus its cached rows (positions count the uncompressed prompt)
   mitok::DevBuf pos_off_d;
   bool pos_off = false;
+  // the last stateless pass's vocab Linear input rows [head_B * head_S][d]
+  // (in act0/act1) and its softmax output (probs), which mitok_backward_head
+  // differentiates; any later call clears head_valid
+  bool head_valid = false;
+  const double2* head_x = nullptr;
+  uint32_t head_B = 0, head_S = 0;
+  mitok::DevBuf tr_g, tr_xh, tr_wh, tr_dw, tr_db, tr_dx, tr_tgt, tr_norm;
 };
 
 namespace mitok {
@@ -506,6 +518,7 @@ static bool is_vocab_linear(const Net* n, uint32_t li) {
 }
 
 static int prepare(Net* n, const Spec& sp) {
+  n->head_valid = false;  // the workspaces that held the last stateless pass's head input are reused
   const Dims dm = net_dims(n);
   const size_t rows = (size_t)sp.B * sp.S;
   const size_t c16 = sizeof(double2);
@@ -798,6 +811,12 @@ static int enqueue_forward(Net* n, const Spec& sp) {
           e.out = n->logits_c.as<double2>();
           TRY(launch_rc(gemm(st, M, Ln->d_out, Ln->d_in, rows_of(x, Ln->d_in), Ln->w.as<double2>(), Ln->d_out, e,
                              nullptr, sy), "vocab"));
+          if (sp.mode == MODE_STATELESS && !sp.last_row) {  // the layer keeps its input for backward
+            n->head_valid = true;
+            n->head_x = x;
+            n->head_B = (uint32_t)B;
+            n->head_S = (uint32_t)S;
+          }
           auto* SM = (SoftmaxLayer*)n->layers.back().get();
           softmax_rows(st, n->logits_c.as<double2>(), M, S, Ln->d_out, mask, SM->mode == MITOK_TRAINING ? 0 : 1,
                        sp.out_prob);
@@ -1865,6 +1884,7 @@ static int validate_batch(const uint32_t* lens, uint32_t B, uint32_t S) {
 // padding mask [B][S] (forward_layers), or null for lens' prefixes.
 static int begin_call(Net* n, const uint32_t* lens, uint32_t B, uint32_t S, const uint32_t* ts, bool forward_only,
                       const uint32_t* mask_src, Spec& sp, std::vector<uint32_t>& mask_h) {
+  n->head_valid = false;
   sp.B = B;
   sp.S = S;
   sp.forward_only = forward_only;
@@ -2459,6 +2479,99 @@ int mitok_decode_step(mitok_network* n, const uint32_t* ids, uint32_t B, uint32_
   const int rc = decode_step_impl(n, ids, B, out_ids, out_logits);
   if (rc) (void)mitok_reset(n);
   return rc;
+}
+
+int mitok_backward_head(mitok_network* n, const uint32_t* targets, const uint32_t* tlens, uint32_t B, uint32_t T,
+                        int update_params, double learning_rate, uint32_t time_step, double* out_grad_input) {
+  if (!n || !targets || !tlens || !B || !T) return fail(ERR_ARG, "bad arguments");
+  if (!n->head_valid) return fail(ERR_STATE, "no stateless (forward_only = 0) predict to differentiate");
+  if (B != n->head_B) return fail(ERR_ARG, "batch %u != the forward pass's %u", B, n->head_B);
+  const uint32_t li = (uint32_t)n->layers.size() - 2;
+  if (!is_vocab_linear(n, li)) return fail(ERR_STATE, "the stack does not end in Linear, Softmax");
+  auto* Ln = (LinearLayer*)n->layers[li].get();
+  const int S = (int)n->head_S, d = (int)Ln->d_in, V = (int)Ln->d_out;
+  const long rows = (long)B * S;
+  // SoftmaxLayer::backward (softmax_output_layer.rs:67-145): which row predicts
+  // which target, checked in the reference's order (a target id at or past the
+  // vocabulary panics there; PAD targets are skipped; the row before the last
+  // ends the sequence's targets); the normalizer B * non-PAD targets
+  std::vector<int> tgt((size_t)rows, -1);
+  std::vector<double> norm(B, 1.0);
+  for (uint32_t b = 0; b < B; ++b) {
+    const uint32_t tl = tlens[b];
+    if (tl > T) return fail(ERR_ARG, "target length %u > %u", tl, T);
+    if ((uint64_t)tl + 1 > (uint64_t)S) return fail(ERR_ARG, "sequence %u: %u targets need more than %d rows", b, tl, S);
+    double unpadded = 0.0;
+    for (uint32_t t = 0; t < tl; ++t)
+      if (targets[(size_t)b * T + t] != 1u) unpadded += 1.0;
+    norm[b] = (double)B * unpadded;
+    const int start = S - (int)tl - 1;
+    for (uint32_t t = 0; t < tl; ++t) {
+      const uint32_t tc = targets[(size_t)b * T + t];
+      if (tc >= (uint32_t)V) return fail(ERR_ARG, "target token %u exceeds vocabulary %d", tc, V);
+      if (tc == 1u) continue;
+      const int s = start + (int)t;
+      if (s >= S - 1) break;
+      tgt[(size_t)b * S + s] = (int)tc;
+    }
+  }
+  TRY(set_device(n));
+  hipStream_t st = n->stream;
+  const size_t c16 = sizeof(double2);
+  TRY(upload(n, n->tr_tgt, tgt.data(), tgt.size() * sizeof(int)));
+  TRY(upload(n, n->tr_norm, norm.data(), norm.size() * sizeof(double)));
+  TRY(reserve(n, n->tr_g, (size_t)rows * V * c16));
+  TRY(reserve(n, n->tr_xh, (size_t)d * rows * c16));
+  TRY(reserve(n, n->tr_wh, (size_t)V * d * c16));
+  TRY(reserve(n, n->tr_dw, (size_t)d * V * c16));
+  TRY(reserve(n, n->tr_db, (size_t)V * c16));
+  TRY(reserve(n, n->tr_dx, (size_t)rows * d * c16));
+  TRY(reserve(n, n->sync_ws, std::max(gemm_ws_bytes(d, V, (int)rows), gemm_ws_bytes((int)rows, d, V))));
+  const Sync sy = sync_of(n);
+  uint32_t* err = n->err_d.as<uint32_t>();
+  double2* G = n->tr_g.as<double2>();
+  softmax_grad(st, n->probs.as<double>(), (int)rows, V, n->tr_tgt.as<int>(), n->tr_norm.as<double>(), S, G);
+  // LinearLayer::backward, complex arm (linear_layer.rs:96-108) grouped over
+  // the sequences: dW = conj(X)^T G, db = column sums, dX = G conj(W)^T
+  conj_transpose(st, n->head_x, rows, d, n->tr_xh.as<double2>());
+  Epi e;
+  e.mode = EPI_STORE;
+  e.err = err;
+  e.out = n->tr_dw.as<double2>();
+  e.ldo = V;
+  TRY(launch_rc(gemm(st, d, V, (int)rows, rows_of(n->tr_xh.as<double2>(), rows), G, V, e, nullptr, sy), "weight grad"));
+  bias_grad(st, G, (int)B, S, V, n->tr_db.as<double2>());
+  conj_transpose(st, Ln->w.as<double2>(), d, V, n->tr_wh.as<double2>());
+  e.out = n->tr_dx.as<double2>();
+  e.ldo = d;
+  TRY(launch_rc(gemm(st, (int)rows, d, V, rows_of(G, V), n->tr_wh.as<double2>(), d, e, nullptr, sy), "input grad"));
+  if (update_params) {  // LinearLayer::update_parameters (linear_layer.rs:130-175)
+    const size_t nw = (size_t)d * V;
+    if (!Ln->mw.p) {
+      TRY(Ln->mw.reserve(nw * c16));
+      TRY(Ln->vw.reserve(nw * c16));
+      TRY(Ln->mb.reserve((size_t)V * c16));
+      TRY(Ln->vb.reserve((size_t)V * c16));
+      fill_const(st, Ln->mw.as<double2>(), nw, make_double2(0.0, 0.0));
+      fill_const(st, Ln->vw.as<double2>(), nw, make_double2(0.0, 0.0));
+      fill_const(st, Ln->mb.as<double2>(), V, make_double2(0.0, 0.0));
+      fill_const(st, Ln->vb.as<double2>(), V, make_double2(0.0, 0.0));
+    }
+    TrainStep ts;
+    ts.first = Ln->updates == 0 ? 1 : 0;
+    ts.lr = learning_rate;
+    ts.batch = (double)B;
+    ts.time_step = (int)time_step;
+    linear_update(st, Ln->w.as<double2>(), n->tr_dw.as<double2>(), Ln->mw.as<double2>(), Ln->vw.as<double2>(),
+                  (long)nw, Ln->b.as<double2>(), n->tr_db.as<double2>(), Ln->mb.as<double2>(), Ln->vb.as<double2>(), V,
+                  ts);
+    Ln->updates++;
+    drop_graph(n);  // the weights changed under any captured step
+  }
+  if (out_grad_input)
+    HIP_TRY(hipMemcpyAsync(out_grad_input, n->tr_dx.p, (size_t)rows * d * c16, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  return check_err_word(n);
 }
 
 int mitok_greedy_decoding(mitok_network* n, const double* logits, uint32_t rows, uint32_t V, uint32_t* out_ids) {

@@ -643,3 +643,112 @@ def test_wavelet_layer_compresses_prompt_rows_and_mask():
     # a cached step (time_step > 0) passes the row through
     step = net.forward_layers(0, 1, x[:, :1], forward_only=True, time_steps=[9, 9])
     np.testing.assert_array_equal(step, x[:, :1])
+
+
+# ---- the output head's training step ----------------------------------------
+
+def _softmax_re(Z):
+    z = Z.real - Z.real.max(axis=-1, keepdims=True)
+    e = np.exp(z)
+    return e / e.sum(axis=-1, keepdims=True)
+
+
+def test_softmax_backward_rows_targets_and_normalizer():
+    """softmax_output_layer.rs:67-145 on a hand case: sequence b's targets sit
+    on rows S - len - 1 + t, PAD (1) targets are skipped but still occupy their
+    row, and every sequence divides by B times its non-PAD target count."""
+    rng = np.random.default_rng(40)
+    P = rng.random((2, 5, 4))
+    P /= P.sum(-1, keepdims=True)
+    targets = np.array([[2, 1, 3], [0, 0, 0]], np.uint32)
+    G = oracle.softmax_backward(P, targets, tlens=[3, 2])
+    want = np.zeros_like(P)
+    want[0, 1] = (P[0, 1] - np.eye(4)[2]) / 4.0  # b 0: rows 1, (2 skipped: PAD), 3; 2 * 2 non-PAD
+    want[0, 3] = (P[0, 3] - np.eye(4)[3]) / 4.0
+    want[1, 2] = (P[1, 2] - np.eye(4)[0]) / 4.0  # b 1: two targets from row 5 - 2 - 1 = 2
+    want[1, 3] = (P[1, 3] - np.eye(4)[0]) / 4.0
+    np.testing.assert_array_equal(G, want)
+    with pytest.raises(oracle.OracleError, match="exceeds vocabulary"):
+        oracle.softmax_backward(P, np.array([[4, 0, 0], [0, 0, 0]], np.uint32))
+    with pytest.raises(oracle.OracleError, match="need more than"):
+        oracle.softmax_backward(P, np.zeros((2, 5), np.uint32))
+
+
+def test_head_gradients_match_finite_differences_of_the_loss():
+    """The gradients of the head are the complex gradients dL/dRe + i dL/dIm of
+    the reference's cross-entropy, L = sum over the predicted targets of
+    -log softmax(Re(X W + b))[target] / (B * non-PAD targets): central finite
+    differences of L in every real coordinate of W, b and X (so conj, the
+    transposes and the normalizer are all checked)."""
+    rng = np.random.default_rng(41)
+    B, S, d, V = 2, 4, 3, 5
+    X = rng.standard_normal((B, S, d)) + 1j * rng.standard_normal((B, S, d))
+    W = 0.7 * (rng.standard_normal((d, V)) + 1j * rng.standard_normal((d, V)))
+    b = rng.standard_normal(V) + 1j * rng.standard_normal(V)
+    targets = np.array([[3, 1], [0, 4]], np.uint32)
+
+    def loss(X, W, b):
+        P = _softmax_re(X @ W + b)
+        L = 0.0
+        for s, (row, tgt) in enumerate([(1, 3), (2, 1), (1, 0), (2, 4)]):
+            bb = s // 2
+            if tgt != 1:
+                L -= np.log(P[bb, row, tgt]) / (B * (2 if bb == 1 else 1))
+        return L
+
+    P = _softmax_re(X @ W + b)
+    G = oracle.softmax_backward(P, targets)
+    dW, db, dX = oracle.linear_backward(X, G, W)
+    h = 1e-6
+    for arr, grad in ((W, dW), (b, db), (X, dX)):
+        for idx in np.ndindex(arr.shape):
+            for unit, part in ((1.0, "real"), (1j, "imag")):
+                args = [X.copy(), W.copy(), b.copy()]
+                k = [a is arr for a in (X, W, b)].index(True)
+                args[k][idx] += h * unit
+                lp = loss(*args)
+                args[k][idx] -= 2 * h * unit
+                lm = loss(*args)
+                fd = (lp - lm) / (2 * h)
+                got = getattr(grad[idx], part)
+                assert abs(got - fd) < 1e-7, (k, idx, part, got, fd)
+
+
+def test_linear_update_first_step_is_clipped_descent():
+    """linear_layer.rs:159-174: no previous gradient -> each element's gradient
+    clipped to norm 1 (utils/matrix.rs:709-717), divided by the batch, times
+    the learning rate; a non-finite gradient leaves its weight alone."""
+    W = np.array([[1 + 1j, 2 - 1j, 0.5j]])
+    b = np.array([0.25 + 0j, -1 + 2j, 3 + 0j])
+    dW = np.array([[0.3 + 0.4j, 3 + 4j, np.inf + 0j]])
+    db = np.array([0.0 + 0j, 0 - 2j, 0.6 + 0.8j])
+    state = [np.zeros((1, 3), np.complex128), np.zeros((1, 3), np.complex128),
+             np.zeros(3, np.complex128), np.zeros(3, np.complex128)]
+    W1, b1 = oracle.linear_update(W, b, dW, db, 4, state, True, 0.1, 7)
+    np.testing.assert_allclose(W1, [[1 + 1j - 0.1 * (0.3 + 0.4j) / 4, 2 - 1j - 0.1 * (0.6 + 0.8j) / 4, 0.5j]],
+                               rtol=1e-15)
+    np.testing.assert_allclose(b1, [0.25, -1 + 2j - 0.1 * (-1j) / 4, 3 - 0.1 * (0.6 + 0.8j) / 4], rtol=1e-15)
+    assert all(np.all(a == 0) for a in state)  # the descent leaves the moments at zero
+
+
+def test_linear_update_adamw_steps_reduce_to_normalised_descent():
+    """utils/adam_w.rs with zero moments and one gradient g (clipped to norm
+    1): at t = 1 and again at t = 2 with the same g, the bias-corrected moments
+    are g and |g|^2, so the step is w (1 - 0.01 lr) - lr g / (|g| + 1e-8); a
+    zero bias gradient leaves only the decay."""
+    rng = np.random.default_rng(42)
+    W = rng.standard_normal((3, 4)) + 1j * rng.standard_normal((3, 4))
+    g = rng.standard_normal((3, 4)) + 1j * rng.standard_normal((3, 4))
+    g[0, 0] = 5 + 5j  # clipped to norm 1
+    b = rng.standard_normal(4) + 1j * rng.standard_normal(4)
+    gb = np.zeros(4, np.complex128)
+    lr = 0.05
+    state = [np.zeros((3, 4), np.complex128), np.zeros((3, 4), np.complex128),
+             np.zeros(4, np.complex128), np.zeros(4, np.complex128)]
+    gc = np.where(np.abs(g) > 1, g / np.abs(g), g)
+    Wt, bt = W, b
+    for t in (1, 2):
+        Wt, bt = oracle.linear_update(Wt, bt, g, gb, 2, state, False, lr, t)
+        want = (W if t == 1 else want) * (1 - 0.01 * lr) - lr * gc / (np.abs(gc) + 1e-8)
+        np.testing.assert_allclose(Wt, want, rtol=1e-12, atol=1e-15)
+        np.testing.assert_allclose(bt, b * (1 - 0.01 * lr) ** t, rtol=1e-15)

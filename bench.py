@@ -177,6 +177,7 @@ def main():
     ap.add_argument("--workload", default="c3b32", choices=sorted(configs.WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-b1", action="store_true", help="skip the batch-1 companion measurement")
+    ap.add_argument("--no-train", action="store_true", help="skip the output-head training-step measurement")
     ap.add_argument("--no-classes", action="store_true",
                     help="skip the per-kernel-class HIP-event pass (profiler runs of the timed region only)")
     ap.add_argument("--direct", action="store_true",
@@ -296,7 +297,39 @@ def run(args, w, net):
         out["batch1"]["decode_step_bytes"] = round(step_bytes)
         out["batch1"]["decode_step_hbm_frac"] = round(step_bytes / (dec1 / (w1.n_new - 1) / 1e3) / 1e9 / HBM_PEAK_GBS, 4)
 
+    if not args.no_train and args.workload.startswith("c3"):
+        log("output-head training step")
+        out["head_train"] = head_train_step(cfg)
+
     return out
+
+
+def head_train_step(cfg, B=8, S=128, T=64, reps=5):
+    """The output head's training step (mitok_backward_head: Softmax
+    cross-entropy gradient, vocab Linear backward, then its AdamW update) at
+    config 3's head shapes, after one TRAINING-mode predict of B x S rows.
+    Algorithmic flops: the two products dW = conj(X)^T G and dX = G conj(W)^T,
+    8 * d * V * rows each."""
+    with ra.Network(0) as h:
+        h.add_embedding(cfg.vocab, cfg.d)
+        h.add_linear(cfg.d, cfg.vocab)
+        h.add_softmax(ra.TRAINING)
+        h.init_seeded(cfg.seed)
+        ids = seeded.prompts(11, [S] * B, cfg.vocab)
+        targets = seeded.prompts(12, [T] * B, cfg.vocab)
+        h.predict(ids, forward_only=False)
+        for t in (1, 2):  # the first update (plain descent), then AdamW
+            h.backward_head(targets, update=True, learning_rate=1e-3, time_step=t, want_grad_input=False)
+        ra.device_synchronize(0)
+        t0 = time.perf_counter()
+        for t in range(reps):
+            h.backward_head(targets, update=True, learning_rate=1e-3, time_step=3 + t, want_grad_input=False)
+        ms = (time.perf_counter() - t0) / reps * 1e3
+    flops = 2 * 8.0 * cfg.d * cfg.vocab * B * S
+    return {"config": f"vocab Linear {cfg.d} x {cfg.vocab}, {B} x {S} rows, {T} targets per sequence, AdamW update",
+            "ms_per_step": round(ms, 3), "alg_gflop": round(flops / 1e9, 2),
+            "tflops": round(flops / (ms / 1e3) / 1e12, 3),
+            "mfma_frac": round(flops / (ms / 1e3) / 1e12 / FP64_MFMA_PEAK_TFS, 4)}
 
 
 if __name__ == "__main__":

@@ -693,11 +693,11 @@ __global__ __launch_bounds__(256) void k_zgemm_skinny_cols(const double2* __rest
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int kk = k + 4 * u + kq;
-      b[buf][u] = (kk < kz && n < N) ? W[(long)kk * ldw + n] : make_double2(0.0, 0.0);
+      b[buf][u] = ld_glb((kk < kz && n < N) ? W + (long)kk * ldw + n : &rows16s_zero);
 #pragma unroll
       for (int t = 0; t < RT; ++t) {
         const int m = 16 * t + i;
-        a[buf][t][u] = (kk < kz && m < M) ? X[(long)m * ldx + kk] : make_double2(0.0, 0.0);
+        a[buf][t][u] = ld_glb((kk < kz && m < M) ? X + (long)m * ldx + kk : &rows16s_zero);
       }
     }
   };
@@ -738,7 +738,7 @@ __global__ __launch_bounds__(256) void k_zgemm_skinny_cols(const double2* __rest
 #pragma unroll
       for (int j = 0; j < PT; ++j) {
         const int e = tid + 256 * j, m = e / CK, kk = k0 + (e - m * CK);
-        st[j] = (m < M && kk < kz) ? X[(long)m * ldx + kk] : make_double2(0.0, 0.0);
+        st[j] = ld_glb((m < M && kk < kz) ? X + (long)m * ldx + kk : &rows16s_zero);
       }
     };
     auto stage = [&](int buf) {
@@ -752,7 +752,7 @@ __global__ __launch_bounds__(256) void k_zgemm_skinny_cols(const double2* __rest
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int kk = k + 4 * u + kq;
-        b[buf][u] = (kk < kz && n < N) ? W[(long)kk * ldw + n] : make_double2(0.0, 0.0);
+        b[buf][u] = ld_glb((kk < kz && n < N) ? W + (long)kk * ldw + n : &rows16s_zero);
       }
     };
     auto frag = [&](int abuf, int wbuf, int kl) {  // a[wbuf] <- the chunk's rows at local k kl

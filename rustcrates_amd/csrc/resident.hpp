@@ -149,6 +149,10 @@ __device__ __forceinline__ void fma_rows(double2 (&acc)[MR], const double2* xw, 
   }
 }
 
+// what a weight load past a lane's rows reads: every lane issues every load,
+// so no load sits under a branch and each wait counts only the loads it needs
+__device__ const double2 res_zero2 = {0.0, 0.0};
+
 template <int C>
 __device__ __forceinline__ void gemv_weights(const ROp& op, int item, double2 (&w)[RES_NPF]) {
   constexpr int RPW = 64 / C;
@@ -162,7 +166,7 @@ __device__ __forceinline__ void gemv_weights(const ROp& op, int item, double2 (&
   const double2* wp = op.W + (long)(k0 + r) * op.ldw + n;
   const long wstep = (long)RPW * op.ldw;
 #pragma unroll
-  for (int u = 0; u < RES_NPF; ++u) w[u] = u < nu ? ld_stream(wp + u * wstep) : make_double2(0.0, 0.0);
+  for (int u = 0; u < RES_NPF; ++u) w[u] = ld_stream(u < nu ? wp + u * wstep : &res_zero2);
 }
 
 // this block's item of a prefetched product (item = blockIdx.x)
@@ -273,7 +277,7 @@ __device__ __forceinline__ void r_gemv3(const ROp& op, int item, double2* lds2, 
 template <int WO, int NW>
 __device__ __forceinline__ void stream_rows(double2 (&w)[NW], const double2* wp, long wstep, int un, int nu) {
 #pragma unroll
-  for (int u = 0; u < 8; ++u) w[WO + u] = un + u < nu ? ld_stream(wp + (un + u) * wstep) : make_double2(0.0, 0.0);
+  for (int u = 0; u < 8; ++u) w[WO + u] = ld_stream(un + u < nu ? wp + (un + u) * wstep : &res_zero2);
 }
 
 // prev: this block's previous item of the operation (-1: none); when it

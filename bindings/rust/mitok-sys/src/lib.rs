@@ -90,6 +90,9 @@ extern "C" {
     pub fn mitok_backward_head(net: *mut MitokNetwork, targets: *const u32, tlens: *const u32, batch: u32, t: u32,
                                update_params: c_int, learning_rate: c_double, time_step: u32,
                                out_grad_input: *mut c_double) -> c_int;
+    pub fn mitok_backward(net: *mut MitokNetwork, targets: *const u32, tlens: *const u32, batch: u32, t: u32,
+                          n_layers: u32, update_params: c_int, learning_rate: c_double, time_step: u32,
+                          out_grad_input: *mut c_double) -> c_int;
     pub fn mitok_greedy_decoding(net: *mut MitokNetwork, logits: *const c_double, rows: u32, vocab: u32,
                                  out_ids: *mut u32) -> c_int;
     pub fn mitok_greedy_decoding_device(net: *mut MitokNetwork, d_logits: *const c_double, rows: u32, vocab: u32,

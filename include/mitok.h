@@ -178,6 +178,16 @@ int mitok_decode_step(mitok_network* net, const uint32_t* ids, uint32_t batch, u
  * are not differentiated. */
 int mitok_backward_head(mitok_network* net, const uint32_t* targets, const uint32_t* tlens, uint32_t batch, uint32_t T,
                         int update_params, double learning_rate, uint32_t time_step, double* out_grad_input);
+/* The same reverse walk through n_layers layers below the Softmax: 1 = the
+ * vocab Linear (mitok_backward_head), 2 = also the FeedForward right below it
+ * (feedforward_layer.rs:140-186: its Linear, then its Dense with the GELU
+ * derivative of utils/derivative.rs:48-84; with update_params both updated,
+ * the Linear at time_step and the Dense at step 1, since Layer::time_step is
+ * never set, layer.rs:111,285).  out_grad_input is then the gradient of that
+ * FeedForward's input [batch][seq'][d]. */
+int mitok_backward(mitok_network* net, const uint32_t* targets, const uint32_t* tlens, uint32_t batch, uint32_t T,
+                   uint32_t n_layers, int update_params, double learning_rate, uint32_t time_step,
+                   double* out_grad_input);
 
 /* greedy_decoding (src/utils/sampling_methods.rs:5-18) on the device for host
  * logits [rows][vocab]: last index among equal maxima; NaN -> MITOK_ERR_NAN. */

@@ -80,6 +80,9 @@ def _load():
         "orc_softmax_backward": (i32, [P, u32, u32, u32, P, P, u32, P]),
         "orc_linear_backward": (i32, [P, P, P, u32, u32, u32, u32, P, P, P]),
         "orc_linear_update": (i32, [P, P, u32, u32, P, P, u32, P, P, P, P, i32, f64, u32]),
+        "orc_linear_backward_c": (i32, [P, P, P, u32, u32, u32, u32, P, P, P]),
+        "orc_gelu_derivative": (_C64, [_C64]),
+        "orc_dense_backward": (i32, [P, P, P, P, P, u32, u32, u32, u32, P, P, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -188,6 +191,39 @@ def linear_backward(X, G, W):
     db = np.empty(V, np.complex128)
     dX = np.empty((B, S, d), np.complex128)
     _check(lib().orc_linear_backward(_ptr(X), _ptr(G), _ptr(W), B, S, d, V, _ptr(dW), _ptr(db), _ptr(dX)))
+    return dW, db, dX
+
+
+def linear_backward_c(X, G, W):
+    """linear_backward with a complex gradient G [B][S][V] (a layer below the head)."""
+    X, G, W = _c128(X), _c128(G), _c128(W)
+    B, S, d = X.shape
+    V = W.shape[1]
+    dW = np.empty((d, V), np.complex128)
+    db = np.empty(V, np.complex128)
+    dX = np.empty((B, S, d), np.complex128)
+    _check(lib().orc_linear_backward_c(_ptr(X), _ptr(G), _ptr(W), B, S, d, V, _ptr(dW), _ptr(db), _ptr(dX)))
+    return dW, db, dX
+
+
+def gelu_derivative(z: complex) -> complex:
+    """gelu_derivative_complex (utils/derivative.rs:48-84)."""
+    r = lib().orc_gelu_derivative(_C64(complex(z).real, complex(z).imag))
+    return complex(r.re, r.im)
+
+
+def dense_backward(X, Z, prev, mask, W):
+    """Layer::backward of the Dense (GELU) layer (layer.rs:168-210):
+    (dW [d][F], db [F], dX [B][S][d])."""
+    X, Z, prev, W = _c128(X), _c128(Z), _c128(prev), _c128(W)
+    m = np.ascontiguousarray(mask, dtype=np.uint32)
+    B, S, d = X.shape
+    F = W.shape[1]
+    dW = np.empty((d, F), np.complex128)
+    db = np.empty(F, np.complex128)
+    dX = np.empty((B, S, d), np.complex128)
+    _check(lib().orc_dense_backward(_ptr(X), _ptr(Z), _ptr(prev), _ptr(m), _ptr(W), B, S, d, F, _ptr(dW), _ptr(db),
+                                    _ptr(dX)))
     return dW, db, dX
 
 

@@ -1281,11 +1281,25 @@ int orc_softmax_backward(const double* P, uint32_t B, uint32_t S, uint32_t V, co
   return ORC_OK;
 }
 
+int orc_linear_backward_c(const oc64* X, const oc64* Gin, const oc64* W, uint32_t B, uint32_t S, uint32_t d,
+                          uint32_t V, oc64* dW, oc64* db, oc64* dX);
+
 int orc_linear_backward(const oc64* X, const double* G, const oc64* W, uint32_t B, uint32_t S, uint32_t d,
                         uint32_t V, oc64* dW, oc64* db, oc64* dX) {
-  if (!X || !G || !W || !dW || !db || !dX || !B || !S || !d || !V) return fail(ORC_ERR_ARG, "bad arguments");
+  if (!G || !B || !S || !V) return fail(ORC_ERR_ARG, "bad arguments");
+  oc64* gc = (oc64*)malloc((size_t)B * S * V * sizeof(oc64)); /* the gradient as Complex (im 0) */
+  if (!gc) return fail(ORC_ERR_NOMEM, "linear backward: out of memory");
+  for (size_t i = 0; i < (size_t)B * S * V; ++i) gc[i] = (oc64){G[i], 0.0};
+  const int rc = orc_linear_backward_c(X, gc, W, B, S, d, V, dW, db, dX);
+  free(gc);
+  return rc;
+}
+
+int orc_linear_backward_c(const oc64* X, const oc64* Gin, const oc64* W, uint32_t B, uint32_t S, uint32_t d,
+                          uint32_t V, oc64* dW, oc64* db, oc64* dX) {
+  if (!X || !Gin || !W || !dW || !db || !dX || !B || !S || !d || !V) return fail(ORC_ERR_ARG, "bad arguments");
   oc64* xh = (oc64*)malloc((size_t)d * S * sizeof(oc64));   /* conjugate_transpose(input_sample) */
-  oc64* gc = (oc64*)malloc((size_t)S * V * sizeof(oc64));   /* the gradient as Complex (im 0) */
+  oc64* gc = (oc64*)malloc((size_t)S * V * sizeof(oc64));   /* one sequence's gradient */
   oc64* wh = (oc64*)malloc((size_t)V * d * sizeof(oc64));   /* conjugate_transpose(weights) */
   oc64* wg = (oc64*)malloc((size_t)d * V * sizeof(oc64));   /* one sequence's weight gradient */
   if (!xh || !gc || !wh || !wg) {
@@ -1306,7 +1320,7 @@ int orc_linear_backward(const oc64* X, const double* G, const oc64* W, uint32_t 
         const oc64 x = xb[(size_t)s * d + k];
         xh[(size_t)k * S + s] = (oc64){x.re, -x.im};
       }
-    for (size_t i = 0; i < (size_t)S * V; ++i) gc[i] = (oc64){G[(size_t)b * S * V + i], 0.0};
+    memcpy(gc, Gin + (size_t)b * S * V, (size_t)S * V * sizeof(oc64));
     orc_zgemm(d, V, S, xh, gc, wg);                                 /* linear_layer.rs:99 */
     for (size_t i = 0; i < (size_t)d * V; ++i) dW[i] = c_add(dW[i], wg[i]); /* group_gradient_batch */
     oc64 bsum; /* bias gradient of this sequence (:101-105), then grouped */
@@ -1380,4 +1394,46 @@ int orc_linear_update(oc64* W, oc64* b, uint32_t d, uint32_t V, const oc64* dW, 
   for (size_t i = 0; i < n; ++i) W[i] = adamw1(W[i], dW[i], &mW[i], &vW[i], lr, time_step, 1);
   for (uint32_t j = 0; j < V; ++j) b[j] = adamw1(b[j], db[j], &mb[j], &vb[j], lr, time_step, 0);
   return ORC_OK;
+}
+
+/* gelu_derivative_complex (utils/derivative.rs:48-84) */
+oc64 orc_gelu_derivative(oc64 z) {
+  const double s2p = sqrt(2.0 / M_PI);
+  const oc64 one = {1.0, 0.0};
+  const oc64 x3 = c_mul(z, c_mul(z, z)); /* powi(3) */
+  const oc64 fx = c_scale(c_add(z, c_mul((oc64){0.044715, 0.0}, x3)), s2p);
+  const int sat = hypot(fx.re, fx.im) > 20.0;
+  const oc64 th = sat ? one : c_tanh(fx);
+  const oc64 sech2 = sat ? (oc64){0.0, 0.0} : c_sub(one, c_mul(th, th)); /* 1 - tanh^2 (powi(2)) */
+  const oc64 fp = c_scale(c_add(one, c_mul((oc64){0.134145, 0.0}, c_mul(z, z))), s2p);
+  const oc64 d = c_add(c_mul((oc64){0.5, 0.0}, c_add(one, th)),
+                       c_mul(c_mul(c_mul((oc64){0.5, 0.0}, z), sech2), fp));
+  const double n = hypot(d.re, d.im);
+  if (n > 1e6) return c_mul(c_unscale(d, n), (oc64){1e6, 0.0});
+  if (n < 1e-12) return (oc64){1e-12, 0.0};
+  return d;
+}
+
+/* Layer::backward for the Dense (GELU) layer (network_components/layer.rs:168-210):
+ * prev [B][S][F] with padded rows zeroed (apply_padding_mask_batch), times
+ * conj(GELU'(Z)) elementwise, then the products of the linear arm */
+int orc_dense_backward(const oc64* X, const oc64* Z, const oc64* prev, const uint32_t* mask, const oc64* W,
+                       uint32_t B, uint32_t S, uint32_t d, uint32_t F, oc64* dW, oc64* db, oc64* dX) {
+  if (!X || !Z || !prev || !mask || !W || !B || !S || !d || !F) return fail(ORC_ERR_ARG, "bad arguments");
+  const size_t n = (size_t)B * S * F;
+  oc64* g = (oc64*)malloc(n * sizeof(oc64));
+  if (!g) return fail(ORC_ERR_NOMEM, "dense backward: out of memory");
+  for (size_t r = 0; r < (size_t)B * S; ++r)
+    for (uint32_t j = 0; j < F; ++j) {
+      const size_t i = r * F + j;
+      if (mask[r] == 0) {
+        g[i] = (oc64){0.0, 0.0};
+      } else {
+        const oc64 dz = orc_gelu_derivative(Z[i]);
+        g[i] = c_mul(prev[i], (oc64){dz.re, -dz.im}); /* hadamard with transpose(conjugate_transpose) */
+      }
+    }
+  const int rc = orc_linear_backward_c(X, g, W, B, S, d, F, dW, db, dX);
+  free(g);
+  return rc;
 }

@@ -135,6 +135,16 @@ int orc_softmax_backward(const double* P, uint32_t B, uint32_t S, uint32_t V, co
  * sum_b sum_s G_b[s], dX [B][S][d] = G_b conj(W)^T. */
 int orc_linear_backward(const oc64* X, const double* G, const oc64* W, uint32_t B, uint32_t S, uint32_t d,
                         uint32_t V, oc64* dW, oc64* db, oc64* dX);
+/* the same with a complex gradient G [B][S][V] (a layer below the head) */
+int orc_linear_backward_c(const oc64* X, const oc64* G, const oc64* W, uint32_t B, uint32_t S, uint32_t d,
+                          uint32_t V, oc64* dW, oc64* db, oc64* dX);
+/* gelu_derivative_complex (utils/derivative.rs:48-84) */
+oc64 orc_gelu_derivative(oc64 z);
+/* Layer::backward of the Dense (GELU) layer (layer.rs:168-210): X [B][S][d]
+ * its input, Z [B][S][F] its pre-activation X W + b, prev [B][S][F] the
+ * gradient of its output, mask [B][S]; dW [d][F], db [F], dX [B][S][d]. */
+int orc_dense_backward(const oc64* X, const oc64* Z, const oc64* prev, const uint32_t* mask, const oc64* W,
+                       uint32_t B, uint32_t S, uint32_t d, uint32_t F, oc64* dW, oc64* db, oc64* dX);
 /* LinearLayer::update_parameters (linear_layer.rs:130-175) for `batch`
  * sequences: first != 0 is the first update (no previous gradient): each
  * element's clipped gradient (clip_gradients, utils/matrix.rs:703-717), if

@@ -59,6 +59,7 @@ SIGNATURES = {
     "mitok_decode_step": (_i32, [_P, _P, _u32, _P, _P]),
     "mitok_greedy_decoding": (_i32, [_P, _P, _u32, _u32, _P]),
     "mitok_backward_head": (_i32, [_P, _P, _P, _u32, _u32, _i32, C.c_double, _u32, _P]),
+    "mitok_backward": (_i32, [_P, _P, _P, _u32, _u32, _u32, _i32, C.c_double, _u32, _P]),
     "mitok_greedy_decoding_device": (_i32, [_P, _P, _u32, _u32, _P]),
     "mitok_forward_layers_device": (_i32, [_P, _u32, _u32, _P, _P, _u32, _u32, _P, _i32, _P]),
     "mitok_greedy_decoding_noalloc": (_i32, [_P, _P, _u32, _u32, _P]),
@@ -387,6 +388,14 @@ class Network:
         stateless predict (transformer_network.rs:506-636 for those two
         layers); with `update`, the Linear's update_parameters.  Returns the
         gradient with respect to the Linear's input [B][S'][d_in] (complex)."""
+        return self.backward(targets, tlens, 1, update, learning_rate, time_step, want_grad_input)
+
+    def backward(self, targets, tlens=None, layers=1, update=True, learning_rate=0.001, time_step=1,
+                 want_grad_input=True):
+        """The reverse walk of backward (transformer_network.rs:506-636)
+        through `layers` layers below the Softmax: 1 the vocab Linear, 2 also
+        the FeedForward right below it.  Returns the gradient of the lowest
+        differentiated layer's input [B][S'][d] (complex)."""
         t = np.ascontiguousarray(targets, dtype=np.uint32)
         if t.ndim != 2:
             raise ValueError(f"targets: shape {t.shape}, expected (batch, T)")
@@ -398,8 +407,8 @@ class Network:
             if rows is None or rows[0] != B:
                 raise MitokError(3, "no stateless predict of this batch to differentiate")
             gx = np.empty((B, rows[1], self._head_in), np.complex128)
-        _check(self._lib.mitok_backward_head(self._h, _ptr(t), _ptr(tl), B, T, int(bool(update)), float(learning_rate),
-                                             int(time_step), _ptr(gx)))
+        _check(self._lib.mitok_backward(self._h, _ptr(t), _ptr(tl), B, T, int(layers), int(bool(update)),
+                                        float(learning_rate), int(time_step), _ptr(gx)))
         return gx
 
     def greedy_decoding(self, logits):

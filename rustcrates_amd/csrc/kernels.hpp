@@ -135,6 +135,9 @@ struct TrainStep {
 // G[r][c] (complex, im 0) = tgt[r] < 0 ? 0 : (P[r][c] - [c == tgt[r]]) / norm[r / S]
 void softmax_grad(hipStream_t st, const double* P, int rows, int V, const int* tgt, const double* norm, int S,
                   double2* G);
+// G = mask[r] ? dH * conj(GELU'(Z)) : 0 (layer.rs:181-192, derivative.rs:48-84); mask may be null (all rows)
+void gelu_backward(hipStream_t st, const double2* dH, const double2* Z, const uint32_t* mask, long rows, int F,
+                   double2* G);
 // out [C][R] = conj(in)^T for in [R][C]
 void conj_transpose(hipStream_t st, const double2* in, long R, long C, double2* out);
 // db [V] = sum_b sum_s G[b][s][:] (per-sequence sums in row order, then in sequence order)

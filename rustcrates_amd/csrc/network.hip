@@ -137,6 +137,10 @@ struct SelfAttentionLayer : Layer {  // self_attention_layer.rs:16-25 + masked_a
 struct FeedForwardLayer : Layer {  // feedforward_layer.rs:14-26, layer.rs:91-112, linear_layer.rs:18-34
   uint32_t hidden = 0;
   DevBuf w1, b1, w2, b2;
+  // training state of the Dense (1) and Linear (2) sublayers: AdamW moments
+  // and updates so far (each sublayer's first update is plain clipped descent)
+  DevBuf mw1, vw1, mb1, vb1, mw2, vw2, mb2, vb2;
+  uint32_t updates1 = 0, updates2 = 0;
   FeedForwardLayer() : Layer(K_FEED_FORWARD) {}
 };
 
@@ -355,8 +359,11 @@ struct mitok_network {
   // differentiates; any later call clears head_valid
   bool head_valid = false;
   const double2* head_x = nullptr;
+  const double2* head_x2 = nullptr;     // the input of a FeedForward right below the vocab Linear
+  const uint32_t* head_mask = nullptr;  // the padding mask of those rows
   uint32_t head_B = 0, head_S = 0;
   mitok::DevBuf tr_g, tr_xh, tr_wh, tr_dw, tr_db, tr_dx, tr_tgt, tr_norm;
+  mitok::DevBuf tr_z, tr_g1, tr_dh, tr_dw1, tr_db1, tr_dw2, tr_db2, tr_dx2;
 };
 
 namespace mitok {
@@ -814,6 +821,9 @@ static int enqueue_forward(Net* n, const Spec& sp) {
           if (sp.mode == MODE_STATELESS && !sp.last_row) {  // the layer keeps its input for backward
             n->head_valid = true;
             n->head_x = x;
+            // a FeedForward right below left its input in the other buffer
+            n->head_x2 = (li > 0 && n->layers[li - 1]->kind == K_FEED_FORWARD) ? nxt : nullptr;
+            n->head_mask = mask;
             n->head_B = (uint32_t)B;
             n->head_S = (uint32_t)S;
           }
@@ -2481,14 +2491,32 @@ int mitok_decode_step(mitok_network* n, const uint32_t* ids, uint32_t B, uint32_
   return rc;
 }
 
-int mitok_backward_head(mitok_network* n, const uint32_t* targets, const uint32_t* tlens, uint32_t B, uint32_t T,
-                        int update_params, double learning_rate, uint32_t time_step, double* out_grad_input) {
+// the AdamW moments of a d x V weight and its bias, allocated and zeroed at the first update
+static int ensure_moments(hipStream_t st, size_t nw, size_t nb, DevBuf& mw, DevBuf& vw, DevBuf& mb, DevBuf& vb) {
+  if (mw.p) return OK;
+  TRY(mw.reserve(nw * sizeof(double2)));
+  TRY(vw.reserve(nw * sizeof(double2)));
+  TRY(mb.reserve(nb * sizeof(double2)));
+  TRY(vb.reserve(nb * sizeof(double2)));
+  fill_const(st, mw.as<double2>(), nw, make_double2(0.0, 0.0));
+  fill_const(st, vw.as<double2>(), nw, make_double2(0.0, 0.0));
+  fill_const(st, mb.as<double2>(), nb, make_double2(0.0, 0.0));
+  fill_const(st, vb.as<double2>(), nb, make_double2(0.0, 0.0));
+  return OK;
+}
+
+static int backward_impl(Net* n, const uint32_t* targets, const uint32_t* tlens, uint32_t B, uint32_t T,
+                         uint32_t n_layers, int update_params, double learning_rate, uint32_t time_step,
+                         double* out_grad_input) {
   if (!n || !targets || !tlens || !B || !T) return fail(ERR_ARG, "bad arguments");
+  if (n_layers < 1 || n_layers > 2) return fail(ERR_ARG, "%u layers: the vocab Linear (1) and the FeedForward below it (2)", n_layers);
   if (!n->head_valid) return fail(ERR_STATE, "no stateless (forward_only = 0) predict to differentiate");
   if (B != n->head_B) return fail(ERR_ARG, "batch %u != the forward pass's %u", B, n->head_B);
   const uint32_t li = (uint32_t)n->layers.size() - 2;
   if (!is_vocab_linear(n, li)) return fail(ERR_STATE, "the stack does not end in Linear, Softmax");
   auto* Ln = (LinearLayer*)n->layers[li].get();
+  if (n_layers >= 2 && (li == 0 || n->layers[li - 1]->kind != K_FEED_FORWARD || !n->head_x2))
+    return fail(ERR_STATE, "no FeedForward right below the vocab Linear to differentiate");
   const int S = (int)n->head_S, d = (int)Ln->d_in, V = (int)Ln->d_out;
   const long rows = (long)B * S;
   // SoftmaxLayer::backward (softmax_output_layer.rs:67-145): which row predicts
@@ -2521,12 +2549,27 @@ int mitok_backward_head(mitok_network* n, const uint32_t* targets, const uint32_
   TRY(upload(n, n->tr_tgt, tgt.data(), tgt.size() * sizeof(int)));
   TRY(upload(n, n->tr_norm, norm.data(), norm.size() * sizeof(double)));
   TRY(reserve(n, n->tr_g, (size_t)rows * V * c16));
-  TRY(reserve(n, n->tr_xh, (size_t)d * rows * c16));
-  TRY(reserve(n, n->tr_wh, (size_t)V * d * c16));
+  // every workspace is sized before the first launch (a reserve that grows frees the old buffer)
+  const int F = n_layers >= 2 ? (int)((FeedForwardLayer*)n->layers[li - 1].get())->hidden : 0;
+  TRY(reserve(n, n->tr_xh, (size_t)std::max(d, F) * rows * c16));
+  TRY(reserve(n, n->tr_wh, (size_t)std::max<size_t>((size_t)V * d, (size_t)F * d) * c16));
   TRY(reserve(n, n->tr_dw, (size_t)d * V * c16));
   TRY(reserve(n, n->tr_db, (size_t)V * c16));
   TRY(reserve(n, n->tr_dx, (size_t)rows * d * c16));
-  TRY(reserve(n, n->sync_ws, std::max(gemm_ws_bytes(d, V, (int)rows), gemm_ws_bytes((int)rows, d, V))));
+  size_t ws = std::max(gemm_ws_bytes(d, V, (int)rows), gemm_ws_bytes((int)rows, d, V));
+  if (F) {
+    TRY(reserve(n, n->tr_z, (size_t)rows * F * c16));
+    TRY(reserve(n, n->tr_g1, (size_t)rows * F * c16));
+    TRY(reserve(n, n->tr_dh, (size_t)rows * F * c16));
+    TRY(reserve(n, n->tr_dw1, (size_t)d * F * c16));
+    TRY(reserve(n, n->tr_db1, (size_t)F * c16));
+    TRY(reserve(n, n->tr_dw2, (size_t)F * d * c16));
+    TRY(reserve(n, n->tr_db2, (size_t)d * c16));
+    TRY(reserve(n, n->tr_dx2, (size_t)rows * d * c16));
+    ws = std::max({ws, gemm_ws_bytes(F, d, (int)rows), gemm_ws_bytes((int)rows, F, d), gemm_ws_bytes(d, F, (int)rows),
+                   gemm_ws_bytes((int)rows, d, F)});
+  }
+  TRY(reserve(n, n->sync_ws, ws));
   const Sync sy = sync_of(n);
   uint32_t* err = n->err_d.as<uint32_t>();
   double2* G = n->tr_g.as<double2>();
@@ -2545,22 +2588,13 @@ int mitok_backward_head(mitok_network* n, const uint32_t* targets, const uint32_
   e.out = n->tr_dx.as<double2>();
   e.ldo = d;
   TRY(launch_rc(gemm(st, (int)rows, d, V, rows_of(G, V), n->tr_wh.as<double2>(), d, e, nullptr, sy), "input grad"));
+  TrainStep ts;
+  ts.lr = learning_rate;
+  ts.batch = (double)B;
   if (update_params) {  // LinearLayer::update_parameters (linear_layer.rs:130-175)
     const size_t nw = (size_t)d * V;
-    if (!Ln->mw.p) {
-      TRY(Ln->mw.reserve(nw * c16));
-      TRY(Ln->vw.reserve(nw * c16));
-      TRY(Ln->mb.reserve((size_t)V * c16));
-      TRY(Ln->vb.reserve((size_t)V * c16));
-      fill_const(st, Ln->mw.as<double2>(), nw, make_double2(0.0, 0.0));
-      fill_const(st, Ln->vw.as<double2>(), nw, make_double2(0.0, 0.0));
-      fill_const(st, Ln->mb.as<double2>(), V, make_double2(0.0, 0.0));
-      fill_const(st, Ln->vb.as<double2>(), V, make_double2(0.0, 0.0));
-    }
-    TrainStep ts;
+    TRY(ensure_moments(st, nw, V, Ln->mw, Ln->vw, Ln->mb, Ln->vb));
     ts.first = Ln->updates == 0 ? 1 : 0;
-    ts.lr = learning_rate;
-    ts.batch = (double)B;
     ts.time_step = (int)time_step;
     linear_update(st, Ln->w.as<double2>(), n->tr_dw.as<double2>(), Ln->mw.as<double2>(), Ln->vw.as<double2>(),
                   (long)nw, Ln->b.as<double2>(), n->tr_db.as<double2>(), Ln->mb.as<double2>(), Ln->vb.as<double2>(), V,
@@ -2568,10 +2602,79 @@ int mitok_backward_head(mitok_network* n, const uint32_t* targets, const uint32_
     Ln->updates++;
     drop_graph(n);  // the weights changed under any captured step
   }
+  const double2* gin = n->tr_dx.as<double2>();  // gradient of the lowest layer's input so far
+  if (n_layers >= 2) {
+    // FeedForwardLayer::backward (feedforward_layer.rs:140-186): its Linear,
+    // then its Dense (GELU) layer, each as LinearLayer::backward's products
+    auto* Fl = (FeedForwardLayer*)n->layers[li - 1].get();
+    const double2* Xf = n->head_x2;               // the FFN's input rows
+    const double2* H = n->hbuf.as<double2>();      // its Dense output, GELU applied, padded rows 0
+    const double2* dY = n->tr_dx.as<double2>();    // the gradient of its output
+    const Sync sy2 = sy;
+    Epi f;
+    f.mode = EPI_STORE;
+    f.err = err;
+    // Linear (W2 [F][d]): dW2 = conj(H)^T dY, db2, dH = dY conj(W2)^T
+    conj_transpose(st, H, rows, F, n->tr_xh.as<double2>());
+    f.out = n->tr_dw2.as<double2>();
+    f.ldo = d;
+    TRY(launch_rc(gemm(st, F, d, (int)rows, rows_of(n->tr_xh.as<double2>(), rows), dY, d, f, nullptr, sy2), "ffn2 weight grad"));
+    bias_grad(st, dY, (int)B, S, d, n->tr_db2.as<double2>());
+    conj_transpose(st, Fl->w2.as<double2>(), F, d, n->tr_wh.as<double2>());
+    f.out = n->tr_dh.as<double2>();
+    f.ldo = F;
+    TRY(launch_rc(gemm(st, (int)rows, F, d, rows_of(dY, d), n->tr_wh.as<double2>(), F, f, nullptr, sy2), "ffn2 input grad"));
+    // Dense (W1 [d][F], GELU): its pre-activation again, Z = X W1 + b1 (layer.rs:135-144)
+    f.out = n->tr_z.as<double2>();
+    f.ldo = F;
+    f.bias = Fl->b1.as<double2>();
+    TRY(launch_rc(gemm(st, (int)rows, F, d, rows_of(Xf, d), Fl->w1.as<double2>(), F, f, nullptr, sy2), "ffn1 pre-activation"));
+    f.bias = nullptr;
+    gelu_backward(st, n->tr_dh.as<double2>(), n->tr_z.as<double2>(), n->head_mask, rows, F, n->tr_g1.as<double2>());
+    conj_transpose(st, Xf, rows, d, n->tr_xh.as<double2>());
+    f.out = n->tr_dw1.as<double2>();
+    f.ldo = F;
+    TRY(launch_rc(gemm(st, d, F, (int)rows, rows_of(n->tr_xh.as<double2>(), rows), n->tr_g1.as<double2>(), F, f, nullptr, sy2),
+                  "ffn1 weight grad"));
+    bias_grad(st, n->tr_g1.as<double2>(), (int)B, S, F, n->tr_db1.as<double2>());
+    conj_transpose(st, Fl->w1.as<double2>(), d, F, n->tr_wh.as<double2>());
+    f.out = n->tr_dx2.as<double2>();
+    f.ldo = d;
+    TRY(launch_rc(gemm(st, (int)rows, d, F, rows_of(n->tr_g1.as<double2>(), F), n->tr_wh.as<double2>(), d, f, nullptr, sy2),
+                  "ffn1 input grad"));
+    gin = n->tr_dx2.as<double2>();
+    if (update_params) {  // FeedForwardLayer::update_parameters (:219-250): the Linear, then the Dense
+      TRY(ensure_moments(st, (size_t)F * d, d, Fl->mw2, Fl->vw2, Fl->mb2, Fl->vb2));
+      TRY(ensure_moments(st, (size_t)d * F, F, Fl->mw1, Fl->vw1, Fl->mb1, Fl->vb1));
+      ts.first = Fl->updates2 == 0 ? 1 : 0;
+      ts.time_step = (int)time_step;  // the FFN passes its time step to its Linear (feedforward_layer.rs:86)
+      linear_update(st, Fl->w2.as<double2>(), n->tr_dw2.as<double2>(), Fl->mw2.as<double2>(), Fl->vw2.as<double2>(),
+                    (long)F * d, Fl->b2.as<double2>(), n->tr_db2.as<double2>(), Fl->mb2.as<double2>(),
+                    Fl->vb2.as<double2>(), d, ts);
+      Fl->updates2++;
+      ts.first = Fl->updates1 == 0 ? 1 : 0;
+      ts.time_step = 0;  // Layer::time_step is never set after construction (layer.rs:111,285): AdamW uses 1
+      linear_update(st, Fl->w1.as<double2>(), n->tr_dw1.as<double2>(), Fl->mw1.as<double2>(), Fl->vw1.as<double2>(),
+                    (long)d * F, Fl->b1.as<double2>(), n->tr_db1.as<double2>(), Fl->mb1.as<double2>(),
+                    Fl->vb1.as<double2>(), F, ts);
+      Fl->updates1++;
+    }
+  }
   if (out_grad_input)
-    HIP_TRY(hipMemcpyAsync(out_grad_input, n->tr_dx.p, (size_t)rows * d * c16, hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipMemcpyAsync(out_grad_input, gin, (size_t)rows * d * c16, hipMemcpyDeviceToHost, st));
   HIP_TRY(hipStreamSynchronize(st));
   return check_err_word(n);
+}
+
+int mitok_backward_head(mitok_network* n, const uint32_t* targets, const uint32_t* tlens, uint32_t B, uint32_t T,
+                        int update_params, double learning_rate, uint32_t time_step, double* out_grad_input) {
+  return backward_impl(n, targets, tlens, B, T, 1, update_params, learning_rate, time_step, out_grad_input);
+}
+
+int mitok_backward(mitok_network* n, const uint32_t* targets, const uint32_t* tlens, uint32_t B, uint32_t T,
+                   uint32_t n_layers, int update_params, double learning_rate, uint32_t time_step,
+                   double* out_grad_input) {
+  return backward_impl(n, targets, tlens, B, T, n_layers, update_params, learning_rate, time_step, out_grad_input);
 }
 
 int mitok_greedy_decoding(mitok_network* n, const double* logits, uint32_t rows, uint32_t V, uint32_t* out_ids) {

@@ -114,6 +114,49 @@ __global__ __launch_bounds__(256) void k_linear_update(double2* __restrict__ W, 
   if (i < V) b[i] = update1(b[i], db[i], &mb[i], &vb[i], ts, false);
 }
 
+// gelu_derivative_complex (utils/derivative.rs:48-84): powi(3) = z (z z),
+// powi(2) = t t; saturated beyond |f(z)| = 20; the result kept to norms in
+// [1e-12, 1e6]
+__device__ __forceinline__ double2 gelu_deriv(double2 z) {
+  const double s2p = sqrt(2.0 / M_PI);
+  const double2 one = make_double2(1.0, 0.0);
+  const double2 x3 = cmul(z, cmul(z, z));
+  const double2 fx = cscale(cadd(z, cmul(make_double2(0.044715, 0.0), x3)), s2p);
+  const bool sat = hypot(fx.x, fx.y) > 20.0;
+  const double2 th = sat ? one : ctanh_nc(fx);
+  const double2 sech2 = sat ? make_double2(0.0, 0.0) : csub(one, cmul(th, th));
+  const double2 fp = cscale(cadd(one, cmul(make_double2(0.134145, 0.0), cmul(z, z))), s2p);
+  const double2 d = cadd(cmul(make_double2(0.5, 0.0), cadd(one, th)),
+                         cmul(cmul(cmul(make_double2(0.5, 0.0), z), sech2), fp));
+  const double n = hypot(d.x, d.y);
+  if (n > 1e6) return cmul(cunscale(d, n), make_double2(1e6, 0.0));
+  if (n < 1e-12) return make_double2(1e-12, 0.0);
+  return d;
+}
+
+// Dense (GELU) backward's elementwise step (layer.rs:181-192): the gradient
+// of the activated output, its padded rows zeroed (apply_padding_mask_batch),
+// times conj(GELU'(Z)) of the pre-activation Z
+__global__ __launch_bounds__(256) void k_gelu_backward(const double2* __restrict__ dH, const double2* __restrict__ Z,
+                                                       const uint32_t* __restrict__ mask, long rows, int F,
+                                                       double2* __restrict__ G) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= rows * F) return;
+  const long r = i / F;
+  double2 g = make_double2(0.0, 0.0);
+  if (!mask || mask[r] != 0) {
+    const double2 dz = gelu_deriv(Z[i]);
+    g = cmul(dH[i], make_double2(dz.x, -dz.y));
+  }
+  G[i] = g;
+}
+
+void gelu_backward(hipStream_t st, const double2* dH, const double2* Z, const uint32_t* mask, long rows, int F,
+                   double2* G) {
+  const long n = rows * F;
+  if (n > 0) MITOK_LAUNCH(k_gelu_backward, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, dH, Z, mask, rows, F, G);
+}
+
 void softmax_grad(hipStream_t st, const double* P, int rows, int V, const int* tgt, const double* norm, int S,
                   double2* G) {
   if (rows > 0) MITOK_LAUNCH(k_softmax_grad, dim3(rows), dim3(256), 0, st, P, V, tgt, norm, S, G);

@@ -752,3 +752,71 @@ def test_linear_update_adamw_steps_reduce_to_normalised_descent():
         want = (W if t == 1 else want) * (1 - 0.01 * lr) - lr * gc / (np.abs(gc) + 1e-8)
         np.testing.assert_allclose(Wt, want, rtol=1e-12, atol=1e-15)
         np.testing.assert_allclose(bt, b * (1 - 0.01 * lr) ** t, rtol=1e-15)
+
+
+def test_gelu_derivative_is_the_complex_derivative_of_gelu():
+    """derivative.rs:48-84 is d/dz of the tanh GELU of activation.rs:195-212
+    (a holomorphic function, so one complex number): central differences along
+    the real and the imaginary axis agree with it; the clamps only act on
+    saturated or vanishing values."""
+    h = 1e-6
+    for z in (0.3 + 0.2j, -1.1 + 0.4j, 2.0 - 0.7j, 0.05j, -0.4 - 0.3j):
+        d = oracle.gelu_derivative(z)
+        g = lambda w: oracle.gelu(w)[0]  # noqa: E731
+        fd_re = (g(z + h) - g(z - h)) / (2 * h)
+        fd_im = (g(z + 1j * h) - g(z - 1j * h)) / (2j * h)
+        assert abs(d - fd_re) < 1e-8 and abs(d - fd_im) < 1e-8, (z, d, fd_re, fd_im)
+    assert oracle.gelu_derivative(40.0 + 0j) == 1.0  # saturated: 0.5 (1 + 1) + 0
+
+
+def test_ffn_and_head_gradients_match_finite_differences():
+    """The reverse walk through the vocab Linear and the FeedForward below it
+    (Dense + GELU -> Linear; feedforward_layer.rs:140-186, layer.rs:168-210,
+    linear_layer.rs:77-128) gives dL/dRe + i dL/dIm of the cross-entropy in
+    every real coordinate of W1, b1, W2, b2 and the FFN input; a padded row
+    (mask 0) gets no gradient through the Dense layer."""
+    rng = np.random.default_rng(43)
+    B, S, d, F, V = 2, 4, 3, 4, 5
+    X = 0.5 * (rng.standard_normal((B, S, d)) + 1j * rng.standard_normal((B, S, d)))
+    W1 = 0.5 * (rng.standard_normal((d, F)) + 1j * rng.standard_normal((d, F)))
+    b1 = 0.3 * (rng.standard_normal(F) + 1j * rng.standard_normal(F))
+    W2 = 0.5 * (rng.standard_normal((F, d)) + 1j * rng.standard_normal((F, d)))
+    b2 = 0.3 * (rng.standard_normal(d) + 1j * rng.standard_normal(d))
+    Wv = 0.7 * (rng.standard_normal((d, V)) + 1j * rng.standard_normal((d, V)))
+    bv = rng.standard_normal(V) + 1j * rng.standard_normal(V)
+    mask = np.array([[1, 1, 1, 1], [1, 1, 1, 0]], np.uint32)
+    targets = np.array([[3, 1], [0, 4]], np.uint32)
+    gelu = np.vectorize(lambda z: oracle.gelu(z)[0])
+
+    def forward(X, W1, b1, W2, b2):
+        Z = X @ W1 + b1
+        H = gelu(Z) * mask[:, :, None]  # activate_output_complex_padding
+        Y = H @ W2 + b2
+        return Z, H, Y
+
+    def loss(X, W1, b1, W2, b2):
+        P = _softmax_re(forward(X, W1, b1, W2, b2)[2] @ Wv + bv)
+        L = 0.0
+        for bb, row, tgt, norm in ((0, 1, 3, 2), (1, 1, 0, 4), (1, 2, 4, 4)):
+            L -= np.log(P[bb, row, tgt]) / norm
+        return L
+
+    Z, H, Y = forward(X, W1, b1, W2, b2)
+    G = oracle.softmax_backward(_softmax_re(Y @ Wv + bv), targets)
+    _, _, dY = oracle.linear_backward(Y, G, Wv)
+    dW2, db2, dH = oracle.linear_backward_c(H, dY, W2)
+    dW1, db1, dX = oracle.dense_backward(X, Z, dH, mask, W1)
+    assert np.all(dX[1, 3] == 0)
+    params = [X, W1, b1, W2, b2]
+    grads = [dX, dW1, db1, dW2, db2]
+    h = 1e-6
+    for k, (arr, grad) in enumerate(zip(params, grads)):
+        for idx in np.ndindex(arr.shape):
+            for unit, part in ((1.0, "real"), (1j, "imag")):
+                args = [p.copy() for p in params]
+                args[k][idx] += h * unit
+                lp = loss(*args)
+                args[k][idx] -= 2 * h * unit
+                lm = loss(*args)
+                fd = (lp - lm) / (2 * h)
+                assert abs(getattr(grad[idx], part) - fd) < 1e-7, (k, idx, part, grad[idx], fd)

@@ -178,13 +178,28 @@ int mitok_decode_step(mitok_network* net, const uint32_t* ids, uint32_t batch, u
  * are not differentiated. */
 int mitok_backward_head(mitok_network* net, const uint32_t* targets, const uint32_t* tlens, uint32_t batch, uint32_t T,
                         int update_params, double learning_rate, uint32_t time_step, double* out_grad_input);
-/* The same reverse walk through n_layers layers below the Softmax: 1 = the
- * vocab Linear (mitok_backward_head), 2 = also the FeedForward right below it
- * (feedforward_layer.rs:140-186: its Linear, then its Dense with the GELU
- * derivative of utils/derivative.rs:48-84; with update_params both updated,
- * the Linear at time_step and the Dense at step 1, since Layer::time_step is
- * never set, layer.rs:111,285).  out_grad_input is then the gradient of that
- * FeedForward's input [batch][seq'][d]. */
+/* The same reverse walk (transformer_network.rs:506-636) through n_layers
+ * layers below the Softmax: 1 = the vocab Linear (mitok_backward_head), up to
+ * every layer the stateless predict ran.  Each layer's backward and, with
+ * update_params, its update_parameters where the walk calls it:
+ *  - Linear: as above, at time_step;
+ *  - FeedForward (feedforward_layer.rs:140-186, 219-250): its Linear at
+ *    time_step, then its Dense with the GELU derivative of
+ *    utils/derivative.rs:48-84 at step 1 (Layer::time_step is never set,
+ *    layer.rs:111,285);
+ *  - SelfAttention (self_attention_layer.rs:135-196, 260-273): its Norm's
+ *    backward (norm_layer.rs:132-209), then every head
+ *    (masked_attention_head.rs:222-345); updates the Norm's gamma and beta,
+ *    wq / wk / wv and Re(bias_pos) on the pass's S x S slice;
+ *  - Norm (backward only), PositionalEncoding (positional_encoding_layer.rs:
+ *    101-144);
+ *  - Embedding: passes the gradient on; with update_params
+ *    EmbeddingLayer::update_parameters (embedding_layer.rs:223-264) moves and
+ *    renormalizes the table rows of the target ids.
+ * A DiscreteWavelet layer in the walk is MITOK_ERR_STATE (its training pass
+ * splits input and target rows, wavelet_discrete_layer.rs:233-279).
+ * out_grad_input: the gradient of the lowest walked layer's input
+ * [batch][seq'][its d_in], or NULL. */
 int mitok_backward(mitok_network* net, const uint32_t* targets, const uint32_t* tlens, uint32_t batch, uint32_t T,
                    uint32_t n_layers, int update_params, double learning_rate, uint32_t time_step,
                    double* out_grad_input);

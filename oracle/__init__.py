@@ -83,6 +83,13 @@ def _load():
         "orc_linear_backward_c": (i32, [P, P, P, u32, u32, u32, u32, P, P, P]),
         "orc_gelu_derivative": (_C64, [_C64]),
         "orc_dense_backward": (i32, [P, P, P, P, P, u32, u32, u32, u32, P, P, P]),
+        "orc_norm_backward": (i32, [P, u64, u32, f64, P, P, P, P, P, P]),
+        "orc_attention_heads_backward": (i32, [P, u32, u32, P, u32, u32, u32, P, P, P, P, P, P, P, P, P, P]),
+        "orc_self_attention_backward": (i32, [P, u32, u32, P, u32, u32, u32, f64, P, P, P, P, P, P, P, P, P, P, P,
+                                              P, P, P]),
+        "orc_rope_backward": (i32, [P, u32, u32, u32, f64, P]),
+        "orc_embedding_update": (i32, [P, u32, u32, P, u32, u32, P, P, u32, f64]),
+        "orc_param_update": (i32, [P, P, P, P, u64, i32, f64, f64, u32, i32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -238,6 +245,94 @@ def linear_update(W, b, dW, db, batch, state, first, lr, time_step):
     _check(lib().orc_linear_update(_ptr(W), _ptr(b), d, V, _ptr(dW), _ptr(db), batch, *[_ptr(a) for a in state],
                                    int(first), float(lr), int(time_step)))
     return W, b
+
+
+def norm_backward(x, gamma, beta, dout, eps):
+    """NormalNormLayer::backward, Complex arm (norm_layer.rs:132-209) on rows
+    x [..][n] of the layer's input: (dx, dgamma, dbeta)."""
+    x, dout = _c128(x), _c128(dout)
+    gamma, beta = _c128(gamma), _c128(beta)
+    n = x.shape[-1]
+    rows = x.size // n
+    dx = np.empty_like(x)
+    dg = np.empty(n, np.complex128)
+    db = np.empty(n, np.complex128)
+    _check(lib().orc_norm_backward(_ptr(x), rows, n, float(eps), _ptr(gamma), _ptr(beta), _ptr(dout), _ptr(dx), _ptr(dg),
+                                   _ptr(db)))
+    return dx, dg, db
+
+
+def attention_heads_backward(X, mask, wq, wk, wv, bias_pos, Gc):
+    """MaskedAttentionHead::backward of every head (masked_attention_head.rs:
+    222-345) for the gradient Gc [B][S][d] of the heads' concatenated output:
+    (dX, dwq, dwk, dwv [H][d][dh], dbias [H][S][S])."""
+    X, Gc = _c128(X), _c128(Gc)
+    wq, wk, wv, bias_pos = _c128(wq), _c128(wk), _c128(wv), _c128(bias_pos)
+    m = np.ascontiguousarray(mask, dtype=np.uint32)
+    B, S, d = X.shape
+    H, mc = bias_pos.shape[0], bias_pos.shape[1]
+    dX = np.empty_like(X)
+    dw = [np.empty_like(wq) for _ in range(3)]
+    dbias = np.empty((H, S, S), np.complex128)
+    _check(lib().orc_attention_heads_backward(_ptr(X), B, S, _ptr(m), H, d, mc, _ptr(wq), _ptr(wk), _ptr(wv),
+                                              _ptr(bias_pos), _ptr(Gc), _ptr(dX), *[_ptr(a) for a in dw], _ptr(dbias)))
+    return (dX, *dw, dbias)
+
+
+def self_attention_backward(X, mask, wq, wk, wv, bias_pos, gamma, beta, G, eps=1e-12):
+    """SelfAttentionLayer::backward (self_attention_layer.rs:135-196): its
+    Norm's backward, then the heads.  (dX, dwq, dwk, dwv, dbias, dgamma,
+    dbeta)."""
+    X, G = _c128(X), _c128(G)
+    wq, wk, wv, bias_pos = _c128(wq), _c128(wk), _c128(wv), _c128(bias_pos)
+    gamma, beta = _c128(gamma), _c128(beta)
+    m = np.ascontiguousarray(mask, dtype=np.uint32)
+    B, S, d = X.shape
+    H, mc = bias_pos.shape[0], bias_pos.shape[1]
+    dX = np.empty_like(X)
+    dw = [np.empty_like(wq) for _ in range(3)]
+    dbias = np.empty((H, S, S), np.complex128)
+    dg = np.empty(d, np.complex128)
+    db = np.empty(d, np.complex128)
+    _check(lib().orc_self_attention_backward(_ptr(X), B, S, _ptr(m), H, d, mc, float(eps), _ptr(wq), _ptr(wk), _ptr(wv),
+                                             _ptr(bias_pos), _ptr(gamma), _ptr(beta), _ptr(G), _ptr(dX),
+                                             *[_ptr(a) for a in dw], _ptr(dbias), _ptr(dg), _ptr(db)))
+    return (dX, *dw, dbias, dg, db)
+
+
+def rope_backward(G, base=1250.0):
+    """PositionalEncodingLayer::backward (positional_encoding_layer.rs:101-144)."""
+    G = _c128(G)
+    B, S, d = G.shape
+    out = np.empty_like(G)
+    _check(lib().orc_rope_backward(_ptr(G), B, S, d, float(base), _ptr(out)))
+    return out
+
+
+def embedding_update(table, G, targets, tlens, lr):
+    """EmbeddingLayer::update_parameters (embedding_layer.rs:223-264): the
+    new table."""
+    table = _c128(table).copy()
+    G = _c128(G)
+    V, d = table.shape
+    B, S, _ = G.shape
+    t = np.ascontiguousarray(targets, dtype=np.uint32)
+    tl = np.ascontiguousarray(tlens, dtype=np.uint32)
+    _check(lib().orc_embedding_update(_ptr(table), V, d, _ptr(G), B, S, _ptr(t), _ptr(tl), t.shape[1], float(lr)))
+    return table
+
+
+def param_update(w, g, state, first, lr, batch, time_step, weight=True):
+    """One parameter array's update arm: clipped descent on the first update,
+    else calculate_adam_w (weight) / calculate_adam_w_bias (adam_w.rs:9-103).
+    Returns the new array; state = [m, v] is updated in place."""
+    w = _c128(w).copy()
+    g = _c128(g)
+    for a in state:
+        assert a.dtype == np.complex128 and a.flags.c_contiguous and a.size == w.size
+    _check(lib().orc_param_update(_ptr(w), _ptr(g), _ptr(state[0]), _ptr(state[1]), w.size, int(first), float(lr),
+                                  float(batch), int(time_step), int(bool(weight))))
+    return w
 
 
 def zgemm(A: np.ndarray, B: np.ndarray) -> np.ndarray:

@@ -822,7 +822,7 @@ static void norm_forward(double eps, const oc64* gamma, const oc64* beta, const 
 /* MaskedAttentionHead::forward for all heads + SelfAttentionLayer::forward
  * (masked_attention_head.rs:122-220, self_attention_layer.rs:55-133). */
 static int self_attention_forward(orc_layer* L, const oc64* x, const uint32_t* mask, const uint32_t* lens,
-                                  uint32_t B, uint32_t S, int forward_only, oc64* out) {
+                                  uint32_t B, uint32_t S, int forward_only, oc64* out, oc64* concat_out) {
   const uint32_t d = L->d_in, H = L->heads, dh = L->dh, mc = L->max_ctx;
   const int decode = forward_only && L->cache_valid;
   if (decode && B != L->cache_B) return fail(ORC_ERR_STATE, "cached batch %u != %u; reset first", L->cache_B, B);
@@ -933,8 +933,9 @@ static int self_attention_forward(orc_layer* L, const oc64* x, const uint32_t* m
     free(q);
     free(sc);
   }
-  /* residual + LayerNorm (:101-124) */
-  norm_forward(L->eps, L->gamma, L->beta, concat, x, (uint64_t)B * S, d, out);
+  /* residual + LayerNorm (:101-124); the heads' output alone on request */
+  if (concat_out) memcpy(concat_out, concat, (size_t)B * S * d * sizeof(oc64));
+  if (out) norm_forward(L->eps, L->gamma, L->beta, concat, x, (uint64_t)B * S, d, out);
   free(concat);
   free(knew);
   free(vnew);
@@ -1005,7 +1006,7 @@ static int run_layer(orc_layer* L, oc64** cur, oc64** nxt, uint64_t* cap, const 
   int rc = ORC_OK;
   switch (L->kind) {
     case ORC_NORM: norm_forward(L->eps, L->gamma, L->beta, *cur, NULL, rows, L->d_in, *nxt); break;
-    case ORC_SELF_ATTENTION: rc = self_attention_forward(L, *cur, mask, lens, B, S, forward_only, *nxt); break;
+    case ORC_SELF_ATTENTION: rc = self_attention_forward(L, *cur, mask, lens, B, S, forward_only, *nxt, NULL); break;
     case ORC_FEED_FORWARD: rc = ffn_forward(L, *cur, mask, rows, *nxt); break;
     case ORC_LINEAR: linear_forward(L, *cur, rows, *nxt); break;
     default: return fail(ORC_ERR_ARG, "layer kind %d is not a hidden-state layer", L->kind);
@@ -1436,4 +1437,361 @@ int orc_dense_backward(const oc64* X, const oc64* Z, const oc64* prev, const uin
   const int rc = orc_linear_backward_c(X, g, W, B, S, d, F, dW, db, dX);
   free(g);
   return rc;
+}
+
+/* ======================================================================
+ * The rest of backward's reverse walk (transformer_network.rs:506-636):
+ * NormalNormLayer::backward, MaskedAttentionHead::backward for every head
+ * under SelfAttentionLayer::backward, PositionalEncodingLayer::backward,
+ * EmbeddingLayer::update_parameters, and the updates of the attention layer.
+ * Parity anchors (tests/test_oracle_pins.py): the heads' gradients against
+ * finite differences of a real loss in every real coordinate; RoPE's
+ * backward as the adjoint of its forward; the Norm backward only through its
+ * structure (real rows, linear plus quadratic in the incoming gradient), as
+ * the formula is the reference's own and no closed form fixes it; the
+ * embedding update through its one-hot reach and the normalized rows.
+ * ====================================================================== */
+
+/* Complex::powf (num-complex 0.4.6): from_polar(r^e, theta * e) */
+static oc64 c_powf(oc64 z, double e) {
+  if (e == 0.0) return (oc64){1.0, 0.0};
+  const double r = pow(hypot(z.re, z.im), e), th = atan2(z.im, z.re) * e;
+  return (oc64){r * cos(th), r * sin(th)};
+}
+
+/* f64 / Complex (num-complex 0.4.6): a (c - i d) / (c c + d d) */
+static oc64 r_div_c(double a, oc64 z) {
+  const double ns = z.re * z.re + z.im * z.im;
+  return (oc64){a * z.re / ns, -a * z.im / ns};
+}
+
+/* NormalNormLayer::backward, Complex arm (norm_layer.rs:132-209), one row at a
+ * time as the reference loops: x the layer's input row, its forward recomputed
+ * (normalize, :64-82) for x_hat, mean and variance.  dgamma / dbeta receive
+ * the row's contribution (added in, so the caller zeroes them first). */
+static void norm_backward_row(const oc64* x, uint32_t n, double eps_fwd, const oc64* gamma, const oc64* beta,
+                              const oc64* dout, oc64* dx, oc64* dgamma, oc64* dbeta, oc64* xhat) {
+  orc_layernorm_row(x, n, eps_fwd, gamma, beta, xhat);
+  const double len = (double)n;
+  oc64 sum = {0.0, 0.0};
+  for (uint32_t i = 0; i < n; ++i) sum = c_add(sum, x[i]);
+  const oc64 mu = c_unscale(sum, len);
+  oc64 vs = {0.0, 0.0};
+  for (uint32_t i = 0; i < n; ++i) {
+    const oc64 t = c_sub(x[i], mu);
+    vs = c_add(vs, c_mul(t, t));
+  }
+  const oc64 var = c_add(c_unscale(vs, len), (oc64){1e-8, 0.0}); /* var_batch + eps (:158-159) */
+  const oc64 std_inv = r_div_c(1.0, c_sqrt(var));
+  const oc64 vpm32 = r_div_c(1.0, c_powf(var, 1.5));
+  const oc64 neg_std_inv = {-std_inv.re, -std_inv.im};
+  for (uint32_t j = 0; j < n; ++j) dx[j] = (oc64){0.0, 0.0};
+  for (uint32_t f = 0; f < n; ++f) {
+    oc64 dvar_sum = {0.0, 0.0}, dmu_sum = {0.0, 0.0}, dxmm_sum = {0.0, 0.0};
+    for (uint32_t d = 0; d < n; ++d) {
+      const oc64 dxm = c_sub(x[d], mu);
+      dgamma[d] = c_add(dgamma[d], c_mul(dout[d], xhat[d]));
+      dbeta[d] = c_add(dbeta[d], dout[d]);
+      const oc64 dxhat = c_mul(dout[d], gamma[f]);
+      dvar_sum = c_add(dvar_sum, c_mul(c_scale(c_mul(dxhat, dxm), -0.5), vpm32));
+      dxmm_sum = c_add(dxmm_sum, c_unscale(c_scale(dxm, -2.0), len));
+    }
+    for (uint32_t d = 0; d < n; ++d) dmu_sum = c_add(dmu_sum, c_mul(dout[d], neg_std_inv));
+    const oc64 dxhat = c_mul(dout[f], gamma[f]);
+    const oc64 dmu = c_add(c_mul(dmu_sum, gamma[f]), c_mul(dvar_sum, dxmm_sum));
+    const oc64 g = c_add(c_add(c_mul(dxhat, std_inv), c_mul(dvar_sum, c_unscale(c_scale(c_sub(x[f], mu), 2.0), len))),
+                         c_unscale(dmu, len));
+    for (uint32_t j = 0; j < n; ++j) {
+      const oc64 t = c_add(c_scale(g, j == f ? 1.0 : 0.0), c_mul(g, dout[j]));
+      dx[j] = c_add(dx[j], (oc64){t.re, 0.0});
+    }
+  }
+}
+
+int orc_norm_backward(const oc64* x, uint64_t rows, uint32_t n, double eps, const oc64* gamma, const oc64* beta,
+                      const oc64* dout, oc64* dx, oc64* dgamma, oc64* dbeta) {
+  if (!x || !gamma || !beta || !dout || !dx || !dgamma || !dbeta || !rows || !n) return fail(ORC_ERR_ARG, "bad arguments");
+  oc64* xhat = (oc64*)malloc((size_t)n * sizeof(oc64));
+  if (!xhat) return fail(ORC_ERR_NOMEM, "norm backward: out of memory");
+  memset(dgamma, 0, (size_t)n * sizeof(oc64));
+  memset(dbeta, 0, (size_t)n * sizeof(oc64));
+  for (uint64_t r = 0; r < rows; ++r)
+    norm_backward_row(x + r * n, n, eps, gamma, beta, dout + r * n, dx + r * n, dgamma, dbeta, xhat);
+  free(xhat);
+  return ORC_OK;
+}
+
+/* multiply_complex_with_f64 (utils/matrix.rs:328-354): complex [m][k] x real [k][n] */
+static void zgemm_cr(uint32_t m, uint32_t n, uint32_t k, const oc64* A, const double* Bm, oc64* C) {
+  for (uint32_t i = 0; i < m; ++i)
+    for (uint32_t j = 0; j < n; ++j) {
+      oc64 acc = {0.0, 0.0};
+      for (uint32_t t = 0; t < k; ++t) acc = c_add(acc, c_scale(A[(size_t)i * k + t], Bm[(size_t)t * n + j]));
+      C[(size_t)i * n + j] = acc;
+    }
+}
+
+/* out[c][r] = conj?(in[r][c]) */
+static void ztrans(uint32_t R, uint32_t C, const oc64* in, int conj, oc64* out) {
+  for (uint32_t r = 0; r < R; ++r)
+    for (uint32_t c = 0; c < C; ++c) {
+      const oc64 v = in[(size_t)r * C + c];
+      out[(size_t)c * R + r] = conj ? (oc64){v.re, -v.im} : v;
+    }
+}
+
+/* MaskedAttentionHead::backward of every head for one batch of rows
+ * (masked_attention_head.rs:222-345), the heads' input gradients summed in
+ * head order (self_attention_layer.rs:160-190).  X [B][S][d] the layer's
+ * input; Gc [B][S][d] the gradient of the heads' concatenated output, head h
+ * in columns h*dh.. (split_gradient_into_heads, :232-258).  The weight and
+ * bias gradients are grouped over the batch (gradient_struct.rs:400-411). */
+int orc_attention_heads_backward(const oc64* X, uint32_t B, uint32_t S, const uint32_t* mask, uint32_t H, uint32_t d,
+                                 uint32_t mc, const oc64* wq, const oc64* wk, const oc64* wv, const oc64* bias_pos,
+                                 const oc64* Gc, oc64* dX, oc64* dwq, oc64* dwk, oc64* dwv, oc64* dbias) {
+  if (!X || !mask || !wq || !wk || !wv || !bias_pos || !Gc || !dX || !dwq || !dwk || !dwv || !dbias || !B || !S || !H ||
+      !d || d % H || S > mc)
+    return fail(ORC_ERR_ARG, "bad arguments");
+  const uint32_t dh = d / H;
+  const size_t wn = (size_t)d * dh;
+  const double c = 1.0 / (1e-8 + sqrt((double)dh)); /* scale_attention_scores with d_k = dh */
+  const size_t SS = (size_t)S * S, Sd = (size_t)S * dh, dS = (size_t)d * S;
+  oc64 *q = malloc(Sd * 16), *k = malloc(Sd * 16), *v = malloc(Sd * 16), *g = malloc(Sd * 16), *gt = malloc(Sd * 16);
+  oc64 *xh = malloc(dS * 16), *grad_wv = malloc(Sd * 16), *t1 = malloc(Sd * 16), *t2 = malloc(Sd * 16);
+  oc64 *ks = malloc(Sd * 16), *qs = malloc(Sd * 16), *vh = malloc(Sd * 16), *dlds = malloc(SS * 16);
+  oc64 *dldq = malloc(Sd * 16), *dldk = malloc(Sd * 16), *wg = malloc(wn * 16), *wh = malloc(wn * 16);
+  oc64 *dx1 = malloc(Sd > dS ? Sd * 16 : dS * 16), *dx2 = malloc(dS * 16), *dx3 = malloc(dS * 16);
+  oc64* sc = malloc((size_t)S * 16);
+  double *A = malloc(SS * 8), *dA = malloc(SS * 8), *dAt = malloc(SS * 8);
+  int rc = ORC_OK;
+  if (!q || !k || !v || !g || !gt || !xh || !grad_wv || !t1 || !t2 || !ks || !qs || !vh || !dlds || !dldq || !dldk ||
+      !wg || !wh || !dx1 || !dx2 || !dx3 || !sc || !A || !dA || !dAt) {
+    rc = fail(ORC_ERR_NOMEM, "attention backward: out of memory");
+    goto done;
+  }
+  memset(dX, 0, (size_t)B * S * d * 16);
+  memset(dwq, 0, (size_t)H * wn * 16);
+  memset(dwk, 0, (size_t)H * wn * 16);
+  memset(dwv, 0, (size_t)H * wn * 16);
+  memset(dbias, 0, (size_t)H * SS * 16);
+  for (uint32_t h = 0; h < H; ++h) {
+    const oc64 *Wq = wq + h * wn, *Wk = wk + h * wn, *Wv = wv + h * wn, *bp = bias_pos + (size_t)h * mc * mc;
+    for (uint32_t b = 0; b < B; ++b) {
+      const oc64* xb = X + (size_t)b * S * d;
+      const uint32_t* mk = mask + (size_t)b * S;
+      zgemm_serial(S, dh, d, xb, Wq, q); /* :239-241 */
+      zgemm_serial(S, dh, d, xb, Wk, k);
+      zgemm_serial(S, dh, d, xb, Wv, v);
+      /* the forward's attention weights (:184-205): softmax of Re over the
+       * scaled, biased, causally masked scores; padded rows 0 */
+      for (uint32_t r = 0; r < S; ++r) {
+        double* a = A + (size_t)r * S;
+        if (mk[r] == 0) {
+          for (uint32_t j = 0; j < S; ++j) a[j] = 0.0;
+          continue;
+        }
+        for (uint32_t j = 0; j < S; ++j) {
+          oc64 s = {0.0, 0.0};
+          for (uint32_t e = 0; e < dh; ++e) s = c_add(s, c_mul(q[(size_t)r * dh + e], k[(size_t)j * dh + e]));
+          s = c_add(c_scale(s, c), bp[(size_t)r * mc + j]);
+          sc[j] = j > r ? (oc64){-1e12, -1e12} : s;
+        }
+        orc_softmax_row_real(sc, S, a);
+      }
+      for (uint32_t r = 0; r < S; ++r) /* this head's slice of the gradient */
+        memcpy(g + (size_t)r * dh, Gc + ((size_t)b * S + r) * d + (size_t)h * dh, dh * 16);
+      ztrans(S, dh, g, 0, gt);                 /* transpose(previous_gradient) [dh][S] */
+      zgemm_cr(dh, S, S, gt, A, grad_wv);      /* :276 */
+      ztrans(S, d, xb, 1, xh);                 /* conjugate_transpose(input) [d][S] */
+      ztrans(dh, S, grad_wv, 0, t1);           /* transpose(grad_wv) [S][dh] */
+      zgemm_serial(d, dh, S, xh, t1, wg);      /* :278 */
+      for (size_t i = 0; i < wn; ++i) dwv[h * wn + i] = c_add(dwv[h * wn + i], wg[i]);
+      ztrans(S, dh, k, 0, ks); /* k_scaled = transpose(k) * c [dh][S] (:281) */
+      for (size_t i = 0; i < Sd; ++i) ks[i] = c_scale(ks[i], c);
+      for (size_t i = 0; i < Sd; ++i) qs[i] = c_scale(q[i], c); /* q_scaled [S][dh] (:282) */
+      ztrans(S, dh, v, 1, vh);                 /* conjugate_transpose(v) [dh][S] */
+      zgemm_serial(S, S, dh, g, vh, dlds);     /* dl_ds (:294) */
+      /* backpropagate_softmax_masked_real over the row Jacobians
+       * s_j (delta_jk - s_k) (utils/derivative.rs:100-131, 253-272) */
+      for (uint32_t i = 0; i < S; ++i)
+        for (uint32_t j = 0; j < S; ++j) {
+          double acc = 0.0;
+          if (mk[i] != 0) {
+            const double* s = A + (size_t)i * S;
+            for (uint32_t kk = 0; kk < S; ++kk) {
+              const double jac = j == kk ? s[j] * (1.0 - s[j]) : -s[j] * s[kk];
+              acc += jac * dlds[(size_t)i * S + kk].re;
+            }
+          }
+          dA[(size_t)i * S + j] = acc;
+        }
+      for (uint32_t i = 0; i < S; ++i)
+        for (uint32_t j = 0; j < S; ++j) dAt[(size_t)j * S + i] = dA[(size_t)i * S + j];
+      zgemm_cr(dh, S, S, ks, dAt, dldq);       /* dl_dq [dh][S] (:301) */
+      ztrans(dh, S, dldq, 1, t1);              /* conjugate_transpose(dl_dq) [S][dh] */
+      zgemm_serial(d, dh, S, xh, t1, wg);      /* :305 */
+      for (size_t i = 0; i < wn; ++i) dwq[h * wn + i] = c_add(dwq[h * wn + i], wg[i]);
+      ztrans(S, dh, qs, 1, t2);                /* conjugate_transpose(q_scaled) [dh][S] */
+      zgemm_cr(dh, S, S, t2, dA, dldk);        /* dl_dk [dh][S] (:312) */
+      ztrans(dh, S, dldk, 0, t2);              /* transpose(dl_dk) [S][dh] */
+      zgemm_serial(d, dh, S, xh, t2, wg);      /* :316 */
+      for (size_t i = 0; i < wn; ++i) dwk[h * wn + i] = c_add(dwk[h * wn + i], wg[i]);
+      ztrans(d, dh, Wq, 1, wh);                /* conjugate_transpose(weights_q) [dh][d] */
+      zgemm_serial(S, d, dh, t1, wh, dx1);     /* dl_dqx (:328) */
+      ztrans(d, dh, Wk, 1, wh);
+      zgemm_serial(S, d, dh, t2, wh, dx2);     /* dl_dkx (:330) */
+      ztrans(dh, S, grad_wv, 0, t1);
+      ztrans(d, dh, Wv, 1, wh);
+      zgemm_serial(S, d, dh, t1, wh, dx3);     /* dl_dvx (:332) */
+      oc64* db = dbias + (size_t)h * SS;
+      for (size_t i = 0; i < SS; ++i) db[i] = c_add(db[i], (oc64){dA[i], 0.0}); /* convert_to_c_f64_2d (:334) */
+      oc64* dxb = dX + (size_t)b * S * d;
+      for (size_t i = 0; i < dS; ++i) dxb[i] = c_add(dxb[i], c_add(c_add(dx1[i], dx2[i]), dx3[i])); /* :335-339 */
+    }
+  }
+done:
+  free(q), free(k), free(v), free(g), free(gt), free(xh), free(grad_wv), free(t1), free(t2), free(ks), free(qs);
+  free(vh), free(dlds), free(dldq), free(dldk), free(wg), free(wh), free(dx1), free(dx2), free(dx3), free(sc);
+  free(A), free(dA), free(dAt);
+  return rc;
+}
+
+/* SelfAttentionLayer::backward (self_attention_layer.rs:135-196): the Norm's
+ * backward on the layer's gradient, its input being Re(heads' output + X)
+ * (the residual, add_matrix_3d_c), then the heads.  No residual gradient is
+ * added: the layer returns the heads' input gradient only. */
+int orc_self_attention_backward(const oc64* X, uint32_t B, uint32_t S, const uint32_t* mask, uint32_t H, uint32_t d,
+                                uint32_t mc, double eps, const oc64* wq, const oc64* wk, const oc64* wv,
+                                const oc64* bias_pos, const oc64* gamma, const oc64* beta, const oc64* G, oc64* dX,
+                                oc64* dwq, oc64* dwk, oc64* dwv, oc64* dbias, oc64* dgamma, oc64* dbeta) {
+  if (!X || !mask || !G || !B || !S || !H || !d || d % H || S > mc) return fail(ORC_ERR_ARG, "bad arguments");
+  const size_t rows = (size_t)B * S;
+  orc_layer L;
+  memset(&L, 0, sizeof L);
+  L.kind = ORC_SELF_ATTENTION;
+  L.heads = H;
+  L.d_in = L.d_out = d;
+  L.dh = d / H;
+  L.max_ctx = mc;
+  L.eps = eps;
+  L.wq = (oc64*)wq, L.wk = (oc64*)wk, L.wv = (oc64*)wv, L.bias_pos = (oc64*)bias_pos;
+  L.gamma = (oc64*)gamma, L.beta = (oc64*)beta;
+  oc64* xn = malloc(rows * d * 16);
+  oc64* gn = malloc(rows * d * 16);
+  uint32_t* lens = malloc((size_t)B * 4);
+  int rc = ORC_OK;
+  if (!xn || !gn || !lens) {
+    rc = fail(ORC_ERR_NOMEM, "self-attention backward: out of memory");
+    goto done;
+  }
+  for (uint32_t b = 0; b < B; ++b) lens[b] = S;
+  /* the Norm's input: the heads' output of a stateless forward plus the
+   * residual, real part only (add_matrix_3d_c) */
+  rc = self_attention_forward(&L, X, mask, lens, B, S, 0, NULL, xn);
+  if (rc) goto done;
+  for (size_t i = 0; i < rows * d; ++i) xn[i] = (oc64){xn[i].re + X[i].re, 0.0};
+  if ((rc = orc_norm_backward(xn, rows, d, eps, gamma, beta, G, gn, dgamma, dbeta))) goto done;
+  rc = orc_attention_heads_backward(X, B, S, mask, H, d, mc, wq, wk, wv, bias_pos, gn, dX, dwq, dwk, dwv, dbias);
+done:
+  free(xn), free(gn), free(lens);
+  return rc;
+}
+
+/* PositionalEncodingLayer::backward (positional_encoding_layer.rs:101-144):
+ * each row's pairs rotated back by its position's angle (the row index) */
+int orc_rope_backward(const oc64* G, uint32_t B, uint32_t S, uint32_t d, double base, oc64* out) {
+  if (!G || !out || !B || !S || !d || d % 2) return fail(ORC_ERR_ARG, "bad arguments");
+  const uint32_t half = d / 2;
+  for (uint32_t b = 0; b < B; ++b)
+    for (uint32_t s = 0; s < S; ++s) {
+      const oc64* g = G + ((size_t)b * S + s) * d;
+      oc64* o = out + ((size_t)b * S + s) * d;
+      for (uint32_t i = 0; i < half; ++i) {
+        double theta = (double)s / pow(base * 1.0, 2.0 * (double)i / (double)d);
+        if (theta < -1.0) theta = -1.0;
+        if (theta > 1.0) theta = 1.0;
+        const double sn = sin(theta), cs = cos(theta);
+        const oc64 ge = g[2 * i], go = g[2 * i + 1];
+        o[2 * i] = (oc64){ge.re * cs + go.re * sn, ge.im * cs + go.im * sn};
+        o[2 * i + 1] = (oc64){-ge.re * sn + go.re * cs, -ge.im * sn + go.im * cs};
+      }
+    }
+  return ORC_OK;
+}
+
+/* utils/normalization.rs:3-20 */
+static void normalize_row(oc64* x, uint32_t n) {
+  const double len = (double)n;
+  oc64 sum = {0.0, 0.0};
+  for (uint32_t i = 0; i < n; ++i) sum = c_add(sum, x[i]);
+  const oc64 mean = c_unscale(sum, len);
+  oc64 vs = {0.0, 0.0};
+  for (uint32_t i = 0; i < n; ++i) {
+    const oc64 t = c_sub(x[i], mean);
+    vs = c_add(vs, c_mul(t, t));
+  }
+  const oc64 sd = c_sqrt(c_add(c_unscale(vs, len), (oc64){0.00000000001, 0.0}));
+  for (uint32_t i = 0; i < n; ++i) x[i] = c_div(c_sub(x[i], mean), sd);
+}
+
+/* EmbeddingLayer::update_parameters (embedding_layer.rs:223-264): per
+ * sequence, its gradient rows clipped elementwise, then for target t the
+ * table row of that target id moves by lr * (row t of the gradient) / (B * V)
+ * and is normalized, in order (a repeated id sees its updated row). */
+int orc_embedding_update(oc64* table, uint32_t V, uint32_t d, const oc64* G, uint32_t B, uint32_t S,
+                         const uint32_t* targets, const uint32_t* tlens, uint32_t T, double lr) {
+  if (!table || !G || !targets || !tlens || !V || !d || !B || !S) return fail(ORC_ERR_ARG, "bad arguments");
+  const double bs = (double)B * (double)V;
+  oc64* g = (oc64*)malloc((size_t)S * d * sizeof(oc64));
+  if (!g) return fail(ORC_ERR_NOMEM, "embedding update: out of memory");
+  int rc = ORC_OK;
+  for (uint32_t b = 0; b < B && !rc; ++b) {
+    for (size_t i = 0; i < (size_t)S * d; ++i) g[i] = clip1(G[(size_t)b * S * d + i], 1.0);
+    if (tlens[b] > T || tlens[b] > S) {
+      rc = fail(ORC_ERR_ARG, "sequence %u: %u targets", b, tlens[b]);
+      break;
+    }
+    for (uint32_t t = 0; t < tlens[b]; ++t) {
+      const uint32_t id = targets[(size_t)b * T + t];
+      if (id >= V) {
+        rc = fail(ORC_ERR_ARG, "No token embedding found: %u", id);
+        break;
+      }
+      oc64* row = table + (size_t)id * d;
+      for (uint32_t j = 0; j < d; ++j) {
+        const oc64 gj = g[(size_t)t * d + j];
+        if (!finite_c(gj)) {
+          rc = fail(ORC_ERR_NAN, "gradient in embedding is invalid");
+          break;
+        }
+        row[j] = c_sub(row[j], c_scale(c_unscale(gj, bs), lr));
+        if (!finite_c(row[j])) {
+          rc = fail(ORC_ERR_NAN, "embedding is invalid");
+          break;
+        }
+      }
+      if (rc) break;
+      normalize_row(row, d);
+    }
+  }
+  free(g);
+  return rc;
+}
+
+/* One parameter array's update_parameters arm: the first update's clipped
+ * descent (lr * clip(g) / batch where finite), later ones calculate_adam_w
+ * (weight = 1, EPSILON floor on v_hat's norm) or calculate_adam_w_bias
+ * (weight = 0) on g as given (adam_w.rs:9-103 clip each element themselves) */
+int orc_param_update(oc64* w, const oc64* g, oc64* m, oc64* v, uint64_t n, int first, double lr, double batch,
+                     uint32_t time_step, int weight) {
+  if (!w || !g || !m || !v) return fail(ORC_ERR_ARG, "bad arguments");
+  for (uint64_t i = 0; i < n; ++i) {
+    if (first) {
+      const oc64 gc = clip1(g[i], 1.0);
+      if (finite_c(gc)) w[i] = c_sub(w[i], c_scale(c_unscale(gc, batch), lr));
+    } else {
+      w[i] = adamw1(w[i], g[i], &m[i], &v[i], lr, time_step, weight);
+    }
+  }
+  return ORC_OK;
 }

@@ -154,6 +154,22 @@ int orc_dense_backward(const oc64* X, const oc64* Z, const oc64* prev, const uin
 int orc_linear_update(oc64* W, oc64* b, uint32_t d, uint32_t V, const oc64* dW, const oc64* db, uint32_t batch,
                       oc64* mW, oc64* vW, oc64* mb, oc64* vb, int first, double lr, uint32_t time_step);
 
+/* the rest of the reverse walk (transformer_network.rs:506-636) */
+int orc_norm_backward(const oc64* x, uint64_t rows, uint32_t n, double eps, const oc64* gamma, const oc64* beta,
+                      const oc64* dout, oc64* dx, oc64* dgamma, oc64* dbeta);
+int orc_attention_heads_backward(const oc64* X, uint32_t B, uint32_t S, const uint32_t* mask, uint32_t H, uint32_t d,
+                                 uint32_t mc, const oc64* wq, const oc64* wk, const oc64* wv, const oc64* bias_pos,
+                                 const oc64* Gc, oc64* dX, oc64* dwq, oc64* dwk, oc64* dwv, oc64* dbias);
+int orc_self_attention_backward(const oc64* X, uint32_t B, uint32_t S, const uint32_t* mask, uint32_t H, uint32_t d,
+                                uint32_t mc, double eps, const oc64* wq, const oc64* wk, const oc64* wv,
+                                const oc64* bias_pos, const oc64* gamma, const oc64* beta, const oc64* G, oc64* dX,
+                                oc64* dwq, oc64* dwk, oc64* dwv, oc64* dbias, oc64* dgamma, oc64* dbeta);
+int orc_rope_backward(const oc64* G, uint32_t B, uint32_t S, uint32_t d, double base, oc64* out);
+int orc_embedding_update(oc64* table, uint32_t V, uint32_t d, const oc64* G, uint32_t B, uint32_t S,
+                         const uint32_t* targets, const uint32_t* tlens, uint32_t T, double lr);
+int orc_param_update(oc64* w, const oc64* g, oc64* m, oc64* v, uint64_t n, int first, double lr, double batch,
+                     uint32_t time_step, int weight);
+
 #ifdef __cplusplus
 }
 #endif

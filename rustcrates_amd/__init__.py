@@ -212,6 +212,7 @@ class Network:
         self._lib = lib
         self.vocab = None
         self.dim = None
+        self._in_dims = []  # each layer's input width, for the gradient backward returns
         _live.add(self)
 
     def close(self):
@@ -239,24 +240,29 @@ class Network:
     # ---- LayerEnum variants ----
     def add_embedding(self, vocab, dim, table=None):
         self.dim = dim
+        self._in_dims.append(dim)
         _check(self._lib.mitok_add_embedding(self._h, vocab, dim, _ptr(_c128(table, vocab * dim, "table"))))
 
     def add_positional_encoding(self, dim, base=1250.0):
+        self._in_dims.append(dim)
         _check(self._lib.mitok_add_positional_encoding(self._h, dim, base))
 
     def add_norm(self, dim, eps, gamma=None, beta=None):
+        self._in_dims.append(dim)
         _check(self._lib.mitok_add_norm(self._h, dim, eps, _ptr(_c128(gamma, dim, "gamma")),
                                         _ptr(_c128(beta, dim, "beta"))))
 
     def add_self_attention(self, heads, dim, max_ctx, eps=1e-12, wq=None, wk=None, wv=None, bias_pos=None,
                            gamma=None, beta=None):
         nw = dim * dim  # [heads][dim][dim / heads]
+        self._in_dims.append(dim)
         _check(self._lib.mitok_add_self_attention(self._h, heads, dim, max_ctx, eps, _ptr(_c128(wq, nw, "wq")),
                                                   _ptr(_c128(wk, nw, "wk")), _ptr(_c128(wv, nw, "wv")),
                                                   _ptr(_c128(bias_pos, heads * max_ctx * max_ctx, "bias_pos")),
                                                   _ptr(_c128(gamma, dim, "gamma")), _ptr(_c128(beta, dim, "beta"))))
 
     def add_feed_forward(self, dim, hidden, w1=None, b1=None, w2=None, b2=None):
+        self._in_dims.append(dim)
         _check(self._lib.mitok_add_feed_forward(self._h, dim, hidden, _ptr(_c128(w1, dim * hidden, "w1")),
                                                 _ptr(_c128(b1, hidden, "b1")), _ptr(_c128(w2, hidden * dim, "w2")),
                                                 _ptr(_c128(b2, dim, "b2"))))
@@ -264,15 +270,18 @@ class Network:
     def add_linear(self, d_in, d_out, w=None, b=None):
         self.vocab = d_out
         self._head_in = d_in
+        self._in_dims.append(d_in)
         _check(self._lib.mitok_add_linear(self._h, d_in, d_out, _ptr(_c128(w, d_in * d_out, "w")),
                                           _ptr(_c128(b, d_out, "b"))))
 
     def add_softmax(self, mode=PRODUCTION):
+        self._in_dims.append(getattr(self, "vocab", 0))
         _check(self._lib.mitok_add_softmax(self._h, mode))
 
     def add_discrete_wavelet(self, dim, wavelet=1, mode=2, is_full_mode=False):
         """DiscreteWaveletLayer over rows of `dim` features; defaults DB2 /
         SYMMETRIC (wavelet_discrete_layer.rs:46-70)."""
+        self._in_dims.append(dim)
         _check(self._lib.mitok_add_discrete_wavelet(self._h, dim, wavelet, mode, int(is_full_mode)))
 
     def seq_out_len(self, S, first=0, last=None):
@@ -393,9 +402,10 @@ class Network:
     def backward(self, targets, tlens=None, layers=1, update=True, learning_rate=0.001, time_step=1,
                  want_grad_input=True):
         """The reverse walk of backward (transformer_network.rs:506-636)
-        through `layers` layers below the Softmax: 1 the vocab Linear, 2 also
-        the FeedForward right below it.  Returns the gradient of the lowest
-        differentiated layer's input [B][S'][d] (complex)."""
+        through `layers` layers below the Softmax (1: the vocab Linear only; up
+        to every layer of the last stateless predict, the Embedding's update
+        included).  Returns the gradient of the lowest differentiated layer's
+        input [B][S'][d] (complex)."""
         t = np.ascontiguousarray(targets, dtype=np.uint32)
         if t.ndim != 2:
             raise ValueError(f"targets: shape {t.shape}, expected (batch, T)")
@@ -406,7 +416,9 @@ class Network:
             rows = getattr(self, "_head_rows", None)
             if rows is None or rows[0] != B:
                 raise MitokError(3, "no stateless predict of this batch to differentiate")
-            gx = np.empty((B, rows[1], self._head_in), np.complex128)
+            lowest = len(self._in_dims) - 1 - int(layers)
+            width = self._in_dims[lowest] if 0 <= lowest < len(self._in_dims) else self._head_in
+            gx = np.empty((B, rows[1], width), np.complex128)
         _check(self._lib.mitok_backward(self._h, _ptr(t), _ptr(tl), B, T, int(layers), int(bool(update)),
                                         float(learning_rate), int(time_step), _ptr(gx)))
         return gx

@@ -59,6 +59,7 @@ enum ErrBits : uint32_t {
   EB_ARGMAX_NAN = 8u,    // greedy_decoding partial_cmp().unwrap() (sampling_methods.rs:12)
   EB_CTX_OVERFLOW = 16u, // a cached sequence outgrew max_ctx
   EB_BARRIER = 32u,      // a grid barrier of the resident decode loop timed out
+  EB_TRAIN_NONFINITE = 64u, // a non-finite embedding gradient or row (embedding_layer.rs:242-250)
 };
 
 // ---- counter generator (identical to oracle.c / seeded.py) ----

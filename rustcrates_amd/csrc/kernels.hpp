@@ -145,6 +145,29 @@ void bias_grad(hipStream_t st, const double2* G, int B, int S, int V, double2* d
 // W [n], b [V] updated in place from dW, db (moments mW, vW, mb, vb)
 void linear_update(hipStream_t st, double2* W, const double2* dW, double2* mW, double2* vW, long n, double2* b,
                    const double2* db, double2* mb, double2* vb, int V, const TrainStep& ts);
+// the Norm's backward per row of x (or Re(x + resid) + 0i); dx real rows, pg = dout * x_hat
+void norm_backward(hipStream_t st, const double2* x, const double2* resid, long rows, int n, double eps,
+                   const double2* gamma, const double2* beta, const double2* dout, double2* dx, double2* pg);
+// out[j] = mult * sum_r X[r][j]
+void colsum(hipStream_t st, const double2* X, long rows, int n, double mult, double2* out);
+// attention weights A and dl_da [B][H][S][S] of a stateless pass from the packed [q | k | v] rows and the
+// gradient G [B*S][d] of the heads' output
+void attn_probs_grad(hipStream_t st, const double2* qkv, const double* bias_re, int mc, const uint32_t* mask,
+                     const double2* G, int B, int S, int H, int dh, double c, double* A, double* dA);
+// the gradient of the packed [q | k | v] rows: dQ = c dA conj(K), dK = c dA^T conj(Q), dV = A^T G
+void attn_dqkv(hipStream_t st, const double2* qkv, const double* A, const double* dA, const double2* G, int B, int S,
+               int H, int dh, double c, double2* dqkv);
+// Re(bias_pos)[h][:S][:S] updated from dA summed over the batch (zero moments each call)
+void attn_bias_update(hipStream_t st, double* bias_re, int mc, const double* dA, int B, int H, int S,
+                      const TrainStep& ts);
+// w [n] updated in place (weight: AdamW's EPSILON floor on v_hat's norm)
+void param_update(hipStream_t st, double2* w, const double2* g, double2* m, double2* v, long n, bool weight,
+                  const TrainStep& ts);
+// RoPE's backward on rows [rows][d] of sequences of S rows (cs: the forward's table)
+void rope_backward(hipStream_t st, const double2* G, long rows, int S, int d, const double2* cs, double2* out);
+// the embedding rows of n_ids distinct ids, each with occurrences occ[start[u] .. start[u+1]) (rows of G)
+void embedding_update(hipStream_t st, double2* table, int d, const uint32_t* ids, int n_ids, const int* start,
+                      const int* occ, const double2* G, double lr, double bs, uint32_t* err);
 
 // ---- attention ----
 struct Attn {

@@ -16,6 +16,7 @@
 #include <memory>
 #include <mutex>
 #include <string>
+#include <map>
 #include <vector>
 
 #include "../../include/mitok.h"
@@ -131,6 +132,10 @@ struct SelfAttentionLayer : Layer {  // self_attention_layer.rs:16-25 + masked_a
   DevBuf bias_re;  // [heads][max_ctx][max_ctx]  Re(bias_pos): only the real part reaches the softmax
   DevBuf gamma, beta;
   DevBuf kc, vc;  // [cache_B][heads][max_ctx][dh]
+  // training state: AdamW moments of wqkv and of the Norm's gamma and beta,
+  // updates so far (the first is plain clipped descent)
+  DevBuf mw, vw, mg, vg, mbt, vbt;
+  uint32_t updates = 0;
   SelfAttentionLayer() : Layer(K_SELF_ATTENTION) {}
 };
 
@@ -359,11 +364,13 @@ struct mitok_network {
   // differentiates; any later call clears head_valid
   bool head_valid = false;
   const double2* head_x = nullptr;
-  const double2* head_x2 = nullptr;     // the input of a FeedForward right below the vocab Linear
   const uint32_t* head_mask = nullptr;  // the padding mask of those rows
-  uint32_t head_B = 0, head_S = 0;
-  mitok::DevBuf tr_g, tr_xh, tr_wh, tr_dw, tr_db, tr_dx, tr_tgt, tr_norm;
-  mitok::DevBuf tr_z, tr_g1, tr_dh, tr_dw1, tr_db1, tr_dw2, tr_db2, tr_dx2;
+  uint32_t head_B = 0, head_S = 0, head_first = 0;
+  // what a stateless pass keeps for backward: each layer's input rows, and
+  // the heads' output of each SelfAttention layer (before its residual + Norm)
+  std::vector<std::unique_ptr<mitok::DevBuf>> tr_in, tr_cat;
+  mitok::DevBuf tr_g, tr_xh, tr_wh, tr_dw, tr_db, tr_ga, tr_gb, tr_tgt, tr_norm;
+  mitok::DevBuf tr_z, tr_h, tr_g1, tr_dh, tr_qkv, tr_dqkv, tr_A, tr_dA, tr_pg, tr_eid, tr_est, tr_eocc;
 };
 
 namespace mitok {
@@ -412,6 +419,7 @@ static int check_err_word(Net* n) {
   if (e & EB_ARGMAX_NAN) return fail(ERR_NAN, "greedy_decoding: NaN in logits (sampling_methods.rs:12)");
   if (e & EB_CTX_OVERFLOW) return fail(ERR_ARG, "context exceeds max_ctx");
   if (e & EB_BARRIER) return fail(ERR_STATE, "resident decode: a grid barrier timed out");
+  if (e & EB_TRAIN_NONFINITE) return fail(ERR_NAN, "gradient in embedding is invalid, contains NaN or infinity values (embedding_layer.rs:242-250)");
   return fail(ERR_STATE, "device error word 0x%x", e);
 }
 
@@ -537,6 +545,15 @@ static int prepare(Net* n, const Spec& sp) {
   TRY(reserve(n, n->gath, (size_t)sp.B * dm.dmax * c16));
   TRY(reserve(n, n->mat0, rows * dm.dmax * c16));
   TRY(reserve(n, n->mat1, rows * dm.dmax * c16));
+  if (sp.mode == MODE_STATELESS) {  // the layer inputs backward reads
+    while (n->tr_in.size() < n->layers.size()) n->tr_in.push_back(std::make_unique<DevBuf>());
+    while (n->tr_cat.size() < n->layers.size()) n->tr_cat.push_back(std::make_unique<DevBuf>());
+    for (uint32_t li = sp.first; li < sp.last; ++li) {
+      const Layer* L = n->layers[li].get();
+      if (L->kind != K_EMBEDDING && L->kind != K_SOFTMAX) TRY(reserve(n, *n->tr_in[li], rows * L->d_in * c16));
+      if (L->kind == K_SELF_ATTENTION) TRY(reserve(n, *n->tr_cat[li], rows * L->d_in * c16));
+    }
+  }
   size_t ws = 0;
   for (uint32_t li = sp.first; li < sp.last; ++li) {
     Layer* L = n->layers[li].get();
@@ -648,6 +665,8 @@ static int enqueue_forward(Net* n, const Spec& sp) {
                                    hipMemcpyDeviceToDevice, st));
   for (uint32_t li = sp.first; li < sp.last; ++li) {
     Layer* L = n->layers[li].get();
+    if (sp.mode == MODE_STATELESS && L->kind != K_EMBEDDING && L->kind != K_SOFTMAX)  // kept for backward
+      HIP_TRY(hipMemcpyAsync(n->tr_in[li]->p, cur, (size_t)rows * L->d_in * sizeof(double2), hipMemcpyDeviceToDevice, st));
     switch (L->kind) {
       case K_EMBEDDING: {
         auto* E = (EmbeddingLayer*)L;
@@ -742,6 +761,9 @@ static int enqueue_forward(Net* n, const Spec& sp) {
             TimeScope ts(n, MITOK_TIME_ATTENTION, 0.0);
             if (!n->tiled_prefill || !attention_prefill(st, a)) attention_rows(st, a);
           }
+          if (sp.mode == MODE_STATELESS)  // the heads' output, kept for backward
+            HIP_TRY(hipMemcpyAsync(n->tr_cat[li]->p, n->concat.p, (size_t)rows * d * sizeof(double2),
+                                   hipMemcpyDeviceToDevice, st));
           layernorm(st, n->concat.as<double2>(), cur, nxt, rows, d, A->eps, A->gamma.as<double2>(),
                     A->beta.as<double2>());
         }
@@ -821,8 +843,7 @@ static int enqueue_forward(Net* n, const Spec& sp) {
           if (sp.mode == MODE_STATELESS && !sp.last_row) {  // the layer keeps its input for backward
             n->head_valid = true;
             n->head_x = x;
-            // a FeedForward right below left its input in the other buffer
-            n->head_x2 = (li > 0 && n->layers[li - 1]->kind == K_FEED_FORWARD) ? nxt : nullptr;
+            n->head_first = sp.first;
             n->head_mask = mask;
             n->head_B = (uint32_t)B;
             n->head_S = (uint32_t)S;
@@ -2491,34 +2512,81 @@ int mitok_decode_step(mitok_network* n, const uint32_t* ids, uint32_t B, uint32_
   return rc;
 }
 
-// the AdamW moments of a d x V weight and its bias, allocated and zeroed at the first update
+// the AdamW moments of a weight (nw) and its bias (nb), allocated and zeroed
+// at the first update; nb = 0: a lone array's pair (mw, vw) only
 static int ensure_moments(hipStream_t st, size_t nw, size_t nb, DevBuf& mw, DevBuf& vw, DevBuf& mb, DevBuf& vb) {
   if (mw.p) return OK;
   TRY(mw.reserve(nw * sizeof(double2)));
   TRY(vw.reserve(nw * sizeof(double2)));
-  TRY(mb.reserve(nb * sizeof(double2)));
-  TRY(vb.reserve(nb * sizeof(double2)));
   fill_const(st, mw.as<double2>(), nw, make_double2(0.0, 0.0));
   fill_const(st, vw.as<double2>(), nw, make_double2(0.0, 0.0));
+  if (!nb) return OK;
+  TRY(mb.reserve(nb * sizeof(double2)));
+  TRY(vb.reserve(nb * sizeof(double2)));
   fill_const(st, mb.as<double2>(), nb, make_double2(0.0, 0.0));
   fill_const(st, vb.as<double2>(), nb, make_double2(0.0, 0.0));
   return OK;
 }
 
+// backward (transformer_network.rs:506-636) on the device: the reverse walk
+// from the Softmax through `n_layers` layers below it, each layer's backward
+// on the inputs the last stateless pass kept, and with update_params each
+// layer's update_parameters where the reference calls it (Linear,
+// FeedForward, SelfAttention with its Norm, Embedding; a standalone Norm and
+// RoPE have no update in the walk).
 static int backward_impl(Net* n, const uint32_t* targets, const uint32_t* tlens, uint32_t B, uint32_t T,
                          uint32_t n_layers, int update_params, double learning_rate, uint32_t time_step,
                          double* out_grad_input) {
   if (!n || !targets || !tlens || !B || !T) return fail(ERR_ARG, "bad arguments");
-  if (n_layers < 1 || n_layers > 2) return fail(ERR_ARG, "%u layers: the vocab Linear (1) and the FeedForward below it (2)", n_layers);
   if (!n->head_valid) return fail(ERR_STATE, "no stateless (forward_only = 0) predict to differentiate");
   if (B != n->head_B) return fail(ERR_ARG, "batch %u != the forward pass's %u", B, n->head_B);
-  const uint32_t li = (uint32_t)n->layers.size() - 2;
-  if (!is_vocab_linear(n, li)) return fail(ERR_STATE, "the stack does not end in Linear, Softmax");
-  auto* Ln = (LinearLayer*)n->layers[li].get();
-  if (n_layers >= 2 && (li == 0 || n->layers[li - 1]->kind != K_FEED_FORWARD || !n->head_x2))
-    return fail(ERR_STATE, "no FeedForward right below the vocab Linear to differentiate");
+  const uint32_t li_top = (uint32_t)n->layers.size() - 2;
+  if (!is_vocab_linear(n, li_top)) return fail(ERR_STATE, "the stack does not end in Linear, Softmax");
+  const uint32_t reach = li_top + 1 - n->head_first;  // layers of the forward pass below the Softmax
+  if (n_layers < 1 || n_layers > reach)
+    return fail(ERR_ARG, "%u layers: from 1 (the vocab Linear) to %u (every layer of the forward pass)", n_layers, reach);
+  const uint32_t stop = li_top + 1 - n_layers;
+  auto* Ln = (LinearLayer*)n->layers[li_top].get();
   const int S = (int)n->head_S, d = (int)Ln->d_in, V = (int)Ln->d_out;
   const long rows = (long)B * S;
+  // what the walk needs, checked and sized before the first launch
+  size_t dmax = (size_t)d, fmax = 0, d3max = 0, att = 0, wmax = (size_t)d * V, bmax = (size_t)V;
+  size_t ws = std::max(gemm_ws_bytes(d, V, (int)rows), gemm_ws_bytes((int)rows, d, V));
+  for (uint32_t li = stop; li < li_top; ++li) {
+    const Layer* L = n->layers[li].get();
+    const int di = (int)L->d_in, dn = (int)L->d_out;
+    dmax = std::max({dmax, (size_t)di, (size_t)dn});
+    switch (L->kind) {
+      case K_WAVELET:
+        return fail(ERR_STATE, "layer %u: backward through the DiscreteWavelet layer is not built (its training pass "
+                               "splits input and target rows, wavelet_discrete_layer.rs:233-279)", li);
+      case K_LINEAR:
+        wmax = std::max(wmax, (size_t)di * dn);
+        bmax = std::max(bmax, (size_t)dn);
+        ws = std::max({ws, gemm_ws_bytes(di, dn, (int)rows), gemm_ws_bytes((int)rows, di, dn)});
+        break;
+      case K_FEED_FORWARD: {
+        const int F = (int)((const FeedForwardLayer*)L)->hidden;
+        fmax = std::max(fmax, (size_t)F);
+        wmax = std::max(wmax, (size_t)di * F);
+        bmax = std::max(bmax, (size_t)F);
+        ws = std::max({ws, gemm_ws_bytes((int)rows, F, di), gemm_ws_bytes(F, dn, (int)rows),
+                       gemm_ws_bytes((int)rows, F, dn), gemm_ws_bytes(di, F, (int)rows), gemm_ws_bytes((int)rows, di, F)});
+        break;
+      }
+      case K_SELF_ATTENTION: {
+        const auto* A = (const SelfAttentionLayer*)L;
+        if ((uint32_t)S > A->max_ctx) return fail(ERR_ARG, "layer %u: %d rows exceed max context %u", li, S, A->max_ctx);
+        d3max = std::max(d3max, (size_t)3 * di);
+        att = std::max(att, (size_t)A->heads * S * S);
+        wmax = std::max(wmax, (size_t)3 * di * di);
+        ws = std::max({ws, gemm_ws_bytes((int)rows, 3 * di, di), gemm_ws_bytes(di, 3 * di, (int)rows),
+                       gemm_ws_bytes((int)rows, di, 3 * di)});
+        break;
+      }
+      default: break;
+    }
+  }
   // SoftmaxLayer::backward (softmax_output_layer.rs:67-145): which row predicts
   // which target, checked in the reference's order (a target id at or past the
   // vocabulary panics there; PAD targets are skipped; the row before the last
@@ -2543,125 +2611,240 @@ static int backward_impl(Net* n, const uint32_t* targets, const uint32_t* tlens,
       tgt[(size_t)b * S + s] = (int)tc;
     }
   }
+  // EmbeddingLayer::update_parameters' order: sequence by sequence, target by
+  // target; grouped per id (a repeated id applies its rows in that order)
+  const bool embed_upd = update_params && stop == 0 && n->layers[0]->kind == K_EMBEDDING;
+  std::vector<uint32_t> eids;
+  std::vector<int> estart, eocc;
+  if (embed_upd) {
+    const uint32_t EV = ((const EmbeddingLayer*)n->layers[0].get())->vocab;
+    std::map<uint32_t, std::vector<int>> by_id;
+    for (uint32_t b = 0; b < B; ++b)
+      for (uint32_t t = 0; t < tlens[b]; ++t) {
+        const uint32_t id = targets[(size_t)b * T + t];
+        if (id >= EV) return fail(ERR_ARG, "No token embedding found: %u (embedding_layer.rs:233)", id);
+        by_id[id].push_back((int)(b * (uint32_t)S + t));
+      }
+    for (auto& kv : by_id) {
+      eids.push_back(kv.first);
+      estart.push_back((int)eocc.size());
+      eocc.insert(eocc.end(), kv.second.begin(), kv.second.end());
+    }
+    estart.push_back((int)eocc.size());
+  }
   TRY(set_device(n));
   hipStream_t st = n->stream;
   const size_t c16 = sizeof(double2);
+  // every workspace is sized before the first launch (a reserve that grows frees the old buffer)
   TRY(upload(n, n->tr_tgt, tgt.data(), tgt.size() * sizeof(int)));
   TRY(upload(n, n->tr_norm, norm.data(), norm.size() * sizeof(double)));
+  if (embed_upd && !eids.empty()) {
+    TRY(upload(n, n->tr_eid, eids.data(), eids.size() * sizeof(uint32_t)));
+    TRY(upload(n, n->tr_est, estart.data(), estart.size() * sizeof(int)));
+    TRY(upload(n, n->tr_eocc, eocc.data(), eocc.size() * sizeof(int)));
+  }
   TRY(reserve(n, n->tr_g, (size_t)rows * V * c16));
-  // every workspace is sized before the first launch (a reserve that grows frees the old buffer)
-  const int F = n_layers >= 2 ? (int)((FeedForwardLayer*)n->layers[li - 1].get())->hidden : 0;
-  TRY(reserve(n, n->tr_xh, (size_t)std::max(d, F) * rows * c16));
-  TRY(reserve(n, n->tr_wh, (size_t)std::max<size_t>((size_t)V * d, (size_t)F * d) * c16));
-  TRY(reserve(n, n->tr_dw, (size_t)d * V * c16));
-  TRY(reserve(n, n->tr_db, (size_t)V * c16));
-  TRY(reserve(n, n->tr_dx, (size_t)rows * d * c16));
-  size_t ws = std::max(gemm_ws_bytes(d, V, (int)rows), gemm_ws_bytes((int)rows, d, V));
-  if (F) {
-    TRY(reserve(n, n->tr_z, (size_t)rows * F * c16));
-    TRY(reserve(n, n->tr_g1, (size_t)rows * F * c16));
-    TRY(reserve(n, n->tr_dh, (size_t)rows * F * c16));
-    TRY(reserve(n, n->tr_dw1, (size_t)d * F * c16));
-    TRY(reserve(n, n->tr_db1, (size_t)F * c16));
-    TRY(reserve(n, n->tr_dw2, (size_t)F * d * c16));
-    TRY(reserve(n, n->tr_db2, (size_t)d * c16));
-    TRY(reserve(n, n->tr_dx2, (size_t)rows * d * c16));
-    ws = std::max({ws, gemm_ws_bytes(F, d, (int)rows), gemm_ws_bytes((int)rows, F, d), gemm_ws_bytes(d, F, (int)rows),
-                   gemm_ws_bytes((int)rows, d, F)});
+  TRY(reserve(n, n->tr_ga, (size_t)rows * dmax * c16));
+  TRY(reserve(n, n->tr_gb, (size_t)rows * dmax * c16));
+  TRY(reserve(n, n->tr_xh, (size_t)rows * std::max(dmax, fmax) * c16));
+  TRY(reserve(n, n->tr_wh, wmax * c16));
+  TRY(reserve(n, n->tr_dw, wmax * c16));
+  TRY(reserve(n, n->tr_db, std::max(bmax, dmax) * c16));
+  TRY(reserve(n, n->tr_dh, (size_t)rows * std::max(fmax, dmax) * c16));
+  TRY(reserve(n, n->tr_pg, (size_t)rows * dmax * c16));
+  if (fmax) {
+    TRY(reserve(n, n->tr_z, (size_t)rows * fmax * c16));
+    TRY(reserve(n, n->tr_h, (size_t)rows * fmax * c16));
+    TRY(reserve(n, n->tr_g1, (size_t)rows * fmax * c16));
+  }
+  if (att) {
+    TRY(reserve(n, n->tr_qkv, (size_t)rows * d3max * c16));
+    TRY(reserve(n, n->tr_dqkv, (size_t)rows * d3max * c16));
+    TRY(reserve(n, n->tr_A, (size_t)B * att * sizeof(double)));
+    TRY(reserve(n, n->tr_dA, (size_t)B * att * sizeof(double)));
   }
   TRY(reserve(n, n->sync_ws, ws));
-  const Sync sy = sync_of(n);
-  uint32_t* err = n->err_d.as<uint32_t>();
-  double2* G = n->tr_g.as<double2>();
-  softmax_grad(st, n->probs.as<double>(), (int)rows, V, n->tr_tgt.as<int>(), n->tr_norm.as<double>(), S, G);
-  // LinearLayer::backward, complex arm (linear_layer.rs:96-108) grouped over
-  // the sequences: dW = conj(X)^T G, db = column sums, dX = G conj(W)^T
-  conj_transpose(st, n->head_x, rows, d, n->tr_xh.as<double2>());
-  Epi e;
-  e.mode = EPI_STORE;
-  e.err = err;
-  e.out = n->tr_dw.as<double2>();
-  e.ldo = V;
-  TRY(launch_rc(gemm(st, d, V, (int)rows, rows_of(n->tr_xh.as<double2>(), rows), G, V, e, nullptr, sy), "weight grad"));
-  bias_grad(st, G, (int)B, S, V, n->tr_db.as<double2>());
-  conj_transpose(st, Ln->w.as<double2>(), d, V, n->tr_wh.as<double2>());
-  e.out = n->tr_dx.as<double2>();
-  e.ldo = d;
-  TRY(launch_rc(gemm(st, (int)rows, d, V, rows_of(G, V), n->tr_wh.as<double2>(), d, e, nullptr, sy), "input grad"));
-  TrainStep ts;
-  ts.lr = learning_rate;
-  ts.batch = (double)B;
-  if (update_params) {  // LinearLayer::update_parameters (linear_layer.rs:130-175)
-    const size_t nw = (size_t)d * V;
-    TRY(ensure_moments(st, nw, V, Ln->mw, Ln->vw, Ln->mb, Ln->vb));
-    ts.first = Ln->updates == 0 ? 1 : 0;
-    ts.time_step = (int)time_step;
-    linear_update(st, Ln->w.as<double2>(), n->tr_dw.as<double2>(), Ln->mw.as<double2>(), Ln->vw.as<double2>(),
-                  (long)nw, Ln->b.as<double2>(), n->tr_db.as<double2>(), Ln->mb.as<double2>(), Ln->vb.as<double2>(), V,
-                  ts);
-    Ln->updates++;
-    drop_graph(n);  // the weights changed under any captured step
-  }
-  const double2* gin = n->tr_dx.as<double2>();  // gradient of the lowest layer's input so far
-  if (n_layers >= 2) {
-    // FeedForwardLayer::backward (feedforward_layer.rs:140-186): its Linear,
-    // then its Dense (GELU) layer, each as LinearLayer::backward's products
-    auto* Fl = (FeedForwardLayer*)n->layers[li - 1].get();
-    const double2* Xf = n->head_x2;               // the FFN's input rows
-    const double2* H = n->hbuf.as<double2>();      // its Dense output, GELU applied, padded rows 0
-    const double2* dY = n->tr_dx.as<double2>();    // the gradient of its output
-    const Sync sy2 = sy;
-    Epi f;
-    f.mode = EPI_STORE;
-    f.err = err;
-    // Linear (W2 [F][d]): dW2 = conj(H)^T dY, db2, dH = dY conj(W2)^T
-    conj_transpose(st, H, rows, F, n->tr_xh.as<double2>());
-    f.out = n->tr_dw2.as<double2>();
-    f.ldo = d;
-    TRY(launch_rc(gemm(st, F, d, (int)rows, rows_of(n->tr_xh.as<double2>(), rows), dY, d, f, nullptr, sy2), "ffn2 weight grad"));
-    bias_grad(st, dY, (int)B, S, d, n->tr_db2.as<double2>());
-    conj_transpose(st, Fl->w2.as<double2>(), F, d, n->tr_wh.as<double2>());
-    f.out = n->tr_dh.as<double2>();
-    f.ldo = F;
-    TRY(launch_rc(gemm(st, (int)rows, F, d, rows_of(dY, d), n->tr_wh.as<double2>(), F, f, nullptr, sy2), "ffn2 input grad"));
-    // Dense (W1 [d][F], GELU): its pre-activation again, Z = X W1 + b1 (layer.rs:135-144)
-    f.out = n->tr_z.as<double2>();
-    f.ldo = F;
-    f.bias = Fl->b1.as<double2>();
-    TRY(launch_rc(gemm(st, (int)rows, F, d, rows_of(Xf, d), Fl->w1.as<double2>(), F, f, nullptr, sy2), "ffn1 pre-activation"));
-    f.bias = nullptr;
-    gelu_backward(st, n->tr_dh.as<double2>(), n->tr_z.as<double2>(), n->head_mask, rows, F, n->tr_g1.as<double2>());
-    conj_transpose(st, Xf, rows, d, n->tr_xh.as<double2>());
-    f.out = n->tr_dw1.as<double2>();
-    f.ldo = F;
-    TRY(launch_rc(gemm(st, d, F, (int)rows, rows_of(n->tr_xh.as<double2>(), rows), n->tr_g1.as<double2>(), F, f, nullptr, sy2),
-                  "ffn1 weight grad"));
-    bias_grad(st, n->tr_g1.as<double2>(), (int)B, S, F, n->tr_db1.as<double2>());
-    conj_transpose(st, Fl->w1.as<double2>(), d, F, n->tr_wh.as<double2>());
-    f.out = n->tr_dx2.as<double2>();
-    f.ldo = d;
-    TRY(launch_rc(gemm(st, (int)rows, d, F, rows_of(n->tr_g1.as<double2>(), F), n->tr_wh.as<double2>(), d, f, nullptr, sy2),
-                  "ffn1 input grad"));
-    gin = n->tr_dx2.as<double2>();
-    if (update_params) {  // FeedForwardLayer::update_parameters (:219-250): the Linear, then the Dense
-      TRY(ensure_moments(st, (size_t)F * d, d, Fl->mw2, Fl->vw2, Fl->mb2, Fl->vb2));
-      TRY(ensure_moments(st, (size_t)d * F, F, Fl->mw1, Fl->vw1, Fl->mb1, Fl->vb1));
-      ts.first = Fl->updates2 == 0 ? 1 : 0;
-      ts.time_step = (int)time_step;  // the FFN passes its time step to its Linear (feedforward_layer.rs:86)
-      linear_update(st, Fl->w2.as<double2>(), n->tr_dw2.as<double2>(), Fl->mw2.as<double2>(), Fl->vw2.as<double2>(),
-                    (long)F * d, Fl->b2.as<double2>(), n->tr_db2.as<double2>(), Fl->mb2.as<double2>(),
-                    Fl->vb2.as<double2>(), d, ts);
-      Fl->updates2++;
-      ts.first = Fl->updates1 == 0 ? 1 : 0;
-      ts.time_step = 0;  // Layer::time_step is never set after construction (layer.rs:111,285): AdamW uses 1
-      linear_update(st, Fl->w1.as<double2>(), n->tr_dw1.as<double2>(), Fl->mw1.as<double2>(), Fl->vw1.as<double2>(),
-                    (long)d * F, Fl->b1.as<double2>(), n->tr_db1.as<double2>(), Fl->mb1.as<double2>(),
-                    Fl->vb1.as<double2>(), F, ts);
-      Fl->updates1++;
+  if (update_params) {  // AdamW moments, zeroed at a layer's first update
+    TRY(ensure_moments(st, (size_t)d * V, V, Ln->mw, Ln->vw, Ln->mb, Ln->vb));
+    for (uint32_t li = stop; li < li_top; ++li) {
+      Layer* L = n->layers[li].get();
+      if (L->kind == K_LINEAR) {
+        auto* H = (LinearLayer*)L;
+        TRY(ensure_moments(st, (size_t)H->d_in * H->d_out, H->d_out, H->mw, H->vw, H->mb, H->vb));
+      } else if (L->kind == K_FEED_FORWARD) {
+        auto* F = (FeedForwardLayer*)L;
+        TRY(ensure_moments(st, (size_t)F->hidden * F->d_out, F->d_out, F->mw2, F->vw2, F->mb2, F->vb2));
+        TRY(ensure_moments(st, (size_t)F->d_in * F->hidden, F->hidden, F->mw1, F->vw1, F->mb1, F->vb1));
+      } else if (L->kind == K_SELF_ATTENTION) {
+        auto* A = (SelfAttentionLayer*)L;
+        TRY(ensure_moments(st, (size_t)3 * A->d_in * A->d_in, A->d_in, A->mw, A->vw, A->mg, A->vg));
+        TRY(ensure_moments(st, A->d_in, 0, A->mbt, A->vbt, A->mbt, A->vbt));
+      }
     }
   }
-  if (out_grad_input)
-    HIP_TRY(hipMemcpyAsync(out_grad_input, gin, (size_t)rows * d * c16, hipMemcpyDeviceToHost, st));
+  const Sync sy = sync_of(n);
+  uint32_t* err = n->err_d.as<uint32_t>();
+  const uint32_t* mask = n->head_mask;
+  double2* xh = n->tr_xh.as<double2>();
+  double2* wh = n->tr_wh.as<double2>();
+  double2* dW = n->tr_dw.as<double2>();
+  double2* db = n->tr_db.as<double2>();
+  // LinearLayer::backward, complex arm (linear_layer.rs:96-108), grouped over
+  // the sequences: dW = conj(X)^T G, db = column sums, dX = G conj(W)^T
+  auto linear_bwd = [&](const double2* X, const double2* G, const double2* W, int din, int dout, double2* dX) -> int {
+    conj_transpose(st, X, rows, din, xh);
+    Epi e;
+    e.mode = EPI_STORE;
+    e.err = err;
+    e.out = dW;
+    e.ldo = dout;
+    TRY(launch_rc(gemm(st, din, dout, (int)rows, rows_of(xh, rows), G, dout, e, nullptr, sy), "weight grad"));
+    bias_grad(st, G, (int)B, S, dout, db);
+    conj_transpose(st, W, din, dout, wh);
+    e.out = dX;
+    e.ldo = din;
+    TRY(launch_rc(gemm(st, (int)rows, din, dout, rows_of(G, dout), wh, din, e, nullptr, sy), "input grad"));
+    return OK;
+  };
+  // update_parameters of a weight and its bias from dW, db (linear_layer.rs:130-175)
+  auto linear_upd = [&](DevBuf& W, DevBuf& b, long nw, int nb, DevBuf& mw, DevBuf& vw, DevBuf& mb, DevBuf& vb,
+                        uint32_t& updates, int tstep) {
+    TrainStep ts;
+    ts.lr = learning_rate;
+    ts.batch = (double)B;
+    ts.first = updates == 0 ? 1 : 0;
+    ts.time_step = tstep;
+    linear_update(st, W.as<double2>(), dW, mw.as<double2>(), vw.as<double2>(), nw, b.as<double2>(), db,
+                  mb.as<double2>(), vb.as<double2>(), nb, ts);
+    updates++;
+  };
+  double2* G = n->tr_g.as<double2>();
+  softmax_grad(st, n->probs.as<double>(), (int)rows, V, n->tr_tgt.as<int>(), n->tr_norm.as<double>(), S, G);
+  double2* gcur = n->tr_ga.as<double2>();  // the gradient of the current layer's output, then its input
+  double2* gnext = n->tr_gb.as<double2>();
+  TRY(linear_bwd(n->head_x, G, Ln->w.as<double2>(), d, V, gcur));
+  if (update_params) linear_upd(Ln->w, Ln->b, (long)d * V, V, Ln->mw, Ln->vw, Ln->mb, Ln->vb, Ln->updates, (int)time_step);
+  for (int li = (int)li_top - 1; li >= (int)stop; --li) {
+    Layer* L = n->layers[li].get();
+    const double2* X = n->tr_in[li]->as<double2>();
+    switch (L->kind) {
+      case K_LINEAR: {
+        auto* H = (LinearLayer*)L;
+        TRY(linear_bwd(X, gcur, H->w.as<double2>(), H->d_in, H->d_out, gnext));
+        if (update_params) linear_upd(H->w, H->b, (long)H->d_in * H->d_out, H->d_out, H->mw, H->vw, H->mb, H->vb, H->updates,
+                                      (int)time_step);
+        std::swap(gcur, gnext);
+        break;
+      }
+      case K_FEED_FORWARD: {
+        // FeedForwardLayer::backward (feedforward_layer.rs:140-186): its Linear,
+        // then its Dense (GELU) layer (layer.rs:168-210)
+        auto* F = (FeedForwardLayer*)L;
+        const int Fh = (int)F->hidden, di = (int)F->d_in, dn = (int)F->d_out;
+        Epi e;
+        e.err = err;
+        e.bias = F->b1.as<double2>();
+        e.ldo = Fh;
+        e.mode = EPI_GELU;  // the Dense output the forward pass gave its Linear: GELU, padded rows 0
+        e.row_mask = mask;
+        e.out = n->tr_h.as<double2>();
+        TRY(launch_rc(gemm(st, (int)rows, Fh, di, rows_of(X, di), F->w1.as<double2>(), Fh, e, nullptr, sy), "ffn1 output"));
+        e.mode = EPI_STORE;  // its pre-activation Z = X W1 + b1 (layer.rs:135-144)
+        e.row_mask = nullptr;
+        e.out = n->tr_z.as<double2>();
+        TRY(launch_rc(gemm(st, (int)rows, Fh, di, rows_of(X, di), F->w1.as<double2>(), Fh, e, nullptr, sy),
+                      "ffn1 pre-activation"));
+        TRY(linear_bwd(n->tr_h.as<double2>(), gcur, F->w2.as<double2>(), Fh, dn, n->tr_dh.as<double2>()));
+        // FeedForwardLayer::update_parameters (:219-250): the Linear at the FFN's time step (:86)
+        if (update_params) linear_upd(F->w2, F->b2, (long)Fh * dn, dn, F->mw2, F->vw2, F->mb2, F->vb2, F->updates2,
+                                      (int)time_step);
+        gelu_backward(st, n->tr_dh.as<double2>(), n->tr_z.as<double2>(), mask, rows, Fh, n->tr_g1.as<double2>());
+        TRY(linear_bwd(X, n->tr_g1.as<double2>(), F->w1.as<double2>(), di, Fh, gnext));
+        // the Dense at step 1: Layer::time_step stays 0 after construction (layer.rs:111,285)
+        if (update_params) linear_upd(F->w1, F->b1, (long)di * Fh, Fh, F->mw1, F->vw1, F->mb1, F->vb1, F->updates1, 0);
+        std::swap(gcur, gnext);
+        break;
+      }
+      case K_SELF_ATTENTION: {
+        // SelfAttentionLayer::backward (self_attention_layer.rs:135-196): the
+        // Norm's backward on Re(heads' output + X), then every head
+        // (masked_attention_head.rs:222-345); no residual gradient is added
+        auto* A = (SelfAttentionLayer*)L;
+        const int da = (int)A->d_in, H = (int)A->heads, dh = (int)A->dh, mc = (int)A->max_ctx;
+        const double c = 1.0 / (1e-8 + sqrt((double)dh));
+        double2* gn = n->tr_dh.as<double2>();
+        norm_backward(st, n->tr_cat[li]->as<double2>(), X, rows, da, A->eps, A->gamma.as<double2>(), A->beta.as<double2>(),
+                      gcur, gn, n->tr_pg.as<double2>());
+        Epi e;
+        e.mode = EPI_STORE;
+        e.err = err;
+        e.out = n->tr_qkv.as<double2>();
+        e.ldo = 3 * da;
+        TRY(launch_rc(gemm(st, (int)rows, 3 * da, da, rows_of(X, da), A->wqkv.as<double2>(), 3 * da, e, nullptr, sy),
+                      "qkv"));
+        attn_probs_grad(st, n->tr_qkv.as<double2>(), A->bias_re.as<double>(), mc, mask, gn, (int)B, S, H, dh, c,
+                        n->tr_A.as<double>(), n->tr_dA.as<double>());
+        attn_dqkv(st, n->tr_qkv.as<double2>(), n->tr_A.as<double>(), n->tr_dA.as<double>(), gn, (int)B, S, H, dh, c,
+                  n->tr_dqkv.as<double2>());
+        // the heads' weight gradients grouped over the batch: conj(X)^T [dq | dk | dv]
+        conj_transpose(st, X, rows, da, xh);
+        e.out = dW;
+        e.ldo = 3 * da;
+        TRY(launch_rc(gemm(st, da, 3 * da, (int)rows, rows_of(xh, rows), n->tr_dqkv.as<double2>(), 3 * da, e, nullptr, sy),
+                      "qkv weight grad"));
+        // the heads' input gradients summed: [dq | dk | dv] conj([Wq | Wk | Wv])^T
+        conj_transpose(st, A->wqkv.as<double2>(), da, 3 * da, wh);
+        e.out = gnext;
+        e.ldo = da;
+        TRY(launch_rc(gemm(st, (int)rows, da, 3 * da, rows_of(n->tr_dqkv.as<double2>(), 3 * da), wh, da, e, nullptr, sy),
+                      "qkv input grad"));
+        if (update_params) {  // SelfAttentionLayer::update_parameters (:260-273): the Norm, then the heads
+          TrainStep ts;
+          ts.lr = learning_rate;
+          ts.first = A->updates == 0 ? 1 : 0;
+          ts.time_step = (int)time_step;
+          ts.batch = (double)da;  // norm_layer.rs:269: gamma's length
+          colsum(st, n->tr_pg.as<double2>(), rows, da, (double)da, db);  // gamma's gradient: n copies per row
+          param_update(st, A->gamma.as<double2>(), db, A->mg.as<double2>(), A->vg.as<double2>(), da, false, ts);
+          colsum(st, gcur, rows, da, (double)da, db);
+          param_update(st, A->beta.as<double2>(), db, A->mbt.as<double2>(), A->vbt.as<double2>(), da, false, ts);
+          ts.batch = (double)B;  // masked_attention_head.rs:352: the sequences
+          param_update(st, A->wqkv.as<double2>(), dW, A->mw.as<double2>(), A->vw.as<double2>(), (long)3 * da * da, true, ts);
+          attn_bias_update(st, A->bias_re.as<double>(), mc, n->tr_dA.as<double>(), (int)B, H, S, ts);
+          A->updates++;
+        }
+        std::swap(gcur, gnext);
+        break;
+      }
+      case K_NORM: {  // NormalNormLayer::backward; the walk does not update a standalone Norm
+        auto* N = (NormLayer*)L;
+        norm_backward(st, X, nullptr, rows, N->d_in, N->eps, N->gamma.as<double2>(), N->beta.as<double2>(), gcur, gnext,
+                      n->tr_pg.as<double2>());
+        std::swap(gcur, gnext);
+        break;
+      }
+      case K_POSENC: {
+        auto* P = (PositionalEncodingLayer*)L;
+        rope_backward(st, gcur, rows, S, P->d_in, P->cs.as<double2>(), gnext);
+        std::swap(gcur, gnext);
+        break;
+      }
+      case K_EMBEDDING: {  // EmbeddingLayer::backward passes the gradient on (embedding_layer.rs:214-221)
+        auto* E = (EmbeddingLayer*)L;
+        if (embed_upd && !eids.empty())
+          embedding_update(st, E->table.as<double2>(), (int)E->d_out, n->tr_eid.as<uint32_t>(), (int)eids.size(),
+                           n->tr_est.as<int>(), n->tr_eocc.as<int>(), gcur, learning_rate, (double)B * (double)E->vocab,
+                           err);
+        break;
+      }
+      default: break;
+    }
+  }
+  if (update_params) drop_graph(n);  // the weights changed under any captured step
+  if (out_grad_input) {
+    const int dlow = (int)n->layers[stop]->d_in;
+    HIP_TRY(hipMemcpyAsync(out_grad_input, gcur, (size_t)rows * dlow * c16, hipMemcpyDeviceToHost, st));
+  }
   HIP_TRY(hipStreamSynchronize(st));
   return check_err_word(n);
 }

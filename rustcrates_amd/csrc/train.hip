@@ -179,4 +179,345 @@ void linear_update(hipStream_t st, double2* W, const double2* dW, double2* mW, d
                  vb, V, ts);
 }
 
+// ---------------------------------------------------------------------------
+// the rest of backward's reverse walk (transformer_network.rs:506-636)
+// ---------------------------------------------------------------------------
+
+// sum over a 256-thread block through LDS; every thread gets the total
+__device__ double2 block_sum2(double2 v, double2* sh) {
+  sh[threadIdx.x] = v;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) sh[threadIdx.x] = cadd(sh[threadIdx.x], sh[threadIdx.x + w]);
+    __syncthreads();
+  }
+  const double2 r = sh[0];
+  __syncthreads();
+  return r;
+}
+__device__ double block_max1(double v, double* sh) {
+  sh[threadIdx.x] = v;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) sh[threadIdx.x] = fmax(sh[threadIdx.x], sh[threadIdx.x + w]);
+    __syncthreads();
+  }
+  const double r = sh[0];
+  __syncthreads();
+  return r;
+}
+
+// f64 / Complex and Complex::powf (num-complex 0.4.6: from_polar(r^e, theta e))
+__device__ __forceinline__ double2 rdivc(double a, double2 z) {
+  const double ns = z.x * z.x + z.y * z.y;
+  return make_double2(a * z.x / ns, -a * z.y / ns);
+}
+__device__ __forceinline__ double2 cpowf(double2 z, double e) {
+  const double r = pow(hypot(z.x, z.y), e), th = atan2(z.y, z.x) * e;
+  return make_double2(r * cos(th), r * sin(th));
+}
+
+// NormalNormLayer::backward, Complex arm (norm_layer.rs:132-209), one block per
+// row.  The row's input is x, or Re(x + resid) + 0i for the Norm inside a
+// SelfAttention layer (add_matrix_3d_c); its forward (normalize, :64-82) is
+// recomputed for x_hat, mean and variance.  The reference's f-loop is
+// collapsed: with t_d = x_d - mu and the row sums P = sum dout_d t_d,
+// D = sum dout_d, M = sum -2 t_d / n, element f's gradient is
+//   g_f = dout_f gamma_f / sqrt(v) + gamma_f P (-1/2) v^-3/2 (2 t_f / n)
+//         + (-D gamma_f / sqrt(v) + gamma_f P (-1/2) v^-3/2 M) / n,
+// v = variance + 1e-8, and the row's input gradient is Re(g_j + (sum_f g_f) dout_j).
+// pg[r][j] = dout_j x_hat_j feeds gamma's gradient (n copies per row).
+__global__ __launch_bounds__(256) void k_norm_backward(const double2* __restrict__ x, const double2* __restrict__ resid,
+                                                       int n, double eps, const double2* __restrict__ gamma,
+                                                       const double2* __restrict__ beta,
+                                                       const double2* __restrict__ dout, double2* __restrict__ dx,
+                                                       double2* __restrict__ pg) {
+  __shared__ double2 sh[256];
+  const long r = blockIdx.x;
+  const double2* xr = x + r * n;
+  const double2* gr = dout + r * n;
+  const double len = (double)n;
+  auto xin = [&](int j) {
+    if (!resid) return xr[j];
+    return make_double2(xr[j].x + resid[r * n + j].x, 0.0);
+  };
+  double2 s = make_double2(0.0, 0.0);
+  for (int j = threadIdx.x; j < n; j += 256) s = cadd(s, xin(j));
+  const double2 mu = cunscale(block_sum2(s, sh), len);
+  s = make_double2(0.0, 0.0);
+  for (int j = threadIdx.x; j < n; j += 256) {
+    const double2 t = csub(xin(j), mu);
+    s = cadd(s, cmul(t, t));
+  }
+  const double2 var = cunscale(block_sum2(s, sh), len);
+  const double2 sd = csqrt_nc(cadd(var, make_double2(eps, 0.0)));
+  const double2 vb = cadd(var, make_double2(1e-8, 0.0));
+  const double2 std_inv = rdivc(1.0, csqrt_nc(vb));
+  const double2 vpm32 = rdivc(1.0, cpowf(vb, 1.5));
+  double2 P = make_double2(0.0, 0.0), D = P, M = P;
+  for (int j = threadIdx.x; j < n; j += 256) {
+    const double2 t = csub(xin(j), mu);
+    P = cadd(P, cmul(gr[j], t));
+    D = cadd(D, gr[j]);
+    M = cadd(M, cunscale(cscale(t, -2.0), len));
+  }
+  P = block_sum2(P, sh);
+  D = block_sum2(D, sh);
+  M = block_sum2(M, sh);
+  const double2 dmu_sum = cmul(D, make_double2(-std_inv.x, -std_inv.y));
+  const double2 pv = cmul(cscale(P, -0.5), vpm32);
+  double2 gs = make_double2(0.0, 0.0);
+  for (int j = threadIdx.x; j < n; j += 256) {
+    const double2 t = csub(xin(j), mu);
+    const double2 dvar = cmul(gamma[j], pv);
+    const double2 dmu = cadd(cmul(dmu_sum, gamma[j]), cmul(dvar, M));
+    const double2 g = cadd(cadd(cmul(cmul(gr[j], gamma[j]), std_inv), cmul(dvar, cunscale(cscale(t, 2.0), len))),
+                           cunscale(dmu, len));
+    gs = cadd(gs, g);
+    dx[r * n + j] = g;  // held until the row total is known
+    const double2 xh = cadd(cmul(cdiv(t, sd), gamma[j]), beta[j]);
+    pg[r * n + j] = cmul(gr[j], make_double2(xh.x, 0.0));
+  }
+  gs = block_sum2(gs, sh);
+  for (int j = threadIdx.x; j < n; j += 256) {
+    const double2 g = dx[r * n + j];
+    dx[r * n + j] = make_double2(g.x + cmul(gs, gr[j]).x, 0.0);
+  }
+}
+
+// out[j] = mult * (sum over rows r of X[r][j]), rows in order
+__global__ __launch_bounds__(256) void k_colsum(const double2* __restrict__ X, long rows, int n, double mult,
+                                                double2* __restrict__ out) {
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  if (j >= n) return;
+  double2 acc = make_double2(0.0, 0.0);
+  for (long r = 0; r < rows; ++r) acc = cadd(acc, X[r * n + j]);
+  out[j] = cscale(acc, mult);
+}
+
+// One query row of one head (grid: S x H x B): the forward's attention
+// weights A (masked_attention_head.rs:184-205: Re of the scaled scores plus
+// Re(bias_pos), the causal mask, softmax_complex_padding_real) and
+// dl_da = backpropagate_softmax_masked_real of dl_ds = G conj(V)^T over the
+// row Jacobian s_j (delta_jk - s_k) (utils/derivative.rs:100-131, 253-272):
+// dA_j = s_j (r_j - sum_k s_k r_k), r_k = Re(dl_ds_k); padded rows 0.
+__global__ __launch_bounds__(256) void k_attn_probs_grad(const double2* __restrict__ qkv, const double* __restrict__ bias_re,
+                                                         int mc, const uint32_t* __restrict__ mask,
+                                                         const double2* __restrict__ G, int S, int H, int dh, double c,
+                                                         double* __restrict__ A, double* __restrict__ dA) {
+  extern __shared__ double dyn[];
+  double* sc = dyn;       // [S] scores, then weights
+  double* rr = dyn + S;   // [S] Re(dl_ds)
+  __shared__ double shm[256];
+  __shared__ double2 sh2[256];
+  const int i = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int d = H * dh, ld = 3 * d;
+  const long row = (long)b * S + i;
+  double* Ar = A + (((long)b * H + h) * S + i) * S;
+  double* dAr = dA + (((long)b * H + h) * S + i) * S;
+  if (mask[row] == 0) {
+    for (int j = threadIdx.x; j < S; j += 256) Ar[j] = dAr[j] = 0.0;
+    return;
+  }
+  const double2* q = qkv + row * ld + (long)h * dh;
+  const double2* g = G + row * d + (long)h * dh;
+  const double* bp = bias_re + ((long)h * mc + i) * mc;
+  double mx = -INFINITY;
+  for (int j = threadIdx.x; j < S; j += 256) {
+    const double2* k = qkv + ((long)b * S + j) * ld + d + (long)h * dh;
+    const double2* v = qkv + ((long)b * S + j) * ld + 2 * d + (long)h * dh;
+    double s = 0.0, rv = 0.0;
+    for (int m = 0; m < dh; ++m) {
+      s = s + (q[m].x * k[m].x - q[m].y * k[m].y);
+      rv = rv + (g[m].x * v[m].x + g[m].y * v[m].y);
+    }
+    s = j > i ? -1e12 : s * c + bp[j];
+    sc[j] = s;
+    rr[j] = rv;
+    mx = fmax(mx, s);
+  }
+  mx = block_max1(mx, shm);
+  double2 acc = make_double2(0.0, 0.0);
+  for (int j = threadIdx.x; j < S; j += 256) {
+    sc[j] = exp(sc[j] - mx);
+    acc.x += sc[j];
+  }
+  const double sum = block_sum2(acc, sh2).x;
+  acc = make_double2(0.0, 0.0);
+  for (int j = threadIdx.x; j < S; j += 256) {
+    sc[j] = sc[j] / sum;
+    acc.x += sc[j] * rr[j];
+  }
+  const double sr = block_sum2(acc, sh2).x;
+  for (int j = threadIdx.x; j < S; j += 256) {
+    Ar[j] = sc[j];
+    dAr[j] = sc[j] * (rr[j] - sr);
+  }
+}
+
+// The three small products of MaskedAttentionHead::backward per (sequence,
+// head), one output element each (masked_attention_head.rs:276-316):
+//   dV = A^T G,  dQ = dA conj(K) c,  dK = dA^T conj(Q) c
+// written as the gradient of the packed [q | k | v] row (head h at h*dh).
+__global__ __launch_bounds__(256) void k_attn_dqkv(const double2* __restrict__ qkv, const double* __restrict__ A,
+                                                   const double* __restrict__ dA, const double2* __restrict__ G, int B,
+                                                   int S, int H, int dh, double c, double2* __restrict__ dqkv) {
+  const long t = (long)blockIdx.x * 256 + threadIdx.x;
+  const long total = (long)B * H * S * dh;
+  if (t >= total) return;
+  const int m = (int)(t % dh);
+  const int i = (int)((t / dh) % S);
+  const int h = (int)((t / ((long)dh * S)) % H);
+  const int b = (int)(t / ((long)dh * S * H));
+  const int d = H * dh, ld = 3 * d;
+  const double* Ab = A + ((long)b * H + h) * S * S;
+  const double* dAb = dA + ((long)b * H + h) * S * S;
+  const double2* base = qkv + (long)b * S * ld + (long)h * dh + m;
+  const double2* gb = G + (long)b * S * d + (long)h * dh + m;
+  double2 dq = make_double2(0.0, 0.0), dk = dq, dv = dq;
+  for (int j = 0; j < S; ++j) {
+    const double2 kj = base[(long)j * ld + d];     // K[j][m]
+    const double2 qj = base[(long)j * ld];         // Q[j][m]
+    const double a = dAb[(long)i * S + j];         // dA[i][j]
+    const double at = dAb[(long)j * S + i];        // dA[j][i]
+    dq = cadd(dq, make_double2(a * kj.x, -a * kj.y));
+    dk = cadd(dk, make_double2(at * qj.x, -at * qj.y));
+    dv = cadd(dv, cscale(gb[(long)j * d], Ab[(long)j * S + i]));
+  }
+  double2* o = dqkv + ((long)b * S + i) * ld + (long)h * dh + m;
+  o[0] = cscale(dq, c);
+  o[d] = cscale(dk, c);
+  o[2 * d] = dv;
+}
+
+// bias_pos's update on its S x S slice (masked_attention_head.rs:387-393,
+// 427-434): the gradient dl_da summed over the sequences (group_gradient_batch),
+// clipped; the first update descends, later ones run AdamW from zero moments
+// (the reference never reloads prev_m/v_bias_pos).  Only Re(bias_pos) reaches
+// the scores, and its update does not depend on the imaginary part.
+__global__ __launch_bounds__(256) void k_attn_bias_update(double* __restrict__ bias_re, int mc,
+                                                          const double* __restrict__ dA, int B, int H, int S,
+                                                          TrainStep ts) {
+  const long t = (long)blockIdx.x * 256 + threadIdx.x;
+  if (t >= (long)H * S * S) return;
+  const int j = (int)(t % S), i = (int)((t / S) % S), h = (int)(t / ((long)S * S));
+  double g = 0.0;
+  for (int b = 0; b < B; ++b) g += dA[(((long)b * H + h) * S + i) * S + j];
+  double* w = bias_re + ((long)h * mc + i) * mc + j;
+  double2 m0 = make_double2(0.0, 0.0), v0 = m0;
+  *w = update1(make_double2(*w, 0.0), make_double2(g, 0.0), &m0, &v0, ts, true).x;
+}
+
+// one parameter array: update1 on every element
+__global__ __launch_bounds__(256) void k_param_update(double2* __restrict__ w, const double2* __restrict__ g,
+                                                      double2* __restrict__ m, double2* __restrict__ v, long n,
+                                                      int weight, TrainStep ts) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) w[i] = update1(w[i], g[i], &m[i], &v[i], ts, weight != 0);
+}
+
+// PositionalEncodingLayer::backward (positional_encoding_layer.rs:101-144):
+// the pairs of row s rotated back by the forward's angle at position s
+// (cs: the forward's (cos, sin) table)
+__global__ __launch_bounds__(256) void k_rope_backward(const double2* __restrict__ G, long rows, int S, int d,
+                                                       const double2* __restrict__ cs, double2* __restrict__ out) {
+  const long t = (long)blockIdx.x * 256 + threadIdx.x;
+  const int half = d / 2;
+  if (t >= rows * half) return;
+  const long r = t / half;
+  const int i = (int)(t % half);
+  const int pos = (int)(r % S);
+  const double2 w = cs[(long)pos * half + i];  // (cos, sin)
+  const double2 ge = G[r * d + 2 * i], go = G[r * d + 2 * i + 1];
+  out[r * d + 2 * i] = make_double2(ge.x * w.x + go.x * w.y, ge.y * w.x + go.y * w.y);
+  out[r * d + 2 * i + 1] = make_double2(-ge.x * w.y + go.x * w.x, -ge.y * w.y + go.y * w.x);
+}
+
+// EmbeddingLayer::update_parameters (embedding_layer.rs:223-264): one block
+// per distinct target id, its occurrences in the reference's order: the row
+// moves by lr * clip(g) / (B V) (g: the gradient row at the target's index),
+// then is normalized (utils/normalization.rs:3-20).  A non-finite gradient or
+// row raises the error word (the reference panics).
+__global__ __launch_bounds__(256) void k_embedding_update(double2* __restrict__ table, int d,
+                                                          const uint32_t* __restrict__ ids,
+                                                          const int* __restrict__ start, const int* __restrict__ occ,
+                                                          const double2* __restrict__ G, double lr, double bs,
+                                                          uint32_t* __restrict__ err) {
+  __shared__ double2 sh[256];
+  double2* row = table + (long)ids[blockIdx.x] * d;
+  const double len = (double)d;
+  bool bad = false;
+  for (int k = start[blockIdx.x]; k < start[blockIdx.x + 1]; ++k) {
+    const double2* g = G + (long)occ[k] * d;
+    double2 s = make_double2(0.0, 0.0);
+    for (int j = threadIdx.x; j < d; j += 256) {
+      double2 gj = g[j];
+      const double gn = hypot(gj.x, gj.y);
+      if (gn > 1.0) gj = cscale(gj, 1.0 / gn);
+      if (!(isfinite(gj.x) && isfinite(gj.y))) bad = true;
+      const double2 w = csub(row[j], cscale(cunscale(gj, bs), lr));
+      if (!(isfinite(w.x) && isfinite(w.y))) bad = true;
+      row[j] = w;
+      s = cadd(s, w);
+    }
+    __syncthreads();
+    const double2 mean = cunscale(block_sum2(s, sh), len);
+    s = make_double2(0.0, 0.0);
+    for (int j = threadIdx.x; j < d; j += 256) {
+      const double2 t = csub(row[j], mean);
+      s = cadd(s, cmul(t, t));
+    }
+    const double2 sd = csqrt_nc(cadd(cunscale(block_sum2(s, sh), len), make_double2(0.00000000001, 0.0)));
+    for (int j = threadIdx.x; j < d; j += 256) row[j] = cdiv(csub(row[j], mean), sd);
+    __syncthreads();
+  }
+  if (bad) atomicOr(err, (uint32_t)EB_TRAIN_NONFINITE);
+}
+
+void norm_backward(hipStream_t st, const double2* x, const double2* resid, long rows, int n, double eps,
+                   const double2* gamma, const double2* beta, const double2* dout, double2* dx, double2* pg) {
+  if (rows > 0) MITOK_LAUNCH(k_norm_backward, dim3((unsigned)rows), dim3(256), 0, st, x, resid, n, eps, gamma, beta, dout, dx, pg);
+}
+
+void colsum(hipStream_t st, const double2* X, long rows, int n, double mult, double2* out) {
+  if (n > 0) MITOK_LAUNCH(k_colsum, dim3((n + 255) / 256), dim3(256), 0, st, X, rows, n, mult, out);
+}
+
+void attn_probs_grad(hipStream_t st, const double2* qkv, const double* bias_re, int mc, const uint32_t* mask,
+                     const double2* G, int B, int S, int H, int dh, double c, double* A, double* dA) {
+  MITOK_LAUNCH(k_attn_probs_grad, dim3(S, H, B), dim3(256), (size_t)2 * S * sizeof(double), st, qkv, bias_re, mc, mask,
+               G, S, H, dh, c, A, dA);
+}
+
+void attn_dqkv(hipStream_t st, const double2* qkv, const double* A, const double* dA, const double2* G, int B, int S,
+               int H, int dh, double c, double2* dqkv) {
+  const long total = (long)B * H * S * dh;
+  if (total > 0)
+    MITOK_LAUNCH(k_attn_dqkv, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, qkv, A, dA, G, B, S, H, dh, c, dqkv);
+}
+
+void attn_bias_update(hipStream_t st, double* bias_re, int mc, const double* dA, int B, int H, int S, const TrainStep& ts) {
+  const long total = (long)H * S * S;
+  if (total > 0)
+    MITOK_LAUNCH(k_attn_bias_update, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, bias_re, mc, dA, B, H, S, ts);
+}
+
+void param_update(hipStream_t st, double2* w, const double2* g, double2* m, double2* v, long n, bool weight,
+                  const TrainStep& ts) {
+  if (n > 0)
+    MITOK_LAUNCH(k_param_update, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, w, g, m, v, n, weight ? 1 : 0, ts);
+}
+
+void rope_backward(hipStream_t st, const double2* G, long rows, int S, int d, const double2* cs, double2* out) {
+  const long total = rows * (d / 2);
+  if (total > 0)
+    MITOK_LAUNCH(k_rope_backward, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, G, rows, S, d, cs, out);
+}
+
+void embedding_update(hipStream_t st, double2* table, int d, const uint32_t* ids, int n_ids, const int* start,
+                      const int* occ, const double2* G, double lr, double bs, uint32_t* err) {
+  if (n_ids > 0)
+    MITOK_LAUNCH(k_embedding_update, dim3(n_ids), dim3(256), 0, st, table, d, ids, start, occ, G, lr, bs, err);
+}
+
 }  // namespace mitok

@@ -820,3 +820,158 @@ def test_ffn_and_head_gradients_match_finite_differences():
                 lm = loss(*args)
                 fd = (lp - lm) / (2 * h)
                 assert abs(getattr(grad[idx], part) - fd) < 1e-7, (k, idx, part, grad[idx], fd)
+
+
+def _np_heads(X, wq, wk, wv, bp, mask):
+    """The heads' concatenated output of a stateless pass, written from the
+    reference text (masked_attention_head.rs:122-220) with numpy."""
+    H, d, dh = wq.shape
+    B, S, _ = X.shape
+    out = np.zeros((B, S, d), complex)
+    for b in range(B):
+        for hh in range(H):
+            q, k, v = X[b] @ wq[hh], X[b] @ wk[hh], X[b] @ wv[hh]
+            sc = (q @ k.T) * (1.0 / (1e-8 + math.sqrt(dh))) + bp[hh, :S, :S]
+            sc = np.where(np.tril(np.ones((S, S))) > 0, sc, -1e12 - 1e12j)
+            re = sc.real - sc.real.max(axis=1, keepdims=True)
+            p = np.exp(re) / np.exp(re).sum(axis=1, keepdims=True)
+            p[mask[b] == 0] = 0
+            out[b, :, hh * dh:(hh + 1) * dh] = p @ v
+    return out
+
+
+def test_attention_heads_gradients_match_finite_differences():
+    """MaskedAttentionHead::backward (masked_attention_head.rs:222-345) gives
+    dL/dRe + i dL/dIm of L = Re sum conj(C) * heads(X) in every real
+    coordinate of X, Wq, Wk, Wv and Re(bias_pos); bias_pos's imaginary part
+    never reaches the softmax, and its gradient is real."""
+    rng = np.random.default_rng(47)
+    B, S, d, H, mc = 2, 4, 4, 2, 6
+    X = 0.6 * (rng.standard_normal((B, S, d)) + 1j * rng.standard_normal((B, S, d)))
+    wq, wk, wv = (0.7 * (rng.standard_normal((H, d, d // H)) + 1j * rng.standard_normal((H, d, d // H)))
+                  for _ in range(3))
+    bp = rng.standard_normal((H, mc, mc)) + 1j * rng.standard_normal((H, mc, mc))
+    mask = np.array([[1, 1, 1, 1], [1, 1, 1, 0]], np.uint32)
+    C = rng.standard_normal((B, S, d)) + 1j * rng.standard_normal((B, S, d))
+
+    def loss(X, wq, wk, wv, bp):
+        return float(np.real(np.sum(np.conj(C) * _np_heads(X, wq, wk, wv, bp, mask))))
+
+    dX, dwq, dwk, dwv, dbias = oracle.attention_heads_backward(X, mask, wq, wk, wv, bp, C)
+    assert np.all(dbias.imag == 0)
+    params = [X, wq, wk, wv, bp]
+    grads = [dX, dwq, dwk, dwv, None]
+    h = 1e-6
+    for k, arr in enumerate(params):
+        for idx in np.ndindex(arr.shape):
+            if k == 4 and (idx[1] >= S or idx[2] >= S):
+                continue
+            for unit, part in ((1.0, "real"), (1j, "imag")):
+                args = [p.copy() for p in params]
+                args[k][idx] += h * unit
+                lp = loss(*args)
+                args[k][idx] -= 2 * h * unit
+                lm = loss(*args)
+                fd = (lp - lm) / (2 * h)
+                g = dbias[idx] if k == 4 else grads[k][idx]
+                assert abs(getattr(g, part) - fd) < 1e-7, (k, idx, part, g, fd)
+
+
+def test_self_attention_backward_runs_the_norm_on_the_residual_sum():
+    """SelfAttentionLayer::backward = the Norm's backward on its input
+    Re(heads(X) + X) (the residual, add_matrix_3d_c), then the heads; the
+    heads' output here comes from an independent numpy forward."""
+    rng = np.random.default_rng(48)
+    B, S, d, H, mc = 2, 5, 8, 2, 8
+    X = rng.standard_normal((B, S, d)) + 1j * rng.standard_normal((B, S, d))
+    wq, wk, wv = (0.4 * (rng.standard_normal((H, d, d // H)) + 1j * rng.standard_normal((H, d, d // H)))
+                  for _ in range(3))
+    bp = rng.standard_normal((H, mc, mc)) + 1j * rng.standard_normal((H, mc, mc))
+    gamma = rng.standard_normal(d) + 1j * rng.standard_normal(d)
+    beta = rng.standard_normal(d) + 1j * rng.standard_normal(d)
+    mask = np.ones((B, S), np.uint32)
+    mask[1, 3:] = 0
+    G = rng.standard_normal((B, S, d)) + 1j * rng.standard_normal((B, S, d))
+    got = oracle.self_attention_backward(X, mask, wq, wk, wv, bp, gamma, beta, G)
+    xn = (_np_heads(X, wq, wk, wv, bp, mask) + X).real.astype(complex)
+    gn, dg, db = oracle.norm_backward(xn, gamma, beta, G, 1e-12)
+    want = oracle.attention_heads_backward(X, mask, wq, wk, wv, bp, gn) + (dg, db)
+    for a, b in zip(got, want):
+        np.testing.assert_allclose(a, b, rtol=1e-10, atol=1e-10 * np.abs(b).max())
+
+
+def test_norm_backward_structure():
+    """NormalNormLayer::backward's Complex arm (norm_layer.rs:157-197) is the
+    reference's own formula, not the derivative of the Norm, so no finite
+    difference fixes it.  What its text fixes: rows are real; per row the
+    result is g_j + (sum_f g_f) dout_j with g linear in dout, so scaling dout
+    by t gives t*a + t^2*b (a dropped identity or product term fails); gamma's
+    gradient gathers n copies of sum(dout * x_hat), beta's n copies of
+    sum(dout)."""
+    rng = np.random.default_rng(49)
+    rows, n = 3, 6
+    x = rng.standard_normal((rows, n)) + 1j * rng.standard_normal((rows, n))
+    gamma = rng.standard_normal(n) + 1j * rng.standard_normal(n)
+    beta = rng.standard_normal(n) + 1j * rng.standard_normal(n)
+    dout = rng.standard_normal((rows, n)) + 1j * rng.standard_normal((rows, n))
+    r = [oracle.norm_backward(x, gamma, beta, t * dout, 1e-5) for t in (1.0, 2.0, 3.0)]
+    for dx, _, _ in r:
+        assert np.all(dx.imag == 0)
+    d1, d2, d3 = (a[0].real for a in r)
+    # f(t) = t a + t^2 b: f(3) - 3 f(2) + 3 f(1) = 0 and b = (f(2) - 2 f(1)) / 2 != 0
+    np.testing.assert_allclose(d3 - 3 * d2 + 3 * d1, 0, atol=1e-9 * np.abs(d3).max())
+    assert np.abs(d2 - 2 * d1).max() > 1e-3 * np.abs(d1).max()
+    np.testing.assert_allclose(oracle.norm_backward(x, gamma, beta, 0 * dout, 1e-5)[0], 0)
+    xhat = np.array([[oracle.layernorm_row(row, 1e-5, gamma, beta)[i] for i in range(n)] for row in x])
+    np.testing.assert_allclose(r[0][1], n * np.sum(dout * xhat, axis=0), rtol=1e-12)
+    np.testing.assert_allclose(r[0][2], n * np.sum(dout, axis=0), rtol=1e-12)
+
+
+def test_rope_backward_is_the_adjoint_of_rope():
+    """PositionalEncodingLayer::backward (positional_encoding_layer.rs:101-144)
+    rotates back by the forward's angle at each row index: for every x and g,
+    Re<backward(g), x> = Re<g, forward(x)>; and it inverts the forward."""
+    rng = np.random.default_rng(50)
+    B, S, d, base = 2, 7, 8, 10.0
+    x = rng.standard_normal((B, S, d)) + 1j * rng.standard_normal((B, S, d))
+    g = rng.standard_normal((B, S, d)) + 1j * rng.standard_normal((B, S, d))
+    fx = np.array([[oracle.rope_row(x[b, s], base, s) for s in range(S)] for b in range(B)])
+    bg = oracle.rope_backward(g, base)
+    lhs = np.real(np.vdot(bg, x))
+    rhs = np.real(np.vdot(g, fx))
+    assert abs(lhs - rhs) < 1e-12 * abs(rhs) + 1e-12
+    np.testing.assert_allclose(oracle.rope_backward(fx, base), x, rtol=1e-13, atol=1e-13)
+
+
+def test_embedding_update_touches_target_rows_and_normalizes():
+    """EmbeddingLayer::update_parameters (embedding_layer.rs:223-264): only
+    target ids' rows change; a single occurrence gives
+    normalize(row - lr * clip(g_t) / (B * V)) (normalize: zero mean, complex
+    variance 1 up to the 1e-11 floor); a repeated id applies its occurrences
+    in order to the already normalized row."""
+    rng = np.random.default_rng(51)
+    V, d, B, S = 9, 6, 2, 5
+    table = rng.standard_normal((V, d)) + 1j * rng.standard_normal((V, d))
+    G = 3 * (rng.standard_normal((B, S, d)) + 1j * rng.standard_normal((B, S, d)))
+    targets = np.array([[4, 7, 4], [2, 0, 0]], np.uint32)
+    tlens = np.array([3, 1], np.uint32)
+    lr = 0.5
+    new = oracle.embedding_update(table, G, targets, tlens, lr)
+    for i in set(range(V)) - {4, 7, 2}:
+        assert np.array_equal(new[i], table[i])
+
+    def clip(z):
+        n = np.abs(z)
+        return np.where(n > 1, z / np.maximum(n, 1e-300), z)
+
+    def norm(r):
+        m = r.mean()
+        return (r - m) / np.sqrt(np.mean((r - m) ** 2) + 1e-11)
+
+    bs = B * V
+    np.testing.assert_allclose(new[7], norm(table[7] - lr * clip(G[0, 1]) / bs), rtol=1e-12, atol=1e-13)
+    np.testing.assert_allclose(new[2], norm(table[2] - lr * clip(G[1, 0]) / bs), rtol=1e-12, atol=1e-13)
+    r4 = norm(norm(table[4] - lr * clip(G[0, 0]) / bs) - lr * clip(G[0, 2]) / bs)
+    np.testing.assert_allclose(new[4], r4, rtol=1e-12, atol=1e-13)
+    for i in (2, 4, 7):
+        assert abs(new[i].mean()) < 1e-13 and abs(np.mean(new[i] ** 2) - 1) < 1e-9

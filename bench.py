@@ -300,6 +300,7 @@ def run(args, w, net):
     if not args.no_train and args.workload.startswith("c3"):
         log("output-head training step")
         out["head_train"] = head_train_step(cfg)
+        out["train_step"] = train_step(cfg)
 
     return out
 
@@ -330,6 +331,43 @@ def head_train_step(cfg, B=8, S=128, T=64, reps=5):
             "ms_per_step": round(ms, 3), "alg_gflop": round(flops / 1e9, 2),
             "tflops": round(flops / (ms / 1e3) / 1e12, 3),
             "mfma_frac": round(flops / (ms / 1e3) / 1e12 / FP64_MFMA_PEAK_TFS, 4)}
+
+
+def train_step(cfg, B=8, S=128, T=64, reps=3):
+    """One step of the reference's train loop (transformer_network.rs:35-163)
+    on config 3: the TRAINING-mode predict of B x S rows (its [B][S][V]
+    softmax output copied to the host for the loss), then backward over every
+    layer with every update (mitok_backward).  Algorithmic flops of the
+    backward's products (8 M N K each): per attention layer the Q/K/V
+    recompute, their weight and input gradients (3 x 24 rows d^2); per
+    FeedForward the Dense recompute twice and four gradient products
+    (6 x 8 rows d F); the vocab Linear's two (16 rows d V)."""
+    rows = B * S
+    with ra.Network(0) as net:
+        configs.build_network(net, cfg, mode=ra.TRAINING)
+        ids = seeded.prompts(21, [S] * B, cfg.vocab)
+        targets = seeded.prompts(22, [T] * B, cfg.vocab)
+        nl = net.num_layers
+        for t in (1, 2):  # every layer's first update (plain descent), then AdamW
+            net.predict(ids, forward_only=False)
+            net.backward(targets, layers=nl - 1, update=True, learning_rate=1e-4, time_step=t, want_grad_input=False)
+        ra.device_synchronize(0)
+        fwd = bwd = 0.0
+        for t in range(reps):
+            t0 = time.perf_counter()
+            net.predict(ids, forward_only=False)
+            t1 = time.perf_counter()
+            net.backward(targets, layers=nl - 1, update=True, learning_rate=1e-4, time_step=3 + t, want_grad_input=False)
+            fwd += t1 - t0
+            bwd += time.perf_counter() - t1
+    fwd_ms, bwd_ms = fwd / reps * 1e3, bwd / reps * 1e3
+    d, F, V = cfg.d, cfg.ffn, cfg.vocab
+    flops = cfg.layers * (3 * 24.0 * rows * d * d + 6 * 8.0 * rows * d * F) + 16.0 * rows * d * V
+    return {"config": f"{cfg.name}, {B} x {S} rows, {T} targets per sequence, backward over all {nl - 1} "
+                      "layers below the Softmax with every update",
+            "forward_ms": round(fwd_ms, 3), "backward_ms": round(bwd_ms, 3),
+            "backward_alg_gflop": round(flops / 1e9, 2),
+            "backward_tflops": round(flops / (bwd_ms / 1e3) / 1e12, 3)}
 
 
 if __name__ == "__main__":

@@ -71,9 +71,10 @@ WORKLOADS = {
 }
 
 
-def build_network(net, cfg: ModelConfig, seed: int | None = None):
+def build_network(net, cfg: ModelConfig, seed: int | None = None, mode: int = PRODUCTION):
     """Appends cfg's layer stack to `net` (HIP Network or the CPU checker) and
-    fills every tensor from the seeded counter generator."""
+    fills every tensor from the seeded counter generator; `mode` is the
+    Softmax's (TRAINING for a network that backward differentiates)."""
     net.add_embedding(cfg.vocab, cfg.d)
     if cfg.rope:
         net.add_positional_encoding(cfg.d, cfg.rope_base)
@@ -82,7 +83,7 @@ def build_network(net, cfg: ModelConfig, seed: int | None = None):
         net.add_self_attention(cfg.heads, cfg.d, cfg.max_ctx, cfg.attn_eps)
         net.add_feed_forward(cfg.d, cfg.ffn)
     net.add_linear(cfg.d, cfg.vocab)
-    net.add_softmax(PRODUCTION)
+    net.add_softmax(mode)
     net.init_seeded(cfg.seed if seed is None else seed)
     return net
 

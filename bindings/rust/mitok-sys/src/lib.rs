@@ -75,6 +75,8 @@ extern "C" {
     pub fn mitok_predict(net: *mut MitokNetwork, ids: *const u32, lens: *const u32, batch: u32, seq: u32,
                          time_steps: *const u32, forward_only: c_int, last_row_only: c_int, out: *mut c_double,
                          out_padding_mask: *mut u32) -> c_int;
+    pub fn mitok_predict_targets(net: *mut MitokNetwork, ids: *const u32, lens: *const u32, batch: u32, seq: u32,
+                                 target_rows: u32, out_probs: *mut c_double, out_padding_mask: *mut u32) -> c_int;
     pub fn mitok_forward_layers(net: *mut MitokNetwork, first: u32, last: u32, inp: *const c_double,
                                 padding_mask: *const u32, batch: u32, seq: u32, time_steps: *const u32,
                                 forward_only: c_int, out: *mut c_double) -> c_int;

@@ -121,6 +121,16 @@ int mitok_reset(mitok_network* net);
 int mitok_predict(mitok_network* net, const uint32_t* ids, const uint32_t* lens, uint32_t batch, uint32_t seq,
                   const uint32_t* time_steps, int forward_only, int last_row_only, double* out,
                   uint32_t* out_padding_mask);
+/* The training pass of train (transformer_network.rs:73-79): mitok_predict with
+ * forward_only = 0 when each sequence's last target_rows ids are its targets
+ * (LayerInput's target_batch_ids).  Only the DiscreteWavelet layer reads them:
+ * it compresses each sequence's first seq - target_rows rows and passes the
+ * target rows on (wavelet_discrete_layer.rs:102-134, separate_input_target
+ * :233-279), so seq' = mitok_seq_out_len(seq - target_rows) + target_rows per
+ * wavelet layer.  With a wavelet layer and target_rows > 0 every sequence
+ * must be unpadded (lens[b] == seq; the reference panics otherwise). */
+int mitok_predict_targets(mitok_network* net, const uint32_t* ids, const uint32_t* lens, uint32_t batch, uint32_t seq,
+                          uint32_t target_rows, double* out_probs, uint32_t* out_padding_mask);
 
 /* Layers [first, last) on hidden states: in [batch][seq][dim_in] complex,
  * out [batch][seq][dim_out] complex; padding_mask [batch][seq] or NULL (all 1).
@@ -196,10 +206,11 @@ int mitok_backward_head(mitok_network* net, const uint32_t* targets, const uint3
  *  - Embedding: passes the gradient on; with update_params
  *    EmbeddingLayer::update_parameters (embedding_layer.rs:223-264) moves and
  *    renormalizes the table rows of the target ids.
- * A DiscreteWavelet layer in the walk is MITOK_ERR_STATE (its training pass
- * splits input and target rows, wavelet_discrete_layer.rs:233-279).
+ *  - DiscreteWavelet (wavelet_discrete_layer.rs:163-207): the gradient of
+ *    the compressed rows through decompress_partial (grad_dwt_1d_trend) and
+ *    align_gradient_rows_complex, the target rows' gradient passed through.
  * out_grad_input: the gradient of the lowest walked layer's input
- * [batch][seq'][its d_in], or NULL. */
+ * [batch][rows of that layer's input][its d_in], or NULL. */
 int mitok_backward(mitok_network* net, const uint32_t* targets, const uint32_t* tlens, uint32_t batch, uint32_t T,
                    uint32_t n_layers, int update_params, double learning_rate, uint32_t time_step,
                    double* out_grad_input);

@@ -90,6 +90,8 @@ def _load():
         "orc_rope_backward": (i32, [P, u32, u32, u32, f64, P]),
         "orc_embedding_update": (i32, [P, u32, u32, P, u32, u32, P, P, u32, f64]),
         "orc_param_update": (i32, [P, P, P, P, u64, i32, f64, f64, u32, i32]),
+        "orc_set_target_rows": (None, [P, u32]),
+        "orc_dwt_backward": (i32, [P, u32, u32, u32, u32, u32, u32, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -335,6 +337,17 @@ def param_update(w, g, state, first, lr, batch, time_step, weight=True):
     return w
 
 
+def dwt_backward(G, S_in, target_rows, wavelet):
+    """DiscreteWaveletLayer::backward, partial mode (wavelet_discrete_layer.rs:
+    163-207): the gradient [B][S_in][d] of the layer's input from that of its
+    S2 output rows, the last target_rows of which passed through."""
+    G = _c128(G)
+    B, S2, d = G.shape
+    out = np.empty((B, S_in, d), np.complex128)
+    _check(lib().orc_dwt_backward(_ptr(G), B, S2, S_in, int(target_rows), int(wavelet), d, _ptr(out)))
+    return out
+
+
 def zgemm(A: np.ndarray, B: np.ndarray) -> np.ndarray:
     A, B = _c128(A), _c128(B)
     m, k = A.shape
@@ -473,34 +486,51 @@ class Network:
     def reset(self):
         _check(lib().orc_reset(self._h))
 
-    def predict(self, ids, lens=None, time_steps=None, forward_only=True, last_row_only=False):
+    def _rows_after(self, S, first, last, T):
+        for li in range(first, last):
+            w = self._wavelets.get(li)
+            if w is not None:
+                S = dwt_rows(S - T, w) + T if T else dwt_rows(S, w)
+        return S
+
+    def predict(self, ids, lens=None, time_steps=None, forward_only=True, last_row_only=False, target_rows=0):
+        """target_rows (stateless passes): the last T rows of every sequence
+        are targets, which a DiscreteWavelet layer passes on uncompressed
+        (wavelet_discrete_layer.rs:102-134)."""
         ids = np.ascontiguousarray(ids, dtype=np.uint32)
         B, S = ids.shape
         lens = np.full(B, S, np.uint32) if lens is None else np.ascontiguousarray(lens, dtype=np.uint32)
         ts = None if time_steps is None else np.ascontiguousarray(time_steps, dtype=np.uint32)
         V = self.vocab
         prompt_pass = not forward_only or ts is None or ts[0] == 0
-        So = self.seq_out_len(S) if prompt_pass else S
+        T = 0 if forward_only else int(target_rows)
+        So = self._rows_after(S, 0, self.num_layers, T) if prompt_pass else S
         out = np.empty((B, V) if last_row_only else (B, So, V), np.float64)
         mask = np.empty((B, So), np.uint32)
-        _check(lib().orc_predict(self._h, _ptr(ids), _ptr(lens), B, S, _ptr(ts), int(forward_only),
-                                 int(last_row_only), _ptr(out), _ptr(mask)))
+        lib().orc_set_target_rows(self._h, T)
+        try:
+            _check(lib().orc_predict(self._h, _ptr(ids), _ptr(lens), B, S, _ptr(ts), int(forward_only),
+                                     int(last_row_only), _ptr(out), _ptr(mask)))
+        finally:
+            lib().orc_set_target_rows(self._h, 0)
         return out, mask
 
-    def forward_layers(self, first, last, x, mask=None, time_steps=None, forward_only=True, d_out=None):
+    def forward_layers(self, first, last, x, mask=None, time_steps=None, forward_only=True, d_out=None,
+                       target_rows=0):
         x = _c128(x)
         B, S, _ = x.shape
         m = None if mask is None else np.ascontiguousarray(mask, dtype=np.uint32)
         ts = None if time_steps is None else np.ascontiguousarray(time_steps, dtype=np.uint32)
         prompt_pass = not forward_only or ts is None or ts[0] == 0
-        So = S
-        if prompt_pass:
-            for li in range(first, last):
-                if self._wavelets.get(li) is not None:  # a wavelet layer in the range
-                    So = dwt_rows(So, self._wavelets[li])
+        T = 0 if forward_only else int(target_rows)
+        So = self._rows_after(S, first, last, T) if prompt_pass else S
         out = np.empty((B, So, d_out if d_out else x.shape[2]), np.complex128)
-        _check(lib().orc_forward_layers(self._h, first, last, _ptr(x), _ptr(m), B, S, _ptr(ts), int(forward_only),
-                                        _ptr(out)))
+        lib().orc_set_target_rows(self._h, T)
+        try:
+            _check(lib().orc_forward_layers(self._h, first, last, _ptr(x), _ptr(m), B, S, _ptr(ts), int(forward_only),
+                                            _ptr(out)))
+        finally:
+            lib().orc_set_target_rows(self._h, 0)
         return out
 
     def generate(self, prompt, lens=None, n_new=1, want_logits=False):

@@ -315,6 +315,7 @@ typedef struct {
 struct orc_net {
   orc_layer* layers;
   int n, cap;
+  uint32_t train_T; /* target rows at the end of each sequence in a stateless pass (wavelet input/target split) */
 };
 
 orc_net* orc_net_create(void) { return (orc_net*)calloc(1, sizeof(orc_net)); }
@@ -1027,8 +1028,16 @@ static int check_lens(const uint32_t* lens, uint32_t B, uint32_t S) {
 
 /* A wavelet layer at a prompt or stateless pass (wavelet_discrete_layer.rs:
  * 102-128): *cur [B][*S][d] becomes [B][S'][d], mask and lens follow. */
+static int run_wavelet_split(const orc_layer* L, oc64** cur, oc64** nxt, uint64_t* cap, uint32_t** mask,
+                             uint32_t* lens, uint32_t B, uint32_t* S, uint32_t d, uint32_t T);
+
+/* DiscreteWaveletLayer::forward, partial mode (wavelet_discrete_layer.rs:72-161).
+ * T > 0 (a stateless pass with T target rows): separate_input_target
+ * (:233-279) keeps the first S - T rows as the input, whose compression is
+ * followed by the T target rows unchanged, mask ones. */
 static int run_wavelet(const orc_layer* L, oc64** cur, oc64** nxt, uint64_t* cap, uint32_t** mask, uint32_t* lens,
-                       uint32_t B, uint32_t* S, uint32_t d) {
+                       uint32_t B, uint32_t* S, uint32_t d, uint32_t T) {
+  if (T) return run_wavelet_split(L, cur, nxt, cap, mask, lens, B, S, d, T);
   const uint32_t M = dwt_len(*S, L->vocab == 0 ? 2 : 4) >> 1;
   const uint64_t need = (uint64_t)B * (M > *S ? M : *S) * d;
   if (need > *cap) {
@@ -1054,6 +1063,68 @@ static int run_wavelet(const orc_layer* L, oc64** cur, oc64** nxt, uint64_t* cap
   *cur = *nxt;
   *nxt = t;
   return ORC_OK;
+}
+
+static int run_wavelet_split(const orc_layer* L, oc64** cur, oc64** nxt, uint64_t* cap, uint32_t** mask,
+                             uint32_t* lens, uint32_t B, uint32_t* S, uint32_t d, uint32_t T) {
+  const uint32_t Sin = *S;
+  if (T >= Sin) return fail(ORC_ERR_ARG, "%u target rows need more than %u rows", T, Sin);
+  for (uint32_t b = 0; b < B; ++b)
+    if (lens[b] != Sin)
+      return fail(ORC_ERR_ARG, "target rows need unpadded sequences: separate_input_target "
+                               "(wavelet_discrete_layer.rs:233-279) panics on padded ones");
+  const uint32_t R = Sin - T, M = dwt_len(R, L->vocab == 0 ? 2 : 4) >> 1, S2 = M + T;
+  oc64* xin = (oc64*)malloc((size_t)B * R * d * sizeof(oc64));
+  oc64* comp = (oc64*)malloc((size_t)B * (M > R ? M : R) * d * sizeof(oc64));
+  uint32_t* min = (uint32_t*)malloc((size_t)B * R * sizeof(uint32_t));
+  uint32_t* m2 = (uint32_t*)malloc((size_t)B * S2 * sizeof(uint32_t));
+  uint32_t* mc = (uint32_t*)malloc((size_t)B * M * sizeof(uint32_t));
+  const uint64_t need = (uint64_t)B * (S2 > Sin ? S2 : Sin) * d;
+  int rc = ORC_OK;
+  if (!xin || !comp || !min || !m2 || !mc) {
+    rc = fail(ORC_ERR_NOMEM, "wavelet: out of memory");
+    goto done;
+  }
+  for (uint32_t b = 0; b < B; ++b) {
+    memcpy(xin + (size_t)b * R * d, *cur + (size_t)b * Sin * d, (size_t)R * d * sizeof(oc64));
+    for (uint32_t s = 0; s < R; ++s) min[(size_t)b * R + s] = 1u;
+  }
+  uint32_t Mo = 0;
+  if ((rc = dwt_compress(L->vocab, (uint32_t)L->mode, xin, min, B, R, d, comp, mc, lens, &Mo))) goto done;
+  if (need > *cap) {
+    free(*nxt);
+    *nxt = (oc64*)malloc(need * sizeof(oc64));
+    oc64* c2 = (oc64*)realloc(*cur, need * sizeof(oc64));
+    if (c2) *cur = c2;
+    if (!*nxt || !c2) {
+      rc = fail(ORC_ERR_NOMEM, "wavelet: out of memory");
+      goto done;
+    }
+    *cap = need;
+  }
+  for (uint32_t b = 0; b < B; ++b) {
+    memcpy(*nxt + (size_t)b * S2 * d, comp + (size_t)b * M * d, (size_t)M * d * sizeof(oc64));
+    memcpy(*nxt + ((size_t)b * S2 + M) * d, *cur + ((size_t)b * Sin + R) * d, (size_t)T * d * sizeof(oc64));
+    memcpy(m2 + (size_t)b * S2, mc + (size_t)b * M, M * sizeof(uint32_t));
+    for (uint32_t t = 0; t < T; ++t) m2[(size_t)b * S2 + M + t] = 1u; /* :130-134 */
+    lens[b] += T;
+  }
+  free(*mask);
+  *mask = m2;
+  m2 = NULL;
+  *S = S2;
+  {
+    oc64* t = *cur;
+    *cur = *nxt;
+    *nxt = t;
+  }
+done:
+  free(xin), free(comp), free(min), free(m2), free(mc);
+  return rc;
+}
+
+void orc_set_target_rows(orc_net* net, uint32_t T) {
+  if (net) net->train_T = T;
 }
 
 int orc_predict(orc_net* net, const uint32_t* ids, const uint32_t* lens_in, uint32_t B, uint32_t S_in,
@@ -1087,7 +1158,7 @@ int orc_predict(orc_net* net, const uint32_t* ids, const uint32_t* lens_in, uint
   for (int li = 1; rc == ORC_OK && li < net->n - 1; ++li) {
     orc_layer* L = &net->layers[li];
     if (L->kind == ORC_DISCRETE_WAVELET) {
-      if (prompt_pass) rc = run_wavelet(L, &cur, &nxt, &cap, &mask, lens, B, &S, d);
+      if (prompt_pass) rc = run_wavelet(L, &cur, &nxt, &cap, &mask, lens, B, &S, d, forward_only ? 0 : net->train_T);
       continue; /* a cached step's row passes through (:112-128) */
     }
     if (out_rows == 1 && forward_only && L->kind == ORC_LINEAR && li == net->n - 2) {
@@ -1188,7 +1259,7 @@ int orc_forward_layers(orc_net* net, uint32_t first, uint32_t last, const oc64* 
   for (uint32_t li = first; rc == ORC_OK && li < last; ++li) {
     orc_layer* L = &net->layers[li];
     if (L->kind == ORC_DISCRETE_WAVELET) {
-      if (prompt_pass) rc = run_wavelet(L, &cur, &nxt, &cap, &mask, lens, B, &S, d);
+      if (prompt_pass) rc = run_wavelet(L, &cur, &nxt, &cap, &mask, lens, B, &S, d, forward_only ? 0 : net->train_T);
       continue;
     }
     rc = run_layer(L, &cur, &nxt, &cap, mask, lens, B, S, time_steps, forward_only);
@@ -1794,4 +1865,70 @@ int orc_param_update(oc64* w, const oc64* g, oc64* m, oc64* v, uint64_t n, int f
     }
   }
   return ORC_OK;
+}
+
+/* inverse_dwt_1d (wavelet_transform/dwt.rs:90-124) with a DB filter of length
+ * L: the inverse low pass is the low pass reversed, the inverse high pass the
+ * high pass (lo reversed, odd entries negated) reversed
+ * (dwt_type_resolver.rs:107-171) */
+static uint32_t inverse_dwt_1d_c(const oc64* data, uint32_t n, const double* lo, uint32_t L, oc64* out) {
+  double ilo[4], hp[4], ihi[4];
+  for (uint32_t k = 0; k < L; ++k) ilo[k] = lo[L - 1 - k];
+  for (uint32_t i = 0; i < L; ++i) hp[i] = (i & 1) ? -lo[L - 1 - i] : lo[L - 1 - i];
+  for (uint32_t k = 0; k < L; ++k) ihi[k] = hp[L - 1 - k];
+  const uint32_t middle = n >> 1, l = n - (L - 2);
+  for (uint32_t i = 0; i < (l >> 1); ++i) {
+    oc64 vl = {0.0, 0.0}, vh = {0.0, 0.0};
+    for (uint32_t p = 0; p < L; p += 2) {
+      const uint32_t il = (p + 1) % L, it = (p / 2 + i) % n, ih = (it + middle) % n;
+      vl = c_add(c_add(vl, c_scale(data[it], ilo[il])), c_scale(data[ih], ihi[il]));
+      vh = c_add(c_add(vh, c_scale(data[it], ilo[p])), c_scale(data[ih], ihi[p]));
+    }
+    out[2 * i] = vl;
+    out[2 * i + 1] = vh;
+  }
+  return l;
+}
+
+/* DiscreteWaveletLayer::backward, partial mode (wavelet_discrete_layer.rs:
+ * 163-207): per sequence, the gradient of the S2 - T compressed rows through
+ * decompress_partial (:288-298: grad_dwt_1d_trend, dwt.rs:272-282, on every
+ * feature), align_gradient_rows_complex (:318-346) when that gives another
+ * row count than the S_in - T input rows, then the T target rows' gradient. */
+int orc_dwt_backward(const oc64* G, uint32_t B, uint32_t S2, uint32_t S_in, uint32_t T, uint32_t wavelet, uint32_t d,
+                     oc64* out) {
+  if (!G || !out || !B || !d || T >= S2 || T >= S_in) return fail(ORC_ERR_ARG, "bad arguments");
+  double lo[4];
+  uint32_t L = 0;
+  int rc = dwt_low_pass(wavelet, lo, &L);
+  if (rc) return rc;
+  const uint32_t M = S2 - T, R = S_in - T;
+  oc64* data = (oc64*)calloc(2 * (size_t)M, sizeof(oc64));
+  oc64* dec = (oc64*)malloc(2 * (size_t)M * sizeof(oc64));
+  if (!data || !dec) {
+    free(data), free(dec);
+    return fail(ORC_ERR_NOMEM, "wavelet backward: out of memory");
+  }
+  for (uint32_t b = 0; b < B && !rc; ++b)
+    for (uint32_t c = 0; c < d; ++c) {
+      for (uint32_t j = 0; j < M; ++j) data[j] = G[((size_t)b * S2 + j) * d + c];
+      for (uint32_t j = M; j < 2 * M; ++j) data[j] = (oc64){0.0, 0.0};
+      const uint32_t lout = inverse_dwt_1d_c(data, 2 * M, lo, L, dec);
+      if (lout < R) {
+        rc = fail(ORC_ERR_STATE, "wavelet backward: %u rows for %u inputs", lout, R);
+        break;
+      }
+      oc64* o = out + (size_t)b * S_in * d + c;
+      if (lout == R) {
+        for (uint32_t r = 0; r < R; ++r) o[(size_t)r * d] = dec[r];
+      } else {
+        for (uint32_t r = 0; r + 1 < R; ++r) o[(size_t)r * d] = dec[r];
+        oc64 last = {0.0, 0.0};
+        for (uint32_t i = R - 1; i < lout; ++i) last = c_add(last, dec[i]);
+        o[(size_t)(R - 1) * d] = last;
+      }
+      for (uint32_t t = 0; t < T; ++t) o[(size_t)(R + t) * d] = G[((size_t)b * S2 + M + t) * d + c];
+    }
+  free(data), free(dec);
+  return rc;
 }

@@ -169,6 +169,11 @@ int orc_embedding_update(oc64* table, uint32_t V, uint32_t d, const oc64* G, uin
                          const uint32_t* targets, const uint32_t* tlens, uint32_t T, double lr);
 int orc_param_update(oc64* w, const oc64* g, oc64* m, oc64* v, uint64_t n, int first, double lr, double batch,
                      uint32_t time_step, int weight);
+/* target rows T at the end of every sequence of later stateless passes (the
+ * DiscreteWavelet layer compresses only the S - T input rows) */
+void orc_set_target_rows(orc_net* net, uint32_t T);
+int orc_dwt_backward(const oc64* G, uint32_t B, uint32_t S2, uint32_t S_in, uint32_t T, uint32_t wavelet, uint32_t d,
+                     oc64* out);
 
 #ifdef __cplusplus
 }

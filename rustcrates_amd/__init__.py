@@ -53,6 +53,7 @@ SIGNATURES = {
     "mitok_get_tensor": (_i32, [_P, _u32, _u32, _P, _u64]),
     "mitok_reset": (_i32, [_P]),
     "mitok_predict": (_i32, [_P, _P, _P, _u32, _u32, _P, _i32, _i32, _P, _P]),
+    "mitok_predict_targets": (_i32, [_P, _P, _P, _u32, _u32, _u32, _P, _P]),
     "mitok_forward_layers": (_i32, [_P, _u32, _u32, _P, _P, _u32, _u32, _P, _i32, _P]),
     "mitok_generate": (_i32, [_P, _P, _P, _u32, _u32, _u32, _P, _P]),
     "mitok_prefill": (_i32, [_P, _P, _P, _u32, _u32, _P, _P]),
@@ -213,6 +214,8 @@ class Network:
         self.vocab = None
         self.dim = None
         self._in_dims = []  # each layer's input width, for the gradient backward returns
+        self._wavelet_filters = []  # filter length of each DiscreteWavelet layer, in order
+        self._kinds = []  # each layer's kind
         _live.add(self)
 
     def close(self):
@@ -241,14 +244,17 @@ class Network:
     def add_embedding(self, vocab, dim, table=None):
         self.dim = dim
         self._in_dims.append(dim)
+        self._kinds.append("embedding")
         _check(self._lib.mitok_add_embedding(self._h, vocab, dim, _ptr(_c128(table, vocab * dim, "table"))))
 
     def add_positional_encoding(self, dim, base=1250.0):
         self._in_dims.append(dim)
+        self._kinds.append("posenc")
         _check(self._lib.mitok_add_positional_encoding(self._h, dim, base))
 
     def add_norm(self, dim, eps, gamma=None, beta=None):
         self._in_dims.append(dim)
+        self._kinds.append("norm")
         _check(self._lib.mitok_add_norm(self._h, dim, eps, _ptr(_c128(gamma, dim, "gamma")),
                                         _ptr(_c128(beta, dim, "beta"))))
 
@@ -256,6 +262,7 @@ class Network:
                            gamma=None, beta=None):
         nw = dim * dim  # [heads][dim][dim / heads]
         self._in_dims.append(dim)
+        self._kinds.append("attention")
         _check(self._lib.mitok_add_self_attention(self._h, heads, dim, max_ctx, eps, _ptr(_c128(wq, nw, "wq")),
                                                   _ptr(_c128(wk, nw, "wk")), _ptr(_c128(wv, nw, "wv")),
                                                   _ptr(_c128(bias_pos, heads * max_ctx * max_ctx, "bias_pos")),
@@ -263,6 +270,7 @@ class Network:
 
     def add_feed_forward(self, dim, hidden, w1=None, b1=None, w2=None, b2=None):
         self._in_dims.append(dim)
+        self._kinds.append("ffn")
         _check(self._lib.mitok_add_feed_forward(self._h, dim, hidden, _ptr(_c128(w1, dim * hidden, "w1")),
                                                 _ptr(_c128(b1, hidden, "b1")), _ptr(_c128(w2, hidden * dim, "w2")),
                                                 _ptr(_c128(b2, dim, "b2"))))
@@ -271,17 +279,21 @@ class Network:
         self.vocab = d_out
         self._head_in = d_in
         self._in_dims.append(d_in)
+        self._kinds.append("linear")
         _check(self._lib.mitok_add_linear(self._h, d_in, d_out, _ptr(_c128(w, d_in * d_out, "w")),
                                           _ptr(_c128(b, d_out, "b"))))
 
     def add_softmax(self, mode=PRODUCTION):
         self._in_dims.append(getattr(self, "vocab", 0))
+        self._kinds.append("softmax")
         _check(self._lib.mitok_add_softmax(self._h, mode))
 
     def add_discrete_wavelet(self, dim, wavelet=1, mode=2, is_full_mode=False):
         """DiscreteWaveletLayer over rows of `dim` features; defaults DB2 /
         SYMMETRIC (wavelet_discrete_layer.rs:46-70)."""
         self._in_dims.append(dim)
+        self._kinds.append("wavelet")
+        self._wavelet_filters.append(2 if wavelet == 0 else 4)
         _check(self._lib.mitok_add_discrete_wavelet(self._h, dim, wavelet, mode, int(is_full_mode)))
 
     def seq_out_len(self, S, first=0, last=None):
@@ -306,21 +318,39 @@ class Network:
         _check(self._lib.mitok_reset(self._h))
 
     # ---- forward paths ----
-    def predict(self, ids, lens=None, time_steps=None, forward_only=True, last_row_only=False):
+    def predict(self, ids, lens=None, time_steps=None, forward_only=True, last_row_only=False, target_rows=0):
+        """predict (transformer_network.rs:315-492).  target_rows (a stateless
+        pass, forward_only=False): the last T rows of every sequence are the
+        targets, which a DiscreteWavelet layer passes on uncompressed
+        (wavelet_discrete_layer.rs:102-134; mitok_predict_targets)."""
         ids = np.ascontiguousarray(ids, dtype=np.uint32)
         B, S = ids.shape
         lens = np.full(B, S, np.uint32) if lens is None else _u32_vec(lens, B, "lens")
         ts = None if time_steps is None else _u32_vec(time_steps, B, "time_steps")
         V = self.vocab
         prompt_pass = not forward_only or ts is None or ts[0] == 0
-        So = self.seq_out_len(S) if prompt_pass else S
+        T = int(target_rows)
+        if T and (forward_only or last_row_only or time_steps is not None):
+            raise ValueError("target_rows applies to a stateless pass of all rows only")
+        if T:
+            So = S
+            for w in self._wavelet_filters:
+                So = (So - T + w - 2 + ((So - T) % 2)) // 2 + T
+        else:
+            So = self.seq_out_len(S) if prompt_pass else S
         out = np.empty((B, V) if last_row_only else (B, So, V), np.float64)
         mask = np.empty((B, So), np.uint32)
         self._head_rows = None
-        _check(self._lib.mitok_predict(self._h, _ptr(ids), _ptr(lens), B, S, _ptr(ts), int(forward_only),
-                                       int(last_row_only), _ptr(out), _ptr(mask)))
+        if T:
+            _check(self._lib.mitok_predict_targets(self._h, _ptr(ids), _ptr(lens), B, S, T, _ptr(out), _ptr(mask)))
+        else:
+            _check(self._lib.mitok_predict(self._h, _ptr(ids), _ptr(lens), B, S, _ptr(ts), int(forward_only),
+                                           int(last_row_only), _ptr(out), _ptr(mask)))
         if not forward_only:
-            self._head_rows = (B, So)  # what backward_head differentiates
+            # what backward differentiates: rows at the head and, below the
+            # first wavelet layer, the uncompressed S rows
+            first_w = self._kinds.index("wavelet") if "wavelet" in self._kinds else -1
+            self._head_rows = (B, So, S if first_w >= 0 else None, first_w)
         return out, mask
 
     def forward_layers(self, first, last, x, mask=None, time_steps=None, forward_only=True, d_out=None):
@@ -418,7 +448,8 @@ class Network:
                 raise MitokError(3, "no stateless predict of this batch to differentiate")
             lowest = len(self._in_dims) - 1 - int(layers)
             width = self._in_dims[lowest] if 0 <= lowest < len(self._in_dims) else self._head_in
-            gx = np.empty((B, rows[1], width), np.complex128)
+            n_rows = rows[2] if rows[2] is not None and lowest <= rows[3] else rows[1]
+            gx = np.empty((B, n_rows, width), np.complex128)
         _check(self._lib.mitok_backward(self._h, _ptr(t), _ptr(tl), B, T, int(layers), int(bool(update)),
                                         float(learning_rate), int(time_step), _ptr(gx)))
         return gx

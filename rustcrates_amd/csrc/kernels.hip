@@ -72,8 +72,9 @@ void rope(hipStream_t st, double2* x, int rows, int d, const double2* cs_table, 
 // compress_partial :260-266): feature c of output row j of sequence b is the
 // low half of dwt_1d (wavelet_transform/dwt.rs:36-90) along the sequence,
 //   v = 0 + t_0 lo[0] + ... + t_(L-1) lo[L-1],   t_l = sgn_l x[b][src_l][c],
-// summed in that order (src -1: a padding zero).  The tap table [S2][L]
-// restates the reference's sequence padding on the host.
+// summed in that order (src -1: a padding zero; src[j][0] = -2 - r: row j is
+// input row r unchanged, a target row of a stateless pass).  The tap table
+// [S2][L] restates the reference's sequence padding on the host.
 __global__ void k_dwt_rows(const double2* __restrict__ x, int B, int S, int d, const int* __restrict__ src,
                            const double* __restrict__ sgn, const double* __restrict__ lo, int L, int S2,
                            double2* __restrict__ out) {
@@ -83,6 +84,11 @@ __global__ void k_dwt_rows(const double2* __restrict__ x, int B, int S, int d, c
   const long bj = i / d;
   const int j = (int)(bj % S2), b = (int)(bj / S2);
   double2 v = make_double2(0.0, 0.0);
+  const int s0 = src[j * L];
+  if (s0 <= -2) {  // a target row of a stateless pass, passed through
+    out[i] = x[((long)b * S + (-2 - s0)) * d + c];
+    return;
+  }
   for (int l = 0; l < L; ++l) {
     const int s = src[j * L + l];
     const double g = sgn[j * L + l];

@@ -165,6 +165,9 @@ void param_update(hipStream_t st, double2* w, const double2* g, double2* m, doub
                   const TrainStep& ts);
 // RoPE's backward on rows [rows][d] of sequences of S rows (cs: the forward's table)
 void rope_backward(hipStream_t st, const double2* G, long rows, int S, int d, const double2* cs, double2* out);
+// the wavelet layer's backward: out [B][Sin][d] from G [B][S2][d] through a tap table [Sin][4]
+void dwt_backward(hipStream_t st, const double2* G, int B, int S2, int Sin, int d, const int* src, const double* w,
+                  double2* out);
 // the embedding rows of n_ids distinct ids, each with occurrences occ[start[u] .. start[u+1]) (rows of G)
 void embedding_update(hipStream_t st, double2* table, int d, const uint32_t* ids, int n_ids, const int* start,
                       const int* occ, const double2* G, double lr, double bs, uint32_t* err);

@@ -350,7 +350,11 @@ struct mitok_network {
   // mask and lens on the host; rows per sequence after the stages
   struct WaveletStage {
     int S_in = 0, S2 = 0, L = 0;
-    mitok::DevBuf src, sgn, lo, mask, lens, pos;
+    int T = 0;                   // target rows passed through after the compressed input rows
+    const uint32_t* mask_in = nullptr;  // the padding mask of the stage's input rows
+    double lo[4] = {0, 0, 0, 0};
+    mitok::DevBuf src, sgn, lo_d, mask, lens, pos;
+    mitok::DevBuf gsrc, gw;  // backward's tap table [S_in][4]
   };
   std::vector<std::unique_ptr<WaveletStage>> wstages;
   std::vector<uint32_t> wmask_h, wlens_h;
@@ -363,6 +367,7 @@ struct mitok_network {
   // (in act0/act1) and its softmax output (probs), which mitok_backward_head
   // differentiates; any later call clears head_valid
   bool head_valid = false;
+  uint32_t train_T = 0;  // target rows of the stateless pass being planned (mitok_predict_targets)
   const double2* head_x = nullptr;
   const uint32_t* head_mask = nullptr;  // the padding mask of those rows
   uint32_t head_B = 0, head_S = 0, head_first = 0;
@@ -861,7 +866,7 @@ static int enqueue_forward(Net* n, const Spec& sp) {
         if (!sp.compress) break;
         if (wi >= n->wstages.size()) return fail(ERR_STATE, "wavelet stage %zu not planned", wi);
         const auto& W = *n->wstages[wi++];
-        dwt_rows(st, cur, B, S, (int)L->d_in, W.src.as<int>(), W.sgn.as<double>(), W.lo.as<double>(), W.L, W.S2, nxt);
+        dwt_rows(st, cur, B, S, (int)L->d_in, W.src.as<int>(), W.sgn.as<double>(), W.lo_d.as<double>(), W.L, W.S2, nxt);
         std::swap(cur, nxt);
         S = W.S2;
         rows = B * S;
@@ -1937,9 +1942,20 @@ static int begin_call(Net* n, const uint32_t* lens, uint32_t B, uint32_t S, cons
   if (!forward_only || !ts || ts[0] == 0)
     for (uint32_t li = sp.first; li < sp.last; ++li)
       if (n->layers[li]->kind == K_WAVELET) wl.push_back((const WaveletLayer*)n->layers[li].get());
+  // a stateless pass with target rows compresses only each sequence's first
+  // S - T rows and passes the T targets on (wavelet_discrete_layer.rs:102-134)
+  const int T = (!forward_only && !wl.empty()) ? (int)n->train_T : 0;
+  if (T) {
+    if ((uint32_t)T >= S) return fail(ERR_ARG, "%d target rows need more than %u rows", T, S);
+    for (uint32_t b = 0; b < B; ++b)
+      if (lens[b] != S || mask_src)
+        return fail(ERR_ARG, "target rows need unpadded sequences: separate_input_target "
+                             "(wavelet_discrete_layer.rs:233-279) panics on padded ones");
+  }
   int S_alloc = (int)S, Sc = (int)S;
   for (const WaveletLayer* W : wl) {
-    Sc = wavelet_rows(Sc, W->L);
+    Sc = T ? wavelet_rows(Sc - T, W->L) + T : wavelet_rows(Sc, W->L);
+    if (T && Sc - T < 1) return fail(ERR_ARG, "%d target rows leave no input rows to compress", T);
     S_alloc = std::max(S_alloc, Sc);
   }
   if (mc != UINT32_MAX && (uint32_t)Sc > mc) return fail(ERR_ARG, "sequence %d exceeds max context %u", Sc, mc);
@@ -1975,21 +1991,30 @@ static int begin_call(Net* n, const uint32_t* lens, uint32_t B, uint32_t S, cons
   std::vector<std::vector<uint32_t>> keep_u;
   std::vector<uint32_t> m = mask_h, ln(lens, lens + B);
   int Sin = (int)S;
+  const uint32_t* mask_prev = n->mask_d.as<uint32_t>();
   for (const WaveletLayer* W : wl) {
-    const WaveletTaps t = wavelet_taps(Sin, W->L, W->mode);
-    const int S2 = t.S2, L = W->L;
+    WaveletTaps t = wavelet_taps(Sin - T, W->L, W->mode);
+    const int M = t.S2, S2 = M + T, L = W->L;
+    for (int j = 0; j < T; ++j) {  // target rows: a copy of input row Sin - T + j (src -2 - row)
+      t.src.push_back(-2 - (Sin - T + j));
+      t.sgn.push_back(1.0);
+      for (int l = 1; l < L; ++l) {
+        t.src.push_back(-1);
+        t.sgn.push_back(0.0);
+      }
+    }
     std::vector<uint32_t> m2((size_t)B * S2), ln2(B);
     std::vector<int> p2((size_t)B * S2);
     for (uint32_t b = 0; b < B; ++b) {
       uint32_t ones = 0;
       for (int j = 0; j < S2; ++j) {
         double v = 0.0;
-        for (int l = 0; l < L; ++l) {
+        for (int l = 0; l < L && j < M; ++l) {
           const int sidx = t.src[(size_t)j * L + l];
           const double x = sidx < 0 ? 0.0 : t.sgn[(size_t)j * L + l] * (double)m[(size_t)b * Sin + sidx];
           v = v + x * W->lo[l];
         }
-        m2[(size_t)b * S2 + j] = v > 0.99 ? 1u : 0u;
+        m2[(size_t)b * S2 + j] = (j >= M || v > 0.99) ? 1u : 0u;  // target rows: mask 1 (:130-134)
         ones += m2[(size_t)b * S2 + j];
         p2[(size_t)b * S2 + j] = j;
       }
@@ -1999,18 +2024,22 @@ static int begin_call(Net* n, const uint32_t* lens, uint32_t B, uint32_t S, cons
     st->S_in = Sin;
     st->S2 = S2;
     st->L = L;
+    st->T = T;
+    st->mask_in = mask_prev;
+    for (int l = 0; l < L; ++l) st->lo[l] = W->lo[l];
     keep_i.push_back(t.src);
     keep_d.push_back(t.sgn);
     keep_d.push_back(std::vector<double>(W->lo, W->lo + L));
     TRY(upload(n, st->src, keep_i.back().data(), keep_i.back().size() * sizeof(int)));
     TRY(upload(n, st->sgn, keep_d[keep_d.size() - 2].data(), t.sgn.size() * sizeof(double)));
-    TRY(upload(n, st->lo, keep_d.back().data(), (size_t)L * sizeof(double)));
+    TRY(upload(n, st->lo_d, keep_d.back().data(), (size_t)L * sizeof(double)));
     keep_u.push_back(m2);
     TRY(upload(n, st->mask, keep_u.back().data(), m2.size() * sizeof(uint32_t)));
     keep_u.push_back(ln2);
     TRY(upload(n, st->lens, keep_u.back().data(), (size_t)B * sizeof(uint32_t)));
     keep_i.push_back(p2);
     TRY(upload(n, st->pos, keep_i.back().data(), p2.size() * sizeof(int)));
+    mask_prev = st->mask.as<uint32_t>();
     n->wstages.push_back(std::move(st));
     m = std::move(m2);
     ln = std::move(ln2);
@@ -2103,6 +2132,15 @@ int mitok_predict(mitok_network* n, const uint32_t* ids, const uint32_t* lens, u
   end_call(n, sp, lens);
   if (out_mask) memcpy(out_mask, n->wstages.empty() ? mask_h.data() : n->wmask_h.data(), orows * sizeof(uint32_t));
   return OK;
+}
+
+int mitok_predict_targets(mitok_network* n, const uint32_t* ids, const uint32_t* lens, uint32_t B, uint32_t S,
+                          uint32_t target_rows, double* out_probs, uint32_t* out_mask) {
+  if (!n) return fail(ERR_ARG, "null network");
+  n->train_T = target_rows;
+  const int rc = mitok_predict(n, ids, lens, B, S, nullptr, 0, 0, out_probs, out_mask);
+  n->train_T = 0;
+  return rc;
 }
 
 // `bytes` of device memory at `p` inside one allocation of the network's
@@ -2549,17 +2587,43 @@ static int backward_impl(Net* n, const uint32_t* targets, const uint32_t* tlens,
   auto* Ln = (LinearLayer*)n->layers[li_top].get();
   const int S = (int)n->head_S, d = (int)Ln->d_in, V = (int)Ln->d_out;
   const long rows = (long)B * S;
+  // rows per sequence of each walked layer's input: a wavelet layer's are its
+  // stage's S_in (the stages of the forward pass, in layer order)
+  std::vector<int> S_in_at(li_top + 1, S);
+  std::vector<Net::WaveletStage*> stage_at(li_top + 1, nullptr);
+  {
+    size_t si = 0;
+    for (uint32_t li = n->head_first; li < li_top; ++li)
+      if (n->layers[li]->kind == K_WAVELET) {
+        if (si >= n->wstages.size()) return fail(ERR_STATE, "layer %u: the forward pass left no wavelet stage", li);
+        stage_at[li] = n->wstages[si++].get();
+      }
+    int Sc = S;
+    for (int li = (int)li_top; li >= (int)stop; --li) {
+      if (stage_at[li]) Sc = stage_at[li]->S_in;
+      S_in_at[li] = Sc;
+    }
+  }
+  long rows_max = rows;
+  for (uint32_t li = stop; li <= li_top; ++li) rows_max = std::max(rows_max, (long)B * S_in_at[li]);
+  // host staging of the uploads, alive until the synchronisation at the end
+  std::vector<std::vector<int>> keep_i;
+  std::vector<std::vector<double>> keep_d;
   // what the walk needs, checked and sized before the first launch
   size_t dmax = (size_t)d, fmax = 0, d3max = 0, att = 0, wmax = (size_t)d * V, bmax = (size_t)V;
   size_t ws = std::max(gemm_ws_bytes(d, V, (int)rows), gemm_ws_bytes((int)rows, d, V));
   for (uint32_t li = stop; li < li_top; ++li) {
     const Layer* L = n->layers[li].get();
     const int di = (int)L->d_in, dn = (int)L->d_out;
+    const long rows = (long)B * S_in_at[li];
     dmax = std::max({dmax, (size_t)di, (size_t)dn});
     switch (L->kind) {
-      case K_WAVELET:
-        return fail(ERR_STATE, "layer %u: backward through the DiscreteWavelet layer is not built (its training pass "
-                               "splits input and target rows, wavelet_discrete_layer.rs:233-279)", li);
+      case K_WAVELET: {
+        const Net::WaveletStage& W = *stage_at[li];
+        if (2 * (W.S2 - W.T) - (W.L - 2) < W.S_in - W.T)
+          return fail(ERR_STATE, "layer %u: fewer decompressed rows than inputs", li);
+        break;
+      }
       case K_LINEAR:
         wmax = std::max(wmax, (size_t)di * dn);
         bmax = std::max(bmax, (size_t)dn);
@@ -2620,10 +2684,10 @@ static int backward_impl(Net* n, const uint32_t* targets, const uint32_t* tlens,
     const uint32_t EV = ((const EmbeddingLayer*)n->layers[0].get())->vocab;
     std::map<uint32_t, std::vector<int>> by_id;
     for (uint32_t b = 0; b < B; ++b)
-      for (uint32_t t = 0; t < tlens[b]; ++t) {
+      for (uint32_t t = 0; t < tlens[b] && (int)t < S_in_at[0]; ++t) {
         const uint32_t id = targets[(size_t)b * T + t];
         if (id >= EV) return fail(ERR_ARG, "No token embedding found: %u (embedding_layer.rs:233)", id);
-        by_id[id].push_back((int)(b * (uint32_t)S + t));
+        by_id[id].push_back((int)(b * (uint32_t)S_in_at[0] + t));
       }
     for (auto& kv : by_id) {
       eids.push_back(kv.first);
@@ -2635,6 +2699,43 @@ static int backward_impl(Net* n, const uint32_t* targets, const uint32_t* tlens,
   TRY(set_device(n));
   hipStream_t st = n->stream;
   const size_t c16 = sizeof(double2);
+  // DiscreteWaveletLayer::backward's tap tables (wavelet_discrete_layer.rs:163-207)
+  for (uint32_t li = stop; li < li_top; ++li) {
+    if (!stage_at[li]) continue;
+    Net::WaveletStage& W = *stage_at[li];
+    const int R = W.S_in - W.T, M = W.S2 - W.T, Lf = W.L, lout = 2 * M - (Lf - 2);
+    std::vector<int> gs((size_t)W.S_in * 4, -1);
+    std::vector<double> gw((size_t)W.S_in * 4, 0.0);
+    // decompressed row k (grad_dwt_1d_trend: inverse_dwt_1d of [g | 0] with the low pass reversed)
+    auto dec = [&](int k, int& slot, int r) {
+      const int i = k / 2;
+      const bool even = (k % 2) == 0;
+      auto put = [&](int src, double w) {
+        gs[(size_t)r * 4 + slot] = src;
+        gw[(size_t)r * 4 + slot] = w;
+        ++slot;
+      };
+      if (Lf == 2) {
+        put(i, even ? W.lo[0] : W.lo[1]);
+      } else {
+        put(i, even ? W.lo[2] : W.lo[3]);
+        put(i + 1, even ? W.lo[0] : W.lo[1]);
+      }
+    };
+    for (int r = 0; r < R; ++r) {
+      int slot = 0;
+      dec(r, slot, r);
+      if (r == R - 1 && lout == R + 1) dec(R, slot, r);  // align_gradient_rows_complex (:318-346)
+    }
+    for (int t = 0; t < W.T; ++t) {
+      gs[(size_t)(R + t) * 4] = M + t;  // the target rows' gradient passes through
+      gw[(size_t)(R + t) * 4] = 1.0;
+    }
+    keep_i.push_back(std::move(gs));
+    keep_d.push_back(std::move(gw));
+    TRY(upload(n, W.gsrc, keep_i.back().data(), keep_i.back().size() * sizeof(int)));
+    TRY(upload(n, W.gw, keep_d.back().data(), keep_d.back().size() * sizeof(double)));
+  }
   // every workspace is sized before the first launch (a reserve that grows frees the old buffer)
   TRY(upload(n, n->tr_tgt, tgt.data(), tgt.size() * sizeof(int)));
   TRY(upload(n, n->tr_norm, norm.data(), norm.size() * sizeof(double)));
@@ -2644,22 +2745,22 @@ static int backward_impl(Net* n, const uint32_t* targets, const uint32_t* tlens,
     TRY(upload(n, n->tr_eocc, eocc.data(), eocc.size() * sizeof(int)));
   }
   TRY(reserve(n, n->tr_g, (size_t)rows * V * c16));
-  TRY(reserve(n, n->tr_ga, (size_t)rows * dmax * c16));
-  TRY(reserve(n, n->tr_gb, (size_t)rows * dmax * c16));
-  TRY(reserve(n, n->tr_xh, (size_t)rows * std::max(dmax, fmax) * c16));
+  TRY(reserve(n, n->tr_ga, (size_t)rows_max * dmax * c16));
+  TRY(reserve(n, n->tr_gb, (size_t)rows_max * dmax * c16));
+  TRY(reserve(n, n->tr_xh, (size_t)rows_max * std::max(dmax, fmax) * c16));
   TRY(reserve(n, n->tr_wh, wmax * c16));
   TRY(reserve(n, n->tr_dw, wmax * c16));
   TRY(reserve(n, n->tr_db, std::max(bmax, dmax) * c16));
-  TRY(reserve(n, n->tr_dh, (size_t)rows * std::max(fmax, dmax) * c16));
-  TRY(reserve(n, n->tr_pg, (size_t)rows * dmax * c16));
+  TRY(reserve(n, n->tr_dh, (size_t)rows_max * std::max(fmax, dmax) * c16));
+  TRY(reserve(n, n->tr_pg, (size_t)rows_max * dmax * c16));
   if (fmax) {
-    TRY(reserve(n, n->tr_z, (size_t)rows * fmax * c16));
-    TRY(reserve(n, n->tr_h, (size_t)rows * fmax * c16));
-    TRY(reserve(n, n->tr_g1, (size_t)rows * fmax * c16));
+    TRY(reserve(n, n->tr_z, (size_t)rows_max * fmax * c16));
+    TRY(reserve(n, n->tr_h, (size_t)rows_max * fmax * c16));
+    TRY(reserve(n, n->tr_g1, (size_t)rows_max * fmax * c16));
   }
   if (att) {
-    TRY(reserve(n, n->tr_qkv, (size_t)rows * d3max * c16));
-    TRY(reserve(n, n->tr_dqkv, (size_t)rows * d3max * c16));
+    TRY(reserve(n, n->tr_qkv, (size_t)rows_max * d3max * c16));
+    TRY(reserve(n, n->tr_dqkv, (size_t)rows_max * d3max * c16));
     TRY(reserve(n, n->tr_A, (size_t)B * att * sizeof(double)));
     TRY(reserve(n, n->tr_dA, (size_t)B * att * sizeof(double)));
   }
@@ -2684,7 +2785,9 @@ static int backward_impl(Net* n, const uint32_t* targets, const uint32_t* tlens,
   }
   const Sync sy = sync_of(n);
   uint32_t* err = n->err_d.as<uint32_t>();
-  const uint32_t* mask = n->head_mask;
+  long rows_c = rows;  // the current layer's rows (a wavelet layer changes them below it)
+  int S_c = S;
+  const uint32_t* mask_c = n->head_mask;
   double2* xh = n->tr_xh.as<double2>();
   double2* wh = n->tr_wh.as<double2>();
   double2* dW = n->tr_dw.as<double2>();
@@ -2692,18 +2795,18 @@ static int backward_impl(Net* n, const uint32_t* targets, const uint32_t* tlens,
   // LinearLayer::backward, complex arm (linear_layer.rs:96-108), grouped over
   // the sequences: dW = conj(X)^T G, db = column sums, dX = G conj(W)^T
   auto linear_bwd = [&](const double2* X, const double2* G, const double2* W, int din, int dout, double2* dX) -> int {
-    conj_transpose(st, X, rows, din, xh);
+    conj_transpose(st, X, rows_c, din, xh);
     Epi e;
     e.mode = EPI_STORE;
     e.err = err;
     e.out = dW;
     e.ldo = dout;
-    TRY(launch_rc(gemm(st, din, dout, (int)rows, rows_of(xh, rows), G, dout, e, nullptr, sy), "weight grad"));
-    bias_grad(st, G, (int)B, S, dout, db);
+    TRY(launch_rc(gemm(st, din, dout, (int)rows_c, rows_of(xh, rows_c), G, dout, e, nullptr, sy), "weight grad"));
+    bias_grad(st, G, (int)B, S_c, dout, db);
     conj_transpose(st, W, din, dout, wh);
     e.out = dX;
     e.ldo = din;
-    TRY(launch_rc(gemm(st, (int)rows, din, dout, rows_of(G, dout), wh, din, e, nullptr, sy), "input grad"));
+    TRY(launch_rc(gemm(st, (int)rows_c, din, dout, rows_of(G, dout), wh, din, e, nullptr, sy), "input grad"));
     return OK;
   };
   // update_parameters of a weight and its bias from dW, db (linear_layer.rs:130-175)
@@ -2727,7 +2830,23 @@ static int backward_impl(Net* n, const uint32_t* targets, const uint32_t* tlens,
   for (int li = (int)li_top - 1; li >= (int)stop; --li) {
     Layer* L = n->layers[li].get();
     const double2* X = n->tr_in[li]->as<double2>();
+    const uint32_t* mask = mask_c;
+    if (!stage_at[li]) {  // every other layer keeps its rows
+      S_c = S_in_at[li];
+      rows_c = (long)B * S_c;
+    }
+    const long rows = rows_c;
+    const int S = S_c;
     switch (L->kind) {
+      case K_WAVELET: {
+        const Net::WaveletStage& W = *stage_at[li];
+        dwt_backward(st, gcur, (int)B, W.S2, W.S_in, (int)L->d_in, W.gsrc.as<int>(), W.gw.as<double>(), gnext);
+        std::swap(gcur, gnext);
+        S_c = W.S_in;  // the layers below see the stage's input rows and mask
+        rows_c = (long)B * S_c;
+        mask_c = W.mask_in;
+        break;
+      }
       case K_LINEAR: {
         auto* H = (LinearLayer*)L;
         TRY(linear_bwd(X, gcur, H->w.as<double2>(), H->d_in, H->d_out, gnext));
@@ -2843,7 +2962,7 @@ static int backward_impl(Net* n, const uint32_t* targets, const uint32_t* tlens,
   if (update_params) drop_graph(n);  // the weights changed under any captured step
   if (out_grad_input) {
     const int dlow = (int)n->layers[stop]->d_in;
-    HIP_TRY(hipMemcpyAsync(out_grad_input, gcur, (size_t)rows * dlow * c16, hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipMemcpyAsync(out_grad_input, gcur, (size_t)rows_c * dlow * c16, hipMemcpyDeviceToHost, st));
   }
   HIP_TRY(hipStreamSynchronize(st));
   return check_err_word(n);

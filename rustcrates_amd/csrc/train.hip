@@ -520,4 +520,33 @@ void embedding_update(hipStream_t st, double2* table, int d, const uint32_t* ids
     MITOK_LAUNCH(k_embedding_update, dim3(n_ids), dim3(256), 0, st, table, d, ids, start, occ, G, lr, bs, err);
 }
 
+// DiscreteWaveletLayer::backward, partial mode (wavelet_discrete_layer.rs:
+// 163-207): input row r of sequence b gets sum_k w[r][k] G[b][src[r][k]]
+// (four taps at most, src -1: none).  The host builds the table from
+// decompress_partial (grad_dwt_1d_trend, dwt.rs:272-282: the low-pass filter
+// transposed over the compressed rows), align_gradient_rows_complex (:318-346)
+// and the target rows, whose gradient passes through (weight 1).
+__global__ __launch_bounds__(256) void k_dwt_backward(const double2* __restrict__ G, int B, int S2, int Sin, int d,
+                                                      const int* __restrict__ src, const double* __restrict__ w,
+                                                      double2* __restrict__ out) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (long)B * Sin * d) return;
+  const int c = (int)(i % d);
+  const long br = i / d;
+  const int r = (int)(br % Sin), b = (int)(br / Sin);
+  double2 v = make_double2(0.0, 0.0);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int s = src[r * 4 + k];
+    if (s >= 0) v = cadd(v, cscale(G[((long)b * S2 + s) * d + c], w[r * 4 + k]));
+  }
+  out[i] = v;
+}
+
+void dwt_backward(hipStream_t st, const double2* G, int B, int S2, int Sin, int d, const int* src, const double* w,
+                  double2* out) {
+  const long n = (long)B * Sin * d;
+  if (n > 0) MITOK_LAUNCH(k_dwt_backward, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, G, B, S2, Sin, d, src, w, out);
+}
+
 }  // namespace mitok

@@ -15,7 +15,7 @@ import pytest
 
 import oracle
 import rustcrates_amd as ra
-from rustcrates_amd import seeded
+from rustcrates_amd import configs, seeded
 
 pytestmark = pytest.mark.gpu
 
@@ -168,9 +168,10 @@ def test_ffn_and_head_training_steps_match_checker(V, d, F, lens, T):
 def test_backward_walk_limits():
     """The walk goes no lower than the forward pass reached; through the
     Embedding it passes the gradient on unchanged (embedding_layer.rs:214-221)
-    and, without update, leaves the table alone; a DiscreteWavelet layer in the
-    walk is refused (its training pass splits input and target rows, which a
-    target-free predict cannot reproduce)."""
+    and, without update, leaves the table alone; below a DiscreteWavelet layer
+    the gradient has the uncompressed rows; target rows with a padded batch
+    are refused where the reference panics (wavelet_discrete_layer.rs:
+    233-279)."""
     rng = np.random.default_rng(4)
     V, d = 30, 4
     table = rng.standard_normal((V, d)) + 0j
@@ -189,10 +190,15 @@ def test_backward_walk_limits():
     w.add_discrete_wavelet(8)
     w.add_linear(8, V, rng.standard_normal((8, V)) + 0j, np.zeros(V, np.complex128))
     w.add_softmax(ra.TRAINING)
-    w.predict(seeded.prompts(7, [9, 9], V), forward_only=False)
-    w.backward(tg, layers=1, update=False)  # the Linear above it still differentiates
-    with pytest.raises(ra.MitokError, match="DiscreteWavelet"):
-        w.backward(tg, layers=2, update=False)
+    ids = seeded.prompts(7, [9, 9], V)
+    w.predict(ids, forward_only=False)
+    assert w.backward(tg, layers=1, update=False).shape == (2, 6, 8)  # DB2 leaves 6 of 9 rows
+    assert w.backward(tg, layers=3, update=False).shape == (2, 9, 8)
+    with pytest.raises(ra.MitokError, match="unpadded"):
+        w.predict(ids, lens=[9, 7], forward_only=False, target_rows=2)
+    P, m = w.predict(ids, forward_only=False, target_rows=2)  # 7 input rows -> 5, plus 2 targets
+    assert P.shape == (2, 7, V) and m.all()
+    assert w.backward(tg, layers=3, update=False).shape == (2, 9, 8)
     w.close()
 
 
@@ -320,6 +326,122 @@ def test_whole_walk_training_steps_match_checker(V, d, H, F, mc, lens, T, hs, ws
         # sits just above the EPSILON floor (|g| ~ 1.4e-4 at step 2) moves by
         # about lr g / |g|, so its error is the gradient's absolute error times
         # lr / 1.4e-4 (~70 here).  The descent step is linear in the gradient.
+        bar = TOL if first else TOL * lr / 1.4e-4
+        assert max(errs.values()) < bar, errs
+        o.close()
+    g.close()
+
+
+@pytest.mark.parametrize("lr", [0.01])
+def test_reference_default_stack_training_matches_checker(lr):
+    """train's step on create_transformer's default stack (transformer_builder.
+    rs:10-72: Embedding, DiscreteWavelet DB2, Norm, RoPE, 2 x [SelfAttention,
+    FeedForward], Linear, Softmax) with seeded weights: the TRAINING predict
+    with the targets as each sequence's last T rows (the wavelet layer passes
+    them on uncompressed), then backward over every layer with every update,
+    two steps, against the checker's pieces composed in the same order."""
+    V, mc, B, S, T = 300, 32, 3, 20, 5
+    g = configs.build_reference_default(ra.Network(0), vocab=V, seed=9, max_ctx=mc, mode=ra.TRAINING)
+    o0 = configs.build_reference_default(oracle.Network(), vocab=V, seed=9, max_ctx=mc, mode=ra.TRAINING)
+    nl = g.num_layers
+    d, kinds = 16, ["emb", "dwt", "norm", "rope", "sa", "ffn", "sa", "ffn", "lin", "sm"]
+    shapes = {}
+    p = {"table": o0.get_tensor(0, 0, V * d).reshape(V, d), "ng": o0.get_tensor(2, 6, d), "nb": o0.get_tensor(2, 7, d),
+         "Wv": o0.get_tensor(8, 0, d * V).reshape(d, V), "bv": o0.get_tensor(8, 4, V)}
+    for li, H, F in ((4, 2, 512), (6, 4, 1024)):
+        dh = d // H
+        shapes[li] = (H, F)
+        for slot, nm in ((0, "wq"), (1, "wk"), (2, "wv")):
+            p[f"{nm}{li}"] = o0.get_tensor(li, slot, H * d * dh).reshape(H, d, dh)
+        p[f"bp{li}"] = o0.get_tensor(li, 3, H * mc * mc).reshape(H, mc, mc)
+        p[f"g{li}"], p[f"be{li}"] = o0.get_tensor(li, 6, d), o0.get_tensor(li, 7, d)
+        p[f"W1{li + 1}"] = o0.get_tensor(li + 1, 0, d * F).reshape(d, F)
+        p[f"W2{li + 1}"] = o0.get_tensor(li + 1, 1, F * d).reshape(F, d)
+        p[f"b1{li + 1}"], p[f"b2{li + 1}"] = o0.get_tensor(li + 1, 4, F), o0.get_tensor(li + 1, 5, d)
+    o0.close()
+    ids = seeded.prompts(44, [S] * B, V)
+    targets = np.ascontiguousarray(ids[:, S - T:])
+    tlens = [T] * B
+    gelu = np.vectorize(lambda z: oracle.gelu(z)[0])
+    state = {}
+
+    def st(key, shape):
+        if key not in state:
+            state[key] = [np.zeros(shape, np.complex128), np.zeros(shape, np.complex128)]
+        return state[key]
+
+    def oracle_net():
+        o = oracle.Network()
+        o.add_embedding(V, d, p["table"])
+        o.add_discrete_wavelet(d, 1, 2)
+        o.add_norm(d, 1e-8, p["ng"], p["nb"])
+        o.add_positional_encoding(d, 1250.0)
+        for li in (4, 6):
+            H, F = shapes[li]
+            o.add_self_attention(H, d, mc, 1e-12, p[f"wq{li}"], p[f"wk{li}"], p[f"wv{li}"], p[f"bp{li}"], p[f"g{li}"],
+                                 p[f"be{li}"])
+            o.add_feed_forward(d, F, p[f"W1{li + 1}"], p[f"b1{li + 1}"], p[f"W2{li + 1}"], p[f"b2{li + 1}"])
+        o.add_linear(d, V, p["Wv"], p["bv"])
+        o.add_softmax(ra.TRAINING)
+        return o
+
+    for step in (1, 2):
+        first = step == 1
+        o = oracle_net()
+        Pg, mg = g.predict(ids, forward_only=False, target_rows=T)
+        Po, mo = o.predict(ids, forward_only=False, target_rows=T)
+        X = [None] * nl
+        X[1] = np.stack([[p["table"][i] if i != 1 else np.zeros(d) for i in row] for row in ids])
+        X[2] = o.forward_layers(1, 2, X[1], mask=np.ones((B, S), np.uint32), forward_only=False, target_rows=T)
+        for li in range(2, nl - 2):
+            X[li + 1] = o.forward_layers(li, li + 1, X[li], mask=mo, forward_only=False)
+        G = oracle.softmax_backward(Po, targets, tlens)
+        dW, db, gr = oracle.linear_backward(X[8], G, p["Wv"])
+        p["Wv"], p["bv"] = oracle.linear_update(p["Wv"], p["bv"], dW, db, B, st("v", (d, V)) + st("vb", V), first, lr, step)
+        for li in (6, 4):
+            H, F = shapes[li]
+            lf = li + 1
+            Xf = X[lf]
+            Z = np.stack([oracle.zgemm(Xf[bb], p[f"W1{lf}"]) for bb in range(B)]) + p[f"b1{lf}"]
+            Hh = gelu(Z) * mo[:, :, None]
+            dW2, db2, dH = oracle.linear_backward_c(Hh, gr, p[f"W2{lf}"])
+            p[f"W2{lf}"], p[f"b2{lf}"] = oracle.linear_update(p[f"W2{lf}"], p[f"b2{lf}"], dW2, db2, B,
+                                                              st(f"W2{lf}", (F, d)) + st(f"b2{lf}", d), first, lr, step)
+            dW1, db1, gr = oracle.dense_backward(Xf, Z, dH, mo, p[f"W1{lf}"])
+            p[f"W1{lf}"], p[f"b1{lf}"] = oracle.linear_update(p[f"W1{lf}"], p[f"b1{lf}"], dW1, db1, B,
+                                                              st(f"W1{lf}", (d, F)) + st(f"b1{lf}", F), first, lr, 0)
+            dX, dwq, dwk, dwv, dbias, dgam, dbet = oracle.self_attention_backward(
+                X[li], mo, p[f"wq{li}"], p[f"wk{li}"], p[f"wv{li}"], p[f"bp{li}"], p[f"g{li}"], p[f"be{li}"], gr)
+            gr = dX
+            p[f"g{li}"] = oracle.param_update(p[f"g{li}"], dgam, st(f"g{li}", d), first, lr, d, step, weight=False)
+            p[f"be{li}"] = oracle.param_update(p[f"be{li}"], dbet, st(f"be{li}", d), first, lr, d, step, weight=False)
+            for nm, dw_ in (("wq", dwq), ("wk", dwk), ("wv", dwv)):
+                p[f"{nm}{li}"] = oracle.param_update(p[f"{nm}{li}"], dw_, st(f"{nm}{li}", (H, d, d // H)), first, lr, B,
+                                                     step)
+            S2 = X[li].shape[1]
+            sl = np.ascontiguousarray(p[f"bp{li}"][:, :S2, :S2])
+            p[f"bp{li}"][:, :S2, :S2] = oracle.param_update(sl, dbias, [np.zeros_like(sl), np.zeros_like(sl)], first, lr,
+                                                            B, step)
+        gr = oracle.rope_backward(gr, 1250.0)
+        gr = oracle.norm_backward(X[2], p["ng"], p["nb"], gr, 1e-8)[0]
+        gr = oracle.dwt_backward(gr, S, T, 1)
+        p["table"] = oracle.embedding_update(p["table"], gr, targets, tlens, lr)
+        dXg = g.backward(targets, tlens, layers=nl - 1, update=True, learning_rate=lr, time_step=step)
+        errs = {"P": close(Pg, Po), "dX": close(dXg, gr),
+                "table": close(g.get_tensor(0, 0, V * d).reshape(V, d), p["table"]),
+                "Wv": close(g.get_tensor(8, 0, d * V).reshape(d, V), p["Wv"]), "bv": close(g.get_tensor(8, 4, V), p["bv"])}
+        for li in (4, 6):
+            H, F = shapes[li]
+            for slot, nm in ((0, "wq"), (1, "wk"), (2, "wv")):
+                errs[f"{nm}{li}"] = close(g.get_tensor(li, slot, H * d * (d // H)).reshape(H, d, d // H), p[f"{nm}{li}"])
+            errs[f"bp{li}"] = close(g.get_tensor(li, 3, H * mc * mc).reshape(H, mc, mc), p[f"bp{li}"].real)
+            errs[f"g{li}"] = close(g.get_tensor(li, 6, d), p[f"g{li}"])
+            errs[f"be{li}"] = close(g.get_tensor(li, 7, d), p[f"be{li}"])
+            for slot, nm, shp in ((0, "W1", (d, F)), (1, "W2", (F, d)), (4, "b1", (F,)), (5, "b2", (d,))):
+                errs[f"{nm}{li + 1}"] = close(g.get_tensor(li + 1, slot, int(np.prod(shp))).reshape(shp), p[f"{nm}{li + 1}"])
+        worst = max(errs, key=errs.get)
+        log(f"default stack step {step}: worst {worst} {errs[worst]:.1e}; " + ", ".join(f"{k} {v:.0e}" for k, v in errs.items()))
+        assert np.array_equal(mg, mo)
         bar = TOL if first else TOL * lr / 1.4e-4
         assert max(errs.values()) < bar, errs
         o.close()

@@ -975,3 +975,78 @@ def test_embedding_update_touches_target_rows_and_normalizes():
     np.testing.assert_allclose(new[4], r4, rtol=1e-12, atol=1e-13)
     for i in (2, 4, 7):
         assert abs(new[i].mean()) < 1e-13 and abs(np.mean(new[i] ** 2) - 1) < 1e-9
+
+
+@pytest.mark.parametrize("wavelet,R", [(1, 10), (1, 11), (0, 8), (0, 9)])
+def test_dwt_backward_interior_gradient_targets_and_align(wavelet, R):
+    """DiscreteWaveletLayer::backward, partial mode (wavelet_discrete_layer.rs:
+    163-207; grad_dwt_1d_trend, dwt.rs:272-282): the transposed low-pass filter
+    over the compressed rows, which ignores the padding, so it is the exact
+    gradient of L = Re sum conj(g) * compress(x) for the rows no padding image
+    reaches (finite differences through the oracle's DWT forward, itself pinned
+    to the reference's known answers); the T target rows pass their gradient
+    through; an odd input count gives one more decompressed row, which
+    align_gradient_rows_complex (:318-346) adds into the last input row; and
+    the reference's own check is the next test."""
+    rng = np.random.default_rng(60 + R)
+    L = 2 if wavelet == 0 else 4
+    T, d, B = 3, 2, 2
+    S = R + T
+    M = oracle.dwt_rows(R, wavelet)
+    net = oracle.Network()
+    net.add_discrete_wavelet(d, wavelet, 2)  # SYMMETRIC
+    x = rng.standard_normal((B, S, d)) + 1j * rng.standard_normal((B, S, d))
+    g = rng.standard_normal((B, M + T, d)) + 1j * rng.standard_normal((B, M + T, d))
+    mask = np.ones((B, S), np.uint32)
+
+    def fwd(x):
+        return net.forward_layers(0, 1, x, mask=mask, forward_only=False, target_rows=T)
+
+    y = fwd(x)
+    assert y.shape == (B, M + T, d)
+    np.testing.assert_array_equal(y[:, M:], x[:, R:])  # the target rows pass through
+    dx = oracle.dwt_backward(g, S, T, wavelet)
+    np.testing.assert_array_equal(dx[:, R:], g[:, M:])
+    h = 1e-6
+    interior = range(L - 2, R - (L - 1))
+    for b in range(B):
+        for r in interior:
+            for c in range(d):
+                for unit, part in ((1.0, "real"), (1j, "imag")):
+                    xp, xm = x.copy(), x.copy()
+                    xp[b, r, c] += h * unit
+                    xm[b, r, c] -= h * unit
+                    fd = (np.real(np.sum(np.conj(g[:, :M]) * fwd(xp)[:, :M]))
+                          - np.real(np.sum(np.conj(g[:, :M]) * fwd(xm)[:, :M]))) / (2 * h)
+                    assert abs(getattr(dx[b, r, c], part) - fd) < 1e-8, (b, r, c, part)
+    lo = {0: [1 / math.sqrt(2)] * 2}.get(wavelet)
+    if R % 2 == 1:  # the align row: decompressed rows R-1 and R summed
+        g0 = np.zeros((1, M + T, 1), complex)
+        g0[0, M - 1, 0] = 1.0
+        dl = oracle.dwt_backward(g0, S, T, wavelet)[0, :, 0]
+        if lo is not None:  # DB1: the last compressed row feeds input rows R-1 (twice, aligned) only
+            assert dl[R - 1] == pytest.approx(lo[0] + lo[1])
+
+
+def test_dwt_backward_reference_sum_check():
+    """The reference's test_1d_wavelet_discrete_layer_backward
+    (network_components/tests/test_wavelet_discrete_layer.rs:93-137) as
+    written: 5 inputs, DB2, SYMMETRIC, a gradient of ones on the 4 trend rows;
+    the sum of grad_dwt_1d_trend's values (6 of them; the layer's align adds
+    the extra one into the last row, which keeps the sum) equals the sum of
+    the first 4 entries of the numerical gradient of sum(trend)."""
+    S, wavelet = 5, 1
+    M = oracle.dwt_rows(S, wavelet)
+    an = oracle.dwt_backward(np.ones((1, M, 1), complex), S, 0, wavelet)[0, :, 0]
+    one = oracle.Network()
+    one.add_discrete_wavelet(1, wavelet, 2)
+    xr = np.random.default_rng(61).standard_normal((1, S, 1)) + 0j
+    m = np.ones((1, S), np.uint32)
+    num = np.zeros(S)
+    for r in range(S):
+        xp, xm = xr.copy(), xr.copy()
+        xp[0, r, 0] += 1e-7
+        xm[0, r, 0] -= 1e-7
+        num[r] = (np.sum(one.forward_layers(0, 1, xp, mask=m, forward_only=False))
+                  - np.sum(one.forward_layers(0, 1, xm, mask=m, forward_only=False))).real / 2e-7
+    assert abs(np.sum(an).real - np.sum(num[:M])) < 1e-6

@@ -1050,3 +1050,59 @@ def test_dwt_backward_reference_sum_check():
         num[r] = (np.sum(one.forward_layers(0, 1, xp, mask=m, forward_only=False))
                   - np.sum(one.forward_layers(0, 1, xm, mask=m, forward_only=False))).real / 2e-7
     assert abs(np.sum(an).real - np.sum(num[:M])) < 1e-6
+
+
+def test_norm_backward_reference_gradient_check():
+    """The reference's own test_norm_backward (network_components/tests/
+    test_norm_layer.rs:15-118) as written: Norm(eps 1e-8, gamma 1, beta 0) on
+    Re(input + input_before), a Linear (4 x 4) and the TRAINING softmax over
+    2 x 4 rows, targets of 3 ids in [2, 3); the Norm's input gradient from
+    backward against central differences (step 1e-7) of cross_entropy_loss_batch
+    (transformer_network.rs:662-711) in re and im of every input element,
+    each within the reference's bar (derivative.rs:1179-1191: |a - b| /
+    max(|a|, |b|, 1e-5) < 1e-5).  With gamma uniform the formula's quadratic
+    term vanishes, so there it is the Norm's gradient."""
+    rng = np.random.default_rng(5)
+    B, S, d, eps = 2, 4, 4, 1e-7
+    gamma, beta = np.ones(d, complex), np.zeros(d, complex)
+    for _ in range(3):
+        x_in = rng.standard_normal((B, S, d)) + 1j * rng.standard_normal((B, S, d))
+        before = rng.standard_normal((B, S, d)) + 1j * rng.standard_normal((B, S, d))
+        W = rng.uniform(-0.6, 0.6, (d, d)) + 1j * rng.uniform(-0.6, 0.6, (d, d))
+        b = np.ones(d, complex)  # LinearLayer's bias init 1 + 0i
+        targets = rng.integers(2, 3, size=(B, S - 1)).astype(np.uint32)
+
+        def forward(xi):
+            xs = (xi + before).real.astype(complex)  # add_matrix_3d_c
+            xn = np.array([[oracle.layernorm_row(xs[bb, s], 1e-8, gamma, beta) for s in range(S)] for bb in range(B)])
+            Y = np.stack([oracle.zgemm(xn[bb], W) for bb in range(B)]) + b
+            return xs, xn, _softmax_re(Y)
+
+        def loss(xi):
+            P = forward(xi)[2]
+            total = 0.0
+            for bb in range(B):
+                lsum, cnt = 0.0, 0.0
+                for t, tg in enumerate(targets[bb]):
+                    row = S - len(targets[bb]) - 1 + t
+                    if tg == 1:
+                        continue
+                    if row >= S - 1:
+                        break
+                    lsum += -np.log(P[bb, row, tg] + 1e-15)
+                    cnt += 1.0
+                total += lsum / cnt
+            return total / B
+
+        xs, xn, P = forward(x_in)
+        _, _, dY = oracle.linear_backward(xn, oracle.softmax_backward(P, targets), W)
+        an = oracle.norm_backward(xs, gamma, beta, dY, 1e-8)[0]
+        for idx in np.ndindex(x_in.shape):
+            g = 0j
+            for unit in (1.0, 1j):
+                xp, xm = x_in.copy(), x_in.copy()
+                xp[idx] += eps * unit
+                xm[idx] -= eps * unit
+                g += unit * (loss(xp) - loss(xm)) / (2 * eps)
+            rel = abs(g - an[idx]) / max(abs(g), abs(an[idx]), 1e-5)
+            assert rel < 1e-5, (idx, g, an[idx], rel)

@@ -140,16 +140,16 @@ void gelu_backward(hipStream_t st, const double2* dH, const double2* Z, const ui
                    double2* G);
 // out [C][R] = conj(in)^T for in [R][C]
 void conj_transpose(hipStream_t st, const double2* in, long R, long C, double2* out);
-// db [V] = sum_b sum_s G[b][s][:] (per-sequence sums in row order, then in sequence order)
-void bias_grad(hipStream_t st, const double2* G, int B, int S, int V, double2* db);
+// db [V] = sum_b sum_s G[b][s][:] (per-sequence sums in row order, then in sequence order); ws [B][V]
+void bias_grad(hipStream_t st, const double2* G, int B, int S, int V, double2* ws, double2* db);
 // W [n], b [V] updated in place from dW, db (moments mW, vW, mb, vb)
 void linear_update(hipStream_t st, double2* W, const double2* dW, double2* mW, double2* vW, long n, double2* b,
                    const double2* db, double2* mb, double2* vb, int V, const TrainStep& ts);
 // the Norm's backward per row of x (or Re(x + resid) + 0i); dx real rows, pg = dout * x_hat
 void norm_backward(hipStream_t st, const double2* x, const double2* resid, long rows, int n, double eps,
                    const double2* gamma, const double2* beta, const double2* dout, double2* dx, double2* pg);
-// out[j] = mult * sum_r X[r][j]
-void colsum(hipStream_t st, const double2* X, long rows, int n, double mult, double2* out);
+// out[j] = mult * (sum over sequences b of the row sum of X[b][:][j]), as bias_grad; ws [B][n]
+void colsum(hipStream_t st, const double2* X, int B, int S, int n, double mult, double2* ws, double2* out);
 // attention weights A and dl_da [B][H][S][S] of a stateless pass from the packed [q | k | v] rows and the
 // gradient G [B*S][d] of the heads' output
 void attn_probs_grad(hipStream_t st, const double2* qkv, const double* bias_re, int mc, const uint32_t* mask,

@@ -375,7 +375,7 @@ struct mitok_network {
   // the heads' output of each SelfAttention layer (before its residual + Norm)
   std::vector<std::unique_ptr<mitok::DevBuf>> tr_in, tr_cat;
   mitok::DevBuf tr_g, tr_xh, tr_wh, tr_dw, tr_db, tr_ga, tr_gb, tr_tgt, tr_norm;
-  mitok::DevBuf tr_z, tr_h, tr_g1, tr_dh, tr_qkv, tr_dqkv, tr_A, tr_dA, tr_pg, tr_eid, tr_est, tr_eocc;
+  mitok::DevBuf tr_z, tr_h, tr_g1, tr_dh, tr_qkv, tr_dqkv, tr_A, tr_dA, tr_pg, tr_eid, tr_est, tr_eocc, tr_bsum;
 };
 
 namespace mitok {
@@ -2117,15 +2117,16 @@ int mitok_predict(mitok_network* n, const uint32_t* ids, const uint32_t* lens, u
     size_t cnt = (sp.last_row ? (size_t)B : orows) * V;
     HIP_TRY(hipMemcpyAsync(out, sp.out_re, cnt * sizeof(double), hipMemcpyDeviceToHost, n->stream));
     HIP_TRY(hipStreamSynchronize(n->stream));
+  } else if (!last_row_only) {  // every row: straight into the caller's buffer
+    HIP_TRY(hipMemcpyAsync(out, sp.out_prob, orows * V * sizeof(double), hipMemcpyDeviceToHost, n->stream));
+    HIP_TRY(hipStreamSynchronize(n->stream));
   } else {
     std::vector<double> all(orows * V);
     HIP_TRY(hipMemcpyAsync(all.data(), sp.out_prob, all.size() * sizeof(double), hipMemcpyDeviceToHost, n->stream));
     HIP_TRY(hipStreamSynchronize(n->stream));
     const uint32_t* ol = cached_lens(n, lens);
-    if (last_row_only)
-      for (uint32_t b = 0; b < B; ++b)
-        memcpy(out + (size_t)b * V, all.data() + ((size_t)b * n->wS + ol[b] - 1) * V, V * sizeof(double));
-    else memcpy(out, all.data(), all.size() * sizeof(double));
+    for (uint32_t b = 0; b < B; ++b)
+      memcpy(out + (size_t)b * V, all.data() + ((size_t)b * n->wS + ol[b] - 1) * V, V * sizeof(double));
   }
   collect_timing(n);
   TRY(check_err_word(n));
@@ -2641,6 +2642,9 @@ static int backward_impl(Net* n, const uint32_t* targets, const uint32_t* tlens,
       case K_SELF_ATTENTION: {
         const auto* A = (const SelfAttentionLayer*)L;
         if ((uint32_t)S > A->max_ctx) return fail(ERR_ARG, "layer %u: %d rows exceed max context %u", li, S, A->max_ctx);
+        // k_attn_probs_grad holds a query row's weights and Re(dl_ds) in LDS (2 S doubles beside 6 KB)
+        if (S > 3072) return fail(ERR_ARG, "layer %u: attention backward of %d rows (at most 3072)", li, S);
+        if (A->dh > 256) return fail(ERR_ARG, "layer %u: attention backward of %u-wide heads (at most 256)", li, A->dh);
         d3max = std::max(d3max, (size_t)3 * di);
         att = std::max(att, (size_t)A->heads * S * S);
         wmax = std::max(wmax, (size_t)3 * di * di);
@@ -2753,6 +2757,7 @@ static int backward_impl(Net* n, const uint32_t* targets, const uint32_t* tlens,
   TRY(reserve(n, n->tr_db, std::max(bmax, dmax) * c16));
   TRY(reserve(n, n->tr_dh, (size_t)rows_max * std::max(fmax, dmax) * c16));
   TRY(reserve(n, n->tr_pg, (size_t)rows_max * dmax * c16));
+  TRY(reserve(n, n->tr_bsum, (size_t)B * std::max({bmax, dmax, fmax}) * c16));  // per-sequence column sums
   if (fmax) {
     TRY(reserve(n, n->tr_z, (size_t)rows_max * fmax * c16));
     TRY(reserve(n, n->tr_h, (size_t)rows_max * fmax * c16));
@@ -2802,7 +2807,7 @@ static int backward_impl(Net* n, const uint32_t* targets, const uint32_t* tlens,
     e.out = dW;
     e.ldo = dout;
     TRY(launch_rc(gemm(st, din, dout, (int)rows_c, rows_of(xh, rows_c), G, dout, e, nullptr, sy), "weight grad"));
-    bias_grad(st, G, (int)B, S_c, dout, db);
+    bias_grad(st, G, (int)B, S_c, dout, n->tr_bsum.as<double2>(), db);
     conj_transpose(st, W, din, dout, wh);
     e.out = dX;
     e.ldo = din;
@@ -2923,9 +2928,9 @@ static int backward_impl(Net* n, const uint32_t* targets, const uint32_t* tlens,
           ts.first = A->updates == 0 ? 1 : 0;
           ts.time_step = (int)time_step;
           ts.batch = (double)da;  // norm_layer.rs:269: gamma's length
-          colsum(st, n->tr_pg.as<double2>(), rows, da, (double)da, db);  // gamma's gradient: n copies per row
+          colsum(st, n->tr_pg.as<double2>(), (int)B, S, da, (double)da, n->tr_bsum.as<double2>(), db);  // gamma's: n copies per row
           param_update(st, A->gamma.as<double2>(), db, A->mg.as<double2>(), A->vg.as<double2>(), da, false, ts);
-          colsum(st, gcur, rows, da, (double)da, db);
+          colsum(st, gcur, (int)B, S, da, (double)da, n->tr_bsum.as<double2>(), db);
           param_update(st, A->beta.as<double2>(), db, A->mbt.as<double2>(), A->vbt.as<double2>(), da, false, ts);
           ts.batch = (double)B;  // masked_attention_head.rs:352: the sequences
           param_update(st, A->wqkv.as<double2>(), dW, A->mw.as<double2>(), A->vw.as<double2>(), (long)3 * da * da, true, ts);

@@ -48,18 +48,34 @@ __global__ __launch_bounds__(256) void k_conj_transpose(const double2* __restric
 
 // db[c] = sum over sequences b of (sum over rows s of G[b][s][c]): each
 // sequence's column sum in row order, then the sequences in order
-// (linear_layer.rs:101-105, group_gradient_batch_bias)
-__global__ __launch_bounds__(256) void k_bias_grad(const double2* __restrict__ G, int B, int S, int V,
-                                                   double2* __restrict__ db) {
+// (linear_layer.rs:101-105, group_gradient_batch_bias).  Two launches: one
+// thread per (sequence, column) sums its rows (eight loads in flight), then
+// one per column adds the sequences' sums, times `mult`.
+__global__ __launch_bounds__(256) void k_seq_colsum(const double2* __restrict__ G, int B, int S, int V,
+                                                    double2* __restrict__ part) {
+  const long t = (long)blockIdx.x * 256 + threadIdx.x;
+  if (t >= (long)B * V) return;
+  const int c = (int)(t % V), b = (int)(t / V);
+  const double2* g = G + (long)b * S * V + c;
+  double2 s = make_double2(0.0, 0.0);
+  int r = 0;
+  for (; r + 8 <= S; r += 8) {
+    double2 u[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) u[q] = g[(long)(r + q) * V];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) s = cadd(s, u[q]);
+  }
+  for (; r < S; ++r) s = cadd(s, g[(long)r * V]);
+  part[t] = s;
+}
+__global__ __launch_bounds__(256) void k_seq_sum(const double2* __restrict__ part, int B, int V, double mult,
+                                                 double2* __restrict__ out) {
   const int c = blockIdx.x * 256 + threadIdx.x;
   if (c >= V) return;
   double2 acc = make_double2(0.0, 0.0);
-  for (int b = 0; b < B; ++b) {
-    double2 s = make_double2(0.0, 0.0);
-    for (int r = 0; r < S; ++r) s = cadd(s, G[((long)b * S + r) * V + c]);
-    acc = cadd(acc, s);
-  }
-  db[c] = acc;
+  for (int b = 0; b < B; ++b) acc = cadd(acc, part[(long)b * V + c]);
+  out[c] = mult == 1.0 ? acc : cscale(acc, mult);
 }
 
 // f64::powi as compiler-rt's __powidf2 (square and multiply over the bits)
@@ -167,8 +183,8 @@ void conj_transpose(hipStream_t st, const double2* in, long R, long C, double2* 
   if (R > 0 && C > 0) MITOK_LAUNCH(k_conj_transpose, grid, dim3(256), 0, st, in, R, C, out);
 }
 
-void bias_grad(hipStream_t st, const double2* G, int B, int S, int V, double2* db) {
-  if (V > 0) MITOK_LAUNCH(k_bias_grad, dim3((V + 255) / 256), dim3(256), 0, st, G, B, S, V, db);
+void bias_grad(hipStream_t st, const double2* G, int B, int S, int V, double2* ws, double2* db) {
+  colsum(st, G, B, S, V, 1.0, ws, db);
 }
 
 void linear_update(hipStream_t st, double2* W, const double2* dW, double2* mW, double2* vW, long n, double2* b,
@@ -285,15 +301,6 @@ __global__ __launch_bounds__(256) void k_norm_backward(const double2* __restrict
   }
 }
 
-// out[j] = mult * (sum over rows r of X[r][j]), rows in order
-__global__ __launch_bounds__(256) void k_colsum(const double2* __restrict__ X, long rows, int n, double mult,
-                                                double2* __restrict__ out) {
-  const int j = blockIdx.x * 256 + threadIdx.x;
-  if (j >= n) return;
-  double2 acc = make_double2(0.0, 0.0);
-  for (long r = 0; r < rows; ++r) acc = cadd(acc, X[r * n + j]);
-  out[j] = cscale(acc, mult);
-}
 
 // One query row of one head (grid: S x H x B): the forward's attention
 // weights A (masked_attention_head.rs:184-205: Re of the scaled scores plus
@@ -308,48 +315,62 @@ __global__ __launch_bounds__(256) void k_attn_probs_grad(const double2* __restri
   extern __shared__ double dyn[];
   double* sc = dyn;       // [S] scores, then weights
   double* rr = dyn + S;   // [S] Re(dl_ds)
+  __shared__ double2 qs[256], gs[256];  // the row's q and gradient (dh <= 256)
   __shared__ double shm[256];
   __shared__ double2 sh2[256];
-  const int i = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int i = blockIdx.x, h = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
   const int d = H * dh, ld = 3 * d;
   const long row = (long)b * S + i;
   double* Ar = A + (((long)b * H + h) * S + i) * S;
   double* dAr = dA + (((long)b * H + h) * S + i) * S;
   if (mask[row] == 0) {
-    for (int j = threadIdx.x; j < S; j += 256) Ar[j] = dAr[j] = 0.0;
+    for (int j = tid; j < S; j += 256) Ar[j] = dAr[j] = 0.0;
     return;
   }
-  const double2* q = qkv + row * ld + (long)h * dh;
-  const double2* g = G + row * d + (long)h * dh;
-  const double* bp = bias_re + ((long)h * mc + i) * mc;
-  double mx = -INFINITY;
-  for (int j = threadIdx.x; j < S; j += 256) {
-    const double2* k = qkv + ((long)b * S + j) * ld + d + (long)h * dh;
-    const double2* v = qkv + ((long)b * S + j) * ld + 2 * d + (long)h * dh;
-    double s = 0.0, rv = 0.0;
-    for (int m = 0; m < dh; ++m) {
-      s = s + (q[m].x * k[m].x - q[m].y * k[m].y);
-      rv = rv + (g[m].x * v[m].x + g[m].y * v[m].y);
-    }
-    s = j > i ? -1e12 : s * c + bp[j];
-    sc[j] = s;
-    rr[j] = rv;
-    mx = fmax(mx, s);
+  for (int m = tid; m < dh; m += 256) {
+    qs[m] = qkv[row * ld + (long)h * dh + m];
+    gs[m] = G[row * d + (long)h * dh + m];
   }
+  __syncthreads();
+  // 16 lanes per key (a key's row read in contiguous 16-lane runs), 16 keys per pass
+  const double* bp = bias_re + ((long)h * mc + i) * mc;
+  const int sub = tid & 15, kq = tid >> 4;
+  for (int j0 = 0; j0 < S; j0 += 16) {
+    const int j = j0 + kq;
+    double s = 0.0, rv = 0.0;
+    if (j < S) {
+      const double2* k = qkv + ((long)b * S + j) * ld + d + (long)h * dh;
+      const double2* v = k + d;
+      for (int m = sub; m < dh; m += 16) {
+        const double2 kk = k[m], vv = v[m];
+        s = s + (qs[m].x * kk.x - qs[m].y * kk.y);
+        rv = rv + (gs[m].x * vv.x + gs[m].y * vv.y);
+      }
+    }
+    s = row16_sum(s);
+    rv = row16_sum(rv);
+    if (j < S && sub == 0) {
+      sc[j] = j > i ? -1e12 : s * c + bp[j];
+      rr[j] = rv;
+    }
+  }
+  __syncthreads();
+  double mx = -INFINITY;
+  for (int j = tid; j < S; j += 256) mx = fmax(mx, sc[j]);
   mx = block_max1(mx, shm);
   double2 acc = make_double2(0.0, 0.0);
-  for (int j = threadIdx.x; j < S; j += 256) {
+  for (int j = tid; j < S; j += 256) {
     sc[j] = exp(sc[j] - mx);
     acc.x += sc[j];
   }
   const double sum = block_sum2(acc, sh2).x;
   acc = make_double2(0.0, 0.0);
-  for (int j = threadIdx.x; j < S; j += 256) {
+  for (int j = tid; j < S; j += 256) {
     sc[j] = sc[j] / sum;
     acc.x += sc[j] * rr[j];
   }
   const double sr = block_sum2(acc, sh2).x;
-  for (int j = threadIdx.x; j < S; j += 256) {
+  for (int j = tid; j < S; j += 256) {
     Ar[j] = sc[j];
     dAr[j] = sc[j] * (rr[j] - sr);
   }
@@ -479,8 +500,10 @@ void norm_backward(hipStream_t st, const double2* x, const double2* resid, long 
   if (rows > 0) MITOK_LAUNCH(k_norm_backward, dim3((unsigned)rows), dim3(256), 0, st, x, resid, n, eps, gamma, beta, dout, dx, pg);
 }
 
-void colsum(hipStream_t st, const double2* X, long rows, int n, double mult, double2* out) {
-  if (n > 0) MITOK_LAUNCH(k_colsum, dim3((n + 255) / 256), dim3(256), 0, st, X, rows, n, mult, out);
+void colsum(hipStream_t st, const double2* X, int B, int S, int n, double mult, double2* ws, double2* out) {
+  if (n <= 0 || B <= 0) return;
+  MITOK_LAUNCH(k_seq_colsum, dim3((unsigned)(((long)B * n + 255) / 256)), dim3(256), 0, st, X, B, S, n, ws);
+  MITOK_LAUNCH(k_seq_sum, dim3((n + 255) / 256), dim3(256), 0, st, ws, B, n, mult, out);
 }
 
 void attn_probs_grad(hipStream_t st, const double2* qkv, const double* bias_re, int mc, const uint32_t* mask,

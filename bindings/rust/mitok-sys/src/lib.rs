@@ -280,6 +280,57 @@ impl Network {
         Ok((logits, m))
     }
 
+    /// train's forward pass (transformer_network.rs:73-79): the stateless
+    /// predict of unpadded sequences whose last `target_rows` ids are the
+    /// targets (a DiscreteWavelet layer passes them on uncompressed).  The
+    /// softmax output [batch][seq'][vocab] and the padding mask; seq' assumes at
+    /// most one wavelet layer, as create_transformer builds.
+    pub fn predict_targets(&mut self, batch_ids: &[Vec<u32>], target_rows: u32)
+                           -> Result<(Vec<Vec<Vec<f64>>>, Vec<Vec<u32>>), MitokError> {
+        let b = batch_ids.len() as u32;
+        let s = batch_ids.iter().map(|r| r.len()).max().unwrap_or(0) as u32;
+        let lens: Vec<u32> = batch_ids.iter().map(|r| r.len() as u32).collect();
+        let mut ids = vec![1u32; (b * s) as usize];
+        for (i, r) in batch_ids.iter().enumerate() {
+            ids[i * s as usize..i * s as usize + r.len()].copy_from_slice(r);
+        }
+        let t = target_rows.min(s);
+        let inner = self.out_rows(s - t)?;
+        let so = if inner != s - t { inner + t } else { s };
+        let v = self.vocab as usize;
+        let mut out = vec![0f64; b as usize * so as usize * v];
+        let mut mask = vec![0u32; b as usize * so as usize];
+        check(unsafe {
+            mitok_predict_targets(self.raw, ids.as_ptr(), lens.as_ptr(), b, s, target_rows, out.as_mut_ptr(),
+                                  mask.as_mut_ptr())
+        })?;
+        let probs = out
+            .chunks(so as usize * v)
+            .map(|seq| seq.chunks(v).map(|r| r.to_vec()).collect())
+            .collect();
+        let m = mask.chunks(so as usize).map(|r| r.to_vec()).collect();
+        Ok((probs, m))
+    }
+
+    /// backward (transformer_network.rs:506-636) over `n_layers` layers below
+    /// the Softmax (num_layers - 1: all of them, the embedding update
+    /// included), with update_parameters when `update`; time_step is train's
+    /// epoch.  The targets are train's target ids, one Vec per sequence.
+    pub fn backward(&mut self, targets: &[Vec<u32>], n_layers: u32, update: bool, learning_rate: f64,
+                    time_step: u32) -> Result<(), MitokError> {
+        let b = targets.len() as u32;
+        let t = targets.iter().map(|r| r.len()).max().unwrap_or(0).max(1) as u32;
+        let tlens: Vec<u32> = targets.iter().map(|r| r.len() as u32).collect();
+        let mut flat = vec![1u32; (b * t) as usize];
+        for (i, r) in targets.iter().enumerate() {
+            flat[i * t as usize..i * t as usize + r.len()].copy_from_slice(r);
+        }
+        check(unsafe {
+            mitok_backward(self.raw, flat.as_ptr(), tlens.as_ptr(), b, t, n_layers, update as c_int, learning_rate,
+                           time_step, std::ptr::null_mut())
+        })
+    }
+
     /// The token loop on ids: `n_new` greedy ids per sequence.
     pub fn generate(&mut self, prompt: &[u32], n_new: u32) -> Result<Vec<u32>, MitokError> {
         let mut out = vec![0u32; n_new as usize];

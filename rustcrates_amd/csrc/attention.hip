@@ -126,7 +126,15 @@ __device__ __forceinline__ void attn_chunk(const Attn& a, const double2* __restr
   __shared__ double2 qs[256], kn[256], vn[256];
   __shared__ double stat[2];
   const int dh = DH > 0 ? DH : a.dh;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // the thread index goes through an empty asm: the compact grid's item loop
+  // then recomputes the per-lane offsets for every chunk instead of holding
+  // them (hoisted) across the loop.  With the q sums spread over the waves
+  // and no load under a branch, DH 64 takes 93 VGPRs (5 blocks per CU) where
+  // it took 160 (3); the decode step measured the same either way, so the
+  // kernel is not bound by its resident blocks
+  int tid_o = threadIdx.x;
+  asm volatile("" : "+v"(tid_o));
+  const int tid = tid_o, lane = tid & 63, wave = tid >> 6;
   const int T = a.kv_len[b] + 1;
   const int CH = o.CH;
   const int c0 = split * CH;
@@ -147,57 +155,47 @@ __device__ __forceinline__ void attn_chunk(const Attn& a, const double2* __restr
   const int e = tid % dh, g = tid / dh;
   constexpr int VG = 256 / (DH > 0 ? DH : 256);
   constexpr int VU = DH > 0 ? (DEC_MAX_CHUNK + VG - 1) / VG : 1;  // keys per value lane
-  // keys and bias rows are in flight while q is summed; values are loaded after
-  // the softmax, which keeps the register count (and the blocks per CU) high
+  // keys and bias rows are in flight while q is summed
   double2 kv[NP][EPL];
   double bj[NP];
   if (DH > 0) {
 #pragma unroll
     for (int pass = 0; pass < NP; ++pass) {
-      const int j = pass * 16 + wave * 4 + kq;
-      const double2* kr = K + (long)(c0 + j) * dh;
+      // keys past the chunk load its last key (every load is issued, none
+      // under a branch); their scores are never stored
+      const int j = min(pass * 16 + wave * 4 + kq, nc - 1);
+      const double2* kr = K + (long)(c0 + j) * dh + sub;
 #pragma unroll
-      for (int t = 0; t < EPL; ++t) {
-        const int ee = sub + t * DEC_LPK;
-        kv[pass][t] = (j < nc && ee < dh) ? kr[ee] : make_double2(0.0, 0.0);
-      }
-      bj[pass] = (j < nc && sub == 0) ? bias0[c0 + j] : 0.0;
+      for (int t = 0; t < EPL; ++t) kv[pass][t] = kr[t * DEC_LPK];
+      bj[pass] = bias0[c0 + j];
     }
   }
 
+  // q, and for the chunk of the new token k and v, each summed over the npart
+  // partials in order; thread i takes vector i / dh (q, k, v) at element
+  // i % dh, so the three sums run in different waves
   const double2* row = qkv + (long)b * ldq + (long)h * dh;
-  for (int ee = tid; ee < dh; ee += 256) {
-    double2 q = make_double2(0.0, 0.0), kk = q, vx = q;
-    for (int p0 = 0; p0 < npart; p0 += 4) {  // partials summed in order, four loads in flight
+  const int nvec = has_new ? 3 : 1;
+  for (int i = tid; i < nvec * dh; i += 256) {
+    const int vec = i / dh, ee = i - vec * dh;
+    const double2* src = row + (long)vec * d + ee;
+    double2 s = make_double2(0.0, 0.0);
+    for (int p0 = 0; p0 < npart; p0 += 4) {  // four loads in flight; past npart they repeat the last
       double2 t[4];
 #pragma unroll
-      for (int p = 0; p < 4; ++p) t[p] = p0 + p < npart ? row[(p0 + p) * pstride + ee] : make_double2(0.0, 0.0);
+      for (int p = 0; p < 4; ++p) t[p] = src[(long)min(p0 + p, npart - 1) * pstride];
 #pragma unroll
       for (int p = 0; p < 4; ++p)
-        if (p0 + p < npart) q = (p0 + p == 0) ? t[p] : cadd(q, t[p]);
-      if (has_new) {
-#pragma unroll
-        for (int p = 0; p < 4; ++p) t[p] = p0 + p < npart ? row[(p0 + p) * pstride + d + ee] : make_double2(0.0, 0.0);
-#pragma unroll
-        for (int p = 0; p < 4; ++p)
-          if (p0 + p < npart) kk = (p0 + p == 0) ? t[p] : cadd(kk, t[p]);
-#pragma unroll
-        for (int p = 0; p < 4; ++p) t[p] = p0 + p < npart ? row[(p0 + p) * pstride + 2 * d + ee] : make_double2(0.0, 0.0);
-#pragma unroll
-        for (int p = 0; p < 4; ++p)
-          if (p0 + p < npart) vx = (p0 + p == 0) ? t[p] : cadd(vx, t[p]);
-      }
+        if (p0 + p < npart) s = (p0 + p == 0) ? t[p] : cadd(s, t[p]);
     }
-    qs[ee] = q;
-    if (has_new) {
-      kn[ee] = kk;
-      vn[ee] = vx;
-      if (T - 1 < a.ctx) {  // append (masked_attention_head.rs:159-178)
-        a.kc_w[(bh * a.ctx + (T - 1)) * dh + ee] = kk;
-        a.vc_w[(bh * a.ctx + (T - 1)) * dh + ee] = vx;
-      } else if (ee == 0) {
+    if (vec == 0) {
+      qs[ee] = s;
+    } else {
+      (vec == 1 ? kn : vn)[ee] = s;
+      if (T - 1 < a.ctx)  // append (masked_attention_head.rs:159-178)
+        (vec == 1 ? a.kc_w : a.vc_w)[(bh * a.ctx + (T - 1)) * dh + ee] = s;
+      else if (vec == 1 && ee == 0)
         atomicOr(a.err, (uint32_t)EB_CTX_OVERFLOW);
-      }
     }
   }
   __syncthreads();
@@ -255,12 +253,12 @@ __device__ __forceinline__ void attn_chunk(const Attn& a, const double2* __restr
   // out[e] over the chunk's keys: group g takes keys g, g + G, ...
   double2 acc = make_double2(0.0, 0.0);
   if (DH > 0) {
+    // the values are requested after the softmax: loading them with the keys
+    // (one memory round trip per chunk instead of two, 126 VGPRs) measured no
+    // faster in the decode step
     double2 vv[VU];
 #pragma unroll
-    for (int u = 0; u < VU; ++u) {
-      const int j = g + u * G;
-      vv[u] = (g < G && j < nc) ? V[(long)(c0 + j) * dh + e] : make_double2(0.0, 0.0);
-    }
+    for (int u = 0; u < VU; ++u) vv[u] = V[(long)(c0 + min(g + u * G, nc - 1)) * dh + e];  // past nc: not summed
     if (has_new)
 #pragma unroll
       for (int u = 0; u < VU; ++u)
@@ -302,7 +300,7 @@ __device__ __forceinline__ void attn_chunk(const Attn& a, const double2* __restr
 // chunk) in that order, so no block starts only to find its chunk empty (a
 // graph replays one grid while the caches grow).  Up to 256 sequences; with
 // more, one block per (chunk, head, sequence) of the launch's maximum.
-constexpr int DEC_MAX_BLOCKS = 1024;
+constexpr int DEC_MAX_BLOCKS = 2048;
 constexpr int DEC_COMPACT_MAX_B = 256;
 
 template <int DH>
@@ -327,7 +325,9 @@ __global__ __launch_bounds__(256) void k_attention_split(Attn a, const double2* 
     s_off[tid + 1] += v;
     __syncthreads();
   }
-  const int total = s_off[a.B];
+  // the item's coordinates are the same in every lane: held in scalar
+  // registers, so the chunk's addresses are scalar too (as in a grid launch)
+  const int total = __builtin_amdgcn_readfirstlane(s_off[a.B]);
   for (int item = blockIdx.x; item < total; item += gridDim.x) {
     int lo = 0, hi = a.B - 1;  // the sequence whose range holds item
     while (lo < hi) {
@@ -335,7 +335,8 @@ __global__ __launch_bounds__(256) void k_attention_split(Attn a, const double2* 
       if (s_off[mid] <= item) lo = mid;
       else hi = mid - 1;
     }
-    const int r = item - s_off[lo], nsb = s_ns[lo];
+    lo = __builtin_amdgcn_readfirstlane(lo);
+    const int r = __builtin_amdgcn_readfirstlane(item - s_off[lo]), nsb = __builtin_amdgcn_readfirstlane(s_ns[lo]);
     attn_chunk<DH>(a, qkv, ldq, npart, pstride, append, o, r % nsb, r / nsb, lo);
     __syncthreads();  // the chunk's LDS is reused by the next item
   }

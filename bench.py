@@ -335,8 +335,9 @@ def head_train_step(cfg, B=8, S=128, T=64, reps=5):
 
 def train_step(cfg, B=8, S=128, T=64, reps=3):
     """One step of the reference's train loop (transformer_network.rs:35-163)
-    on config 3: the TRAINING-mode predict of B x S rows (its [B][S][V]
-    softmax output copied to the host for the loss), then backward over every
+    on config 3: the TRAINING-mode predict of B x S rows and
+    cross_entropy_loss_batch on its softmax output, both on the device (only
+    the loss crosses PCIe, mitok_cross_entropy_loss), then backward over every
     layer with every update (mitok_backward).  Algorithmic flops of the
     backward's products (8 M N K each): per attention layer the Q/K/V
     recompute, their weight and input gradients (3 x 24 rows d^2); per
@@ -349,13 +350,16 @@ def train_step(cfg, B=8, S=128, T=64, reps=3):
         targets = seeded.prompts(22, [T] * B, cfg.vocab)
         nl = net.num_layers
         for t in (1, 2):  # every layer's first update (plain descent), then AdamW
-            net.predict(ids, forward_only=False)
+            net.predict(ids, forward_only=False, want_output=False)
+            net.cross_entropy_loss(targets)
             net.backward(targets, layers=nl - 1, update=True, learning_rate=1e-4, time_step=t, want_grad_input=False)
         ra.device_synchronize(0)
         fwd = bwd = 0.0
+        losses = []
         for t in range(reps):
             t0 = time.perf_counter()
-            net.predict(ids, forward_only=False)
+            net.predict(ids, forward_only=False, want_output=False)
+            losses.append(net.cross_entropy_loss(targets).real)
             t1 = time.perf_counter()
             net.backward(targets, layers=nl - 1, update=True, learning_rate=1e-4, time_step=3 + t, want_grad_input=False)
             fwd += t1 - t0
@@ -366,6 +370,7 @@ def train_step(cfg, B=8, S=128, T=64, reps=3):
     return {"config": f"{cfg.name}, {B} x {S} rows, {T} targets per sequence, backward over all {nl - 1} "
                       "layers below the Softmax with every update",
             "forward_ms": round(fwd_ms, 3), "backward_ms": round(bwd_ms, 3),
+            "loss": [round(x, 6) for x in losses],
             "backward_alg_gflop": round(flops / 1e9, 2),
             "backward_tflops": round(flops / (bwd_ms / 1e3) / 1e12, 3)}
 

@@ -77,6 +77,8 @@ extern "C" {
                          out_padding_mask: *mut u32) -> c_int;
     pub fn mitok_predict_targets(net: *mut MitokNetwork, ids: *const u32, lens: *const u32, batch: u32, seq: u32,
                                  target_rows: u32, out_probs: *mut c_double, out_padding_mask: *mut u32) -> c_int;
+    pub fn mitok_cross_entropy_loss(net: *mut MitokNetwork, targets: *const u32, target_lens: *const u32, batch: u32,
+                                    max_t: u32, out_loss: *mut c_double) -> c_int;
     pub fn mitok_forward_layers(net: *mut MitokNetwork, first: u32, last: u32, inp: *const c_double,
                                 padding_mask: *const u32, batch: u32, seq: u32, time_steps: *const u32,
                                 forward_only: c_int, out: *mut c_double) -> c_int;
@@ -310,6 +312,22 @@ impl Network {
             .collect();
         let m = mask.chunks(so as usize).map(|r| r.to_vec()).collect();
         Ok((probs, m))
+    }
+
+    /// cross_entropy_loss_batch (transformer_network.rs:662-711) of the softmax
+    /// output the last predict_targets left on the device: train's loss
+    /// (:81) without the probabilities crossing PCIe.
+    pub fn cross_entropy_loss(&mut self, targets: &[Vec<u32>]) -> Result<Complex<f64>, MitokError> {
+        let b = targets.len() as u32;
+        let t = targets.iter().map(|r| r.len()).max().unwrap_or(0).max(1) as u32;
+        let tlens: Vec<u32> = targets.iter().map(|r| r.len() as u32).collect();
+        let mut flat = vec![1u32; (b * t) as usize];
+        for (i, r) in targets.iter().enumerate() {
+            flat[i * t as usize..i * t as usize + r.len()].copy_from_slice(r);
+        }
+        let mut out = [0f64; 2];
+        check(unsafe { mitok_cross_entropy_loss(self.raw, flat.as_ptr(), tlens.as_ptr(), b, t, out.as_mut_ptr()) })?;
+        Ok(Complex::new(out[0], out[1]))
     }
 
     /// backward (transformer_network.rs:506-636) over `n_layers` layers below

@@ -128,9 +128,23 @@ int mitok_predict(mitok_network* net, const uint32_t* ids, const uint32_t* lens,
  * target rows on (wavelet_discrete_layer.rs:102-134, separate_input_target
  * :233-279), so seq' = mitok_seq_out_len(seq - target_rows) + target_rows per
  * wavelet layer.  With a wavelet layer and target_rows > 0 every sequence
- * must be unpadded (lens[b] == seq; the reference panics otherwise). */
+ * must be unpadded (lens[b] == seq; the reference panics otherwise).
+ * out_probs [batch][seq'][vocab] or NULL: the softmax output then stays on the
+ * device, where mitok_cross_entropy_loss and mitok_backward read it. */
 int mitok_predict_targets(mitok_network* net, const uint32_t* ids, const uint32_t* lens, uint32_t batch, uint32_t seq,
                           uint32_t target_rows, double* out_probs, uint32_t* out_padding_mask);
+/* cross_entropy_loss_batch (transformer_network.rs:662-711), which train
+ * (:81) computes on predict's softmax output, computed on the device from the
+ * output the last stateless predict left there, so the [batch][seq'][vocab]
+ * probabilities need not cross PCIe.  targets [batch][max_t] (target_lens[b]
+ * used of each row, max_t <= 8192), the same arrays mitok_backward takes.
+ * out_loss[2] = the complex loss (re, im): per sequence the mean of
+ * -ln(p + 1e-15) over its non-PAD targets (p at row seq' - len - 1 + t),
+ * then the mean over the batch.  MITOK_ERR_ARG where the reference would
+ * panic (a target id >= vocab, fewer than len + 1 rows); the forward pass
+ * stays valid for mitok_backward. */
+int mitok_cross_entropy_loss(mitok_network* net, const uint32_t* targets, const uint32_t* target_lens, uint32_t batch,
+                             uint32_t max_t, double* out_loss);
 
 /* Layers [first, last) on hidden states: in [batch][seq][dim_in] complex,
  * out [batch][seq][dim_out] complex; padding_mask [batch][seq] or NULL (all 1).

@@ -78,6 +78,7 @@ def _load():
         "orc_forward_layers": (i32, [P, u32, u32, P, P, u32, u32, P, i32, P]),
         "orc_generate": (i32, [P, P, P, u32, u32, u32, P, P]),
         "orc_softmax_backward": (i32, [P, u32, u32, u32, P, P, u32, P]),
+        "orc_cross_entropy_loss_batch": (i32, [P, u32, u32, u32, P, P, u32, P]),
         "orc_linear_backward": (i32, [P, P, P, u32, u32, u32, u32, P, P, P]),
         "orc_linear_update": (i32, [P, P, u32, u32, P, P, u32, P, P, P, P, i32, f64, u32]),
         "orc_linear_backward_c": (i32, [P, P, P, u32, u32, u32, u32, P, P, P]),
@@ -187,6 +188,19 @@ def softmax_backward(P, targets, tlens=None) -> np.ndarray:
     G = np.empty_like(P)
     _check(lib().orc_softmax_backward(_ptr(P), B, S, V, _ptr(t), _ptr(tl), T, _ptr(G)))
     return G
+
+
+def cross_entropy_loss_batch(P, targets, tlens=None) -> complex:
+    """cross_entropy_loss_batch (transformer_network.rs:662-711) of the softmax
+    output P [B][S][V]: the complex loss train computes (:81)."""
+    P = np.ascontiguousarray(P, dtype=np.float64)
+    B, S, V = P.shape
+    t = np.ascontiguousarray(targets, dtype=np.uint32)
+    T = t.shape[1]
+    tl = np.full(B, T, np.uint32) if tlens is None else np.ascontiguousarray(tlens, dtype=np.uint32)
+    out = np.empty(2, np.float64)
+    _check(lib().orc_cross_entropy_loss_batch(_ptr(P), B, S, V, _ptr(t), _ptr(tl), T, _ptr(out)))
+    return complex(out[0], out[1])
 
 
 def linear_backward(X, G, W):

@@ -1353,6 +1353,39 @@ int orc_softmax_backward(const double* P, uint32_t B, uint32_t S, uint32_t V, co
   return ORC_OK;
 }
 
+/* cross_entropy_loss_batch (transformer_network.rs:662-676) and
+ * cross_entropy_loss (:678-711): per sequence, -ln(p + 1e-15) of each non-PAD
+ * target's probability at row len - target_len - 1 + t, summed in target
+ * order and divided by their count; then the sequences summed in order, as
+ * Complex<f64> with im 0, divided by the batch size.  out[2] = (re, im).
+ * The padding mask the reference passes is not read there (only counted). */
+int orc_cross_entropy_loss_batch(const double* P, uint32_t B, uint32_t S, uint32_t V, const uint32_t* targets,
+                                 const uint32_t* tlens, uint32_t T, double* out) {
+  if (!P || !targets || !tlens || !out || !B || !S || !V) return fail(ORC_ERR_ARG, "bad arguments");
+  double re = 0.0, im = 0.0;
+  for (uint32_t b = 0; b < B; ++b) {
+    const uint32_t tl = tlens[b];
+    if (tl > T) return fail(ORC_ERR_ARG, "target length %u > %u", tl, T);
+    /* seq_ind_start = predictions.len() - target_len - 1 in usize (:692) */
+    if ((uint64_t)tl + 1 > S) return fail(ORC_ERR_ARG, "sequence %u: %u targets need more than %u rows", b, tl, S);
+    const uint32_t start = S - tl - 1, end = S - 1;
+    double loss = 0.0, count = 0.0;
+    for (uint32_t t = 0; t < tl; ++t) {
+      const uint32_t tc = targets[(size_t)b * T + t];
+      if (tc == 1) continue; /* :697-699 */
+      const uint32_t s = start + t;
+      if (s >= end) break; /* :701-704 */
+      if (tc >= V) return fail(ORC_ERR_ARG, "target token %u exceeds vocabulary %u", tc, V); /* indexing panics */
+      loss += -log(P[((size_t)b * S + s) * V + tc] + 1e-15);                               /* :706-708 */
+      count += 1.0;
+    }
+    re += loss / count; /* total_loss += f64 adds to the real part */
+  }
+  out[0] = re / (double)B;
+  out[1] = im / (double)B;
+  return ORC_OK;
+}
+
 int orc_linear_backward_c(const oc64* X, const oc64* Gin, const oc64* W, uint32_t B, uint32_t S, uint32_t d,
                           uint32_t V, oc64* dW, oc64* db, oc64* dX);
 

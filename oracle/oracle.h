@@ -129,6 +129,9 @@ int orc_generate(orc_net* net, const uint32_t* prompt, const uint32_t* lens, uin
  * (real; the reference stores it as Complex with im 0). */
 int orc_softmax_backward(const double* P, uint32_t B, uint32_t S, uint32_t V, const uint32_t* targets,
                          const uint32_t* tlens, uint32_t T, double* G);
+/* cross_entropy_loss_batch (transformer_network.rs:662-711) of P [B][S][V]; out[2] = (re, im) */
+int orc_cross_entropy_loss_batch(const double* P, uint32_t B, uint32_t S, uint32_t V, const uint32_t* targets,
+                                 const uint32_t* tlens, uint32_t T, double* out);
 /* LinearLayer::backward (linear_layer.rs:77-128), complex arm, grouped over
  * the batch (gradient_struct.rs:360-436): X [B][S][d] the layer's input,
  * G [B][S][V], W [d][V]; dW [d][V] = sum_b conj(X_b)^T G_b, db [V] =

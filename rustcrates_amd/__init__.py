@@ -54,6 +54,7 @@ SIGNATURES = {
     "mitok_reset": (_i32, [_P]),
     "mitok_predict": (_i32, [_P, _P, _P, _u32, _u32, _P, _i32, _i32, _P, _P]),
     "mitok_predict_targets": (_i32, [_P, _P, _P, _u32, _u32, _u32, _P, _P]),
+    "mitok_cross_entropy_loss": (_i32, [_P, _P, _P, _u32, _u32, _P]),
     "mitok_forward_layers": (_i32, [_P, _u32, _u32, _P, _P, _u32, _u32, _P, _i32, _P]),
     "mitok_generate": (_i32, [_P, _P, _P, _u32, _u32, _u32, _P, _P]),
     "mitok_prefill": (_i32, [_P, _P, _P, _u32, _u32, _P, _P]),
@@ -318,11 +319,15 @@ class Network:
         _check(self._lib.mitok_reset(self._h))
 
     # ---- forward paths ----
-    def predict(self, ids, lens=None, time_steps=None, forward_only=True, last_row_only=False, target_rows=0):
+    def predict(self, ids, lens=None, time_steps=None, forward_only=True, last_row_only=False, target_rows=0,
+                want_output=True):
         """predict (transformer_network.rs:315-492).  target_rows (a stateless
         pass, forward_only=False): the last T rows of every sequence are the
         targets, which a DiscreteWavelet layer passes on uncompressed
-        (wavelet_discrete_layer.rs:102-134; mitok_predict_targets)."""
+        (wavelet_discrete_layer.rs:102-134; mitok_predict_targets).
+        want_output=False (a stateless pass of all rows): the softmax output
+        stays on the device for cross_entropy_loss and backward, and the
+        first value returned is None."""
         ids = np.ascontiguousarray(ids, dtype=np.uint32)
         B, S = ids.shape
         lens = np.full(B, S, np.uint32) if lens is None else _u32_vec(lens, B, "lens")
@@ -332,16 +337,18 @@ class Network:
         T = int(target_rows)
         if T and (forward_only or last_row_only or time_steps is not None):
             raise ValueError("target_rows applies to a stateless pass of all rows only")
+        if not want_output and (forward_only or last_row_only or time_steps is not None):
+            raise ValueError("want_output=False applies to a stateless pass of all rows only")
         if T:
             So = S
             for w in self._wavelet_filters:
                 So = (So - T + w - 2 + ((So - T) % 2)) // 2 + T
         else:
             So = self.seq_out_len(S) if prompt_pass else S
-        out = np.empty((B, V) if last_row_only else (B, So, V), np.float64)
+        out = np.empty((B, V) if last_row_only else (B, So, V), np.float64) if want_output else None
         mask = np.empty((B, So), np.uint32)
         self._head_rows = None
-        if T:
+        if T or not want_output:
             _check(self._lib.mitok_predict_targets(self._h, _ptr(ids), _ptr(lens), B, S, T, _ptr(out), _ptr(mask)))
         else:
             _check(self._lib.mitok_predict(self._h, _ptr(ids), _ptr(lens), B, S, _ptr(ts), int(forward_only),
@@ -453,6 +460,19 @@ class Network:
         _check(self._lib.mitok_backward(self._h, _ptr(t), _ptr(tl), B, T, int(layers), int(bool(update)),
                                         float(learning_rate), int(time_step), _ptr(gx)))
         return gx
+
+    def cross_entropy_loss(self, targets, tlens=None):
+        """cross_entropy_loss_batch (transformer_network.rs:662-711) of the
+        softmax output the last stateless predict left on the device
+        (mitok_cross_entropy_loss); targets as backward takes them."""
+        t = np.ascontiguousarray(targets, dtype=np.uint32)
+        if t.ndim != 2:
+            raise ValueError(f"targets: shape {t.shape}, expected (batch, T)")
+        B, T = t.shape
+        tl = np.full(B, T, np.uint32) if tlens is None else _u32_vec(tlens, B, "tlens")
+        out = np.empty(2, np.float64)
+        _check(self._lib.mitok_cross_entropy_loss(self._h, _ptr(t), _ptr(tl), B, T, _ptr(out)))
+        return complex(out[0], out[1])
 
     def greedy_decoding(self, logits):
         logits = np.ascontiguousarray(logits, dtype=np.float64)

@@ -135,6 +135,11 @@ struct TrainStep {
 // G[r][c] (complex, im 0) = tgt[r] < 0 ? 0 : (P[r][c] - [c == tgt[r]]) / norm[r / S]
 void softmax_grad(hipStream_t st, const double* P, int rows, int V, const int* tgt, const double* norm, int S,
                   double2* G);
+// cross_entropy_loss_batch of P [B][S][V] for targets [B][T] (tlen[b] each):
+// part [B] the sequences' losses, out [2] the batch loss (re, im); T <= CE_MAX_T
+constexpr int CE_MAX_T = 8192;
+void cross_entropy(hipStream_t st, const double* P, int B, int S, int V, const uint32_t* tgt, const uint32_t* tlen,
+                   int T, double* part, double* out);
 // G = mask[r] ? dH * conj(GELU'(Z)) : 0 (layer.rs:181-192, derivative.rs:48-84); mask may be null (all rows)
 void gelu_backward(hipStream_t st, const double2* dH, const double2* Z, const uint32_t* mask, long rows, int F,
                    double2* G);

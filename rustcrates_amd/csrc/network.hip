@@ -376,6 +376,7 @@ struct mitok_network {
   std::vector<std::unique_ptr<mitok::DevBuf>> tr_in, tr_cat;
   mitok::DevBuf tr_g, tr_xh, tr_wh, tr_dw, tr_db, tr_ga, tr_gb, tr_tgt, tr_norm;
   mitok::DevBuf tr_z, tr_h, tr_g1, tr_dh, tr_qkv, tr_dqkv, tr_A, tr_dA, tr_pg, tr_eid, tr_est, tr_eocc, tr_bsum;
+  mitok::DevBuf ce_buf;  // mitok_cross_entropy_loss: targets, lengths, per-sequence losses, the result
 };
 
 namespace mitok {
@@ -2090,9 +2091,12 @@ static void end_call(Net* n, const Spec& sp, const uint32_t* lens) {
   }
 }
 
-int mitok_predict(mitok_network* n, const uint32_t* ids, const uint32_t* lens, uint32_t B, uint32_t S,
-                  const uint32_t* time_steps, int forward_only, int last_row_only, double* out, uint32_t* out_mask) {
-  if (!n || !ids || !lens || !out) return fail(ERR_ARG, "null argument");
+// out may be null only for a stateless pass of every row (mitok_predict_targets
+// without out_probs): the softmax output then stays on the device
+static int predict_impl(mitok_network* n, const uint32_t* ids, const uint32_t* lens, uint32_t B, uint32_t S,
+                        const uint32_t* time_steps, int forward_only, int last_row_only, double* out,
+                        uint32_t* out_mask) {
+  if (!n || !ids || !lens || (!out && (forward_only || last_row_only))) return fail(ERR_ARG, "null argument");
   TRY(validate_batch(lens, B, S));
   TRY(check_stack(n));
   TRY(set_device(n));
@@ -2118,7 +2122,7 @@ int mitok_predict(mitok_network* n, const uint32_t* ids, const uint32_t* lens, u
     HIP_TRY(hipMemcpyAsync(out, sp.out_re, cnt * sizeof(double), hipMemcpyDeviceToHost, n->stream));
     HIP_TRY(hipStreamSynchronize(n->stream));
   } else if (!last_row_only) {  // every row: straight into the caller's buffer
-    HIP_TRY(hipMemcpyAsync(out, sp.out_prob, orows * V * sizeof(double), hipMemcpyDeviceToHost, n->stream));
+    if (out) HIP_TRY(hipMemcpyAsync(out, sp.out_prob, orows * V * sizeof(double), hipMemcpyDeviceToHost, n->stream));
     HIP_TRY(hipStreamSynchronize(n->stream));
   } else {
     std::vector<double> all(orows * V);
@@ -2135,13 +2139,52 @@ int mitok_predict(mitok_network* n, const uint32_t* ids, const uint32_t* lens, u
   return OK;
 }
 
+int mitok_predict(mitok_network* n, const uint32_t* ids, const uint32_t* lens, uint32_t B, uint32_t S,
+                  const uint32_t* time_steps, int forward_only, int last_row_only, double* out, uint32_t* out_mask) {
+  if (!out) return fail(ERR_ARG, "null argument");
+  return predict_impl(n, ids, lens, B, S, time_steps, forward_only, last_row_only, out, out_mask);
+}
+
 int mitok_predict_targets(mitok_network* n, const uint32_t* ids, const uint32_t* lens, uint32_t B, uint32_t S,
                           uint32_t target_rows, double* out_probs, uint32_t* out_mask) {
   if (!n) return fail(ERR_ARG, "null network");
   n->train_T = target_rows;
-  const int rc = mitok_predict(n, ids, lens, B, S, nullptr, 0, 0, out_probs, out_mask);
+  const int rc = predict_impl(n, ids, lens, B, S, nullptr, 0, 0, out_probs, out_mask);
   n->train_T = 0;
   return rc;
+}
+
+int mitok_cross_entropy_loss(mitok_network* n, const uint32_t* targets, const uint32_t* tlens, uint32_t B, uint32_t T,
+                             double* out_loss) {
+  if (!n || !targets || !tlens || !B || !T || !out_loss) return fail(ERR_ARG, "bad arguments");
+  if (!n->head_valid) return fail(ERR_STATE, "no stateless (forward_only = 0) predict whose output to score");
+  if (B != n->head_B) return fail(ERR_ARG, "batch %u != the forward pass's %u", B, n->head_B);
+  if (T > (uint32_t)CE_MAX_T) return fail(ERR_ARG, "%u targets per sequence: at most %d", T, CE_MAX_T);
+  const uint32_t V = n->layers[n->layers.size() - 2]->d_out, S = n->head_S;
+  // what cross_entropy_loss (transformer_network.rs:674-711) would panic on
+  for (uint32_t b = 0; b < B; ++b) {
+    const uint32_t tl = tlens[b];
+    if (tl > T) return fail(ERR_ARG, "target length %u > %u", tl, T);
+    if ((uint64_t)tl + 1 > (uint64_t)S) return fail(ERR_ARG, "sequence %u: %u targets need more than %u rows", b, tl, S);
+    for (uint32_t t = 0; t < tl; ++t) {
+      const uint32_t tc = targets[(size_t)b * T + t];
+      if (tc != 1u && tc >= V) return fail(ERR_ARG, "target token %u exceeds vocabulary %u", tc, V);
+    }
+  }
+  TRY(set_device(n));
+  const size_t tb = ((size_t)B * T + B) * sizeof(uint32_t), tb8 = (tb + 7) & ~(size_t)7;
+  TRY(n->ce_buf.reserve(tb8 + ((size_t)B + 2) * sizeof(double)));  // no graph holds it
+  char* base = (char*)n->ce_buf.p;
+  uint32_t* tgt_d = (uint32_t*)base;
+  uint32_t* tlen_d = tgt_d + (size_t)B * T;
+  double* part = (double*)(base + tb8);
+  HIP_TRY(hipMemcpyAsync(tgt_d, targets, (size_t)B * T * sizeof(uint32_t), hipMemcpyHostToDevice, n->stream));
+  HIP_TRY(hipMemcpyAsync(tlen_d, tlens, (size_t)B * sizeof(uint32_t), hipMemcpyHostToDevice, n->stream));
+  cross_entropy(n->stream, n->probs.as<double>(), (int)B, (int)S, (int)V, tgt_d, tlen_d, (int)T, part, part + B);
+  HIP_TRY(hipGetLastError());
+  HIP_TRY(hipMemcpyAsync(out_loss, part + B, 2 * sizeof(double), hipMemcpyDeviceToHost, n->stream));
+  HIP_TRY(hipStreamSynchronize(n->stream));
+  return OK;
 }
 
 // `bytes` of device memory at `p` inside one allocation of the network's

@@ -178,6 +178,51 @@ void softmax_grad(hipStream_t st, const double* P, int rows, int V, const int* t
   if (rows > 0) MITOK_LAUNCH(k_softmax_grad, dim3(rows), dim3(256), 0, st, P, V, tgt, norm, S, G);
 }
 
+// cross_entropy_loss_batch (transformer_network.rs:662-711) on the softmax
+// output P [B][S][V].  Block b: its targets' terms -ln(p + 1e-15), p at row
+// S - tl - 1 + t, are formed in parallel into LDS (PAD targets, id 1, marked
+// skipped), then one thread sums them in target order and divides by their
+// count (cross_entropy_loss, :674-711; no target is left out by its
+// `seq_ind >= end_ind` break, since the rows end at S - 2).  part[b] holds it.
+__global__ __launch_bounds__(256) void k_ce_seq(const double* __restrict__ P, int S, int V,
+                                                const uint32_t* __restrict__ tgt, const uint32_t* __restrict__ tlen,
+                                                int T, double* __restrict__ part) {
+  extern __shared__ double lp[];  // [T]
+  const int b = blockIdx.x, tl = (int)tlen[b];
+  const int start = S - tl - 1;
+  for (int t = threadIdx.x; t < tl; t += 256) {
+    const uint32_t tc = tgt[(long)b * T + t];
+    lp[t] = tc == 1u ? NAN : -log(P[((long)b * S + start + t) * V + tc] + 1e-15);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double loss = 0.0, count = 0.0;
+    for (int t = 0; t < tl; ++t)
+      if (tgt[(long)b * T + t] != 1u) {
+        loss += lp[t];
+        count += 1.0;
+      }
+    part[b] = loss / count;
+  }
+}
+
+// the batch: sum of the sequences' losses in order, divided by B, as the
+// complex (sum / B, 0 / B) the reference returns
+__global__ void k_ce_batch(const double* __restrict__ part, int B, double* __restrict__ out) {
+  if (threadIdx.x != 0) return;
+  double re = 0.0;
+  for (int b = 0; b < B; ++b) re += part[b];
+  out[0] = re / (double)B;
+  out[1] = 0.0 / (double)B;
+}
+
+void cross_entropy(hipStream_t st, const double* P, int B, int S, int V, const uint32_t* tgt, const uint32_t* tlen,
+                   int T, double* part, double* out) {
+  if (B <= 0) return;
+  MITOK_LAUNCH(k_ce_seq, dim3(B), dim3(256), (size_t)T * sizeof(double), st, P, S, V, tgt, tlen, T, part);
+  MITOK_LAUNCH(k_ce_batch, dim3(1), dim3(64), 0, st, part, B, out);
+}
+
 void conj_transpose(hipStream_t st, const double2* in, long R, long C, double2* out) {
   const dim3 grid((unsigned)((C + 15) / 16), (unsigned)((R + 15) / 16));
   if (R > 0 && C > 0) MITOK_LAUNCH(k_conj_transpose, grid, dim3(256), 0, st, in, R, C, out);

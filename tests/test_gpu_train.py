@@ -104,6 +104,44 @@ def test_backward_head_errors():
     g.close()
 
 
+@pytest.mark.parametrize("V,d,lens,T", [(40, 8, [7, 5, 7], 3), (4000, 64, [24, 17, 24, 9], 6)])
+def test_device_cross_entropy_loss(V, d, lens, T):
+    """cross_entropy_loss_batch (transformer_network.rs:662-711) on the
+    device-resident softmax output (mitok_cross_entropy_loss) against the
+    checker on the same probabilities: ragged target lengths, PAD targets
+    skipped.  A pass that keeps its output on the device (want_output=False)
+    gives the same loss, and backward after it the same gradient."""
+    rng = np.random.default_rng(V + 7)
+    table = rng.standard_normal((V, d)) + 1j * rng.standard_normal((V, d))
+    W = 0.2 * (rng.standard_normal((d, V)) + 1j * rng.standard_normal((d, V)))
+    b = 0.1 * (rng.standard_normal(V) + 1j * rng.standard_normal(V))
+    B, S = len(lens), max(lens)
+    ids = seeded.prompts(90 + V, lens, V)
+    targets = rng.integers(0, V, size=(B, T)).astype(np.uint32)
+    targets[0, 1] = 1
+    targets[1, 0] = 1
+    tlens = [min(T, S - 1), 2] + [min(T, S - 1)] * (B - 2)  # sequence 1: one PAD and one counted target
+    with ra.Network(0) as g:
+        head_net(g, table, W, b)
+        P, _ = g.predict(ids, lens=lens, forward_only=False)
+        L = g.cross_entropy_loss(targets, tlens)
+        want = oracle.cross_entropy_loss_batch(P, targets, tlens)
+        log(f"loss V={V}: gpu {L.real:.17g} checker {want.real:.17g}")
+        assert L.imag == 0.0 and abs(L - want) <= 1e-14 * abs(want)
+        dx1 = g.backward_head(targets, tlens, update=False)
+        out, _ = g.predict(ids, lens=lens, forward_only=False, want_output=False)
+        assert out is None
+        assert g.cross_entropy_loss(targets, tlens) == L
+        assert np.array_equal(g.backward_head(targets, tlens, update=False), dx1)
+        with pytest.raises(ra.MitokError, match="exceeds vocabulary"):
+            g.cross_entropy_loss(np.full((B, 2), V, np.uint32))
+        with pytest.raises(ra.MitokError, match="need more than"):
+            g.cross_entropy_loss(np.zeros((B, S), np.uint32))
+        g.predict(ids, lens=lens, forward_only=True)  # a cached pass leaves nothing to score
+        with pytest.raises(ra.MitokError, match="no stateless"):
+            g.cross_entropy_loss(targets, tlens)
+
+
 def ffn_net(net, table, W1, b1, W2, b2, Wv, bv):
     V, d = table.shape
     net.add_embedding(V, d, table)
@@ -390,6 +428,11 @@ def test_reference_default_stack_training_matches_checker(lr):
         o = oracle_net()
         Pg, mg = g.predict(ids, forward_only=False, target_rows=T)
         Po, mo = o.predict(ids, forward_only=False, target_rows=T)
+        # train's loss (transformer_network.rs:81) on the device, between the
+        # forward pass and backward, which must still see that pass
+        Lg = g.cross_entropy_loss(targets, tlens)
+        assert abs(Lg - oracle.cross_entropy_loss_batch(Pg, targets, tlens)) <= 1e-14 * abs(Lg)
+        assert abs(Lg - oracle.cross_entropy_loss_batch(Po, targets, tlens)) <= TOL * abs(Lg)
         X = [None] * nl
         X[1] = np.stack([[p["table"][i] if i != 1 else np.zeros(d) for i in row] for row in ids])
         X[2] = o.forward_layers(1, 2, X[1], mask=np.ones((B, S), np.uint32), forward_only=False, target_rows=T)

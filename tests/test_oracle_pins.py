@@ -1106,3 +1106,55 @@ def test_norm_backward_reference_gradient_check():
                 g += unit * (loss(xp) - loss(xm)) / (2 * eps)
             rel = abs(g - an[idx]) / max(abs(g), abs(an[idx]), 1e-5)
             assert rel < 1e-5, (idx, g, an[idx], rel)
+
+
+def test_cross_entropy_loss_closed_forms_rows_and_pad_targets():
+    """cross_entropy_loss_batch (transformer_network.rs:662-711).  Every
+    probability 1/V: the loss is -ln(1/V + 1e-15), imaginary part 0.  A hand
+    case whose target rows hold e^-1, e^-2, e^-3 and every other entry 1/2:
+    sequence 0 (targets 2, PAD) costs 1 with one counted target, sequence 1
+    (targets 3, 4 on rows S - 3, S - 2) costs (2 + 3) / 2, the batch their mean
+    1.75; a row one off, a PAD counted or a sum instead of a mean each give
+    another value.  A sequence of PAD targets only is 0 / 0 (NaN)."""
+    B, S, V = 3, 6, 7
+    L = oracle.cross_entropy_loss_batch(np.full((B, S, V), 1.0 / V), np.array([[2, 3], [5, 6], [0, 2]], np.uint32))
+    want = -math.log(1.0 / V + 1e-15)
+    assert L.imag == 0.0 and abs(L.real - want) <= 4e-16 * want
+
+    P = np.full((2, 4, 5), 0.5)
+    P[0, 1, 2] = math.exp(-1.0)
+    P[1, 1, 3] = math.exp(-2.0)
+    P[1, 2, 4] = math.exp(-3.0)
+    L = oracle.cross_entropy_loss_batch(P, np.array([[2, 1], [3, 4]], np.uint32))
+    assert L.imag == 0.0 and abs(L.real - 1.75) < 1e-13, L
+    # ragged target lengths: sequence 1 with one target sits on row S - 2
+    P2 = np.full((2, 4, 5), 0.5)
+    P2[0, 1, 2] = math.exp(-1.0)
+    P2[1, 2, 3] = math.exp(-4.0)
+    L = oracle.cross_entropy_loss_batch(P2, np.array([[2, 1], [3, 0]], np.uint32), tlens=[2, 1])
+    assert abs(L.real - 2.5) < 1e-13, L
+    assert math.isnan(oracle.cross_entropy_loss_batch(P, np.array([[1, 1], [3, 4]], np.uint32)).real)
+    with pytest.raises(oracle.OracleError):  # seq_ind_start would underflow: the reference panics
+        oracle.cross_entropy_loss_batch(P, np.array([[2, 2, 2, 2], [3, 3, 3, 3]], np.uint32))
+
+
+def test_cross_entropy_loss_gradient_is_the_softmax_backward():
+    """The loss the reference's gradient tests differentiate numerically
+    (test_self_attention_layer_with_loss.rs:62-72): central differences of
+    cross_entropy_loss_batch(softmax(Re Y)) in every logit equal the
+    SoftmaxLayer::backward gradient (softmax_output_layer.rs:67-145), so the
+    two share their rows, PAD handling and normalizer B * count."""
+    rng = np.random.default_rng(17)
+    B, S, V = 3, 5, 6
+    Y = rng.standard_normal((B, S, V))
+    targets = np.array([[2, 1, 4], [0, 5, 3], [4, 4, 1]], np.uint32)
+    tl = np.array([3, 2, 3], np.uint32)
+    G = oracle.softmax_backward(_softmax_re(Y), targets, tl)
+    h = 1e-6
+    for idx in np.ndindex(Y.shape):
+        yp, ym = Y.copy(), Y.copy()
+        yp[idx] += h
+        ym[idx] -= h
+        fd = (oracle.cross_entropy_loss_batch(_softmax_re(yp), targets, tl).real
+              - oracle.cross_entropy_loss_batch(_softmax_re(ym), targets, tl).real) / (2 * h)
+        assert abs(fd - G[idx]) < 1e-8, (idx, fd, G[idx])

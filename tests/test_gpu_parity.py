@@ -293,6 +293,41 @@ def test_c3_batch32_equals_batch1_runs():
         _check_deep(f"c3 b32 seq {b} vs b1", ids[b:b + 1], lg[:, b:b + 1], i1, l1, floor)
 
 
+def test_c3_well_conditioned_meets_the_strict_bar():
+    """Config 3's exact shapes and depth, with the imaginary part of every
+    weight of the 6 blocks scaled by 0.3 (the embedding table and the vocab
+    Linear as seeded).  No complex
+    LayerNorm variance then cancels, the checker's own valid summation orders
+    agree to about 1e-12, and the GPU meets north_star's bar as stated: ids
+    bit-exact and logits within 1e-9 max relative error (REL_TOL) over all
+    128 generated tokens, at batch 1 (the resident loop) and for a ragged
+    batch of three (the launch-per-operation plan)."""
+    from conftest import build_explicit, seeded_tensors
+
+    cfg = configs.C3
+    t = seeded_tensors(cfg)
+    for k, layer in enumerate(t):
+        for name, v in layer.items():
+            if 0 < k < len(t) - 1 and np.iscomplexobj(v):  # no Norm follows the vocab Linear
+                layer[name] = v.real + 0.3j * v.imag
+    g, o = build_explicit(ra.Network(0), cfg, t), build_explicit(oracle.Network(), cfg, t)
+    for lens in ([128], [128, 77, 100]):
+        prompt = seeded.prompts(3, lens, cfg.vocab)
+        log(f"c3 well-conditioned lens {lens}: gpu generate")
+        ig, lg = g.generate(prompt, lens=lens, n_new=128, want_logits=True)
+        log("oracle generate")
+        io, lo = o.generate(prompt, lens=lens, n_new=128, want_logits=True)
+        floor = oracle_noise_floor(o, prompt[:1], lens[:1], 16, lo[:16, :1])
+        err, nerr = max_rel_err(lg, lo), normwise_rel_err(lg, lo)
+        log(f"  ids match {np.array_equal(ig, io)}; elementwise {err:.3e} (checker's own spread {floor[0]:.3e}), "
+            f"normwise {nerr:.3e}")
+        assert floor[0] < 1e-11
+        assert np.array_equal(ig, io)
+        assert err <= REL_TOL
+    g.close()
+    o.close()
+
+
 # ---------------------------------------------------------------------------
 # error paths (reference panics -> status codes)
 # ---------------------------------------------------------------------------

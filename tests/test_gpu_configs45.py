@@ -12,6 +12,11 @@ oracle's noise floor, as for config 3) and two more sequences against their
 own batch-1 runs (ids).  Config 5: its layer at the full 1920-token prompt
 against the oracle, and the full model's two decode plans against each other.
 
+With the imaginary parts of the block weights scaled by 0.3 (no LayerNorm
+variance cancels), both full configurations against the oracle at REL_TOL
+itself: config 4's batch of 64 (three sequences) and config 5's 1920-token
+prompt at full depth.
+
 Bar: ids bit-exact; logits within REL_TOL or NOISE_FACTOR x the noise floor
 (conftest).
 """
@@ -116,6 +121,73 @@ def test_config4_full_batch64_vs_oracle():
         log(f"  seq {b}: ids match its batch-1 run {np.array_equal(ids[b:b + 1], i1)}, "
             f"normwise {normwise_rel_err(lg[:, b:b + 1], l1):.3e}")
         assert np.array_equal(ids[b:b + 1], i1)
+
+
+def test_config4_well_conditioned_meets_the_strict_bar():
+    """Config 4 at full depth (12 layers, d 768, vocab 32000) and its full
+    ragged batch of 64, with the imaginary part of every block weight scaled
+    by 0.3 (embedding table and vocab Linear as seeded), so no LayerNorm's
+    complex variance cancels: the checker's valid summation orders agree to
+    about 3e-12 where the seeded weights spread 1.7e-2.  Sequences 0, 37 and
+    63 against the checker at north_star's bar as stated: ids bit-exact,
+    logits within REL_TOL (1e-9) max relative error."""
+    from conftest import build_explicit, seeded_tensors
+
+    w = configs.WORKLOADS["c4"]
+    cfg, n_new = w.model, 12
+    t = seeded_tensors(cfg)
+    for k, layer in enumerate(t):
+        for name, v in layer.items():
+            if 0 < k < len(t) - 1 and np.iscomplexobj(v):  # no Norm follows the vocab Linear
+                layer[name] = v.real + 0.3j * v.imag
+    lens = configs.prompt_lengths(w)
+    prompt = seeded.prompts(w.prompt_seed, lens, cfg.vocab, max_len=w.prompt_len)
+    g, o = build_explicit(ra.Network(0), cfg, t), build_explicit(oracle.Network(), cfg, t)
+    log("config 4 well-conditioned: batch 64")
+    ids, lg = g.generate(prompt, lens=lens, n_new=n_new, want_logits=True)
+    for b in (0, 37, 63):
+        pb, lb = prompt[b:b + 1, :lens[b]], [lens[b]]
+        io, lo = o.generate(pb, lens=lb, n_new=n_new, want_logits=True)
+        err, nerr = max_rel_err(lg[:, b:b + 1], lo), normwise_rel_err(lg[:, b:b + 1], lo)
+        log(f"  seq {b} (prompt {lens[b]}): ids match {np.array_equal(ids[b:b + 1], io)}; elementwise {err:.3e}, "
+            f"normwise {nerr:.3e}")
+        assert np.array_equal(ids[b:b + 1], io)
+        assert err <= REL_TOL
+    g.close()
+    o.close()
+
+
+def test_config5_well_conditioned_full_prompt_meets_the_strict_bar():
+    """Config 5 at full depth and its full 1920-token prompt (12 layers,
+    context 2048), the block weights' imaginary parts scaled by 0.3 as above:
+    the checker's summation orders agree to about 2e-12 where the seeded
+    weights' 12 layers leave its orders unrelated.  Sequence 0 of the
+    workload's batch of 4 against the checker, 4 generated tokens: ids
+    bit-exact, logits within REL_TOL."""
+    from conftest import build_explicit, seeded_tensors
+
+    w = configs.WORKLOADS["c5"]
+    cfg, n_new = w.model, 4
+    log("config 5 well-conditioned: tensors")
+    t = seeded_tensors(cfg)
+    for k, layer in enumerate(t):
+        for name, v in layer.items():
+            if 0 < k < len(t) - 1 and np.iscomplexobj(v):  # no Norm follows the vocab Linear
+                layer[name] = v.real + 0.3j * v.imag
+    prompt = seeded.prompts(w.prompt_seed, [w.prompt_len] * w.batch, cfg.vocab, max_len=w.prompt_len)
+    g = build_explicit(ra.Network(0), cfg, t)
+    log("gpu generate, batch 4")
+    ids, lg = g.generate(prompt, n_new=n_new, want_logits=True)
+    g.close()
+    o = build_explicit(oracle.Network(), cfg, t)
+    del t
+    log("checker generate, sequence 0")
+    io, lo = o.generate(prompt[:1], n_new=n_new, want_logits=True)
+    o.close()
+    err, nerr = max_rel_err(lg[:, :1], lo), normwise_rel_err(lg[:, :1], lo)
+    log(f"  seq 0: ids match {np.array_equal(ids[:1], io)}; elementwise {err:.3e}, normwise {nerr:.3e}")
+    assert np.array_equal(ids[:1], io)
+    assert err <= REL_TOL
 
 
 def test_config5_prompt1920_one_layer_vs_oracle():

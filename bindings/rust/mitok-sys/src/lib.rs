@@ -252,6 +252,28 @@ impl Network {
         Ok(s)
     }
 
+    /// The entries of the layer list (LayerEnum order).
+    pub fn num_layers(&self) -> u32 {
+        let n = unsafe { mitok_num_layers(self.raw) };
+        n.max(0) as u32
+    }
+
+    /// predict_targets with the softmax output left on the device, where
+    /// cross_entropy_loss and backward read it: only the ids cross PCIe.
+    pub fn forward_targets(&mut self, batch_ids: &[Vec<u32>], target_rows: u32) -> Result<(), MitokError> {
+        let b = batch_ids.len() as u32;
+        let s = batch_ids.iter().map(|r| r.len()).max().unwrap_or(0) as u32;
+        let lens: Vec<u32> = batch_ids.iter().map(|r| r.len() as u32).collect();
+        let mut ids = vec![1u32; (b * s) as usize];
+        for (i, r) in batch_ids.iter().enumerate() {
+            ids[i * s as usize..i * s as usize + r.len()].copy_from_slice(r);
+        }
+        check(unsafe {
+            mitok_predict_targets(self.raw, ids.as_ptr(), lens.as_ptr(), b, s, target_rows, std::ptr::null_mut(),
+                                  std::ptr::null_mut())
+        })
+    }
+
     /// `predict` on right-padded ids: Re-logits [batch][seq'][vocab] when
     /// `forward_only` (the KV caches advance), else the softmax output; and the
     /// padding mask [batch][seq'].

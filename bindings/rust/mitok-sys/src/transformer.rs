@@ -18,6 +18,7 @@
 //!     (:293-297).
 
 use crate::{MitokError, Network};
+use num_complex::Complex;
 
 pub const MAX_CONTEXT_WINDOW_SIZE: usize = 512;
 pub const MAX_NEW_TOKENS: usize = 21;
@@ -95,4 +96,22 @@ pub fn generate_ids_device(net: &mut Network, prompt: &[u32], eos: u32) -> Resul
         id = net.decode_step(None, None)?;
     }
     Ok(out)
+}
+
+/// One batch of `train` (transformer_network.rs:73-104) on the device: the
+/// TRAINING predict of the concatenated input + target ids (the last
+/// `target_ids[b].len()` ids of each row; a DiscreteWavelet layer passes them
+/// on uncompressed and needs unpadded rows, as the reference does), its loss
+/// (cross_entropy_loss_batch, :81), then backward over every layer with
+/// update_parameters at time_step = epoch (:100).  Returns the loss.  The
+/// epoch loop, the loss bookkeeping, the learning-rate schedule and the sled
+/// checkpoints of `train` stay on the host around it.
+pub fn train_batch_device(net: &mut Network, batch_ids: &[Vec<u32>], target_ids: &[Vec<u32>], epoch: u32,
+                          learning_rate: f64) -> Result<Complex<f64>, MitokError> {
+    let t = target_ids.iter().map(|r| r.len()).max().unwrap_or(0) as u32;
+    net.forward_targets(batch_ids, t)?;
+    let loss = net.cross_entropy_loss(target_ids)?;
+    let below_softmax = net.num_layers().saturating_sub(1);
+    net.backward(target_ids, below_softmax, true, learning_rate, epoch)?;
+    Ok(loss)
 }

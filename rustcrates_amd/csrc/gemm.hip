@@ -301,9 +301,80 @@ __global__ __launch_bounds__(256) void k_rowops(RowOps ro, int K, double2* __res
   }
 }
 
+// The chunk combine alone for long caches, one 64-lane block per (row,
+// head): out[m][h*dh + e] = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M).
+// The weights and their sum are ro_prepare's (same lanes, same reductions)
+// and each element sums its chunks in order, so the rows equal those
+// rowops_att forms; there one block per row requests its chunks eight at a
+// time, which at thousands of keys (64 chunks per head) is eight dependent
+// round trips in one CU.
+constexpr int COMBINE_BATCH = 16;
+__global__ __launch_bounds__(64) void k_attn_combine(AttnSplit a, double2* __restrict__ out, long ldo) {
+  __shared__ double wts[256];  // nsplit <= 256
+  const int m = blockIdx.x / a.H, h = blockIdx.x - m * a.H;
+  const int lane = threadIdx.x;
+  const int ns = (a.kv_len[m] + 1 + a.CH - 1) / a.CH;
+  const long base = ((long)m * a.H + h) * a.nsplit;
+  double vm[4], vl[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int sidx = lane + 64 * j;
+    const bool in = sidx < a.nsplit;
+    vm[j] = in ? a.pm[base + sidx] : -INFINITY;
+    vl[j] = in ? a.pl[base + sidx] : 0.0;
+  }
+  double mx = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    if (lane + 64 * j < ns) mx = fmax(mx, vm[j]);
+  mx = wave_max(mx);
+  double l = 0.0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int sidx = lane + 64 * j;
+    if (sidx < ns) {
+      const double w = exp(vm[j] - mx);
+      wts[sidx] = w;
+      l += vl[j] * w;
+    }
+  }
+  l = wave_sum(l);
+  __syncthreads();
+  for (int e = lane; e < a.dh; e += 64) {
+    double2 o = make_double2(0.0, 0.0);
+    for (int s0 = 0; s0 < ns; s0 += COMBINE_BATCH) {
+      double2 t[COMBINE_BATCH];
+#pragma unroll
+      for (int q = 0; q < COMBINE_BATCH; ++q) t[q] = a.po[(base + min(s0 + q, ns - 1)) * a.dh + e];
+#pragma unroll
+      for (int q = 0; q < COMBINE_BATCH; ++q)
+        if (s0 + q < ns) {
+          o.x += t[q].x * wts[s0 + q];
+          o.y += t[q].y * wts[s0 + q];
+        }
+    }
+    out[(long)m * ldo + (long)h * a.dh + e] = make_double2(o.x / l, o.y / l);
+  }
+}
+
 void rowops_apply(hipStream_t st, int M, int K, const RowOps& ro, double2* out, long ldo) {
+  if (M <= 0) return;
+  if (ro.att.po && ro.att.nsplit > RO_ATT_CH && ro.att.nsplit <= 256 && !ro.table && !ro.rope_cs && !ro.bias &&
+      !ro.gelu && !ro.finite_check && ro.att.H * ro.att.dh == K) {
+    // long caches: combine per (row, head) into `out`, then residual and
+    // LayerNorm on those rows in place (k_rowops reads a row whole before
+    // writing it)
+    MITOK_LAUNCH(k_attn_combine, dim3(M * ro.att.H), dim3(64), 0, st, ro.att, out, ldo);
+    RowOps r = ro;
+    r.att = AttnSplit();
+    r.x = out;
+    r.ldx = ldo;
+    r.npart = 0;
+    MITOK_LAUNCH(k_rowops, dim3(M), dim3(256), (size_t)K * sizeof(double2), st, r, K, out, ldo);
+    return;
+  }
   const size_t shm = (size_t)K * sizeof(double2) + (ro.att.po ? (size_t)ro.att.H * (ro.att.nsplit + 1) * sizeof(double) : 0);
-  if (M > 0) MITOK_LAUNCH(k_rowops, dim3(M), dim3(256), shm, st, ro, K, out, ldo);
+  MITOK_LAUNCH(k_rowops, dim3(M), dim3(256), shm, st, ro, K, out, ldo);
 }
 
 

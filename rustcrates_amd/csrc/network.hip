@@ -1071,7 +1071,13 @@ static int enqueue_decode_fused(Net* n, const Spec& sp) {
       case K_FEED_FORWARD: {
         auto* F = (FeedForwardLayer*)L;
         RowOps h;
-        if (mat) {  // Dense: + b1, GELU in the epilogue (layer.rs:132-166)
+        // Dense: + b1, GELU in the epilogue (layer.rs:132-166).  From 4
+        // sequences also for the GEMV: in FFN Linear's prologue every column
+        // block would evaluate GELU again over its K range (96 times over at
+        // config 5).  Measured on MI355X, decode per step 1791 -> 1643 us at
+        // config 5 with 4 sequences, 713 -> 707 at config 3 with 8, 494 -> 496
+        // with 4, 421 -> 428 with 2; ids unchanged
+        if (mat || B >= 4) {
           need_plain();
           Epi e1;
           e1.mode = EPI_GELU;

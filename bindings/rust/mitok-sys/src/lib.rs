@@ -29,6 +29,11 @@ pub const MITOK_ERR_NOMEM: c_int = 5;
 pub const MITOK_TRAINING: c_int = 0;
 pub const MITOK_PRODUCTION: c_int = 1;
 
+/// mitok_set_learning_rate's "every layer" and mitok_get_learning_rate's
+/// "the network's own rate"
+pub const MITOK_ALL_LAYERS: u32 = 0xFFFF_FFFF;
+pub const MITOK_NETWORK_RATE: u32 = 0xFFFF_FFFF;
+
 pub const MITOK_TIME_VOCAB: c_int = 1;
 pub const MITOK_TIME_LAYER_GEMM: c_int = 2;
 pub const MITOK_TIME_ATTENTION: c_int = 3;
@@ -97,6 +102,12 @@ extern "C" {
     pub fn mitok_backward(net: *mut MitokNetwork, targets: *const u32, tlens: *const u32, batch: u32, t: u32,
                           n_layers: u32, update_params: c_int, learning_rate: c_double, time_step: u32,
                           out_grad_input: *mut c_double) -> c_int;
+    pub fn mitok_backward_walk(net: *mut MitokNetwork, targets: *const u32, tlens: *const u32, batch: u32, t: u32,
+                               update_params: c_int, time_step: u32, out_grad_input: *mut c_double) -> c_int;
+    pub fn mitok_set_learning_rate(net: *mut MitokNetwork, layer: u32, learning_rate: c_double) -> c_int;
+    pub fn mitok_get_learning_rate(net: *const MitokNetwork, layer: u32, out: *mut c_double) -> c_int;
+    pub fn mitok_set_network_learning_rate(net: *mut MitokNetwork, learning_rate: c_double) -> c_int;
+    pub fn mitok_reset_previous_gradient(net: *mut MitokNetwork) -> c_int;
     pub fn mitok_greedy_decoding(net: *mut MitokNetwork, logits: *const c_double, rows: u32, vocab: u32,
                                  out_ids: *mut u32) -> c_int;
     pub fn mitok_greedy_decoding_device(net: *mut MitokNetwork, d_logits: *const c_double, rows: u32, vocab: u32,
@@ -369,6 +380,65 @@ impl Network {
             mitok_backward(self.raw, flat.as_ptr(), tlens.as_ptr(), b, t, n_layers, update as c_int, learning_rate,
                            time_step, std::ptr::null_mut())
         })
+    }
+
+    /// backward(transformer_network, target_ids, update_params) as train calls
+    /// it (transformer_network.rs:129): every layer, each at its own learning
+    /// rate and the Embedding at the network's.
+    pub fn backward_walk(&mut self, targets: &[Vec<u32>], update: bool, time_step: u32) -> Result<(), MitokError> {
+        let b = targets.len() as u32;
+        let t = targets.iter().map(|r| r.len()).max().unwrap_or(0).max(1) as u32;
+        let tlens: Vec<u32> = targets.iter().map(|r| r.len() as u32).collect();
+        let mut flat = vec![1u32; (b * t) as usize];
+        for (i, r) in targets.iter().enumerate() {
+            flat[i * t as usize..i * t as usize + r.len()].copy_from_slice(r);
+        }
+        check(unsafe {
+            mitok_backward_walk(self.raw, flat.as_ptr(), tlens.as_ptr(), b, t, update as c_int, time_step,
+                                std::ptr::null_mut())
+        })
+    }
+
+    /// update_learning_rate (neural_network_generic.rs:115-186): every layer.
+    pub fn update_learning_rate(&mut self, learning_rate: f64) -> Result<(), MitokError> {
+        check(unsafe { mitok_set_learning_rate(self.raw, MITOK_ALL_LAYERS, learning_rate) })
+    }
+
+    /// One layer's learning_rate field.
+    pub fn set_layer_learning_rate(&mut self, layer: u32, learning_rate: f64) -> Result<(), MitokError> {
+        check(unsafe { mitok_set_learning_rate(self.raw, layer, learning_rate) })
+    }
+
+    /// NeuralNetwork::learning_rate (the Embedding's update rate).
+    pub fn learning_rate(&self) -> Result<f64, MitokError> {
+        let mut out = 0.0;
+        check(unsafe { mitok_get_learning_rate(self.raw, MITOK_NETWORK_RATE, &mut out) })?;
+        Ok(out)
+    }
+
+    pub fn set_learning_rate(&mut self, learning_rate: f64) -> Result<(), MitokError> {
+        check(unsafe { mitok_set_network_learning_rate(self.raw, learning_rate) })
+    }
+
+    /// reset_previous_gradient (neural_network_generic.rs:188-242).
+    pub fn reset_previous_gradient(&mut self) -> Result<(), MitokError> {
+        check(unsafe { mitok_reset_previous_gradient(self.raw) })
+    }
+
+    /// update_step_lr_scheduler (neural_network_generic.rs:57-67): every layer
+    /// at learning_rate * gamma^(epoch / step_size), the network's rate kept.
+    pub fn update_step_lr_scheduler(&mut self, epoch: usize, step_size: usize, gamma: f64) -> Result<(), MitokError> {
+        let factor = (epoch / step_size) as f64;
+        let lr = self.learning_rate()? * gamma.powf(factor);
+        self.update_learning_rate(lr)
+    }
+
+    /// decay_learning_rate (neural_network_generic.rs:69-73): the network's
+    /// rate times the factor, then every layer at it.
+    pub fn decay_learning_rate(&mut self, decay_factor: f64) -> Result<(), MitokError> {
+        let lr = self.learning_rate()? * decay_factor;
+        self.set_learning_rate(lr)?;
+        self.update_learning_rate(lr)
     }
 
     /// The token loop on ids: `n_new` greedy ids per sequence.

@@ -106,12 +106,87 @@ pub fn generate_ids_device(net: &mut Network, prompt: &[u32], eos: u32) -> Resul
 /// update_parameters at time_step = epoch (:100).  Returns the loss.  The
 /// epoch loop, the loss bookkeeping, the learning-rate schedule and the sled
 /// checkpoints of `train` stay on the host around it.
-pub fn train_batch_device(net: &mut Network, batch_ids: &[Vec<u32>], target_ids: &[Vec<u32>], epoch: u32,
-                          learning_rate: f64) -> Result<Complex<f64>, MitokError> {
+pub fn train_batch_device(net: &mut Network, batch_ids: &[Vec<u32>], target_ids: &[Vec<u32>], epoch: u32)
+                          -> Result<Complex<f64>, MitokError> {
     let t = target_ids.iter().map(|r| r.len()).max().unwrap_or(0) as u32;
     net.forward_targets(batch_ids, t)?;
     let loss = net.cross_entropy_loss(target_ids)?;
-    let below_softmax = net.num_layers().saturating_sub(1);
-    net.backward(target_ids, below_softmax, true, learning_rate, epoch)?;
+    net.backward_walk(target_ids, true, epoch)?;
     Ok(loss)
+}
+
+/// What `train` decides at the end of an epoch (transformer_network.rs:
+/// 112-162), kept apart from the device so it reads like the reference.
+#[derive(Default)]
+pub struct EpochBook {
+    pub previous_last_losses: Vec<f64>,
+    pub total_loss_exp_ma: f64,
+    pub epoch_processed: usize,
+}
+
+pub const LOSS_THRESHOLD: f64 = 0.004;
+pub const LOSS_EMA_ALPHA: f64 = 0.2;
+
+impl EpochBook {
+    /// The exponential moving average (:116-120) and the rising-loss test
+    /// (:127-154): true when the learning rate is to be halved and the
+    /// previous gradients dropped.
+    pub fn end_epoch(&mut self, epoch: usize, total_loss: Complex<f64>) -> bool {
+        if self.total_loss_exp_ma == 0.0 && epoch == 0 {
+            self.total_loss_exp_ma = total_loss.re;
+        }
+        self.total_loss_exp_ma = LOSS_EMA_ALPHA * total_loss.re + (1.0 - LOSS_EMA_ALPHA) * self.total_loss_exp_ma;
+        if self.previous_last_losses.len() <= 4 {
+            self.previous_last_losses.push(total_loss.re);
+        }
+        let len = self.previous_last_losses.len();
+        self.previous_last_losses[epoch % len] = total_loss.re;
+        if len >= 4 {
+            let end_ind = epoch % len;
+            if end_ind >= 4 {
+                let start_ind = end_ind - 4;
+                let mut rising = 0;
+                for i in start_ind..end_ind - 1 {
+                    if self.previous_last_losses[i] < self.previous_last_losses[i + 1] {
+                        rising += 1;
+                    }
+                }
+                if rising > 2 && self.epoch_processed != epoch {
+                    self.epoch_processed = epoch;
+                    return true;
+                }
+            }
+        }
+        false
+    }
+}
+
+/// `train` (transformer_network.rs:35-163) on the device, over batches of
+/// (input + target ids, target ids) already tokenized and windowed: per batch
+/// the TRAINING predict, its loss, backward with every update at time_step =
+/// epoch and update_step_lr_scheduler(epoch, 100, 0.9); per epoch the loss
+/// bookkeeping, decay_learning_rate(0.5) with reset_previous_gradient when the
+/// loss keeps rising, and the stop at a total loss of norm 0.004.  The sled
+/// checkpoints and the progress prints are the caller's.  Returns each
+/// epoch's total loss.
+pub fn train_device(net: &mut Network, batches: &[(Vec<Vec<u32>>, Vec<Vec<u32>>)], num_epochs: usize)
+                    -> Result<Vec<Complex<f64>>, MitokError> {
+    let mut book = EpochBook::default();
+    let mut totals = Vec::new();
+    for epoch in 0..num_epochs {
+        let mut total_loss = Complex::new(0.0, 0.0);
+        for (batch_ids, target_ids) in batches {
+            total_loss += train_batch_device(net, batch_ids, target_ids, epoch as u32)?;
+            net.update_step_lr_scheduler(epoch, 100, 0.9)?;
+        }
+        totals.push(total_loss);
+        if book.end_epoch(epoch, total_loss) {
+            net.decay_learning_rate(0.5)?;
+            net.reset_previous_gradient()?;
+        }
+        if total_loss.norm() <= LOSS_THRESHOLD {
+            break;
+        }
+    }
+    Ok(totals)
 }

@@ -45,6 +45,11 @@ extern "C" {
 #define MITOK_TRAINING 0
 #define MITOK_PRODUCTION 1
 
+/* mitok_set_learning_rate: every layer; mitok_get_learning_rate: the
+ * network's own rate (NeuralNetwork::learning_rate) */
+#define MITOK_ALL_LAYERS 0xFFFFFFFFu
+#define MITOK_NETWORK_RATE 0xFFFFFFFFu
+
 /* kernel classes for mitok_timing_enable */
 #define MITOK_TIME_VOCAB 1       /* the vocab Linear (the Linear before Softmax) */
 #define MITOK_TIME_LAYER_GEMM 2  /* Q/K/V and FFN projections of one-row (decode) calls */
@@ -229,6 +234,34 @@ int mitok_backward(mitok_network* net, const uint32_t* targets, const uint32_t* 
                    uint32_t n_layers, int update_params, double learning_rate, uint32_t time_step,
                    double* out_grad_input);
 
+/* backward(transformer_network, target_ids, update_params) as train calls it
+ * (transformer_network.rs:129, 506-636): the whole reverse walk over every
+ * layer the last stateless predict ran, each layer updated at its own
+ * learning rate (mitok_set_learning_rate) and the Embedding at the network's
+ * (transformer_network.rs:520, mitok_set_network_learning_rate); otherwise as
+ * mitok_backward. */
+int mitok_backward_walk(mitok_network* net, const uint32_t* targets, const uint32_t* tlens, uint32_t batch, uint32_t T,
+                        int update_params, uint32_t time_step, double* out_grad_input);
+
+/* Learning rates (neural_network_generic.rs:57-73, 115-186).  Every layer
+ * starts at 0.01 (create_transformer's rate, transformer_builder.rs:16), the
+ * network too.  mitok_set_learning_rate(net, MITOK_ALL_LAYERS, lr) is
+ * update_learning_rate (what update_step_lr_scheduler calls); with a layer
+ * index it sets that layer's field (a SelfAttention's heads and Norm, a
+ * FeedForward's Dense and Linear together).  mitok_set_network_learning_rate
+ * sets NeuralNetwork::learning_rate, which decay_learning_rate halves and the
+ * Embedding's update reads; mitok_get_learning_rate(net, MITOK_NETWORK_RATE)
+ * reads it back. */
+int mitok_set_learning_rate(mitok_network* net, uint32_t layer, double learning_rate);
+int mitok_get_learning_rate(const mitok_network* net, uint32_t layer, double* out);
+int mitok_set_network_learning_rate(mitok_network* net, double learning_rate);
+/* reset_previous_gradient (neural_network_generic.rs:188-242), which train
+ * calls when the loss keeps rising (transformer_network.rs:147-151): the next
+ * update of every Linear, FeedForward sublayer and attention head is the
+ * clipped descent again, and the AdamW after it starts from zero moments.  An
+ * attention layer's Norm keeps its moments, as in the reference. */
+int mitok_reset_previous_gradient(mitok_network* net);
+
 /* greedy_decoding (src/utils/sampling_methods.rs:5-18) on the device for host
  * logits [rows][vocab]: last index among equal maxima; NaN -> MITOK_ERR_NAN. */
 int mitok_greedy_decoding(mitok_network* net, const double* logits, uint32_t rows, uint32_t vocab, uint32_t* out_ids);
@@ -239,8 +272,11 @@ int mitok_greedy_decoding_device(mitok_network* net, const double* d_logits, uin
                                  uint32_t* d_out_ids);
 
 /* mitok_greedy_decoding without any device allocation.  No counterpart in the
- * reference: it is for callers that cannot allocate device memory (code under
- * HIP graph capture, tight serving loops).  The logits and ids are staged in a
+ * reference: it is for callers that cannot allocate device memory (tight
+ * serving loops, harnesses that forbid hipMalloc).  It copies the host logits
+ * in and synchronises the network's stream before it returns, so it must not
+ * be called while that stream is being captured into a graph, and it is not
+ * recorded into a capture on another stream.  The logits and ids are staged in a
  * fixed per-GPU array of the library (8 MiB + 16 KiB, held by every GPU the
  * library runs on until the process ends): rows * vocab <= 1048576 and
  * rows <= 4096, else MITOK_ERR_ARG.  All calls on one GPU share that array, so

@@ -1484,7 +1484,12 @@ int orc_linear_update(oc64* W, oc64* b, uint32_t d, uint32_t V, const oc64* dW, 
   if (!W || !b || !dW || !db || !mW || !vW || !mb || !vb || !d || !V || !batch) return fail(ORC_ERR_ARG, "bad arguments");
   const size_t n = (size_t)d * V;
   const double bs = (double)batch;
-  if (first) { /* linear_layer.rs:159-174: the clipped copies, gradient descent */
+  if (first) { /* linear_layer.rs:159-174: the clipped copies, gradient descent; the
+                  moments it stores are the zeros of :141-145 (:176-180) */
+    memset(mW, 0, n * sizeof(oc64));
+    memset(vW, 0, n * sizeof(oc64));
+    memset(mb, 0, V * sizeof(oc64));
+    memset(vb, 0, V * sizeof(oc64));
     for (size_t i = 0; i < n; ++i) {
       const oc64 g = clip1(dW[i], 1.0);
       if (finite_c(g)) W[i] = c_sub(W[i], c_scale(c_unscale(g, bs), lr));
@@ -1890,7 +1895,9 @@ int orc_param_update(oc64* w, const oc64* g, oc64* m, oc64* v, uint64_t n, int f
                      uint32_t time_step, int weight) {
   if (!w || !g || !m || !v) return fail(ORC_ERR_ARG, "bad arguments");
   for (uint64_t i = 0; i < n; ++i) {
-    if (first) {
+    if (first) { /* the descent leaves zero moments behind it */
+      m[i] = (oc64){0.0, 0.0};
+      v[i] = (oc64){0.0, 0.0};
       const oc64 gc = clip1(g[i], 1.0);
       if (finite_c(gc)) w[i] = c_sub(w[i], c_scale(c_unscale(gc, batch), lr));
     } else {

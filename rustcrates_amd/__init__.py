@@ -62,6 +62,11 @@ SIGNATURES = {
     "mitok_greedy_decoding": (_i32, [_P, _P, _u32, _u32, _P]),
     "mitok_backward_head": (_i32, [_P, _P, _P, _u32, _u32, _i32, C.c_double, _u32, _P]),
     "mitok_backward": (_i32, [_P, _P, _P, _u32, _u32, _u32, _i32, C.c_double, _u32, _P]),
+    "mitok_backward_walk": (_i32, [_P, _P, _P, _u32, _u32, _i32, _u32, _P]),
+    "mitok_set_learning_rate": (_i32, [_P, _u32, C.c_double]),
+    "mitok_get_learning_rate": (_i32, [_P, _u32, _P]),
+    "mitok_set_network_learning_rate": (_i32, [_P, C.c_double]),
+    "mitok_reset_previous_gradient": (_i32, [_P]),
     "mitok_greedy_decoding_device": (_i32, [_P, _P, _u32, _u32, _P]),
     "mitok_forward_layers_device": (_i32, [_P, _u32, _u32, _P, _P, _u32, _u32, _P, _i32, _P]),
     "mitok_greedy_decoding_noalloc": (_i32, [_P, _P, _u32, _u32, _P]),
@@ -448,18 +453,63 @@ class Network:
             raise ValueError(f"targets: shape {t.shape}, expected (batch, T)")
         B, T = t.shape
         tl = np.full(B, T, np.uint32) if tlens is None else _u32_vec(tlens, B, "tlens")
-        gx = None
-        if want_grad_input:
-            rows = getattr(self, "_head_rows", None)
-            if rows is None or rows[0] != B:
-                raise MitokError(3, "no stateless predict of this batch to differentiate")
-            lowest = len(self._in_dims) - 1 - int(layers)
-            width = self._in_dims[lowest] if 0 <= lowest < len(self._in_dims) else self._head_in
-            n_rows = rows[2] if rows[2] is not None and lowest <= rows[3] else rows[1]
-            gx = np.empty((B, n_rows, width), np.complex128)
+        gx = self._grad_input_buffer(B, int(layers)) if want_grad_input else None
         _check(self._lib.mitok_backward(self._h, _ptr(t), _ptr(tl), B, T, int(layers), int(bool(update)),
                                         float(learning_rate), int(time_step), _ptr(gx)))
         return gx
+
+    def _grad_input_buffer(self, B, layers):
+        """[B][rows][d_in] for the input gradient of the lowest of `layers`
+        walked layers (below the first wavelet layer: the uncompressed rows)."""
+        rows = getattr(self, "_head_rows", None)
+        if rows is None or rows[0] != B:
+            raise MitokError(3, "no stateless predict of this batch to differentiate")
+        lowest = len(self._in_dims) - 1 - layers
+        width = self._in_dims[lowest] if 0 <= lowest < len(self._in_dims) else self._head_in
+        n_rows = rows[2] if rows[2] is not None and lowest <= rows[3] else rows[1]
+        return np.empty((B, n_rows, width), np.complex128)
+
+    def backward_walk(self, targets, tlens=None, update=True, time_step=1, want_grad_input=False):
+        """backward(transformer_network, target_ids, update) as train calls it
+        (transformer_network.rs:506-636): every layer of the last stateless
+        predict, each updated at its own learning rate (set_learning_rate) and
+        the Embedding at the network's (set_network_learning_rate)."""
+        t = np.ascontiguousarray(targets, dtype=np.uint32)
+        if t.ndim != 2:
+            raise ValueError(f"targets: shape {t.shape}, expected (batch, T)")
+        B, T = t.shape
+        tl = np.full(B, T, np.uint32) if tlens is None else _u32_vec(tlens, B, "tlens")
+        gx = self._grad_input_buffer(B, self.num_layers - 1) if want_grad_input else None
+        _check(self._lib.mitok_backward_walk(self._h, _ptr(t), _ptr(tl), B, T, int(bool(update)), int(time_step),
+                                             _ptr(gx)))
+        return gx
+
+    ALL_LAYERS = 0xFFFFFFFF
+    NETWORK_RATE = 0xFFFFFFFF
+
+    def set_learning_rate(self, learning_rate, layer=None):
+        """update_learning_rate (neural_network_generic.rs:115-186) for every
+        layer, or one layer's learning_rate field when `layer` is given."""
+        _check(self._lib.mitok_set_learning_rate(self._h, self.ALL_LAYERS if layer is None else int(layer),
+                                                 float(learning_rate)))
+
+    def learning_rate(self, layer=None):
+        """A layer's learning rate, or the network's (layer None)."""
+        out = C.c_double()
+        _check(self._lib.mitok_get_learning_rate(self._h, self.NETWORK_RATE if layer is None else int(layer),
+                                                 C.byref(out)))
+        return out.value
+
+    def set_network_learning_rate(self, learning_rate):
+        """NeuralNetwork::learning_rate: the Embedding's update rate, halved by
+        decay_learning_rate (neural_network_generic.rs:69-73)."""
+        _check(self._lib.mitok_set_network_learning_rate(self._h, float(learning_rate)))
+
+    def reset_previous_gradient(self):
+        """reset_previous_gradient (neural_network_generic.rs:188-242): the
+        next update of every Linear, FeedForward sublayer and attention head
+        is the clipped descent; attention Norms keep their moments."""
+        _check(self._lib.mitok_reset_previous_gradient(self._h))
 
     def cross_entropy_loss(self, targets, tlens=None):
         """cross_entropy_loss_batch (transformer_network.rs:662-711) of the

@@ -26,8 +26,14 @@ CFLAGS = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
     # keep packed-FP32 instructions out of the device code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    "-Wall", "-Wno-unused-function", "-Wno-unused-result",
+    # warnings fail the build: -Wuninitialized and its kin find on the CPU
+    # what would otherwise surface as a GPU memory fault
+    "-Wall", "-Wno-unused-function", "-Wno-unused-result", "-Werror",
 ]
+
+# hipcc's host pass does not know the packed-FP32 target feature and says so
+# once per translation unit; that line is not a diagnostic of the source
+_HOST_FEATURE_NOTE = "'-packed-fp32-ops' is not a recognized feature"
 
 
 # per-file flags: the prompt-pass GEMM keeps its MFMA accumulators in VGPRs
@@ -57,6 +63,9 @@ def _compile(src: str) -> str:
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stderr}")
+    rest = [ln for ln in r.stderr.splitlines() if _HOST_FEATURE_NOTE not in ln and ln.strip()]
+    if rest:
+        print(f"hipcc output for {src}:", *rest, sep="\n", file=sys.stderr)
     return obj
 
 

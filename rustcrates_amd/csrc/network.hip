@@ -13,6 +13,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <cmath>
 #include <memory>
 #include <mutex>
 #include <string>
@@ -102,6 +103,10 @@ enum Kind {
 struct Layer {
   int kind;
   uint32_t d_in = 0, d_out = 0;
+  // the layer's learning_rate field (every sublayer's, as update_learning_rate
+  // sets them, neural_network_generic.rs:115-186); create_transformer builds
+  // its layers at 0.01 (transformer_builder.rs:16)
+  double lr = 0.01;
   explicit Layer(int k) : kind(k) {}
   virtual ~Layer() = default;
 };
@@ -132,10 +137,13 @@ struct SelfAttentionLayer : Layer {  // self_attention_layer.rs:16-25 + masked_a
   DevBuf bias_re;  // [heads][max_ctx][max_ctx]  Re(bias_pos): only the real part reaches the softmax
   DevBuf gamma, beta;
   DevBuf kc, vc;  // [cache_B][heads][max_ctx][dh]
-  // training state: AdamW moments of wqkv and of the Norm's gamma and beta,
-  // updates so far (the first is plain clipped descent)
+  // training state: AdamW moments of wqkv and of the Norm's gamma and beta;
+  // updates so far of the heads and of the Norm, counted apart because
+  // reset_previous_gradient resets the heads' previous gradient but not the
+  // Norm's (neural_network_generic.rs:196-205); each one's first update is
+  // plain clipped descent
   DevBuf mw, vw, mg, vg, mbt, vbt;
-  uint32_t updates = 0;
+  uint32_t updates = 0, norm_updates = 0;
   SelfAttentionLayer() : Layer(K_SELF_ATTENTION) {}
 };
 
@@ -307,6 +315,10 @@ struct mitok_network {
   void* scratch = nullptr;   // this device's copy of the no-allocation staging array
   bool cooperative = false;  // cooperative launches supported
   hipStream_t stream = nullptr;
+  // NeuralNetwork::learning_rate: the rate backward passes to the Embedding's
+  // update (transformer_network.rs:520), changed by decay_learning_rate
+  // (neural_network_generic.rs:69-73) and not by update_learning_rate
+  double lr = 0.01;
   std::vector<std::unique_ptr<mitok::Layer>> layers;
   // session (KV cache) state
   bool cache_valid = false;
@@ -2627,9 +2639,12 @@ static int ensure_moments(hipStream_t st, size_t nw, size_t nb, DevBuf& mw, DevB
 // layer's update_parameters where the reference calls it (Linear,
 // FeedForward, SelfAttention with its Norm, Embedding; a standalone Norm and
 // RoPE have no update in the walk).
+// own_rates: each layer updates at its own learning rate and the Embedding at
+// the network's, as backward does (transformer_network.rs:506-636); else every
+// update uses learning_rate.
 static int backward_impl(Net* n, const uint32_t* targets, const uint32_t* tlens, uint32_t B, uint32_t T,
                          uint32_t n_layers, int update_params, double learning_rate, uint32_t time_step,
-                         double* out_grad_input) {
+                         double* out_grad_input, bool own_rates = false) {
   if (!n || !targets || !tlens || !B || !T) return fail(ERR_ARG, "bad arguments");
   if (!n->head_valid) return fail(ERR_STATE, "no stateless (forward_only = 0) predict to differentiate");
   if (B != n->head_B) return fail(ERR_ARG, "batch %u != the forward pass's %u", B, n->head_B);
@@ -2869,10 +2884,11 @@ static int backward_impl(Net* n, const uint32_t* targets, const uint32_t* tlens,
     return OK;
   };
   // update_parameters of a weight and its bias from dW, db (linear_layer.rs:130-175)
+  auto rate = [&](const Layer* L) { return own_rates ? L->lr : learning_rate; };
   auto linear_upd = [&](DevBuf& W, DevBuf& b, long nw, int nb, DevBuf& mw, DevBuf& vw, DevBuf& mb, DevBuf& vb,
-                        uint32_t& updates, int tstep) {
+                        uint32_t& updates, int tstep, double lr) {
     TrainStep ts;
-    ts.lr = learning_rate;
+    ts.lr = lr;
     ts.batch = (double)B;
     ts.first = updates == 0 ? 1 : 0;
     ts.time_step = tstep;
@@ -2885,7 +2901,8 @@ static int backward_impl(Net* n, const uint32_t* targets, const uint32_t* tlens,
   double2* gcur = n->tr_ga.as<double2>();  // the gradient of the current layer's output, then its input
   double2* gnext = n->tr_gb.as<double2>();
   TRY(linear_bwd(n->head_x, G, Ln->w.as<double2>(), d, V, gcur));
-  if (update_params) linear_upd(Ln->w, Ln->b, (long)d * V, V, Ln->mw, Ln->vw, Ln->mb, Ln->vb, Ln->updates, (int)time_step);
+  if (update_params)
+    linear_upd(Ln->w, Ln->b, (long)d * V, V, Ln->mw, Ln->vw, Ln->mb, Ln->vb, Ln->updates, (int)time_step, rate(Ln));
   for (int li = (int)li_top - 1; li >= (int)stop; --li) {
     Layer* L = n->layers[li].get();
     const double2* X = n->tr_in[li]->as<double2>();
@@ -2910,7 +2927,7 @@ static int backward_impl(Net* n, const uint32_t* targets, const uint32_t* tlens,
         auto* H = (LinearLayer*)L;
         TRY(linear_bwd(X, gcur, H->w.as<double2>(), H->d_in, H->d_out, gnext));
         if (update_params) linear_upd(H->w, H->b, (long)H->d_in * H->d_out, H->d_out, H->mw, H->vw, H->mb, H->vb, H->updates,
-                                      (int)time_step);
+                                      (int)time_step, rate(H));
         std::swap(gcur, gnext);
         break;
       }
@@ -2935,11 +2952,11 @@ static int backward_impl(Net* n, const uint32_t* targets, const uint32_t* tlens,
         TRY(linear_bwd(n->tr_h.as<double2>(), gcur, F->w2.as<double2>(), Fh, dn, n->tr_dh.as<double2>()));
         // FeedForwardLayer::update_parameters (:219-250): the Linear at the FFN's time step (:86)
         if (update_params) linear_upd(F->w2, F->b2, (long)Fh * dn, dn, F->mw2, F->vw2, F->mb2, F->vb2, F->updates2,
-                                      (int)time_step);
+                                      (int)time_step, rate(F));
         gelu_backward(st, n->tr_dh.as<double2>(), n->tr_z.as<double2>(), mask, rows, Fh, n->tr_g1.as<double2>());
         TRY(linear_bwd(X, n->tr_g1.as<double2>(), F->w1.as<double2>(), di, Fh, gnext));
         // the Dense at step 1: Layer::time_step stays 0 after construction (layer.rs:111,285)
-        if (update_params) linear_upd(F->w1, F->b1, (long)di * Fh, Fh, F->mw1, F->vw1, F->mb1, F->vb1, F->updates1, 0);
+        if (update_params) linear_upd(F->w1, F->b1, (long)di * Fh, Fh, F->mw1, F->vw1, F->mb1, F->vb1, F->updates1, 0, rate(F));
         std::swap(gcur, gnext);
         break;
       }
@@ -2978,14 +2995,16 @@ static int backward_impl(Net* n, const uint32_t* targets, const uint32_t* tlens,
                       "qkv input grad"));
         if (update_params) {  // SelfAttentionLayer::update_parameters (:260-273): the Norm, then the heads
           TrainStep ts;
-          ts.lr = learning_rate;
-          ts.first = A->updates == 0 ? 1 : 0;
+          ts.lr = rate(A);
+          ts.first = A->norm_updates == 0 ? 1 : 0;
           ts.time_step = (int)time_step;
           ts.batch = (double)da;  // norm_layer.rs:269: gamma's length
           colsum(st, n->tr_pg.as<double2>(), (int)B, S, da, (double)da, n->tr_bsum.as<double2>(), db);  // gamma's: n copies per row
           param_update(st, A->gamma.as<double2>(), db, A->mg.as<double2>(), A->vg.as<double2>(), da, false, ts);
           colsum(st, gcur, (int)B, S, da, (double)da, n->tr_bsum.as<double2>(), db);
           param_update(st, A->beta.as<double2>(), db, A->mbt.as<double2>(), A->vbt.as<double2>(), da, false, ts);
+          A->norm_updates++;
+          ts.first = A->updates == 0 ? 1 : 0;
           ts.batch = (double)B;  // masked_attention_head.rs:352: the sequences
           param_update(st, A->wqkv.as<double2>(), dW, A->mw.as<double2>(), A->vw.as<double2>(), (long)3 * da * da, true, ts);
           attn_bias_update(st, A->bias_re.as<double>(), mc, n->tr_dA.as<double>(), (int)B, H, S, ts);
@@ -3011,7 +3030,8 @@ static int backward_impl(Net* n, const uint32_t* targets, const uint32_t* tlens,
         auto* E = (EmbeddingLayer*)L;
         if (embed_upd && !eids.empty())
           embedding_update(st, E->table.as<double2>(), (int)E->d_out, n->tr_eid.as<uint32_t>(), (int)eids.size(),
-                           n->tr_est.as<int>(), n->tr_eocc.as<int>(), gcur, learning_rate, (double)B * (double)E->vocab,
+                           n->tr_est.as<int>(), n->tr_eocc.as<int>(), gcur, own_rates ? n->lr : learning_rate,
+                           (double)B * (double)E->vocab,
                            err);
         break;
       }
@@ -3036,6 +3056,65 @@ int mitok_backward(mitok_network* n, const uint32_t* targets, const uint32_t* tl
                    uint32_t n_layers, int update_params, double learning_rate, uint32_t time_step,
                    double* out_grad_input) {
   return backward_impl(n, targets, tlens, B, T, n_layers, update_params, learning_rate, time_step, out_grad_input);
+}
+
+int mitok_backward_walk(mitok_network* n, const uint32_t* targets, const uint32_t* tlens, uint32_t B, uint32_t T,
+                        int update_params, uint32_t time_step, double* out_grad_input) {
+  if (!n) return fail(ERR_ARG, "null network");
+  if (!n->head_valid) return fail(ERR_STATE, "no stateless (forward_only = 0) predict to differentiate");
+  if (n->layers.size() < 2) return fail(ERR_STATE, "the stack does not end in Linear, Softmax");
+  const uint32_t reach = (uint32_t)n->layers.size() - 1 - n->head_first;
+  return backward_impl(n, targets, tlens, B, T, reach, update_params, 0.0, time_step, out_grad_input, true);
+}
+
+int mitok_set_learning_rate(mitok_network* n, uint32_t layer, double lr) {
+  if (!n) return fail(ERR_ARG, "null network");
+  if (!(lr >= 0.0) || !std::isfinite(lr)) return fail(ERR_ARG, "learning rate %g", lr);
+  if (layer == MITOK_ALL_LAYERS) {
+    for (auto& L : n->layers) L->lr = lr;
+    return OK;
+  }
+  if (layer >= n->layers.size()) return fail(ERR_ARG, "layer %u of %zu", layer, n->layers.size());
+  n->layers[layer]->lr = lr;
+  return OK;
+}
+
+int mitok_get_learning_rate(const mitok_network* n, uint32_t layer, double* out) {
+  if (!n || !out) return fail(ERR_ARG, "bad arguments");
+  if (layer == MITOK_NETWORK_RATE) {
+    *out = n->lr;
+    return OK;
+  }
+  if (layer >= n->layers.size()) return fail(ERR_ARG, "layer %u of %zu", layer, n->layers.size());
+  *out = n->layers[layer]->lr;
+  return OK;
+}
+
+int mitok_set_network_learning_rate(mitok_network* n, double lr) {
+  if (!n) return fail(ERR_ARG, "null network");
+  if (!(lr >= 0.0) || !std::isfinite(lr)) return fail(ERR_ARG, "learning rate %g", lr);
+  n->lr = lr;
+  return OK;
+}
+
+// reset_previous_gradient (neural_network_generic.rs:188-242): the next update
+// of every Linear, every FeedForward's Dense and Linear and every attention
+// layer's heads is the clipped descent again, which leaves zero moments for
+// the AdamW after it (update1 in train.hip clears them).  Norms keep theirs;
+// the Embedding's update never reads a previous gradient.
+int mitok_reset_previous_gradient(mitok_network* n) {
+  if (!n) return fail(ERR_ARG, "null network");
+  for (auto& L : n->layers) switch (L->kind) {
+      case K_LINEAR: ((LinearLayer*)L.get())->updates = 0; break;
+      case K_FEED_FORWARD: {
+        auto* F = (FeedForwardLayer*)L.get();
+        F->updates1 = F->updates2 = 0;
+        break;
+      }
+      case K_SELF_ATTENTION: ((SelfAttentionLayer*)L.get())->updates = 0; break;
+      default: break;
+    }
+  return OK;
 }
 
 int mitok_greedy_decoding(mitok_network* n, const double* logits, uint32_t rows, uint32_t V, uint32_t* out_ids) {

@@ -99,6 +99,10 @@ __device__ __forceinline__ double powi_f64(double a, int e) {
 __device__ __forceinline__ double2 update1(double2 w, double2 g, double2* m, double2* v, const TrainStep& ts,
                                            bool weight) {
   if (ts.first) {
+    // the descent stores zero moments for the AdamW that follows it
+    // (linear_layer.rs:141-145,176-180): after reset_previous_gradient too
+    *m = make_double2(0.0, 0.0);
+    *v = make_double2(0.0, 0.0);
     const double n = hypot(g.x, g.y);
     if (n > 1.0) g = cscale(g, 1.0 / n);
     if (!(isfinite(g.x) && isfinite(g.y))) return w;

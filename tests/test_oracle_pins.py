@@ -8,7 +8,11 @@ chosen so a dropped term, a wrong sign/index or a transposed operand fails.
 Parity unpinned (no independent answer exists here): the exact summation
 order of OpenBLAS zgemm_ (utils/matrix.rs:55) and the last-ulp rounding of
 the platform libm the reference links; both are covered only to the 1e-9
-tolerance the HIP path is held to.
+tolerance the HIP path is held to.  The Norm's backward (norm_layer.rs:
+157-197) with a non-uniform gamma: the reference's own gradient check pins it
+at gamma = 1, where its quadratic term vanishes, and only its structure
+(real rows, linear plus quadratic in the incoming gradient, gamma's and beta's
+n-fold sums) pins it otherwise.
 """
 from __future__ import annotations
 
@@ -752,6 +756,62 @@ def test_linear_update_adamw_steps_reduce_to_normalised_descent():
         want = (W if t == 1 else want) * (1 - 0.01 * lr) - lr * gc / (np.abs(gc) + 1e-8)
         np.testing.assert_allclose(Wt, want, rtol=1e-12, atol=1e-15)
         np.testing.assert_allclose(bt, b * (1 - 0.01 * lr) ** t, rtol=1e-15)
+
+
+def test_adamw_two_steps_with_different_gradients_closed_form():
+    """utils/adam_w.rs:3-4,26-35 with B_1 = 0.9, B_2 = 0.999 over two AdamW
+    steps from zero moments with different (clipped) gradients g1 != g2, at
+    t = 1 then t = 2:  m_hat2 = (0.9 * 0.1 g1 + 0.1 g2) / (1 - 0.9^2),
+    v_hat2 = (0.999 * 0.001 |g1|^2 + 0.001 |g2|^2) / (1 - 0.999^2); the step
+    is w (1 - 0.01 lr) - lr m_hat / (sqrt(max(|v_hat|, 1e-8)) + 1e-8), the bias
+    arm without the floor.  A swapped B_1 / B_2, a dropped bias correction or a
+    moment that does not persist between the calls each move the result by
+    far more than the tolerance."""
+    rng = np.random.default_rng(7)
+    W = rng.standard_normal((3, 5)) + 1j * rng.standard_normal((3, 5))
+    b = rng.standard_normal(5) + 1j * rng.standard_normal(5)
+    g1 = 0.3 * (rng.standard_normal((3, 5)) + 1j * rng.standard_normal((3, 5)))
+    g2 = 0.3 * (rng.standard_normal((3, 5)) + 1j * rng.standard_normal((3, 5)))
+    g1[0, 0], g2[1, 1] = 4 - 3j, 0.0  # one clipped to norm 1, one zero in the second step
+    gb1 = 0.2 * (rng.standard_normal(5) + 1j * rng.standard_normal(5))
+    gb2 = 0.2 * (rng.standard_normal(5) + 1j * rng.standard_normal(5))
+    lr = 0.02
+    state = [np.zeros((3, 5), np.complex128), np.zeros((3, 5), np.complex128),
+             np.zeros(5, np.complex128), np.zeros(5, np.complex128)]
+    W1, b1 = oracle.linear_update(W, b, g1, gb1, 2, state, False, lr, 1)
+    W2, b2 = oracle.linear_update(W1, b1, g2, gb2, 2, state, False, lr, 2)
+
+    def clip(g):
+        n = np.abs(g)
+        return np.where(n > 1, g / np.where(n > 1, n, 1), g)
+
+    def step2(w0, ga, gb_, floor):
+        a, c = clip(ga), clip(gb_)
+        m1, v1 = 0.1 * a, 0.001 * np.abs(a) ** 2
+        vn1 = np.abs(v1 / (1 - 0.999))
+        vn1 = np.maximum(vn1, 1e-8) if floor else vn1
+        w1 = w0 * (1 - 0.01 * lr) - lr * (m1 / (1 - 0.9)) / (np.sqrt(vn1) + 1e-8)
+        mh = (0.9 * 0.1 * a + 0.1 * c) / (1 - 0.9 ** 2)
+        vh = (0.999 * 0.001 * np.abs(a) ** 2 + 0.001 * np.abs(c) ** 2) / (1 - 0.999 ** 2)
+        vn = np.maximum(np.abs(vh), 1e-8) if floor else np.abs(vh)
+        return w1, w1 * (1 - 0.01 * lr) - lr * mh / (np.sqrt(vn) + 1e-8), (0.9 * 0.1 * a + 0.1 * c)
+
+    w1_want, w2_want, m2_want = step2(W, g1, g2, True)
+    b1_want, b2_want, mb2_want = step2(b, gb1, gb2, False)
+    np.testing.assert_allclose(W1, w1_want, rtol=1e-13, atol=1e-15)
+    np.testing.assert_allclose(W2, w2_want, rtol=1e-13, atol=1e-15)
+    np.testing.assert_allclose(b2, b2_want, rtol=1e-13, atol=1e-15)
+    np.testing.assert_allclose(state[0], m2_want, rtol=1e-14, atol=1e-16)  # the first moment persisted
+    np.testing.assert_allclose(state[2], mb2_want, rtol=1e-14, atol=1e-16)
+    # param_update (the attention and Norm arms) runs the same arithmetic
+    st = [np.zeros((3, 5), np.complex128), np.zeros((3, 5), np.complex128)]
+    p1 = oracle.param_update(W, g1, st, False, lr, 2, 1)
+    np.testing.assert_array_equal(oracle.param_update(p1, g2, st, False, lr, 2, 2), W2)
+    # a descent after them (reset_previous_gradient) leaves zero moments behind
+    oracle.linear_update(W2, b2, g1, gb1, 2, state, True, lr, 3)
+    assert all(np.all(a == 0) for a in state)
+    oracle.param_update(p1, g2, st, True, lr, 2, 3)
+    assert all(np.all(a == 0) for a in st)
 
 
 def test_gelu_derivative_is_the_complex_derivative_of_gelu():

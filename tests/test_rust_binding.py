@@ -71,10 +71,14 @@ def test_crate_declares_every_header_entry_point_with_its_types():
 
 
 def test_crate_constants_match_the_header():
-    hdr = dict(re.findall(r"#define (MITOK_[A-Z_]+) (\d+)", open(HEADER).read()))
+    def value(v):  # 5, 0xFFFFFFFFu (C) or 0xFFFF_FFFF (Rust)
+        return int(v.rstrip("uU").replace("_", ""), 0)
+
+    text = open(HEADER).read()
+    hdr = {k: value(v) for k, v in re.findall(r"#define (MITOK_[A-Z_]+) (0x[0-9A-Fa-f]+[uU]?|\d+)\b", text)}
     src = open(os.path.join(CRATE, "src", "lib.rs")).read()
-    rs = dict(re.findall(r"pub const (MITOK_[A-Z_]+): c_int = (\d+);", src))
-    assert hdr == rs
+    rs = {k: value(v) for k, v in re.findall(r"pub const (MITOK_[A-Z_]+): (?:c_int|u32) = (0x[0-9A-Fa-f_]+|\d+);", src)}
+    assert hdr == rs and "MITOK_ALL_LAYERS" in hdr
 
 
 def test_crate_manifest_links_the_library():

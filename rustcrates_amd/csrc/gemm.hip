@@ -68,15 +68,36 @@ __global__ __launch_bounds__(256) void k_argmax_finalize(Argmax am, int tiles) {
 // GEMV for M <= 8 rows: HBM-bound weight stream.  A block owns C columns and a
 // K range of 4*kw rows; lane (r, c) = (lane / C, lane % C) reads row r of each
 // group of 64/C rows, so one wave instruction covers 64/C rows x C columns.
-// The first 8 weight loads per lane are in flight while the prologue builds
-// the block's input rows in LDS.  Lanes of a column are summed by shuffles,
+// The first 16 weight loads per lane -- every row of the lane for the layer
+// products of config 3 -- are in flight while the prologue builds the block's
+// input rows in LDS; longer ranges keep two buffers of 8 loads in flight, each
+// refilled once consumed.  Every lane issues every load (rows past its range
+// read a zero constant), so each wait covers only the loads it needs.  Lanes of a column are summed by shuffles,
 // the 4 waves through LDS; blockIdx.y splits K (at most 8 ways, so few blocks
 // meet at each completion counter).
 // ===========================================================================
 constexpr int GEMV_MAX_SPLIT = 8;
+__device__ const double2 gemv_zero2 = {0.0, 0.0};  // what a load past a lane's rows reads
+// w[u] <- rows u0 + u of the lane's column, u < 8 (zero past its nu rows)
+__device__ __forceinline__ void gemv_rows(double2 (&w)[8], const double2* wp, long wstep, int u0, int nu) {
+#pragma unroll
+  for (int u = 0; u < 8; ++u) w[u] = ld_stream(u0 + u < nu ? wp + (u0 + u) * wstep : &gemv_zero2);
+}
+// acc[m] += x[m][row u0 + u] * w[u], u < 8; rows past nu (zero weights) read
+// the lane's first row, so they add exact zeros
+template <int MR>
+__device__ __forceinline__ void gemv_fma(double2 (&acc)[MR], const double2* xw, int RL, int RPW, int u0, int nu,
+                                         const double2 (&w)[8]) {
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const int iu = u0 + u < nu ? u0 + u : 0;
+#pragma unroll
+    for (int m = 0; m < MR; ++m) acc[m] = cadd(acc[m], cmul(xw[m * RL + iu * RPW], w[u]));
+  }
+}
 constexpr int SKINNY_MAX_SPLIT = 8;
 
-template <int MR, int C>
+template <int MR, int C, int NS>
 __global__ __launch_bounds__(256) void k_gemv(RowOps ro, int M, const double2* __restrict__ W, long ldw, int N, int K,
                                               int kw, Epi ep, Argmax am, double2* __restrict__ ws,
                                               uint32_t* __restrict__ cnt) {
@@ -102,9 +123,13 @@ __global__ __launch_bounds__(256) void k_gemv(RowOps ro, int M, const double2* _
   L.lsum = L.wts + (ro.att.po ? (size_t)M * ro.att.H * ro.att.nsplit : 0);
   L.m0 = 0;
 
-  double2 w[8];
-#pragma unroll
-  for (int u = 0; u < 8; ++u) w[u] = (col_ok && u < nu) ? wp[u * wstep] : make_double2(0.0, 0.0);
+  const int nuc = col_ok ? nu : 0;  // rows this lane loads
+  const int nu_max = (kw + RPW - 1) / RPW;  // the most rows of any lane (block-uniform)
+  static_assert(NS == 16 || NS == 24, "rows requested before the prologue");
+  double2 w0[8], w1[8], w2[8];
+  gemv_rows(w0, wp, wstep, 0, nuc);
+  gemv_rows(w1, wp, wstep, 8, nuc);
+  if constexpr (NS == 24) gemv_rows(w2, wp, wstep, 16, nuc);
 
   ro_prepare(ro, M, L);
   ro_build<MR>(ro, M, K, ka, RL, kb0, min(K, kb0 + KB), lds2, L, st_mean, st_sd);
@@ -119,26 +144,18 @@ __global__ __launch_bounds__(256) void k_gemv(RowOps ro, int M, const double2* _
   double2 acc[MR];
 #pragma unroll
   for (int m = 0; m < MR; ++m) acc[m] = make_double2(0.0, 0.0);
-  if (col_ok) {
-    const double2* xw = xs + wave * kw + r;  // row u of this lane: xw[m * RL + u * RPW]
-#pragma unroll
-    for (int u = 0; u < 8; ++u)
-      if (u < nu)
-#pragma unroll
-        for (int m = 0; m < MR; ++m) acc[m] = cadd(acc[m], cmul(xw[m * RL + u * RPW], w[u]));
-    int u0 = 8;
-    for (; u0 + 8 <= nu; u0 += 8) {
-#pragma unroll
-      for (int u = 0; u < 8; ++u) w[u] = wp[(u0 + u) * wstep];
-#pragma unroll
-      for (int u = 0; u < 8; ++u)
-#pragma unroll
-        for (int m = 0; m < MR; ++m) acc[m] = cadd(acc[m], cmul(xw[m * RL + (u0 + u) * RPW], w[u]));
-    }
-    for (; u0 < nu; ++u0) {
-      const double2 wv = wp[u0 * wstep];
-#pragma unroll
-      for (int m = 0; m < MR; ++m) acc[m] = cadd(acc[m], cmul(xw[m * RL + u0 * RPW], wv));
+  {
+    // row u of this lane: xw[m * RL + u * RPW]; a row past the lane's range
+    // has a zero weight and reads the lane's first row (a lane with no rows:
+    // the block's first), so it adds an exact zero
+    const double2* xw = xs + (nuc > 0 ? wave * kw + r : 0);
+    gemv_fma<MR>(acc, xw, RL, RPW, 0, nuc, w0);
+    gemv_fma<MR>(acc, xw, RL, RPW, 8, nuc, w1);
+    if constexpr (NS == 24) gemv_fma<MR>(acc, xw, RL, RPW, 16, nuc, w2);
+    // rows past the first NS (the wide vocab product), 8 at a time
+    for (int u0 = NS; u0 < nu_max; u0 += 8) {
+      gemv_rows(w0, wp, wstep, u0, nuc);
+      gemv_fma<MR>(acc, xw, RL, RPW, u0, nuc, w0);
     }
   }
   // lanes of one column (same c, r = 0 .. RPW-1) -> r = 0
@@ -981,7 +998,11 @@ static GemvPlan plan_gemv(int M, int N, int K, bool part, bool narrow = false) {
   p.C = wide ? 64 : (part || (narrow && cdiv_i(N, 8) >= 256) ? 8 : 16);
   const int rpw = 64 / p.C;
   p.ncb = cdiv_i(N, p.C);
-  const int P = std::min(GEMV_MAX_SPLIT, std::max(1, cdiv_i(256, p.ncb)));
+  int P = std::min(GEMV_MAX_SPLIT, std::max(1, cdiv_i(256, p.ncb)));
+  // a split product takes as many splits as keep every lane's range within
+  // the 24 weight rows k_gemv requests before its prologue (config 5's FFN
+  // Linear: 4 splits of 768 rows, not 3 of 1024)
+  if (part && !wide) P = std::min(GEMV_MAX_SPLIT, std::max(P, cdiv_i(K, 4 * 24 * rpw)));
   // rows per block: a multiple of 4 waves x rpw, and its input rows fit 64 KB of LDS
   const int unit = 4 * rpw;
   int KB = cdiv_i(cdiv_i(K, P), unit) * unit;
@@ -1141,8 +1162,14 @@ static void launch_gemv(hipStream_t st, const GemvPlan& p, const RowOps& ro, int
                         int K, const Epi& ep, const Argmax& am, const Sync& sy) {
   dim3 grid(p.ncb, p.P);
   const size_t shm = gemv_lds_bytes(p, ro, M, K);
-  MITOK_LAUNCH((k_gemv<MR, C>), grid, dim3(256), shm, st, ro, M, W, ldw, N, K, p.kw, ep, am, (double2*)sy.ws,
-                     sy.counters);
+  // 24 rows per lane requested before the prologue where 16 would not cover
+  // the lane's range (both keep two blocks per CU within the registers)
+  if ((p.kw + 64 / C - 1) / (64 / C) > 16)
+    MITOK_LAUNCH((k_gemv<MR, C, 24>), grid, dim3(256), shm, st, ro, M, W, ldw, N, K, p.kw, ep, am, (double2*)sy.ws,
+                 sy.counters);
+  else
+    MITOK_LAUNCH((k_gemv<MR, C, 16>), grid, dim3(256), shm, st, ro, M, W, ldw, N, K, p.kw, ep, am, (double2*)sy.ws,
+                 sy.counters);
 }
 template <int MR>
 static void launch_gemv_c(hipStream_t st, const GemvPlan& p, const RowOps& ro, int M, const double2* W, long ldw, int N,

@@ -74,6 +74,7 @@ extern "C" {
     pub fn mitok_seq_out_len(net: *const MitokNetwork, first: u32, last: u32, seq: u32, out: *mut u32) -> c_int;
 
     pub fn mitok_init_seeded(net: *mut MitokNetwork, seed: u64) -> c_int;
+    pub fn mitok_init_embedding_wavelet(net: *mut MitokNetwork, layer: u32, seed: u64, src_dim: u32) -> c_int;
     pub fn mitok_get_tensor(net: *mut MitokNetwork, layer: u32, slot: u32, out: *mut c_double, n: u64) -> c_int;
     pub fn mitok_reset(net: *mut MitokNetwork) -> c_int;
 

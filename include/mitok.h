@@ -109,6 +109,17 @@ int mitok_seq_out_len(const mitok_network* net, uint32_t first, uint32_t last, u
 /* Seeded Xavier-uniform weights (initialize_weights_complex, utils/weights_initializer.rs:73-89),
  * computed on the device from a counter generator: the CPU checker holds the same values. */
 int mitok_init_seeded(mitok_network* net, uint64_t seed);
+/* EmbeddingLayer::new's embeddings (embedding_layer.rs:40-77) for the
+ * Embedding at `layer`: for every token id, create_embedding draws src_dim
+ * values uniform in [-0.4, 0.5) (here the counter generator on stream
+ * (layer << 12) | 0xFFF, index id * src_dim + k, where the reference draws
+ * from the unseeded rand::rng()), decomposes them with
+ * decompose_in_wavelet_2d_default (network_types/wavelet_network.rs:42-135:
+ * 5 levels of DB1/SYMMETRIC dwt_2d_full keeping the LL quadrant, then the
+ * CMOR CWT at scales 2, 8, 16, 32) and keeps the first scale's row.  src_dim:
+ * a power of two up to 4096 (512 in create_transformer) whose decomposed
+ * width is the layer's dim (16 for 512). */
+int mitok_init_embedding_wavelet(mitok_network* net, uint32_t layer, uint64_t seed, uint32_t src_dim);
 /* Reads a weight tensor back (slots as in oracle/oracle.h; slot 3 = Re(bias_pos), n doubles). */
 int mitok_get_tensor(mitok_network* net, uint32_t layer, uint32_t slot, double* out, uint64_t n);
 /* Drops every KV cache (k_cache = v_cache = None, masked_attention_head.rs:54-57). */

@@ -93,6 +93,10 @@ def _load():
         "orc_param_update": (i32, [P, P, P, P, u64, i32, f64, f64, u32, i32]),
         "orc_set_target_rows": (None, [P, u32]),
         "orc_dwt_backward": (i32, [P, u32, u32, u32, u32, u32, u32, P]),
+        "orc_dwt_2d_full": (i32, [P, u32, u32, u32, u32, P, P, P]),
+        "orc_cwt_cmor": (i32, [P, u32, f64, f64, f64, P]),
+        "orc_embedding_wavelet": (i32, [u64, u64, u32, u32, P, P]),
+        "orc_init_embedding_wavelet": (i32, [P, u32, u64, u32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -175,6 +179,34 @@ def dwt_1d(x, wavelet: int, mode: int) -> np.ndarray:
     n = C.c_uint32(0)
     _check(lib().orc_dwt_1d(_ptr(x), x.shape[0], wavelet, mode, _ptr(out), C.byref(n)))
     return out[:n.value].copy()
+
+
+def dwt_2d_full(x, wavelet: int, mode: int) -> np.ndarray:
+    """dwt_2d_full (wavelet_transform/dwt.rs:20-34) of a real matrix."""
+    x = np.ascontiguousarray(x, dtype=np.float64)
+    R, Cn = x.shape
+    out = np.empty((R + 4) * (Cn + 4), np.float64)
+    r2, c2 = C.c_uint32(0), C.c_uint32(0)
+    _check(lib().orc_dwt_2d_full(_ptr(x), R, Cn, wavelet, mode, _ptr(out), C.byref(r2), C.byref(c2)))
+    return out[:r2.value * c2.value].reshape(r2.value, c2.value).copy()
+
+
+def cwt_cmor(x, scale: float, fb: float = 1.5, fc: float = 1.0) -> np.ndarray:
+    """get_wavelet_complex (wavelet_transform/cwt_complex.rs:195-211) with the
+    CMOR wavelet at one scale, of a real row."""
+    x = np.ascontiguousarray(x, dtype=np.float64)
+    out = np.empty(x.shape[0], np.complex128)
+    _check(lib().orc_cwt_cmor(_ptr(x), x.shape[0], float(scale), float(fb), float(fc), _ptr(out)))
+    return out
+
+
+def embedding_wavelet(seed: int, stream: int, vocab: int, src_dim: int = 512) -> np.ndarray:
+    """EmbeddingLayer::create_embedding (embedding_layer.rs:65-77) for every
+    token with the seeded draw: the [vocab][dim] table."""
+    out = np.empty(vocab * src_dim, np.complex128)
+    dim = C.c_uint32(0)
+    _check(lib().orc_embedding_wavelet(seed, stream, vocab, src_dim, _ptr(out), C.byref(dim)))
+    return out[:vocab * dim.value].reshape(vocab, dim.value).copy()
 
 
 def softmax_backward(P, targets, tlens=None) -> np.ndarray:
@@ -491,6 +523,10 @@ class Network:
 
     def init_seeded(self, seed):
         _check(lib().orc_init_seeded(self._h, seed))
+
+    def init_embedding_wavelet(self, layer, seed, src_dim=512):
+        """EmbeddingLayer::new's create_embedding for every token (embedding_layer.rs:40-77)."""
+        _check(lib().orc_init_embedding_wavelet(self._h, layer, seed, src_dim))
 
     def get_tensor(self, layer, slot, n):
         out = np.empty(n, np.complex128)

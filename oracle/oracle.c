@@ -1972,3 +1972,195 @@ int orc_dwt_backward(const oc64* G, uint32_t B, uint32_t S2, uint32_t S_in, uint
   free(data), free(dec);
   return rc;
 }
+
+/* ------------------------------------------------------------------------ */
+/* EmbeddingLayer::create_embedding (embedding_layer.rs:65-77)               */
+/* ------------------------------------------------------------------------ */
+
+int orc_dwt_2d_full(const double* x, uint32_t rows, uint32_t cols, uint32_t wavelet, uint32_t mode, double* out,
+                    uint32_t* out_rows, uint32_t* out_cols) {
+  if (!x || !out || !rows || !cols) return fail(ORC_ERR_ARG, "bad arguments");
+  /* dwt_2d_partial over the rows (dwt.rs:8-18) */
+  double* t = (double*)malloc((size_t)rows * (cols + 4) * sizeof(double));
+  double* col = (double*)malloc((size_t)(rows + 4) * 2 * sizeof(double));
+  if (!t || !col) {
+    free(t), free(col);
+    return fail(ORC_ERR_NOMEM, "dwt_2d_full: out of memory");
+  }
+  uint32_t C2 = 0, R2 = 0;
+  int rc = ORC_OK;
+  for (uint32_t r = 0; r < rows && !rc; ++r) rc = orc_dwt_1d(x + (size_t)r * cols, cols, wavelet, mode, t + (size_t)r * (cols + 4), &C2);
+  /* transpose, dwt_2d_partial over the former columns, transpose back (:27-33) */
+  for (uint32_t c = 0; c < C2 && !rc; ++c) {
+    double* in = col + rows + 4;
+    for (uint32_t r = 0; r < rows; ++r) in[r] = t[(size_t)r * (cols + 4) + c];
+    rc = orc_dwt_1d(in, rows, wavelet, mode, col, &R2);
+    for (uint32_t r = 0; r < R2 && !rc; ++r) out[(size_t)r * C2 + c] = col[r];
+  }
+  free(t), free(col);
+  if (rc) return rc;
+  *out_rows = R2;
+  *out_cols = C2;
+  return ORC_OK;
+}
+
+/* The CMOR wavelet's cumulative integral resampled at the scale and reversed
+ * (integrate_complex, utils/array_complex.rs:122-149) from wavefun_complex
+ * (cwt_complex.rs:268-289): x = linspace_complex(-8, 8, 1024, true)
+ * (utils/array_complex.rs:10-33: start + step added one by one, the end
+ * set exactly), y = cmorl(x) (cwt_type_resolver.rs:114-123:
+ * cos(2 pi fc x) E^(-x^2 / fb) / sqrt(pi fb), minus the sine likewise;
+ * E.powf is pow with base e, not exp).  *klen = scale * 16 + 1 entries. */
+static int cmor_kernel(double scale, double fb, double fc, oc64** kern, uint32_t* klen) {
+  enum { NP = 1024 };
+  static double xs[NP];
+  static oc64 integral[NP];
+  const double start = -8.0, end = 8.0, span = end - start;
+  const double step_ls = span / ((double)NP - 1.0);
+  double t = start;
+  for (int i = 0; i < NP; ++i) {
+    xs[i] = t;
+    t = t + step_ls;
+  }
+  xs[NP - 1] = end;
+  const double step = xs[1] - xs[0];
+  for (int i = 0; i < NP; ++i) {
+    const double re = xs[i];
+    const double ang = 2.0 * M_PI * fc * re;
+    const double g = pow(M_E, -pow(re, 2.0) / fb);
+    const double den = sqrt(M_PI * fb);
+    const oc64 y = {cos(ang) * g / den, -1.0 * (sin(ang) * g / den)};
+    oc64 sum = {y.re * step, y.im * step};
+    if (i > 0) sum = c_add(sum, integral[i - 1]);
+    integral[i] = sum;
+  }
+  const double range = xs[NP - 1] - xs[0];
+  const double a_end = scale * range + 1.0;
+  const size_t K = (size_t)((a_end - 0.0) / 1.0); /* arange(0, end, 1), utils/array.rs:8-20 */
+  oc64* k = (oc64*)malloc((K ? K : 1) * sizeof(oc64));
+  if (!k) return fail(ORC_ERR_NOMEM, "cwt: out of memory");
+  double v = 0.0;
+  for (size_t j = 0; j < K; ++j) {
+    const size_t idx = (size_t)(v / (scale * step));
+    if (idx >= NP) {
+      free(k);
+      return fail(ORC_ERR_ARG, "cwt: scale %g reaches past the wavelet's integral", scale);
+    }
+    k[K - 1 - j] = integral[idx]; /* reversed */
+    v = v + 1.0;
+  }
+  *kern = k;
+  *klen = (uint32_t)K;
+  return ORC_OK;
+}
+
+static int cwt_with_kernel(const double* x, uint32_t n, const oc64* kern, uint32_t K, double scale, oc64* out);
+
+int orc_cwt_cmor(const double* x, uint32_t n, double scale, double fb, double fc, oc64* out) {
+  if (!x || !out || !n) return fail(ORC_ERR_ARG, "bad arguments");
+  oc64* kern = NULL;
+  uint32_t K = 0;
+  int rc = cmor_kernel(scale, fb, fc, &kern, &K);
+  if (rc) return rc;
+  rc = cwt_with_kernel(x, n, kern, K, scale, out);
+  free(kern);
+  return rc;
+}
+
+/* get_wavelet_complex's convolution and coefficients for a kernel from
+ * cmor_kernel */
+static int cwt_with_kernel(const double* x, uint32_t n, const oc64* kern, uint32_t K, double scale, oc64* out) {
+  /* convolve_complex(data, kernel, FULL) (utils/array_complex.rs:38-94): the
+   * shorter operand is reversed and slides over the longer one padded by
+   * (n_out - longer) zeros on each side; each output sums in order from 0 */
+  oc64* data = (oc64*)malloc((size_t)n * sizeof(oc64));
+  if (!data) return fail(ORC_ERR_NOMEM, "cwt: out of memory");
+  for (uint32_t i = 0; i < n; ++i) data[i] = (oc64){x[i], 0.0};
+  const oc64* shortv = K < n ? kern : data;
+  const oc64* longv = K < n ? data : kern;
+  const uint32_t ls = K < n ? K : n, ll = K < n ? n : K;
+  const uint32_t nout = n + K - 1, pad = nout - ll, flen = ll + 2 * pad;
+  oc64* fp = (oc64*)calloc(flen, sizeof(oc64));
+  oc64* conv = (oc64*)malloc((size_t)nout * sizeof(oc64));
+  if (!fp || !conv) {
+    free(data), free(fp), free(conv);
+    return fail(ORC_ERR_NOMEM, "cwt: out of memory");
+  }
+  for (uint32_t i = 0; i < ll; ++i) fp[pad + i] = longv[i];
+  for (uint32_t j = 0; j < nout; ++j) {
+    oc64 sum = {0.0, 0.0};
+    for (uint32_t i = 0; i < ls; ++i) sum = c_add(sum, c_mul(fp[(i + j) % flen], shortv[ls - 1 - i]));
+    conv[j] = sum;
+  }
+  /* get_coef_complex (:154-164): -sqrt(scale) times successive differences;
+   * then the centre n of them (cwt_complex.rs:205-211) */
+  const double ss = -1.0 * sqrt(scale);
+  const uint32_t clen = nout - 1;
+  const double half = (double)(clen - n) / 2.0;
+  const uint32_t down = (uint32_t)floor(half);
+  for (uint32_t i = 0; i < n; ++i) {
+    const uint32_t c = down + i;
+    out[i] = c_scale(c_sub(conv[c + 1], conv[c]), ss);
+  }
+  free(data), free(fp), free(conv);
+  return ORC_OK;
+}
+
+int orc_embedding_wavelet(uint64_t seed, uint64_t stream, uint32_t vocab, uint32_t src_dim, oc64* table,
+                          uint32_t* dim) {
+  if (!table || !dim || !vocab || src_dim < 2) return fail(ORC_ERR_ARG, "bad arguments");
+  const uint32_t DB1 = 0, SYMMETRIC = 2, LEVELS = 5, MIN_WIDTH = 28; /* wavelet_network.rs:13,43-53 */
+  const double SCALE0 = 2.0, FB = 1.5, FC = 1.0;                      /* the first of scales 2, 8, 16, 32 */
+  oc64* kern = NULL;
+  uint32_t K = 0;
+  int rc = cmor_kernel(SCALE0, FB, FC, &kern, &K); /* the same for every token */
+  if (rc) return rc;
+  double* pix = (double*)malloc((size_t)src_dim * sizeof(double));
+  double* t = (double*)malloc((size_t)(src_dim + 8) * 8 * sizeof(double));
+  oc64* row = (oc64*)malloc((size_t)src_dim * sizeof(oc64));
+  if (!pix || !t || !row) {
+    free(kern), free(pix), free(t), free(row);
+    return fail(ORC_ERR_NOMEM, "embedding: out of memory");
+  }
+  uint32_t width = 0;
+  for (uint32_t tok = 0; tok < vocab && !rc; ++tok) {
+    const double lo = -0.4, hi = 0.5;
+    for (uint32_t k = 0; k < src_dim; ++k) {
+      const double u = (double)(orc_draw(seed, stream, (uint64_t)tok * src_dim + k) >> 11) * 0x1.0p-53;
+      pix[k] = lo + (hi - lo) * u;
+    }
+    /* decompose_in_wavelets (:75-120) of a one-dimensional input: one row */
+    uint32_t w = src_dim;
+    for (uint32_t lv = 0; lv < LEVELS && !rc; ++lv) {
+      uint32_t R2 = 0, C2 = 0;
+      rc = orc_dwt_2d_full(pix, 1, w, DB1, SYMMETRIC, t, &R2, &C2);
+      if (rc || C2 < MIN_WIDTH) break;
+      /* get_ll_hl_lh_hh (dwt.rs:379-401): the first R2/2 rows, first C2/2 columns */
+      const uint32_t w2 = C2 >> 1;
+      for (uint32_t k = 0; k < w2; ++k) pix[k] = t[k];
+      w = w2;
+    }
+    if (rc) break;
+    rc = cwt_with_kernel(pix, w, kern, K, SCALE0, row);
+    for (uint32_t k = 0; k < w && !rc; ++k) table[(size_t)tok * w + k] = row[k];
+    width = w;
+  }
+  free(kern), free(pix), free(t), free(row);
+  if (rc) return rc;
+  *dim = width;
+  return ORC_OK;
+}
+
+int orc_init_embedding_wavelet(orc_net* net, uint32_t layer, uint64_t seed, uint32_t src_dim) {
+  if (!net || layer >= (uint32_t)net->n) return fail(ORC_ERR_ARG, "bad layer index");
+  orc_layer* L = &net->layers[layer];
+  if (L->kind != ORC_EMBEDDING) return fail(ORC_ERR_ARG, "layer %u is not an Embedding", layer);
+  oc64* t = (oc64*)malloc((size_t)L->vocab * src_dim * sizeof(oc64));
+  if (!t) return fail(ORC_ERR_NOMEM, "embedding: out of memory");
+  uint32_t dim = 0;
+  int rc = orc_embedding_wavelet(seed, stream_id(layer, 0xFFF), L->vocab, src_dim, t, &dim);
+  if (!rc && dim != L->d_out) rc = fail(ORC_ERR_ARG, "a %u-value draw decomposes to %u, not %u", src_dim, dim, L->d_out);
+  if (!rc) memcpy(L->table, t, (size_t)L->vocab * dim * sizeof(oc64));
+  free(t);
+  return rc;
+}

@@ -178,6 +178,29 @@ void orc_set_target_rows(orc_net* net, uint32_t T);
 int orc_dwt_backward(const oc64* G, uint32_t B, uint32_t S2, uint32_t S_in, uint32_t T, uint32_t wavelet, uint32_t d,
                      oc64* out);
 
+/* ---- EmbeddingLayer::create_embedding (embedding_layer.rs:65-77) ---- */
+/* dwt_2d_full (wavelet_transform/dwt.rs:20-34) of a rows x cols real matrix:
+ * dwt_1d of every row, then of every column of the result.  out holds at
+ * least (rows + 4) x (cols + 4) doubles; *out_rows, *out_cols its shape. */
+int orc_dwt_2d_full(const double* x, uint32_t rows, uint32_t cols, uint32_t wavelet, uint32_t mode, double* out,
+                    uint32_t* out_rows, uint32_t* out_cols);
+/* get_wavelet_complex (wavelet_transform/cwt_complex.rs:195-211) with the CMOR
+ * wavelet (cwt_type_resolver.rs:114-123; wavefun_complex at 2^10 points on
+ * its range -8..8, cwt_complex.rs:268-289) at one scale: the n complex
+ * coefficients of a real row of n. */
+int orc_cwt_cmor(const double* x, uint32_t n, double scale, double fb, double fc, oc64* out);
+/* create_embedding for tokens 0..vocab-1 with the project's seeded draw in
+ * place of rand::rng(): src_dim values uniform in [-0.4, 0.5) (index
+ * token * src_dim + k of the counter stream `stream`), then
+ * decompose_in_wavelet_2d_default (network_types/wavelet_network.rs:42-135)
+ * and its first scale's row.  table: vocab x *dim complex. */
+int orc_embedding_wavelet(uint64_t seed, uint64_t stream, uint32_t vocab, uint32_t src_dim, oc64* table,
+                          uint32_t* dim);
+/* EmbeddingLayer::new (embedding_layer.rs:40-62) for an Embedding layer:
+ * create_embedding for every token id, the draw on counter stream
+ * (layer << 12) | 0xFFF; the decomposed width must be the layer's dim. */
+int orc_init_embedding_wavelet(orc_net* net, uint32_t layer, uint64_t seed, uint32_t src_dim);
+
 #ifdef __cplusplus
 }
 #endif

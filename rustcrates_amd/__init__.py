@@ -50,6 +50,7 @@ SIGNATURES = {
     "mitok_add_discrete_wavelet": (_i32, [_P, _u32, _u32, _u32, _i32]),
     "mitok_seq_out_len": (_i32, [_P, _u32, _u32, _u32, _P]),
     "mitok_init_seeded": (_i32, [_P, _u64]),
+    "mitok_init_embedding_wavelet": (_i32, [_P, _u32, _u64, _u32]),
     "mitok_get_tensor": (_i32, [_P, _u32, _u32, _P, _u64]),
     "mitok_reset": (_i32, [_P]),
     "mitok_predict": (_i32, [_P, _P, _P, _u32, _u32, _P, _i32, _i32, _P, _P]),
@@ -311,6 +312,12 @@ class Network:
 
     def init_seeded(self, seed):
         _check(self._lib.mitok_init_seeded(self._h, seed))
+
+    def init_embedding_wavelet(self, layer=0, seed=0, src_dim=512):
+        """EmbeddingLayer::new's create_embedding for every token id
+        (embedding_layer.rs:40-77): a seeded uniform draw of src_dim values in
+        [-0.4, 0.5) decomposed by decompose_in_wavelet_2d_default."""
+        _check(self._lib.mitok_init_embedding_wavelet(self._h, int(layer), int(seed), int(src_dim)))
 
     def get_tensor(self, layer, slot, n):
         if slot == 3:

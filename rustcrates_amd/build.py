@@ -18,7 +18,7 @@ SRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libmitok.so")
 SOURCES = ["kernels.hip", "gemm.hip", "gemm_mfma.hip", "attention.hip", "resident.hip", "resident_k1.hip", "resident_k2.hip",
-           "resident_k4.hip", "resident_k8.hip", "train.hip", "network.hip"]
+           "resident_k4.hip", "resident_k8.hip", "train.hip", "wavelet_init.hip", "network.hip"]
 ARCH = os.environ.get("MITOK_ARCH", "gfx950")
 
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
@@ -40,7 +40,9 @@ _HOST_FEATURE_NOTE = "'-packed-fp32-ops' is not a recognized feature"
 # (the reason is in gemm_mfma.hip's header)
 FILE_FLAGS = {"gemm_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
               # the optimizer's arithmetic rounds every multiply and add, as Rust does
-              "train.hip": ["-ffp-contract=off"]}
+              "train.hip": ["-ffp-contract=off"],
+              # the wavelet embedding follows the reference's multiply and add order
+              "wavelet_init.hip": ["-ffp-contract=off"]}
 
 
 def source_hash() -> str:

@@ -94,15 +94,21 @@ REFERENCE_DIM = 16  # 512 / 2^DECOMPOSITION_LEVELS (wavelet_network.rs:13)
 WAVELET_DB2, WAVELET_MODE_SYMMETRIC = 1, 2  # DiscreteWaveletLayer::new (wavelet_discrete_layer.rs:46-70)
 
 
+REFERENCE_EMBEDDING_SRC = 512  # embedding_dim_original (transformer_builder.rs:23)
+
+
 def build_reference_default(net, vocab: int = REFERENCE_VOCAB, seed: int = 0, max_ctx: int = 512,
-                            mode: int = PRODUCTION):
+                            mode: int = PRODUCTION, wavelet_embedding: bool = True):
     """The layer stack create_transformer builds, in its order, with seeded
-    Xavier weights (the reference draws them unseeded):
+    weights where the reference draws them unseeded:
 
         Embedding(V, 16) -> DiscreteWavelet(DB2, SYMMETRIC) -> Norm(16, 1e-8)
         -> PositionalEncoding(16) -> SelfAttention(2 heads) -> FeedForward(16, 512)
         -> SelfAttention(4 heads) -> FeedForward(16, 1024) -> Linear(16, V) -> Softmax
-    """
+
+    The embedding table is EmbeddingLayer::new's (create_embedding of a
+    512-value draw per token, embedding_layer.rs:40-77), or with
+    wavelet_embedding=False Xavier-uniform like the other weights."""
     d = REFERENCE_DIM
     net.add_embedding(vocab, d)
     net.add_discrete_wavelet(d, WAVELET_DB2, WAVELET_MODE_SYMMETRIC)
@@ -114,6 +120,8 @@ def build_reference_default(net, vocab: int = REFERENCE_VOCAB, seed: int = 0, ma
     net.add_linear(d, vocab)
     net.add_softmax(mode)
     net.init_seeded(seed)
+    if wavelet_embedding:
+        net.init_embedding_wavelet(0, seed, REFERENCE_EMBEDDING_SRC)
     return net
 
 

@@ -283,6 +283,15 @@ int resident_grid(int cus, bool cooperative, int mr, int dh, size_t shm, int* gr
 int resident_launch(hipStream_t st, const ROp* ops_d, int nops, int nsteps, const RStep& step, int mr, int dh,
                     size_t shm, int grid, uint32_t* flags, uint32_t epoch0, uint32_t* err, uint64_t* stamps);
 
+// ---- EmbeddingLayer::create_embedding (wavelet_init.hip) ----
+constexpr int EW_MAX_SRC = 4096;  // drawn values per token (LDS: two rows of doubles)
+// width of a src-wide draw after decompose_in_wavelet_2d_default (0: src not a power of two in [2, EW_MAX_SRC])
+int embedding_wavelet_dim(int src);
+// table [vocab][dim] <- create_embedding of every token (key: the draw's counter stream);
+// kern_d: device room for kern_cap complex values (the CMOR integral, 33 at scale 2)
+int embedding_wavelet_init(hipStream_t st, double2* table, int vocab, int dim, int src, uint64_t key,
+                           double2* kern_d, size_t kern_cap);
+
 // ---- row kernels ----
 void embed(hipStream_t st, const double2* table, int V, int d, const uint32_t* ids, int rows, double2* out,
            uint32_t* err);

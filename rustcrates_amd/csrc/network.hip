@@ -1869,6 +1869,26 @@ int mitok_init_seeded(mitok_network* n, uint64_t seed) {
   return OK;
 }
 
+int mitok_init_embedding_wavelet(mitok_network* n, uint32_t layer, uint64_t seed, uint32_t src_dim) {
+  if (!n) return fail(ERR_ARG, "null network");
+  if (layer >= n->layers.size() || n->layers[layer]->kind != K_EMBEDDING)
+    return fail(ERR_ARG, "layer %u is not an Embedding", layer);
+  auto* E = (EmbeddingLayer*)n->layers[layer].get();
+  const int dim = embedding_wavelet_dim((int)src_dim);
+  if (dim == 0) return fail(ERR_ARG, "a draw of %u values: a power of two from 2 to %d", src_dim, EW_MAX_SRC);
+  if ((uint32_t)dim != E->d_out)
+    return fail(ERR_ARG, "a %u-value draw decomposes to %d values, the layer's dim is %u", src_dim, dim, E->d_out);
+  TRY(set_device(n));
+  DevBuf kern;
+  TRY(kern.reserve(64 * sizeof(double2)));
+  const int rc = embedding_wavelet_init(n->stream, E->table.as<double2>(), (int)E->vocab, dim, (int)src_dim,
+                                        stream_key(seed, stream_id(layer, 0xFFF)), kern.as<double2>(), 64);
+  if (rc == ERR_HIP) return fail(ERR_HIP, "embedding wavelet init: %s", hipGetErrorString(hipGetLastError()));
+  if (rc) return fail(rc, "embedding wavelet init: the CMOR integral");
+  n->cache_valid = false;
+  return check_err_word(n);
+}
+
 int mitok_get_tensor(mitok_network* n, uint32_t layer, uint32_t slot, double* out, uint64_t count) {
   if (!n || !out || layer >= n->layers.size()) return fail(ERR_ARG, "bad layer index");
   TRY(set_device(n));

@@ -110,3 +110,31 @@ def test_wavelet_after_attention_is_refused():
     with pytest.raises(ra.MitokError, match="after a SelfAttentionLayer"):
         g.add_discrete_wavelet(8, 1, 2)
     g.close()
+
+
+@pytest.mark.parametrize("vocab,src", [(300, 512), (50280, 512), (40, 1024), (40, 64), (40, 16)])
+def test_wavelet_embedding_init_matches_oracle(vocab, src):
+    """EmbeddingLayer::new's tables (create_embedding, embedding_layer.rs:
+    40-77) on the device against the checker: the seeded draw, five levels of
+    DB1/SYMMETRIC dwt_2d_full keeping LL, the CMOR CWT at scale 2.  The
+    device forms each value with the reference's multiplies and adds in its
+    order, no fused multiply-add, and the wavelet's integral from the same
+    host libm as the checker, so the tables are equal bit for bit."""
+    dim = {512: 16, 1024: 32, 64: 16, 16: 16}[src]
+    g, o = ra.Network(0), oracle.Network()
+    for net in (g, o):
+        net.add_embedding(vocab, dim)
+        net.add_linear(dim, 4)
+        net.init_seeded(7)
+        net.init_embedding_wavelet(0, 7, src)
+    tg = g.get_tensor(0, 0, vocab * dim).reshape(vocab, dim)
+    to = o.get_tensor(0, 0, vocab * dim).reshape(vocab, dim)
+    diff = int(np.sum(tg != to))
+    log(f"wavelet embedding vocab {vocab} src {src}: {diff} values differ, max |diff| {np.max(np.abs(tg - to)):.1e}")
+    assert diff == 0
+    with pytest.raises(ra.MitokError, match="power of two"):
+        g.init_embedding_wavelet(0, 7, 48)
+    with pytest.raises(ra.MitokError, match="decomposes"):
+        g.init_embedding_wavelet(0, 7, 2048 if dim == 16 else 512)  # decomposes to 64 or 16 values
+    g.close()
+    o.close()

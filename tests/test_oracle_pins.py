@@ -1218,3 +1218,90 @@ def test_cross_entropy_loss_gradient_is_the_softmax_backward():
         fd = (oracle.cross_entropy_loss_batch(_softmax_re(yp), targets, tl).real
               - oracle.cross_entropy_loss_batch(_softmax_re(ym), targets, tl).real) / (2 * h)
         assert abs(fd - G[idx]) < 1e-8, (idx, fd, G[idx])
+
+
+# --------------------------------------------------------------------------
+# EmbeddingLayer::create_embedding (embedding_layer.rs:65-77): the wavelet
+# decomposition of a seeded draw (network_types/wavelet_network.rs:42-135)
+# --------------------------------------------------------------------------
+def test_dwt_2d_full_reference_known_answers():
+    """wavelet_transform/tests.rs test_dwt: dwt_2d_full with DB1 and DB2 under
+    CONSTANT padding on a 2 x 5 matrix, and its quadrants, as the reference
+    asserts them (bit for bit)."""
+    t = oracle.dwt_2d_full(np.array([[1.0, 2.0, 3.0, 4.0, 5.0], [6.0, 7.0, 8.0, 9.0, 10.0]]), 0, 1)
+    np.testing.assert_array_equal(t, [[8.0, 12.000000000000004, 15.000000000000004, -0.9999999999999998,
+                                       -1.0000000000000004, 0.0],
+                                      [-5.0, -5.000000000000001, -5.000000000000001, -4.440892098500626e-16,
+                                       3.3306690738754696e-16, 0.0]])
+    t = oracle.dwt_2d_full(np.array([[1.15, 2.22, 3.36, 4.45, 5.59], [6.61, 7.72, 8.83, 9.94, 10.17]]), 1, 1)
+    r2, c2 = t.shape[0] // 2, t.shape[1] // 2
+    ll, lh, hl, hh = t[:r2, :c2], t[:r2, c2:], t[r2:, :c2], t[r2:, c2:]  # get_ll_hl_lh_hh's slicing
+    np.testing.assert_array_equal(ll, [[1.1055969296248855, 2.659056465474454, 7.315913630276377, 10.341801825333636],
+                                       [9.290106548568122, 10.882806465474454, 15.449230777830874, 17.21180182533364]])
+    np.testing.assert_array_equal(hl, [[-3.7267493523315185, -3.744617138124092, -3.7034392801983413,
+                                        -3.128198174666365],
+                                       [0.9985794793504406, 1.0033671381240925, 0.992333564346846,
+                                        0.838198174666366]])
+    np.testing.assert_array_equal(lh, [[-0.7283235910246749, 0.02329246824526906, 0.8107842982524609,
+                                        1.3710127121807463e-15],
+                                       [-0.7488139720814411, 0.0072876587736526175, 0.4722794887808437,
+                                        4.289572369704812e-16]])
+    np.testing.assert_array_equal(hh, [[0.009330127018921996, 0.007287658773652618, 0.15413538968048013,
+                                        4.2895723697048124e-16],
+                                       [-0.0025000000000000022, -0.0019527222831138048, -0.04130045318994102,
+                                        -1.1493874523372615e-16]])
+
+
+def test_cwt_cmor_reference_known_answers():
+    """wavelet_transform/tests.rs test_complex_cwt: the CMOR wavelet (fb 1.5,
+    fc 1.0) at scales 1 and 2 of [1, 0, 2, 3].  The reference's libm (cos, sin,
+    pow in the wavelet's samples) is not glibc, so the bar is the last few
+    bits: 4 ulp of the largest coefficient."""
+    want = {1.0: [-0.004341207903904784 - 0.04792095170673179j, 0.009888120380320968 - 0.039007421710709075j,
+                  0.008843541261772966 - 0.14354137865436362j, -0.03933261631675025 - 0.03484465231455147j],
+            2.0: [0.018158346044917232 - 0.26244860575825796j, 0.022844562479819492 + 0.26068461379594915j,
+                  -0.06664009905986391 - 0.11052301044784954j, 0.06891862214051149 - 0.12373587474793302j]}
+    for scale, w in want.items():
+        got = oracle.cwt_cmor([1.0, 0.0, 2.0, 3.0], scale)
+        w = np.array(w)
+        assert np.max(np.abs(got - w)) <= 4 * np.finfo(float).eps * np.max(np.abs(w)), (scale, got, w)
+
+
+def _wavelet_draw(seed, stream, tok, src):
+    u = (seeded.draw_np(seed, stream, np.arange(tok * src, (tok + 1) * src, dtype=np.uint64)) >> np.uint64(11))
+    u = u.astype(np.float64) * 2.0 ** -53
+    lo, hi = -0.4, 0.5
+    return lo + (hi - lo) * u
+
+
+def test_embedding_wavelet_is_the_decomposition_of_the_draw():
+    """create_embedding's pipeline (embedding_layer.rs:65-77) restated from the
+    pinned pieces: five levels of dwt_2d_full (DB1, SYMMETRIC) on the one-row
+    draw, each keeping the LL quadrant (the first row, first half), then the
+    CMOR CWT at the first scale (2.0).  Each DB1 level of a one-row input sums
+    neighbouring pairs (1/sqrt2 along the row, then sqrt2 down the one-element
+    columns), so after five levels every value is the sum of 32 consecutive
+    draws, which numpy checks independently; the draws lie in [-0.4, 0.5)."""
+    seed, stream, src = 11, (0 << 12) | 0xFFF, 512
+    table = oracle.embedding_wavelet(seed, stream, 6, src)
+    assert table.shape == (6, 16)
+    for tok in (0, 3, 5):
+        x = _wavelet_draw(seed, stream, tok, src)
+        assert x.min() >= -0.4 and x.max() < 0.5
+        row = x[None, :]
+        for _ in range(5):
+            t = oracle.dwt_2d_full(row, 0, 2)
+            assert t.shape == (2, row.shape[1])
+            row = t[:1, : t.shape[1] // 2]
+        np.testing.assert_allclose(row[0], x.reshape(16, 32).sum(axis=1), rtol=0, atol=1e-13)
+        np.testing.assert_array_equal(table[tok], oracle.cwt_cmor(row[0], 2.0))
+
+
+def test_embedding_wavelet_width_follows_the_minimum_width_rule():
+    """wavelet_network.rs:97-102: a level is skipped, and the loop ends, when
+    the transformed width is below 28; so 16- to 512-value draws end at 16
+    values (16: no level at all; 32: one), 1024 at 32."""
+    for src, dim in ((16, 16), (32, 16), (64, 16), (512, 16), (1024, 32)):
+        assert oracle.embedding_wavelet(1, 0xFFF, 2, src).shape == (2, dim), src
+    x16 = _wavelet_draw(1, 0xFFF, 0, 16)
+    np.testing.assert_array_equal(oracle.embedding_wavelet(1, 0xFFF, 1, 16)[0], oracle.cwt_cmor(x16, 2.0))

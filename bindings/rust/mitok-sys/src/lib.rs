@@ -129,6 +129,7 @@ extern "C" {
     pub fn mitok_set_decode_plan(net: *mut MitokNetwork, plan: c_int) -> c_int;
     pub fn mitok_resident_profile(net: *mut MitokNetwork, enable: c_int, max_ops: c_int, nops: *mut c_int,
                                   kinds: *mut c_int, us: *mut c_double) -> c_int;
+    pub fn mitok_resident_exchange(net: *mut MitokNetwork, mode: c_int, polled: *mut c_int) -> c_int;
 }
 
 /// A non-zero status and the library's message for it.

@@ -331,6 +331,14 @@ int mitok_set_decode_plan(mitok_network* net, int plan);
  * us[i], the microseconds from the previous barrier to the one after op i,
  * averaged over the steps.  No counterpart in the reference (instrumentation). */
 int mitok_resident_profile(mitok_network* net, int enable, int max_ops, int* nops, int* kinds, double* us);
+/* How the blocks of the resident decode loop hand values to each other.
+ * mode 1 (default): polling -- every exchanged value starts a step as a
+ * sentinel and its reader re-reads it until written, one grid barrier per
+ * step -- where that variant is built (one sequence, no RoPE); mode 0: a grid
+ * barrier after every operation.  mode -1 leaves it unchanged.  *polled (if
+ * not NULL): whether the last resident launch polled.  No counterpart in the
+ * reference (a scheduling choice; the arithmetic is the same either way). */
+int mitok_resident_exchange(mitok_network* net, int mode, int* polled);
 
 #ifdef __cplusplus
 }

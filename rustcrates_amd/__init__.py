@@ -77,6 +77,7 @@ SIGNATURES = {
     "mitok_device_synchronize": (_i32, [_i32]),
     "mitok_set_graph_mode": (_i32, [_P, _i32]),
     "mitok_set_decode_plan": (_i32, [_P, _i32]),
+    "mitok_resident_exchange": (_i32, [_P, _i32, C.POINTER(_i32)]),
     "mitok_resident_profile": (_i32, [_P, _i32, _i32, C.POINTER(_i32), C.POINTER(_i32), C.POINTER(C.c_double)]),
 }
 
@@ -568,6 +569,15 @@ class Network:
         _check(self._lib.mitok_resident_profile(self._h, int(enable), mx, C.byref(n), kinds, us))
         names = {0: "gemv", 1: "attn", 2: "rows"}
         return [(names.get(kinds[i], "?"), us[i]) for i in range(n.value)]
+
+    def resident_exchange(self, mode: int = -1) -> bool:
+        """mode 1: the resident loop's blocks exchange values by polling them
+        (one grid barrier per step) where that is built; 0: a grid barrier
+        after every operation; -1: unchanged.  Returns whether the last
+        resident launch polled."""
+        polled = _i32()
+        _check(self._lib.mitok_resident_exchange(self._h, int(mode), C.byref(polled)))
+        return bool(polled.value)
 
     def set_decode_plan(self, plan: int):
         """3: generate's decode loop for up to 8 sequences as one resident

@@ -265,6 +265,13 @@ struct RStep {
   int* hist_cnt = nullptr;  // [B] ids generated so far (also the logits-history slot)
   int* kv_len = nullptr;    // [B]
   uint32_t* err = nullptr;
+  // polling exchange (the ops of even steps, then those of odd steps): the odd
+  // steps' argmax partials, and the exchange arena [2][arena_half doubles]
+  // whose half of the previous step each step fills with the sentinel
+  const double* part_v1 = nullptr;
+  const int* part_i1 = nullptr;
+  double* arena = nullptr;
+  long arena_half = 0;
 };
 struct ResGemvPlan {
   int mr, C, kw, P, ncb, waves;
@@ -276,12 +283,28 @@ ResGemvPlan resident_gemv_plan(int M, int N, int K, bool part, int grid);
 size_t resident_op_lds(const ROp& op);  // dynamic LDS of one operation
 // blocks of the launch (one per CU: `cus` compute units, cooperative launch
 // supported) if the kernel for (mr, dh) fits with `shm`
-int resident_grid(int cus, bool cooperative, int mr, int dh, size_t shm, int* grid);
+int resident_grid(int cus, bool cooperative, int mr, int dh, size_t shm, int* grid, bool poll = false);
+// the polling exchange is built for mr rows
+bool resident_poll_built(int mr);
 // flags: one word per block, epochs below epoch0 + 1 (zeroed at set-up); the
-// launch performs nsteps * nops barriers.  stamps (optional, nsteps * nops + 1
-// words): block 0's wall clock (100 MHz) after each barrier, then at the start.
+// launch performs resident_barriers(nops, nsteps, poll) barriers.  poll: the
+// polling exchange; ops_d then holds 2 * nops operations (the even steps',
+// then the odd steps'), and step.arena both halves already filled with the
+// sentinel.  stamps (optional, nsteps * nops + 1 words): block 0's wall clock
+// (100 MHz) after each operation, then at the start.
 int resident_launch(hipStream_t st, const ROp* ops_d, int nops, int nsteps, const RStep& step, int mr, int dh,
-                    size_t shm, int grid, uint32_t* flags, uint32_t epoch0, uint32_t* err, uint64_t* stamps);
+                    size_t shm, int grid, uint32_t* flags, uint32_t epoch0, uint32_t* err, uint64_t* stamps,
+                    bool poll = false);
+// grid barriers a launch performs (the epochs it consumes)
+inline uint32_t resident_barriers(int nops, int nsteps, bool poll) {
+  return poll ? (uint32_t)(nsteps > 0 ? nsteps - 1 : 0) : (uint32_t)nops * (uint32_t)nsteps;
+}
+// polling exchange: the sentinel every exchanged value starts a step as
+// (all bits set: a NaN no arithmetic produces; as an int, -1), and the rows of
+// positions [kv_len[b], kv_len[b] + n) of the caches [B][H][ctx][dh] filled with it
+constexpr unsigned long long RES_SENT = 0xFFFFFFFFFFFFFFFFull;
+void resident_kv_sentinel(hipStream_t st, double2* kc, double2* vc, int B, int H, int ctx, int dh, const int* kv_len,
+                          int n);
 
 // ---- EmbeddingLayer::create_embedding (wavelet_init.hip) ----
 constexpr int EW_MAX_SRC = 4096;  // drawn values per token (LDS: two rows of doubles)

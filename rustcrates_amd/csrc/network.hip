@@ -339,7 +339,11 @@ struct mitok_network {
   // one barrier flag per block (zeroed when allocated), the next barrier epoch
   std::vector<mitok::ROp> res_ops_h;
   mitok::DevBuf res_ops, res_flags, res_stamps;
-  mitok::DevBuf res_cnt;  // per (sequence, head) attention-chunk counters
+  mitok::DevBuf res_cnt;    // per (layer, sequence, head) attention-chunk counters
+  mitok::DevBuf res_arena;  // polling exchange: the exchanged values, two halves
+  int res_nops = 0;         // operations per step (res_ops_h holds two programs when polling)
+  int res_poll = 1;         // the polling exchange where it is built (else the grid barrier)
+  bool res_polled = false;  // the last resident launch polled
   uint32_t res_epoch = 0;
   int res_profile = 0;  // record per-operation times of the next resident launches
   uint32_t res_steps = 0;
@@ -436,7 +440,7 @@ static int check_err_word(Net* n) {
   if (e & EB_FFN_NONFINITE) return fail(ERR_NAN, "output ffn dense: The value is Not Valid (transformer_network.rs:408)");
   if (e & EB_ARGMAX_NAN) return fail(ERR_NAN, "greedy_decoding: NaN in logits (sampling_methods.rs:12)");
   if (e & EB_CTX_OVERFLOW) return fail(ERR_ARG, "context exceeds max_ctx");
-  if (e & EB_BARRIER) return fail(ERR_STATE, "resident decode: a grid barrier timed out");
+  if (e & EB_BARRIER) return fail(ERR_STATE, "resident decode: a grid barrier or an exchange poll timed out");
   if (e & EB_TRAIN_NONFINITE) return fail(ERR_NAN, "gradient in embedding is invalid, contains NaN or infinity values (embedding_layer.rs:242-250)");
   return fail(ERR_STATE, "device error word 0x%x", e);
 }
@@ -1217,12 +1221,35 @@ static bool resident_ok(const Net* n, const Spec& sp) {
   return true;
 }
 
-// Builds the step program into n->res_ops_h; *dh = the head dim the kernel
-// is specialised for (0: generic), *shm = its dynamic LDS, *tiles = the vocab
-// product's argmax partials per row.
-static int resident_build(Net* n, const Spec& sp, int grid, int* dh_out, size_t* shm_out, int* tiles_out) {
+// The polling exchange's buffers: every value one operation of a step hands
+// to another is carved, 256-byte aligned, from one half of the arena.
+struct ResArena {
+  char* base = nullptr;
+  size_t used = 0;  // bytes
+  template <class T>
+  T* take(size_t count) {
+    T* p = (T*)(base + used);
+    used += (count * sizeof(T) + 255) & ~(size_t)255;
+    return p;
+  }
+};
+
+struct ResBuilt {
+  int dh = 0;       // the head dim the kernel is specialised for (0: generic)
+  size_t shm = 0;   // its dynamic LDS
+  int tiles = 0;    // the vocab product's argmax partials per row
+  double* part_v = nullptr;  // where the vocab product leaves them
+  int* part_i = nullptr;
+  bool poll_ok = true;  // (with an arena) every operation reads its inputs by polling
+};
+
+// Builds the step program into n->res_ops_h.  With an arena, the exchanged
+// buffers come from it and poll_ok says whether the program is one the
+// polling exchange runs (no materialised rows, no RoPE, at most 8 partials).
+static int resident_build(Net* n, const Spec& sp, int grid, ResBuilt* rb, ResArena* ar = nullptr) {
   std::vector<ROp>& ops = n->res_ops_h;
   ops.clear();
+  *rb = ResBuilt();
   uint32_t* err = n->err_d.as<uint32_t>();
   const int B = sp.B, mr = res_mr(B);
   int* kv_len = n->kv_len_d.as<int>();
@@ -1233,13 +1260,17 @@ static int resident_build(Net* n, const Spec& sp, int grid, int* dh_out, size_t*
   int mat_next = 0;
   double2* parts[2] = {n->dp0.as<double2>(), n->dp1.as<double2>()};
   int part_next = 0;
+  size_t cnt_next = 0;  // chunk counters: distinct per layer
+  // the buffers of one exchange: the arena's, else the workspace's
+  auto rows_buf = [&](double2* ws, size_t count) { return ar ? ar->take<double2>(count) : ws; };
   auto materialize = [&]() {
+    if (ar) rb->poll_ok = false;
     ROp op;
     op.kind = ROP_ROWS;
     op.M = B;
     op.ro = pro;
     op.K = width;
-    op.out = mats[mat_next];
+    op.out = rows_buf(mats[mat_next], (size_t)B * width);
     op.ldo = width;
     op.cw = 256;
     op.items = pro.ln ? B : B * ((width + op.cw - 1) / op.cw);
@@ -1296,6 +1327,7 @@ static int resident_build(Net* n, const Spec& sp, int grid, int* dh_out, size_t*
       case K_POSENC: {
         auto* P = (PositionalEncodingLayer*)L;
         if (pro.rope_cs || pro.resid || pro.ln || pro.att.po) materialize();
+        if (ar) rb->poll_ok = false;  // RoPE is not in the polled prologue
         pro.rope_cs = P->cs.as<double2>();
         pro.rope_pos = sp.pos ? sp.pos : kv_len;
         pro.rope_off = sp.pos ? nullptr : rope_offsets(n);
@@ -1317,12 +1349,12 @@ static int resident_build(Net* n, const Spec& sp, int grid, int* dh_out, size_t*
         dh_k = (dh_k < 0 || dh_k == dh) ? dh : 0;
         if (pro.resid) materialize();  // its residual source is about to be overwritten
         fit_prologue(d);
-        double2* x1 = n->act0.as<double2>();  // the block input, kept for the residual
+        double2* x1 = rows_buf(n->act0.as<double2>(), (size_t)B * d);  // the block input, kept for the residual
         pro.save = x1;
         pro.ldsave = d;
         Epi e;
         e.mode = EPI_QKV;
-        e.out = n->qbuf.as<double2>();
+        e.out = rows_buf(n->qbuf.as<double2>(), (size_t)B * d);
         e.ldo = d;
         e.d = d;
         e.dh = dh;
@@ -1354,17 +1386,24 @@ static int resident_build(Net* n, const Spec& sp, int grid, int* dh_out, size_t*
         at.M = B;
         at.a = a;
         at.o = split_buffers(n, attention_split_plan(a), B, H);
-        at.q = n->qbuf.as<double2>();
+        if (ar) {
+          const size_t np = (size_t)B * H * at.o.nsplit;
+          at.o.pm = ar->take<double>(np);
+          at.o.pl = ar->take<double>(np);
+          at.o.po = ar->take<double2>(np * dh);
+        }
+        at.q = e.out;
         at.ldq = d;
         at.items = at.o.nsplit * H * B;
         // chunk combine + residual by the last chunk of each (sequence, head),
         // then the Norm (self_attention_layer.rs:101-124) in the next
         // product's prologue
-        if ((size_t)B * H > n->res_cnt.bytes / sizeof(uint32_t)) return fail(ERR_STATE, "chunk counters");
-        at.cnt = n->res_cnt.as<uint32_t>();
+        if (cnt_next + (size_t)B * H > n->res_cnt.bytes / sizeof(uint32_t)) return fail(ERR_STATE, "chunk counters");
+        at.cnt = n->res_cnt.as<uint32_t>() + cnt_next;
+        cnt_next += (size_t)B * H;
         at.ro.resid = x1;
         at.ro.ldr = d;
-        at.out = mats[mat_next];
+        at.out = rows_buf(mats[mat_next], (size_t)B * d);
         at.ldo = d;
         mat_next ^= 1;
         ops.push_back(at);
@@ -1383,18 +1422,19 @@ static int resident_build(Net* n, const Spec& sp, int grid, int* dh_out, size_t*
         Epi e1;  // Dense: + b1, GELU, pad rows 0 (layer.rs:132-166)
         e1.mode = EPI_GELU;
         e1.bias = F->b1.as<double2>();
-        e1.out = n->hbuf.as<double2>();
+        e1.out = rows_buf(n->hbuf.as<double2>(), (size_t)B * F->hidden);
         e1.ldo = F->hidden;
         e1.row_mask = sp.mask;
         e1.err = err;
         gemv(pro, F->w1.as<double2>(), F->hidden, F->d_in, e1, nullptr);
-        double2* out = parts[part_next];
+        const int P2 = resident_gemv_plan(B, F->d_out, F->hidden, true, grid).P;
+        double2* out = rows_buf(parts[part_next], (size_t)P2 * B * F->d_out);
         part_next ^= 1;
         Epi e2;
         e2.mode = EPI_PART;
         e2.out = out;
         e2.err = err;
-        RowOps h = rows_of(n->hbuf.as<double2>(), F->hidden);
+        RowOps h = rows_of(e1.out, F->hidden);
         h.err = err;
         const int p2 = gemv(h, F->w2.as<double2>(), F->d_out, F->hidden, e2, nullptr).P;
         pro = part_rows(out, p2, F->d_out);  // Linear: + b2; non-finite check (transformer_network.rs:408)
@@ -1416,13 +1456,23 @@ static int resident_build(Net* n, const Spec& sp, int grid, int* dh_out, size_t*
           e.hist_re = sp.hist_re;
           e.hist_cnt = sp.hist_cnt;
           Argmax am = *sp.am;
-          am.part_v = n->am_v.as<double>();
-          am.part_i = n->am_i.as<int>();
-          const int ncb = gemv(pro, Ln->w.as<double2>(), Ln->d_out, Ln->d_in, e, &am).ncb;
-          if ((size_t)B * ncb > n->am_v.bytes / sizeof(double)) return fail(ERR_STATE, "argmax partials");
-          *tiles_out = ncb;
+          const int ncb = resident_gemv_plan(B, Ln->d_out, Ln->d_in, false, grid).ncb;
+          if (ar) {
+            am.part_v = ar->take<double>((size_t)B * ncb);
+            am.part_i = ar->take<int>((size_t)B * ncb);
+          } else {
+            am.part_v = n->am_v.as<double>();
+            am.part_i = n->am_i.as<int>();
+            if ((size_t)B * ncb > n->am_v.bytes / sizeof(double)) return fail(ERR_STATE, "argmax partials");
+          }
+          if (gemv(pro, Ln->w.as<double2>(), Ln->d_out, Ln->d_in, e, &am).ncb != ncb)
+            return fail(ERR_STATE, "resident decode: vocab tiles");
+          rb->tiles = ncb;
+          rb->part_v = am.part_v;
+          rb->part_i = am.part_i;
         } else {
-          double2* out = parts[part_next];
+          const int PL = resident_gemv_plan(B, Ln->d_out, Ln->d_in, true, grid).P;
+          double2* out = rows_buf(parts[part_next], (size_t)PL * B * Ln->d_out);
           part_next ^= 1;
           Epi e;
           e.mode = EPI_PART;
@@ -1440,11 +1490,15 @@ static int resident_build(Net* n, const Spec& sp, int grid, int* dh_out, size_t*
     }
   }
   size_t shm = 0;
-  for (const ROp& op : ops) shm = std::max(shm, resident_op_lds(op));
+  for (const ROp& op : ops) {
+    shm = std::max(shm, resident_op_lds(op));
+    if (ar && op.kind == ROP_GEMV && (op.ro.npart > 8 || op.ro.att.po || op.ro.rope_cs || op.ro.resid))
+      rb->poll_ok = false;
+  }
   if (shm > RES_MAX_DYN_LDS) return fail(ERR_ARG, "resident decode: %zu bytes of LDS", shm);
-  if (*tiles_out <= 0) return fail(ERR_ARG, "resident decode: no vocab product");
-  *dh_out = dh_k < 0 ? 0 : dh_k;
-  *shm_out = shm;
+  if (rb->tiles <= 0) return fail(ERR_ARG, "resident decode: no vocab product");
+  rb->dh = dh_k < 0 ? 0 : dh_k;
+  rb->shm = shm;
   return OK;
 }
 
@@ -1459,11 +1513,11 @@ static int run_resident(Net* n, const Spec& sp, uint32_t nsteps) {
       am_elems = (size_t)sp.B * resident_gemv_plan(sp.B, n->layers[li]->d_out, n->layers[li]->d_in, false, grid).ncb;
   TRY(reserve(n, n->am_v, am_elems * sizeof(double)));
   TRY(reserve(n, n->am_i, am_elems * sizeof(int)));
-  // attention-chunk counters, zeroed before every launch (a launch that ran
-  // out on a barrier time-out may leave counts behind)
+  // attention-chunk counters, one set per layer, zeroed before every launch (a
+  // launch that ran out on a time-out may leave counts behind)
   size_t bh = 0;
   for (auto& L : n->layers)
-    if (L->kind == K_SELF_ATTENTION) bh = std::max(bh, (size_t)sp.B * ((const SelfAttentionLayer*)L.get())->heads);
+    if (L->kind == K_SELF_ATTENTION) bh += (size_t)sp.B * ((const SelfAttentionLayer*)L.get())->heads;
   TRY(reserve(n, n->res_cnt, std::max<size_t>(bh, 1) * sizeof(uint32_t)));
   HIP_TRY(hipMemsetAsync(n->res_cnt.p, 0, n->res_cnt.bytes, n->stream));
   if (n->res_flags.bytes < (size_t)grid * sizeof(uint32_t)) {
@@ -1476,16 +1530,42 @@ static int run_resident(Net* n, const Spec& sp, uint32_t nsteps) {
   am.part_i = n->am_i.as<int>();
   Spec s2 = sp;
   s2.am = &am;
-  int dh = 0, tiles = 0;
-  size_t shm = 0;
-  TRY(resident_build(n, s2, grid, &dh, &shm, &tiles));
+  const int mr = res_mr(sp.B);
+  // the polling exchange: the program once per half of the arena (even and
+  // odd steps), if every operation of it polls its inputs
+  bool poll = n->res_poll && resident_poll_built(mr) && nsteps > 0;
+  ResBuilt rb, rb1;
+  size_t half = 0;
+  if (poll) {
+    TRY(reserve(n, n->res_arena, std::max<size_t>(n->res_arena.bytes, 1 << 20)));
+    for (;;) {
+      ResArena ar;
+      ar.base = (char*)n->res_arena.p;
+      TRY(resident_build(n, s2, grid, &rb, &ar));
+      half = ar.used;
+      if (!rb.poll_ok || 2 * half <= n->res_arena.bytes) break;
+      TRY(reserve(n, n->res_arena, 2 * half));  // grown: carve again from the new base
+    }
+    poll = rb.poll_ok;
+  }
+  if (poll) {
+    std::vector<ROp> even = n->res_ops_h;
+    ResArena ar;
+    ar.base = (char*)n->res_arena.p + half;
+    TRY(resident_build(n, s2, grid, &rb1, &ar));
+    if (ar.used != half || n->res_ops_h.size() != even.size()) return fail(ERR_STATE, "resident decode: arena halves");
+    n->res_ops_h.insert(n->res_ops_h.begin(), even.begin(), even.end());
+  } else {
+    TRY(resident_build(n, s2, grid, &rb));
+  }
+  const int nops = poll ? (int)n->res_ops_h.size() / 2 : (int)n->res_ops_h.size();
+  n->res_nops = nops;
   int g2 = 0;
-  TRY(launch_rc(resident_grid(n->cus, n->cooperative, res_mr(sp.B), dh, shm, &g2), "resident decode (grid)"));
+  TRY(launch_rc(resident_grid(n->cus, n->cooperative, mr, rb.dh, rb.shm, &g2, poll), "resident decode (grid)"));
   if (g2 != grid) return fail(ERR_STATE, "resident decode: grid %d != %d", g2, grid);
   const size_t ob = n->res_ops_h.size() * sizeof(ROp);
   TRY(reserve(n, n->res_ops, ob));
   HIP_TRY(hipMemcpyAsync(n->res_ops.p, n->res_ops_h.data(), ob, hipMemcpyHostToDevice, n->stream));
-  const int nops = (int)n->res_ops_h.size();
   uint64_t* stamps = nullptr;
   if (n->res_profile) {
     TRY(reserve(n, n->res_stamps, ((size_t)nops * nsteps + 1) * sizeof(uint64_t)));
@@ -1494,19 +1574,36 @@ static int run_resident(Net* n, const Spec& sp, uint32_t nsteps) {
   n->res_steps = nsteps;
   RStep rst;
   rst.B = sp.B;
-  rst.part_v = am.part_v;
-  rst.part_i = am.part_i;
-  rst.tiles = tiles;
+  rst.part_v = rb.part_v;
+  rst.part_i = rb.part_i;
+  rst.tiles = rb.tiles;
   rst.ids = am.ids;
   rst.hist = am.hist;
   rst.hist_stride = am.hist_stride;
   rst.hist_cnt = am.hist_cnt;
   rst.kv_len = am.kv_len;
   rst.err = n->err_d.as<uint32_t>();
-  TRY(launch_rc(resident_launch(n->stream, n->res_ops.as<ROp>(), nops, (int)nsteps, rst, res_mr(sp.B), dh, shm, grid,
-                                n->res_flags.as<uint32_t>(), n->res_epoch, n->err_d.as<uint32_t>(), stamps),
+  if (poll) {
+    rst.part_v1 = rb1.part_v;
+    rst.part_i1 = rb1.part_i;
+    rst.arena = n->res_arena.as<double>();
+    rst.arena_half = (long)(half / sizeof(double));
+    // every exchanged value starts as the sentinel: both halves of the arena,
+    // and the cache rows this launch appends
+    HIP_TRY(hipMemsetAsync(n->res_arena.p, 0xFF, 2 * half, n->stream));
+    for (auto& L : n->layers)
+      if (L->kind == K_SELF_ATTENTION) {
+        auto* A = (SelfAttentionLayer*)L.get();
+        resident_kv_sentinel(n->stream, A->kc.as<double2>(), A->vc.as<double2>(), sp.B, A->heads, A->max_ctx, A->dh,
+                             n->kv_len_d.as<int>(), (int)nsteps);
+        HIP_TRY(hipGetLastError());
+      }
+  }
+  n->res_polled = poll;
+  TRY(launch_rc(resident_launch(n->stream, n->res_ops.as<ROp>(), nops, (int)nsteps, rst, mr, rb.dh, rb.shm, grid,
+                                n->res_flags.as<uint32_t>(), n->res_epoch, n->err_d.as<uint32_t>(), stamps, poll),
                 "resident decode"));
-  n->res_epoch += (uint32_t)nops * nsteps;
+  n->res_epoch += resident_barriers(nops, (int)nsteps, poll);
   return OK;
 }
 
@@ -3221,7 +3318,7 @@ int mitok_resident_profile(mitok_network* n, int enable, int max_ops, int* nops,
   n->res_profile = enable;
   if (!nops) return OK;
   *nops = 0;
-  const int no = (int)n->res_ops_h.size();
+  const int no = n->res_nops;
   if (!n->res_stamps.p || !n->res_steps || !no) return OK;
   const size_t cnt = (size_t)no * n->res_steps + 1;
   if (n->res_stamps.bytes < cnt * sizeof(uint64_t)) return OK;
@@ -3239,6 +3336,14 @@ int mitok_resident_profile(mitok_network* n, int enable, int max_ops, int* nops,
     if (us) us[i] = t / n->res_steps;
   }
   *nops = m;
+  return OK;
+}
+
+int mitok_resident_exchange(mitok_network* n, int mode, int* polled) {
+  if (!n) return fail(ERR_ARG, "null network");
+  if (mode < -1 || mode > 1) return fail(ERR_ARG, "resident exchange %d (-1 to 1)", mode);
+  if (mode >= 0) n->res_poll = mode;
+  if (polled) *polled = n->res_polled ? 1 : 0;
   return OK;
 }
 

@@ -6,20 +6,23 @@
 
 namespace mitok {
 
-// kernels of resident_k1/2/4/8.hip for a head dim (64 specialised, others generic)
-const void* resident_kernel_1(int dh);
+// kernels of resident_k1/2/4/8.hip for a head dim (64 specialised, others
+// generic); the polling exchange is built for one row (null elsewhere)
+const void* resident_kernel_1(int dh, bool poll);
 const void* resident_kernel_2(int dh);
 const void* resident_kernel_4(int dh);
 const void* resident_kernel_8(int dh);
 
-static const void* pick_kernel(int mr, int dh) {
+static const void* pick_kernel(int mr, int dh, bool poll) {
   switch (mr) {
-    case 1: return resident_kernel_1(dh);
-    case 2: return resident_kernel_2(dh);
-    case 4: return resident_kernel_4(dh);
-    default: return resident_kernel_8(dh);
+    case 1: return resident_kernel_1(dh, poll);
+    case 2: return poll ? nullptr : resident_kernel_2(dh);
+    case 4: return poll ? nullptr : resident_kernel_4(dh);
+    default: return poll ? nullptr : resident_kernel_8(dh);
   }
 }
+
+bool resident_poll_built(int mr) { return pick_kernel(mr, 0, true) != nullptr; }
 
 ResGemvPlan resident_gemv_plan(int M, int N, int K, bool part, int grid) {
   ResGemvPlan p;
@@ -64,25 +67,58 @@ size_t resident_op_lds(const ROp& op) {
   return 0;
 }
 
-int resident_grid(int cus, bool cooperative, int mr, int dh, size_t shm, int* grid) {
+int resident_grid(int cus, bool cooperative, int mr, int dh, size_t shm, int* grid, bool poll) {
   if (!cooperative) return ERR_STATE;
+  const void* k = pick_kernel(mr, dh, poll);
+  if (!k) return ERR_STATE;
   int occ = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, pick_kernel(mr, dh), 256, shm) != hipSuccess) return ERR_HIP;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k, 256, shm) != hipSuccess) return ERR_HIP;
   if (occ < 1) return ERR_STATE;
   *grid = cus;
   return OK;
 }
 
 int resident_launch(hipStream_t st, const ROp* ops_d, int nops, int nsteps, const RStep& step, int mr, int dh,
-                    size_t shm, int grid, uint32_t* flags, uint32_t epoch0, uint32_t* err, uint64_t* stamps) {
+                    size_t shm, int grid, uint32_t* flags, uint32_t epoch0, uint32_t* err, uint64_t* stamps,
+                    bool poll) {
   if (nops <= 0 || nsteps <= 0) return OK;
   if (step.B < 1 || step.B > 8 || step.B > mr) return ERR_ARG;
+  if (poll && (!step.arena || step.arena_half <= 0 || !step.part_v1 || !step.part_i1)) return ERR_ARG;
+  const void* k = pick_kernel(mr, dh, poll);
+  if (!k) return ERR_STATE;
   RStep sa = step;
   void* args[] = {(void*)&ops_d, (void*)&nops, (void*)&nsteps, (void*)&sa, (void*)&flags, (void*)&epoch0, (void*)&err,
                   (void*)&stamps};
-  if (hipLaunchCooperativeKernel(pick_kernel(mr, dh), dim3(grid), dim3(256), args, (unsigned)shm, st) != hipSuccess)
-    return ERR_HIP;
+  if (hipLaunchCooperativeKernel(k, dim3(grid), dim3(256), args, (unsigned)shm, st) != hipSuccess) return ERR_HIP;
   return OK;
+}
+
+// rows [kv_len[b], kv_len[b] + n) of every (sequence, head) cache, clipped to
+// ctx, set to the sentinel; one thread per complex element
+__global__ __launch_bounds__(256) void k_kv_sentinel(double2* kc, double2* vc, int H, int ctx, int dh,
+                                                     const int* kv_len, int n, long total) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total) return;
+  const long per_seq = (long)H * n * dh;
+  const int b = (int)(i / per_seq);
+  const long r = i - b * per_seq;
+  const int h = (int)(r / ((long)n * dh));
+  const long r2 = r - (long)h * n * dh;
+  const int j = (int)(r2 / dh), e = (int)(r2 - (long)j * dh);
+  const int p = kv_len[b] + j;
+  if (p < 0 || p >= ctx) return;
+  const long at = (((long)b * H + h) * ctx + p) * dh + e;
+  const double s = __longlong_as_double((long long)RES_SENT);
+  kc[at] = make_double2(s, s);
+  vc[at] = make_double2(s, s);
+}
+
+void resident_kv_sentinel(hipStream_t st, double2* kc, double2* vc, int B, int H, int ctx, int dh, const int* kv_len,
+                          int n) {
+  const long total = (long)B * H * n * dh;
+  if (total <= 0) return;
+  MITOK_LAUNCH(k_kv_sentinel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, kc, vc, H, ctx, dh, kv_len, n,
+               total);
 }
 
 }  // namespace mitok

@@ -63,6 +63,202 @@ struct AccRes {
   static __device__ __forceinline__ int cnt(const int*) { return res_cnt; }
 };
 
+// ---- polling exchange ---------------------------------------------------------
+// In the polling mode (k_resident<.., POLL = true>) no grid barrier separates
+// the operations of a step.  Every exchanged value -- activations, split
+// partials, the chunk outputs of attention, the cache rows appended this
+// step, the argmax partials -- starts the step as the sentinel RES_SENT and
+// its consumer re-reads it until it is not, so the data is its own flag: one
+// memory round trip where a barrier costs the producers' store
+// acknowledgements, a flag round trip and then the data's.  Each operation
+// reads only what earlier operations of the step wrote, and no producer ever
+// waits for a consumer, so the polls cannot deadlock.  Exchange buffers are
+// distinct per operation within a step and alternate between two halves of an
+// arena from step to step; after one grid barrier at the start of each step
+// (every block has finished the previous one) the blocks fill the previous
+// step's half with the sentinel again.  Every poll is bounded: past
+// RES_POLL_LIMIT rounds, or once another block has given up, it sets
+// EB_BARRIER and returns what it has, so the grid always drains.
+constexpr uint32_t RES_POLL_LIMIT = 1u << 20;
+static __shared__ uint32_t* res_err;  // the launch's error word (for the polls)
+
+__device__ __forceinline__ unsigned long long ld_bits(const double* p) {
+  return __hip_atomic_load((MITOK_GLOBAL unsigned long long*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool poll_give_up(uint32_t spin) {
+  if (spin >= RES_POLL_LIMIT) {
+    atomicOr(res_err, (uint32_t)EB_BARRIER);
+    return true;
+  }
+  return (spin & 63u) == 63u && (ld_dev(res_err) & EB_BARRIER);
+}
+// v[j] <- *p[j] for need[j], each re-read until it is not the sentinel; every
+// load is issued before the first check
+template <int N>
+__device__ __forceinline__ void poll2(const double2* const (&p)[N], const bool (&need)[N], double2 (&v)[N]) {
+  unsigned long long x[N], y[N];
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    x[j] = need[j] ? ld_bits(&p[j]->x) : 0ull;
+    y[j] = need[j] ? ld_bits(&p[j]->y) : 0ull;
+  }
+  for (uint32_t spin = 0;; ++spin) {
+    bool ok = true;
+#pragma unroll
+    for (int j = 0; j < N; ++j) ok &= x[j] != RES_SENT && y[j] != RES_SENT;
+    if (ok || poll_give_up(spin)) break;
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      if (x[j] == RES_SENT) x[j] = ld_bits(&p[j]->x);
+      if (y[j] == RES_SENT) y[j] = ld_bits(&p[j]->y);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < N; ++j) v[j] = make_double2(__longlong_as_double((long long)x[j]), __longlong_as_double((long long)y[j]));
+}
+__device__ __forceinline__ double2 poll2_one(const double2* p) {
+  const double2* a[1] = {p};
+  const bool n[1] = {true};
+  double2 v[1];
+  poll2<1>(a, n, v);
+  return v[0];
+}
+template <int N>
+__device__ __forceinline__ void poll_f64(const double* const (&p)[N], const bool (&need)[N], double (&v)[N]) {
+  unsigned long long x[N];
+#pragma unroll
+  for (int j = 0; j < N; ++j) x[j] = need[j] ? ld_bits(p[j]) : 0ull;
+  for (uint32_t spin = 0;; ++spin) {
+    bool ok = true;
+#pragma unroll
+    for (int j = 0; j < N; ++j) ok &= x[j] != RES_SENT;
+    if (ok || poll_give_up(spin)) break;
+#pragma unroll
+    for (int j = 0; j < N; ++j)
+      if (x[j] == RES_SENT) x[j] = ld_bits(p[j]);
+  }
+#pragma unroll
+  for (int j = 0; j < N; ++j) v[j] = __longlong_as_double((long long)x[j]);
+}
+template <int N>
+__device__ __forceinline__ void poll_i32(const int* const (&p)[N], const bool (&need)[N], int (&v)[N]) {
+#pragma unroll
+  for (int j = 0; j < N; ++j) v[j] = need[j] ? ld_dev(p[j]) : 0;
+  for (uint32_t spin = 0;; ++spin) {
+    bool ok = true;
+#pragma unroll
+    for (int j = 0; j < N; ++j) ok &= v[j] != -1;
+    if (ok || poll_give_up(spin)) break;
+#pragma unroll
+    for (int j = 0; j < N; ++j)
+      if (v[j] == -1) v[j] = ld_dev(p[j]);
+  }
+}
+
+// The prologue of a product in the polling exchange, block-wide: the block's
+// input rows m < M, columns [ka, ka + RL) -- an embedding gather, or rows or
+// the sum of split partials, polled until written -- then bias, the finite
+// check and GELU as ro_base, into LDS; with a LayerNorm (ka = 0, RL = K),
+// ro_ln on them.  The same operations in the same order as ro_build, so both
+// exchanges give the same bits.  Sources ro_build has and this does not
+// (RoPE, a residual, an attention combine) are refused on the host.  Ends
+// with a barrier.
+
+// RES_POLL_LOADS loads per thread in flight each round: NPP partial slots (the
+// partial count rounded up to a power of two) of RES_POLL_LOADS / NPP elements
+constexpr int RES_POLL_LOADS = 16;
+template <int NPP>
+__device__ __forceinline__ void rows_poll_src(const RowOps& r, int M, int K, int ka, int RL, int tot, int np,
+                                              double2* buf) {
+  constexpr int E = RES_POLL_LOADS / NPP;
+  for (int i0 = threadIdx.x; i0 < tot; i0 += 256 * E) {
+    double2 v[E];
+    int mm[E], kk[E];
+    bool ok[E];
+#pragma unroll
+    for (int u = 0; u < E; ++u) {
+      const int i = i0 + 256 * u;
+      mm[u] = i / RL;
+      kk[u] = ka + (i - mm[u] * RL);
+      ok[u] = i < tot && mm[u] < M && kk[u] < K;
+    }
+    if (r.table) {
+#pragma unroll
+      for (int u = 0; u < E; ++u) {
+        v[u] = make_double2(0.0, 0.0);
+        if (ok[u]) {
+          const uint32_t id = res_ids[mm[u]];
+          if (!(id == 1u || id >= (uint32_t)r.vocab)) v[u] = ld_glb(r.table + (long)id * K + kk[u]);  // PAD -> 0
+        }
+      }
+    } else {
+      const double2* pp[E * NPP];
+      bool need[E * NPP];
+      double2 t[E * NPP];
+#pragma unroll
+      for (int u = 0; u < E; ++u)
+#pragma unroll
+        for (int q = 0; q < NPP; ++q) {
+          need[u * NPP + q] = ok[u] && q < np;
+          pp[u * NPP + q] = r.x + (long)(ok[u] ? mm[u] : 0) * r.ldx + (ok[u] ? kk[u] : 0) + (long)q * r.part_stride;
+        }
+      poll2<E * NPP>(pp, need, t);
+#pragma unroll
+      for (int u = 0; u < E; ++u) {
+        v[u] = t[u * NPP];
+#pragma unroll
+        for (int q = 1; q < NPP; ++q)
+          if (q < np) v[u] = cadd(v[u], t[u * NPP + q]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < E; ++u) {
+      const int i = i0 + 256 * u;
+      if (i >= tot) continue;
+      double2 x = make_double2(0.0, 0.0);
+      if (ok[u]) {
+        x = v[u];
+        if (r.bias) x = cadd(x, ld_glb(r.bias + kk[u]));
+        if (r.finite_check && !(isfinite(x.x) && isfinite(x.y))) atomicOr(r.err, (uint32_t)EB_FFN_NONFINITE);
+        if (r.gelu) {
+          if (r.row_mask && ld_glb(r.row_mask + mm[u]) == 0u) {
+            x = make_double2(0.0, 0.0);
+          } else {
+            bool nan = false;
+            x = gelu_nc(x, &nan);
+            if (nan) atomicOr(r.err, (uint32_t)EB_GELU_NAN);
+          }
+        }
+      }
+      buf[i] = x;
+    }
+  }
+}
+
+template <int MR>
+__device__ __forceinline__ void res_rows_poll(const RowOps& r, int M, int K, int ka, int RL, int n0, int n1,
+                                              double2* buf, double2* st_mean, double2* st_sd) {
+  const int tot = MR * RL;
+  const int np = r.npart > 1 ? r.npart : 1;
+  if (r.table || np == 1) rows_poll_src<1>(r, M, K, ka, RL, tot, 1, buf);
+  else if (np == 2) rows_poll_src<2>(r, M, K, ka, RL, tot, np, buf);
+  else if (np <= 4) rows_poll_src<4>(r, M, K, ka, RL, tot, np, buf);
+  else rows_poll_src<8>(r, M, K, ka, RL, tot, np, buf);
+  __syncthreads();
+  if (!r.ln) return;
+  // gamma and beta: requested here (their latency hidden by the statistics),
+  // not with the polled rows (registers)
+  double2 gpre[LN_PRE], bpre[LN_PRE];
+#pragma unroll
+  for (int j = 0; j < LN_PRE; ++j) {
+    const int k = n0 + (int)threadIdx.x + 256 * j;
+    const bool ok = k < n1;
+    gpre[j] = ok ? ld_glb(r.gamma + k) : make_double2(0.0, 0.0);
+    bpre[j] = ok ? ld_glb(r.beta + k) : make_double2(0.0, 0.0);
+  }
+  ro_ln<MR, AccRes>(r, M, K, RL, n0, n1, buf, st_mean, st_sd, gpre, bpre);
+}
+
 // ---- grid barrier ----------------------------------------------------------
 constexpr uint32_t RES_SPIN_LIMIT = 1u << 22;  // ~several seconds of polling
 
@@ -179,7 +375,7 @@ __device__ __forceinline__ void prefetch_weights(const ROp& nx, double2 (&w)[RES
   }
 }
 
-template <int MR, int C>
+template <int MR, int C, bool POLL>
 __device__ __forceinline__ void r_gemv3(const ROp& op, int item, double2* lds2, double2* red, double2* st_mean,
                                         double2* st_sd, double2 (&w)[RES_NPF], bool have) {
   constexpr int RPW = 64 / C;
@@ -192,14 +388,16 @@ __device__ __forceinline__ void r_gemv3(const ROp& op, int item, double2* lds2, 
   const int kb0 = by * KB;
   const int n = bx * C + c;
   const bool col_ok = n < N;
-  if (!have && wave >= 1) gemv_weights<C>(op, item, w);
   const int ka = ro.ln ? 0 : kb0, RL = ro.ln ? K : KB;
-  RoLds L;
-  L.wts = (double*)(lds2 + MR * RL);
-  L.lsum = L.wts + (ro.att.po ? (size_t)M * ro.att.H * ro.att.nsplit : 0);
-  L.m0 = 0;
-  ro_prepare<AccRes>(ro, M, L);
-  ro_build<MR, AccRes>(ro, M, K, ka, RL, kb0, min(K, kb0 + KB), lds2, L, st_mean, st_sd);
+  if constexpr (!POLL) {  // polling: the caller requested the weights and built the rows
+    if (!have && wave >= 1) gemv_weights<C>(op, item, w);
+    RoLds L;
+    L.wts = (double*)(lds2 + MR * RL);
+    L.lsum = L.wts + (ro.att.po ? (size_t)M * ro.att.H * ro.att.nsplit : 0);
+    L.m0 = 0;
+    ro_prepare<AccRes>(ro, M, L);
+    ro_build<MR, AccRes>(ro, M, K, ka, RL, kb0, min(K, kb0 + KB), lds2, L, st_mean, st_sd);
+  }
   if (bx == 0 && by == 0 && tid < M) ro_check<AccRes>(ro, tid);
   const double2* xs = lds2 + (kb0 - ka);
   if (ro.save && bx == 0)
@@ -266,7 +464,8 @@ __device__ __forceinline__ void r_gemv3(const ROp& op, int item, double2* lds2, 
           wave_argmax(bv, bi);
           if (lane == 0) {
             st_dev(am.part_v + (long)m * op.ncb + bx, bv);
-            st_dev(am.part_i + (long)m * op.ncb + bx, bi);
+            // the polling exchange reads -1 as "not written": "no value" is -2 there
+            st_dev(am.part_i + (long)m * op.ncb + bx, (POLL && bi < 0) ? -2 : bi);
           }
         }
   }
@@ -283,9 +482,33 @@ __device__ __forceinline__ void stream_rows(double2 (&w)[NW], const double2* wp,
 // prev: this block's previous item of the operation (-1: none); when it
 // built the same rows (a LayerNorm's whole rows, or the same K split) they
 // are still in LDS and are not built again.
-template <int MR, int C>
+// The weights a product's item starts with, for the polling exchange: a
+// 3-wave product's RES_NPF rows of waves 1-3 (as gemv_weights), or a 4-wave
+// product's first 16 rows of every wave.  One code path for both layouts
+// (two sibling paths storing to the same registers defeat their promotion).
+template <int C>
+__device__ __forceinline__ void gemv_issue(const ROp& op, int item, double2 (&w)[RES_NPF], bool w3) {
+  constexpr int RPW = 64 / C;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int cw = w3 ? wave - 1 : wave;
+  const int r = lane / C, c = lane - (lane / C) * C;
+  const int bx = item % op.ncb, by = item / op.ncb;
+  const int k0 = by * op.waves * op.kw + cw * op.kw;
+  const int n = bx * C + c;
+  const int kmax = max(0, min(op.kw, op.K - k0));
+  const int nu = (n < op.N && kmax > r) ? (kmax - r + RPW - 1) / RPW : 0;
+  const double2* wp = op.W + (long)(k0 + r) * op.ldw + n;
+  const long wstep = (long)RPW * op.ldw;
+#pragma unroll
+  for (int u = 0; u < RES_NPF; ++u)
+    if (u < 16 || w3) w[u] = ld_stream(u < nu ? wp + u * wstep : &res_zero2);
+}
+
+// POLL: wf[0 .. 15] holds the first 16 weight rows and the rows are built
+// (the caller)
+template <int MR, int C, bool POLL>
 __device__ __forceinline__ void r_gemv4(const ROp& op, int item, int prev, double2* lds2, double2* red, double2* st_mean,
-                                        double2* st_sd) {
+                                        double2* st_sd, double2 (&wf)[RES_NPF]) {
   constexpr int RPW = 64 / C;
   const RowOps& ro = op.ro;
   const int M = op.M, N = op.N, K = op.K, kw = op.kw;
@@ -302,7 +525,7 @@ __device__ __forceinline__ void r_gemv4(const ROp& op, int item, int prev, doubl
   const double2* wp = op.W + (long)(k0 + r) * op.ldw + n;
   const long wstep = (long)RPW * op.ldw;
   const int ka = ro.ln ? 0 : kb0, RL = ro.ln ? K : KB;
-  RoLds L;
+  [[maybe_unused]] RoLds L;
   L.wts = (double*)(lds2 + MR * RL);
   L.lsum = L.wts + (ro.att.po ? (size_t)M * ro.att.H * ro.att.nsplit : 0);
   L.m0 = 0;
@@ -310,13 +533,17 @@ __device__ __forceinline__ void r_gemv4(const ROp& op, int item, int prev, doubl
   // two buffers of 8 rows per lane keep 16 weight loads in flight (a third
   // spills this kernel's registers); rows past nu load as zero
   double2 w0[8], w1[8];
-  stream_rows<0>(w0, wp, wstep, col_ok ? 0 : nu, nu);
-  stream_rows<0>(w1, wp, wstep, col_ok ? 8 : nu, nu);
-
-  const bool built = prev >= 0 && (ro.ln || prev / op.ncb == by);
-  if (!built) {
-    ro_prepare<AccRes>(ro, M, L);
-    ro_build<MR, AccRes>(ro, M, K, ka, RL, kb0, min(K, kb0 + KB), lds2, L, st_mean, st_sd);
+  if constexpr (POLL) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) w0[u] = wf[u], w1[u] = wf[8 + u];
+  } else {
+    stream_rows<0>(w0, wp, wstep, col_ok ? 0 : nu, nu);
+    stream_rows<0>(w1, wp, wstep, col_ok ? 8 : nu, nu);
+    const bool built = prev >= 0 && (ro.ln || prev / op.ncb == by);
+    if (!built) {
+      ro_prepare<AccRes>(ro, M, L);
+      ro_build<MR, AccRes>(ro, M, K, ka, RL, kb0, min(K, kb0 + KB), lds2, L, st_mean, st_sd);
+    }
   }
   if (bx == 0 && by == 0 && tid < M) ro_check<AccRes>(ro, tid);
   const double2* xs = lds2 + (kb0 - ka);
@@ -395,7 +622,8 @@ __device__ __forceinline__ void r_gemv4(const ROp& op, int item, int prev, doubl
           wave_argmax(bv, bi);
           if (lane == 0) {
             st_dev(am.part_v + (long)m * op.ncb + bx, bv);
-            st_dev(am.part_i + (long)m * op.ncb + bx, bi);
+            // the polling exchange reads -1 as "not written": "no value" is -2 there
+            st_dev(am.part_i + (long)m * op.ncb + bx, (POLL && bi < 0) ? -2 : bi);
           }
         }
   }
@@ -408,6 +636,7 @@ __device__ __forceinline__ void r_gemv4(const ROp& op, int item, int prev, doubl
 // sum, masked_attention_head.rs:201-208, then add_matrix_3d_c, utils/matrix.rs:
 // 600-613).  Thread (g, e) takes chunks g, g + G, ...; every load of the item
 // is requested before the first is used.
+template <bool POLL>
 __device__ __forceinline__ void r_combine(const ROp& op, int item) {
   constexpr int UPT = 16;  // chunks per thread kept in flight (ns <= 256, G >= 1)
   __shared__ double cw_s[256];
@@ -425,15 +654,40 @@ __device__ __forceinline__ void r_combine(const ROp& op, int item) {
   const int e = tid % dh, g = tid / dh;
   const bool act = g < G;
   double2 po[UPT];
-#pragma unroll
-  for (int u = 0; u < UPT; ++u) {
-    const int sidx = g + u * G;
-    po[u] = (act && sidx < ns) ? ld_dev(o.po + (base + sidx) * dh + e) : make_double2(0.0, 0.0);
-  }
-  const double pm = tid < ns ? ld_dev(o.pm + base + tid) : -INFINITY;
-  const double pl = tid < ns ? ld_dev(o.pl + base + tid) : 0.0;
+  double pm, pl, rres;
   const long col = (long)h * dh + e;
-  const double rres = (g == 0 && op.ro.resid) ? ld_dev(op.ro.resid + (long)b * op.ro.ldr + col).x : 0.0;
+  if constexpr (POLL) {  // the chunk outputs and the residual, polled together
+    const double2* pp[UPT + 1];
+    bool need[UPT + 1];
+    double2 t[UPT + 1];
+#pragma unroll
+    for (int u = 0; u < UPT; ++u) {
+      const int sidx = g + u * G;
+      need[u] = act && sidx < ns;
+      pp[u] = o.po + (base + (need[u] ? sidx : 0)) * dh + e;
+    }
+    need[UPT] = g == 0 && op.ro.resid;
+    pp[UPT] = need[UPT] ? op.ro.resid + (long)b * op.ro.ldr + col : o.po;
+    const double* pq[2] = {o.pm + base + (tid < ns ? tid : 0), o.pl + base + (tid < ns ? tid : 0)};
+    const bool nq[2] = {tid < ns, tid < ns};
+    double q2[2];
+    poll2<UPT + 1>(pp, need, t);
+    poll_f64<2>(pq, nq, q2);
+#pragma unroll
+    for (int u = 0; u < UPT; ++u) po[u] = need[u] ? t[u] : make_double2(0.0, 0.0);
+    rres = need[UPT] ? t[UPT].x : 0.0;
+    pm = tid < ns ? q2[0] : -INFINITY;
+    pl = tid < ns ? q2[1] : 0.0;
+  } else {
+#pragma unroll
+    for (int u = 0; u < UPT; ++u) {
+      const int sidx = g + u * G;
+      po[u] = (act && sidx < ns) ? ld_dev(o.po + (base + sidx) * dh + e) : make_double2(0.0, 0.0);
+    }
+    pm = tid < ns ? ld_dev(o.pm + base + tid) : -INFINITY;
+    pl = tid < ns ? ld_dev(o.pl + base + tid) : 0.0;
+    rres = (g == 0 && op.ro.resid) ? ld_dev(op.ro.resid + (long)b * op.ro.ldr + col).x : 0.0;
+  }
   // common max and chunk weights
   double mx = wave_max(pm);
   if (lane == 0) red_s[wave] = mx;
@@ -455,7 +709,7 @@ __device__ __forceinline__ void r_combine(const ROp& op, int item) {
     }
   }
   for (int sidx = g + UPT * G; act && sidx < ns; sidx += G) {  // beyond UPT chunks per thread
-    const double2 v = ld_dev(o.po + (base + sidx) * dh + e);
+    const double2 v = POLL ? poll2_one(o.po + (base + sidx) * dh + e) : ld_dev(o.po + (base + sidx) * dh + e);
     const double ww = cw_s[sidx];
     acc.x += v.x * ww;
     acc.y += v.y * ww;
@@ -477,7 +731,7 @@ __device__ __forceinline__ void r_combine(const ROp& op, int item) {
 // chunk's max m and sum l of exp(s - m), and o = sum exp(s - m) v.  The new
 // token's k and v were appended by the QKV epilogue of this step.  Keys,
 // values, bias and q are all requested before the first is used.
-template <int DH>
+template <int DH, bool POLL>
 __device__ __forceinline__ void r_attn(const ROp& op, int item) {
   constexpr int MAXC = 32;
   __shared__ double sc[MAXC];
@@ -509,7 +763,41 @@ __device__ __forceinline__ void r_attn(const ROp& op, int item) {
   double2 kv[NP][EPL];
   double bj[NP];
   double2 vv[VU];
-  if (DH > 0) {
+  if (DH > 0 && POLL) {
+    // keys, values (the new token's appended this step) and q, polled together
+    constexpr int NK = NP * EPL, NALL = NP * EPL + VU + 1;
+    const double2* pp[NALL];
+    bool need[NALL];
+    double2 t[NALL];
+#pragma unroll
+    for (int pass = 0; pass < NP; ++pass) {
+      const int j = pass * 16 + wave * 4 + kq;
+      const double2* kr = K + (long)(c0 + (j < nc ? j : 0)) * dh;
+#pragma unroll
+      for (int tt = 0; tt < EPL; ++tt) {
+        const int ee = sub + tt * LPK;
+        need[pass * EPL + tt] = j < nc && ee < dh;
+        pp[pass * EPL + tt] = kr + (ee < dh ? ee : 0);
+      }
+      bj[pass] = (j < nc && sub == 0) ? ld_glb(bias0 + c0 + j) : 0.0;
+    }
+#pragma unroll
+    for (int u = 0; u < VU; ++u) {
+      const int j = g + u * G;
+      need[NK + u] = g < G && j < nc;
+      pp[NK + u] = V + (long)(c0 + (need[NK + u] ? j : 0)) * dh + e;
+    }
+    need[NALL - 1] = tid < dh;
+    pp[NALL - 1] = op.q + (long)b * op.ldq + (long)h * dh + (tid < dh ? tid : 0);
+    poll2<NALL>(pp, need, t);
+#pragma unroll
+    for (int pass = 0; pass < NP; ++pass)
+#pragma unroll
+      for (int tt = 0; tt < EPL; ++tt) kv[pass][tt] = need[pass * EPL + tt] ? t[pass * EPL + tt] : make_double2(0.0, 0.0);
+#pragma unroll
+    for (int u = 0; u < VU; ++u) vv[u] = need[NK + u] ? t[NK + u] : make_double2(0.0, 0.0);
+    if (tid < dh) qs[tid] = t[NALL - 1];
+  } else if (DH > 0) {
 #pragma unroll
     for (int pass = 0; pass < NP; ++pass) {
       const int j = pass * 16 + wave * 4 + kq;
@@ -527,7 +815,11 @@ __device__ __forceinline__ void r_attn(const ROp& op, int item) {
       vv[u] = (g < G && j < nc) ? ld_dev(V + (long)(c0 + j) * dh + e) : make_double2(0.0, 0.0);
     }
   }
-  for (int ee = tid; ee < dh; ee += 256) qs[ee] = ld_dev(op.q + (long)b * op.ldq + (long)h * dh + ee);
+  if (!(DH > 0 && POLL))
+    for (int ee = tid; ee < dh; ee += 256) {
+      const double2* qp = op.q + (long)b * op.ldq + (long)h * dh + ee;
+      qs[ee] = POLL ? poll2_one(qp) : ld_dev(qp);
+    }
   __syncthreads();
   if (DH > 0) {
 #pragma unroll
@@ -549,7 +841,7 @@ __device__ __forceinline__ void r_attn(const ROp& op, int item) {
       if (j < nc) {
         const double2* kr = K + (long)(c0 + j) * dh;
         for (int ee = sub; ee < dh; ee += LPK) {
-          const double2 k2 = ld_dev(kr + ee), qv = qs[ee];
+          const double2 k2 = POLL ? poll2_one(kr + ee) : ld_dev(kr + ee), qv = qs[ee];
           acc += qv.x * k2.x - qv.y * k2.y;
         }
       }
@@ -581,7 +873,7 @@ __device__ __forceinline__ void r_attn(const ROp& op, int item) {
   } else if (g < G) {
     for (int j = g; j < nc; j += G) {
       const double p = sc[j];
-      const double2 v = ld_dev(V + (long)(c0 + j) * dh + e);
+      const double2 v = POLL ? poll2_one(V + (long)(c0 + j) * dh + e) : ld_dev(V + (long)(c0 + j) * dh + e);
       acc.x += p * v.x;
       acc.y += p * v.y;
     }
@@ -601,7 +893,7 @@ __device__ __forceinline__ void r_attn(const ROp& op, int item) {
   __syncthreads();  // LDS reuse by the next item
   // the last of the ceil(T / CH) chunks of (b, h) combines them: one grid
   // barrier per layer fewer than a separate combine operation
-  if (op.cnt && arrive_last(op.cnt + bh, (uint32_t)((T + CH - 1) / CH))) r_combine(op, (int)bh);
+  if (op.cnt && arrive_last(op.cnt + bh, (uint32_t)((T + CH - 1) / CH))) r_combine<POLL>(op, (int)bh);
 }
 
 // ---- ROP_ROWS --------------------------------------------------------------
@@ -631,8 +923,11 @@ __device__ __forceinline__ void r_rows(const ROp& op, int item, double2* lds2, d
 // Every block reduces the vocab product's per-tile (max, last index) partials
 // of each row (ties to the larger index) and advances its step state; block 0
 // writes ids, history, counts and KV lengths back for the host.
-__device__ __forceinline__ void step_argmax(const RStep& st, bool write) {
+template <bool POLL>
+__device__ __forceinline__ void step_argmax(const RStep& st, bool write, int prev_parity) {
   constexpr int U = 16;
+  const double* part_v = (POLL && prev_parity) ? st.part_v1 : st.part_v;
+  const int* part_i = (POLL && prev_parity) ? st.part_i1 : st.part_i;
   __shared__ double sv[4][8];
   __shared__ int si[4][8];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -644,11 +939,29 @@ __device__ __forceinline__ void step_argmax(const RStep& st, bool write) {
   for (int i0 = 0; i0 < tot; i0 += 256 * U) {
     double v[U];
     int ix[U];
+    if constexpr (POLL) {
+      const double* pv[U];
+      const int* pi[U];
+      bool need[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int i = i0 + tid + 256 * u;
-      v[u] = i < tot ? ld_dev(st.part_v + i) : -INFINITY;
-      ix[u] = i < tot ? ld_dev(st.part_i + i) : -1;
+      for (int u = 0; u < U; ++u) {
+        const int i = i0 + tid + 256 * u;
+        need[u] = i < tot;
+        pv[u] = part_v + (need[u] ? i : 0);
+        pi[u] = part_i + (need[u] ? i : 0);
+      }
+      poll_f64<U>(pv, need, v);
+      poll_i32<U>(pi, need, ix);
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (!need[u]) v[u] = -INFINITY, ix[u] = -1;
+    } else {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int i = i0 + tid + 256 * u;
+        v[u] = i < tot ? ld_dev(part_v + i) : -INFINITY;
+        ix[u] = i < tot ? ld_dev(part_i + i) : -1;
+      }
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -691,27 +1004,48 @@ __device__ __forceinline__ void step_argmax(const RStep& st, bool write) {
 }
 
 // ---- the resident kernel -----------------------------------------------------
-template <int MR>
+template <int MR, bool POLL>
 __device__ __forceinline__ void run_gemv(const ROp& op, int it, int prev, double2* lds2, double2* red, double2* st_mean,
                                          double2* st_sd, double2 (&w)[RES_NPF], bool have) {
+  if constexpr (POLL) {
+    // the weights are requested first, then the rows are polled and built
+    // (here, not per column width: one copy of the prologue in the kernel)
+    const int wave = threadIdx.x >> 6;
+    const bool w3 = op.waves == 3;
+    // (no product prefetches into a 4-wave one: w is free there)
+    if (!(w3 && (have || wave == 0))) switch (op.C) {
+        case 8: gemv_issue<8>(op, it, w, w3); break;
+        case 16: gemv_issue<16>(op, it, w, w3); break;
+        case 32: gemv_issue<32>(op, it, w, w3); break;
+        default: gemv_issue<64>(op, it, w, w3); break;
+      }
+    const RowOps& ro = op.ro;
+    const int by = it / op.ncb, KB = op.waves * op.kw, kb0 = by * KB;
+    const int ka = ro.ln ? 0 : kb0, RL = ro.ln ? op.K : KB;
+    // a block's earlier item of the product with the same rows left them in LDS
+    const bool built = !w3 && prev >= 0 && (ro.ln || prev / op.ncb == by);
+    if (!built) res_rows_poll<MR>(ro, op.M, op.K, ka, RL, kb0, min(op.K, kb0 + KB), lds2, st_mean, st_sd);
+  }
   if (op.waves == 3) {
     switch (op.C) {
-      case 8: r_gemv3<MR, 8>(op, it, lds2, red, st_mean, st_sd, w, have); break;
-      case 16: r_gemv3<MR, 16>(op, it, lds2, red, st_mean, st_sd, w, have); break;
-      case 32: r_gemv3<MR, 32>(op, it, lds2, red, st_mean, st_sd, w, have); break;
-      default: r_gemv3<MR, 64>(op, it, lds2, red, st_mean, st_sd, w, have); break;
+      case 8: r_gemv3<MR, 8, POLL>(op, it, lds2, red, st_mean, st_sd, w, have); break;
+      case 16: r_gemv3<MR, 16, POLL>(op, it, lds2, red, st_mean, st_sd, w, have); break;
+      case 32: r_gemv3<MR, 32, POLL>(op, it, lds2, red, st_mean, st_sd, w, have); break;
+      default: r_gemv3<MR, 64, POLL>(op, it, lds2, red, st_mean, st_sd, w, have); break;
     }
     return;
   }
   switch (op.C) {
-    case 8: r_gemv4<MR, 8>(op, it, prev, lds2, red, st_mean, st_sd); break;
-    case 16: r_gemv4<MR, 16>(op, it, prev, lds2, red, st_mean, st_sd); break;
-    case 32: r_gemv4<MR, 32>(op, it, prev, lds2, red, st_mean, st_sd); break;
-    default: r_gemv4<MR, 64>(op, it, prev, lds2, red, st_mean, st_sd); break;
+    case 8: r_gemv4<MR, 8, POLL>(op, it, prev, lds2, red, st_mean, st_sd, w); break;
+    case 16: r_gemv4<MR, 16, POLL>(op, it, prev, lds2, red, st_mean, st_sd, w); break;
+    case 32: r_gemv4<MR, 32, POLL>(op, it, prev, lds2, red, st_mean, st_sd, w); break;
+    default: r_gemv4<MR, 64, POLL>(op, it, prev, lds2, red, st_mean, st_sd, w); break;
   }
 }
 
-template <int MR, int DH>
+// POLL: the polling exchange (no barrier between operations; ops holds the
+// even steps' program, then the odd steps', nops each)
+template <int MR, int DH, bool POLL = false>
 __global__ __launch_bounds__(256) void k_resident(const ROp* __restrict__ ops, int nops, int nsteps, RStep step,
                                                   uint32_t* flags, uint32_t epoch0, uint32_t* err,
                                                   uint64_t* stamps) {
@@ -723,40 +1057,58 @@ __global__ __launch_bounds__(256) void k_resident(const ROp* __restrict__ ops, i
     res_kvl[threadIdx.x] = ld_dev(step.kv_len + threadIdx.x);
     res_ids[threadIdx.x] = ld_dev(step.ids + threadIdx.x);
   }
-  if (threadIdx.x == 0) res_cnt = ld_dev(step.hist_cnt);
+  if (threadIdx.x == 0) res_cnt = ld_dev(step.hist_cnt), res_err = err;
   __syncthreads();
   double2 wpf[RES_NPF];  // the next product's weights (waves 1-3)
   bool have = false;
   uint32_t epoch = epoch0;
   for (int s = 0; s < nsteps; ++s) {
-    if (s > 0) step_argmax(step, blockIdx.x == 0);
+    const ROp* sops = POLL ? ops + (long)(s & 1) * nops : ops;
+    if (s > 0) {
+      step_argmax<POLL>(step, blockIdx.x == 0, (s - 1) & 1);
+      if constexpr (POLL) {
+        // every block is past the previous step: its half of the arena becomes
+        // the sentinel again, for the step after this one
+        grid_barrier(flags, ++epoch, err, []() {});
+        double* half = step.arena + ((s - 1) & 1) * step.arena_half;
+        const long per = (step.arena_half + gridDim.x - 1) / gridDim.x;
+        const long lo = (long)blockIdx.x * per, hi = min(step.arena_half, lo + per);
+        for (long k = lo + threadIdx.x; k < hi; k += 256) st_dev(half + k, __longlong_as_double((long long)RES_SENT));
+      }
+    }
     for (int i = 0; i < nops; ++i) {
-      const ROp& op = ops[i];
+      const ROp& op = sops[i];
       for (int it = blockIdx.x; it < op.items; it += gridDim.x) {
         switch (op.kind) {
           case ROP_GEMV:
-            run_gemv<MR>(op, it, it == (int)blockIdx.x ? -1 : it - (int)gridDim.x, lds2, red, st_mean, st_sd, wpf,
-                         have && it == (int)blockIdx.x);
+            run_gemv<MR, POLL>(op, it, it == (int)blockIdx.x ? -1 : it - (int)gridDim.x, lds2, red, st_mean, st_sd,
+                               wpf, have && it == (int)blockIdx.x);
             break;
-          case ROP_ATTN: r_attn<DH>(op, it); break;
+          case ROP_ATTN: r_attn<DH, POLL>(op, it); break;
           default: r_rows(op, it, lds2, st_mean, st_sd); break;
         }
       }
       // the next operation (the next step's first after the last); a
-      // prefetched product has at most one item per block.  Its weights are
-      // requested during the barrier: requested earlier, they delay this
-      // operation's own stores and so the barrier.
+      // prefetched product has at most one item per block
       const bool last = s + 1 == nsteps && i + 1 == nops;
-      const ROp& nx = ops[i + 1 < nops ? i + 1 : 0];
+      const ROp& nx = i + 1 < nops ? sops[i + 1] : (POLL ? ops + (long)((s + 1) & 1) * nops : ops)[0];
       const bool pf = !last && nx.kind == ROP_GEMV && nx.waves == 3 && (int)blockIdx.x < nx.items;
-      grid_barrier(flags, ++epoch, err, [&]() {
-        if (pf) prefetch_weights(nx, wpf);
-      });
+      if constexpr (POLL) {
+        // no barrier: waves 1-3 request the next product's weights now, while
+        // wave 0 goes on to poll its inputs
+        if (pf && threadIdx.x >= 64) prefetch_weights(nx, wpf);
+      } else {
+        // its weights are requested during the barrier: requested earlier,
+        // they delay this operation's own stores and so the barrier
+        grid_barrier(flags, ++epoch, err, [&]() {
+          if (pf) prefetch_weights(nx, wpf);
+        });
+      }
       have = pf;
       if (stamps && blockIdx.x == 0 && threadIdx.x == 0) stamps[(long)s * nops + i] = wall_clock64();
     }
   }
-  if (blockIdx.x == 0) step_argmax(step, true);
+  if (blockIdx.x == 0) step_argmax<POLL>(step, true, (nsteps - 1) & 1);
 }
 
 }  // namespace mitok

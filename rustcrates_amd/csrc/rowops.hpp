@@ -254,7 +254,7 @@ __device__ void ro_stats(const RowOps& r, int M, int K, const RoLds& L, double2*
 // gpre/bpre: gamma and beta of this thread's first LN_PRE columns, requested
 // by the caller with the source rows.  Block-wide; ends with a barrier.
 template <int MR, class Acc = AccPlain>
-__device__ void ro_ln(const RowOps& r, int M, int K, int RL, int n0, int n1, double2* buf, double2* st_mean,
+__device__ __forceinline__ void ro_ln(const RowOps& r, int M, int K, int RL, int n0, int n1, double2* buf, double2* st_mean,
                       double2* st_sd, const double2 (&gpre)[LN_PRE], const double2 (&bpre)[LN_PRE]) {
   __shared__ double red_s[4][2 * MR], red_v[4][2 * MR];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;

@@ -241,13 +241,17 @@ struct ROp {
   Epi ep;
   Argmax am;
   // ATTN: chunks of attention_split_plan (items nsplit x H x B); q of sequence b at q + b * ldq.
-  //   cnt != null: per (b, h) chunk counters [B][H]; the last chunk of (b, h) to finish
-  //   combines the chunks: out[b][h*dh + e] = Re(chunk combine + ro.resid)
+  //   The combine out[b][h*dh + e] = Re(chunk combine + ro.resid) of (b, h):
+  //   barrier exchange: the last chunk to finish (cnt: counters [B][H]);
+  //   polling exchange: the item of (b, h)'s last split, after its chunk if
+  //   that has keys (comb_items 0), or items nsplit x H x B + b * H + h
+  //   after all the chunks (comb_items 1: more items than blocks)
   Attn a;
   AttnSplit o;
   const double2* q = nullptr;
   long ldq = 0;
   uint32_t* cnt = nullptr;
+  int comb_items = 0;
   // ROWS: out[m][k] = rowops(ro)[m][k], k < K, in column chunks of cw (whole rows with a LayerNorm)
   double2* out = nullptr;
   long ldo = 0;

@@ -1394,7 +1394,13 @@ static int resident_build(Net* n, const Spec& sp, int grid, ResBuilt* rb, ResAre
         }
         at.q = e.out;
         at.ldq = d;
+        // polling: (b, h)'s last split combines it where every chunk has a
+        // block of its own, else the combines are items after the chunks
         at.items = at.o.nsplit * H * B;
+        if (ar && at.items > grid) {
+          at.comb_items = 1;
+          at.items += B * H;
+        }
         // chunk combine + residual by the last chunk of each (sequence, head),
         // then the Norm (self_attention_layer.rs:101-124) in the next
         // product's prologue

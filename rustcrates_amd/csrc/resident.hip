@@ -72,7 +72,10 @@ int resident_grid(int cus, bool cooperative, int mr, int dh, size_t shm, int* gr
   const void* k = pick_kernel(mr, dh, poll);
   if (!k) return ERR_STATE;
   int occ = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k, 256, shm) != hipSuccess) return ERR_HIP;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k, 256, shm) != hipSuccess) {
+    (void)hipGetLastError();  // a size the device refuses: no fault to report later
+    return ERR_STATE;
+  }
   if (occ < 1) return ERR_STATE;
   *grid = cus;
   return OK;

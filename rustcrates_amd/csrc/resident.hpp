@@ -238,6 +238,16 @@ __device__ __forceinline__ void rows_poll_src(const RowOps& r, int M, int K, int
 template <int MR>
 __device__ __forceinline__ void res_rows_poll(const RowOps& r, int M, int K, int ka, int RL, int n0, int n1,
                                               double2* buf, double2* st_mean, double2* st_sd) {
+  // the LayerNorm's gamma and beta of this thread's first columns are
+  // requested with the polled rows, not after the statistics
+  double2 gpre[LN_PRE], bpre[LN_PRE];
+#pragma unroll
+  for (int j = 0; j < LN_PRE; ++j) {
+    const int k = n0 + (int)threadIdx.x + 256 * j;
+    const bool ok = r.ln && k < n1;
+    gpre[j] = ok ? ld_glb(r.gamma + k) : make_double2(0.0, 0.0);
+    bpre[j] = ok ? ld_glb(r.beta + k) : make_double2(0.0, 0.0);
+  }
   const int tot = MR * RL;
   const int np = r.npart > 1 ? r.npart : 1;
   if (r.table || np == 1) rows_poll_src<1>(r, M, K, ka, RL, tot, 1, buf);
@@ -245,18 +255,7 @@ __device__ __forceinline__ void res_rows_poll(const RowOps& r, int M, int K, int
   else if (np <= 4) rows_poll_src<4>(r, M, K, ka, RL, tot, np, buf);
   else rows_poll_src<8>(r, M, K, ka, RL, tot, np, buf);
   __syncthreads();
-  if (!r.ln) return;
-  // gamma and beta: requested here (their latency hidden by the statistics),
-  // not with the polled rows (registers)
-  double2 gpre[LN_PRE], bpre[LN_PRE];
-#pragma unroll
-  for (int j = 0; j < LN_PRE; ++j) {
-    const int k = n0 + (int)threadIdx.x + 256 * j;
-    const bool ok = k < n1;
-    gpre[j] = ok ? ld_glb(r.gamma + k) : make_double2(0.0, 0.0);
-    bpre[j] = ok ? ld_glb(r.beta + k) : make_double2(0.0, 0.0);
-  }
-  ro_ln<MR, AccRes>(r, M, K, RL, n0, n1, buf, st_mean, st_sd, gpre, bpre);
+  if (r.ln) ro_ln<MR, AccRes>(r, M, K, RL, n0, n1, buf, st_mean, st_sd, gpre, bpre);
 }
 
 // ---- grid barrier ----------------------------------------------------------
@@ -741,12 +740,28 @@ __device__ __forceinline__ void r_attn(const ROp& op, int item) {
   const Attn& a = op.a;
   const AttnSplit& o = op.o;
   const int dh = DH > 0 ? DH : a.dh;
+  if constexpr (POLL) {
+    // items past the chunks: the combine of (sequence, head) item - chunks,
+    // polling the chunks' outputs (every chunk item precedes every combine
+    // item in a block's order, so no block waits on its own later work)
+    const int nchunk = o.nsplit * a.H * op.M;
+    if (item >= nchunk) {
+      r_combine<true>(op, item - nchunk);
+      return;
+    }
+  }
   const int split = item % o.nsplit, h = (item / o.nsplit) % a.H, b = item / (o.nsplit * a.H);
+  // polling, one item per block: the last split's block combines (b, h); its
+  // chunk is empty unless the keys reach it, so it polls the other chunks at once
+  const bool comb_here = POLL && !op.comb_items && split == o.nsplit - 1;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int T = res_kvl[b] + 1;
   const int CH = o.CH;
   const int c0 = split * CH;
-  if (c0 >= T) return;  // uniform over the block
+  if (c0 >= T) {  // uniform over the block
+    if (comb_here) r_combine<true>(op, b * a.H + h);
+    return;
+  }
   const int nc = min(CH, T - c0);
   const long bh = (long)b * a.H + h;
   const double2* K = a.kc + bh * a.ctx * dh;
@@ -891,9 +906,10 @@ __device__ __forceinline__ void r_attn(const ROp& op, int item) {
     st_dev((double*)o.pl + pidx, stat[1]);
   }
   __syncthreads();  // LDS reuse by the next item
-  // the last of the ceil(T / CH) chunks of (b, h) combines them: one grid
-  // barrier per layer fewer than a separate combine operation
-  if (op.cnt && arrive_last(op.cnt + bh, (uint32_t)((T + CH - 1) / CH))) r_combine<POLL>(op, (int)bh);
+  // barrier exchange: the last of the ceil(T / CH) chunks of (b, h) combines
+  // them (one grid barrier per layer fewer than a separate combine operation)
+  if (!POLL && op.cnt && arrive_last(op.cnt + bh, (uint32_t)((T + CH - 1) / CH))) r_combine<POLL>(op, (int)bh);
+  if (comb_here) r_combine<true>(op, (int)bh);
 }
 
 // ---- ROP_ROWS --------------------------------------------------------------
@@ -1078,6 +1094,29 @@ __global__ __launch_bounds__(256) void k_resident(const ROp* __restrict__ ops, i
     }
     for (int i = 0; i < nops; ++i) {
       const ROp& op = sops[i];
+      // the next operation (the next step's first after the last); a
+      // prefetched product has at most one item per block
+      const bool last = s + 1 == nsteps && i + 1 == nops;
+      const ROp& nx = i + 1 < nops ? sops[i + 1] : (POLL ? ops + (long)((s + 1) & 1) * nops : ops)[0];
+      const bool pf = !last && nx.kind == ROP_GEMV && nx.waves == 3 && (int)blockIdx.x < nx.items;
+      bool early = false;
+      if constexpr (POLL) {
+        // a block whose attention item has no keys (at most a combine, which
+        // waits for the other chunks anyway) requests the next product's
+        // weights now: a late request would hold up its next poll
+        if (pf && op.kind == ROP_ATTN && !op.comb_items) {
+          const int it = blockIdx.x;
+          bool empty = it >= op.items;
+          if (!empty) {
+            const int b = it / (op.o.nsplit * op.a.H);
+            empty = (it % op.o.nsplit) * op.o.CH >= res_kvl[b] + 1;
+          }
+          if (empty) {
+            if (threadIdx.x >= 64) prefetch_weights(nx, wpf);
+            early = true;
+          }
+        }
+      }
       for (int it = blockIdx.x; it < op.items; it += gridDim.x) {
         switch (op.kind) {
           case ROP_GEMV:
@@ -1088,15 +1127,9 @@ __global__ __launch_bounds__(256) void k_resident(const ROp* __restrict__ ops, i
           default: r_rows(op, it, lds2, st_mean, st_sd); break;
         }
       }
-      // the next operation (the next step's first after the last); a
-      // prefetched product has at most one item per block
-      const bool last = s + 1 == nsteps && i + 1 == nops;
-      const ROp& nx = i + 1 < nops ? sops[i + 1] : (POLL ? ops + (long)((s + 1) & 1) * nops : ops)[0];
-      const bool pf = !last && nx.kind == ROP_GEMV && nx.waves == 3 && (int)blockIdx.x < nx.items;
       if constexpr (POLL) {
-        // no barrier: waves 1-3 request the next product's weights now, while
-        // wave 0 goes on to poll its inputs
-        if (pf && threadIdx.x >= 64) prefetch_weights(nx, wpf);
+        // no barrier: waves 1-3 request the next product's weights now
+        if (pf && !early && threadIdx.x >= 64) prefetch_weights(nx, wpf);
       } else {
         // its weights are requested during the barrier: requested earlier,
         // they delay this operation's own stores and so the barrier

@@ -36,6 +36,9 @@ def log(msg):
 C3S = configs.ModelConfig("c3s", layers=2, d=512, heads=8, ffn=2048, vocab=4000, max_ctx=192, seed=2)
 # head dim 16: the generic attention path of the kernel
 SMALL = configs.ModelConfig("small", layers=2, d=64, heads=4, ffn=128, vocab=1000, max_ctx=160, seed=21)
+# a long context: more attention chunks than blocks, so the combines are
+# items of their own after the chunks
+LONG = configs.ModelConfig("long", layers=2, d=128, heads=8, ffn=256, vocab=1000, max_ctx=2048, seed=33)
 # RoPE after the embedding: a prologue the polled loop does not run
 ROPE = configs.ModelConfig("rope", layers=2, d=64, heads=4, ffn=128, vocab=1000, max_ctx=96, seed=5, rope=True)
 
@@ -48,11 +51,13 @@ def _run(g, prompt, n_new, mode):
     return ids, lg, loop, g.resident_exchange(-1)
 
 
-@pytest.mark.parametrize("cfg,plen,n_new", [(C3S, 40, 20), (C3S, 150, 33), (SMALL, 12, 64), (SMALL, 90, 7)])
+@pytest.mark.parametrize("cfg,plen,n_new", [(C3S, 40, 20), (C3S, 150, 33), (SMALL, 12, 64), (SMALL, 90, 7),
+                                            (LONG, 300, 12), (LONG, 1990, 9)])
 def test_polled_and_barrier_loops_match_oracle(cfg, plen, n_new):
     """Batch 1: both exchanges against the oracle, at even and odd step
-    counts (the last step's argmax partials in either half of the arena) and
-    with many attention chunks (prompts near the context)."""
+    counts (the last step's argmax partials in either half of the arena),
+    with many attention chunks (prompts near the context) and with more
+    chunks than blocks."""
     g = configs.build_network(ra.Network(0), cfg)
     o = configs.build_network(oracle.Network(), cfg)
     prompt = seeded.prompts(80 + plen, [plen], cfg.vocab)

@@ -314,8 +314,10 @@ int mitok_device_synchronize(int device);
 /* 0 = replay decode steps as HIP graphs (default), 1 = launch kernels directly. */
 int mitok_set_graph_mode(mitok_network* net, int direct_launch);
 /* 3 = generate's decode loop for up to 8 sequences runs as one resident
- *     cooperative launch (one block per CU, grid barriers between operations);
- * 2 = the resident loop at batch 1, plan 1 for 2 to 64 sequences (default);
+ *     cooperative launch (one block per CU; how its blocks exchange values:
+ *     mitok_resident_exchange);
+ * 2 = the resident loop for 1 and 2 sequences (1 if the polling exchange is
+ *     off or a RoPE layer rules it out), plan 1 above (default);
  * 1 = decode steps of up to 64 sequences run the fused plan (up to 8: GEMV
  *     products with the row transforms in their prologues; 9 to 64: skinny
  *     MFMA products after a row-transform launch), replayed as a graph;
@@ -334,9 +336,9 @@ int mitok_resident_profile(mitok_network* net, int enable, int max_ops, int* nop
 /* How the blocks of the resident decode loop hand values to each other.
  * mode 1 (default): polling -- every exchanged value starts a step as a
  * sentinel and its reader re-reads it until written, one grid barrier per
- * step -- where that variant is built (one sequence, no RoPE); mode 0: a grid
- * barrier after every operation.  mode -1 leaves it unchanged.  *polled (if
- * not NULL): whether the last resident launch polled.  No counterpart in the
+ * step -- where the program allows it (no RoPE); mode 0: a grid barrier
+ * after every operation.  mode -1 leaves it unchanged.  *polled (if not
+ * NULL): whether the last resident launch polled.  No counterpart in the
  * reference (a scheduling choice; the arithmetic is the same either way). */
 int mitok_resident_exchange(mitok_network* net, int mode, int* polled);
 

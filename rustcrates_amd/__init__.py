@@ -572,16 +572,17 @@ class Network:
 
     def resident_exchange(self, mode: int = -1) -> bool:
         """mode 1: the resident loop's blocks exchange values by polling them
-        (one grid barrier per step) where that is built; 0: a grid barrier
-        after every operation; -1: unchanged.  Returns whether the last
-        resident launch polled."""
+        (one grid barrier per step) where the program allows it (no RoPE);
+        0: a grid barrier after every operation; -1: unchanged.  Returns
+        whether the last resident launch polled."""
         polled = _i32()
         _check(self._lib.mitok_resident_exchange(self._h, int(mode), C.byref(polled)))
         return bool(polled.value)
 
     def set_decode_plan(self, plan: int):
         """3: generate's decode loop for up to 8 sequences as one resident
-        launch; 2: resident at batch 1, fused above (default); 1 (True):
+        launch; 2: resident for 1 and 2 sequences (1 without the polling
+        exchange), fused above (default); 1 (True):
         fused launches, replayed as a graph; 0 (False): one launch per
         reference operation."""
         _check(self._lib.mitok_set_decode_plan(self._h, int(plan)))

@@ -1202,9 +1202,15 @@ static int res_mr(int B) { return B <= 1 ? 1 : B <= 2 ? 2 : B <= 4 ? 4 : 8; }
 // measured on MI355X at config 3: the resident loop wins at batch 1; from
 // batch 4 the fused launches (graph) are faster
 constexpr int RES_AUTO_MAX_B = 1;
+// with the polling exchange (config 3, 2 sequences: 349 against 377 us per
+// step for plan 1; from 4 sequences plan 1 is faster, 443 against 482)
+constexpr int RES_AUTO_MAX_B_POLL = 2;
 
 static bool resident_ok(const Net* n, const Spec& sp) {
-  const int max_b = n->resident == 2 ? 8 : n->resident == 1 ? RES_AUTO_MAX_B : 0;
+  bool rope = false;
+  for (auto& L : n->layers) rope = rope || L->kind == K_POSENC;
+  const int auto_b = (n->res_poll && !rope) ? RES_AUTO_MAX_B_POLL : RES_AUTO_MAX_B;  // RoPE: the barrier exchange
+  const int max_b = n->resident == 2 ? 8 : n->resident == 1 ? auto_b : 0;
   if (sp.mode != MODE_CACHED || sp.S != 1 || sp.B > max_b || !sp.forward_only || !sp.am || sp.compress) return false;
   if (sp.first != 0 || sp.last != n->layers.size() || sp.kv_row || sp.out_hidden) return false;
   for (auto& L : n->layers)

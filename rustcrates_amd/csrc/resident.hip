@@ -7,18 +7,18 @@
 namespace mitok {
 
 // kernels of resident_k1/2/4/8.hip for a head dim (64 specialised, others
-// generic); the polling exchange is built for one row (null elsewhere)
+// generic), with the barrier or the polling exchange
 const void* resident_kernel_1(int dh, bool poll);
-const void* resident_kernel_2(int dh);
-const void* resident_kernel_4(int dh);
-const void* resident_kernel_8(int dh);
+const void* resident_kernel_2(int dh, bool poll);
+const void* resident_kernel_4(int dh, bool poll);
+const void* resident_kernel_8(int dh, bool poll);
 
 static const void* pick_kernel(int mr, int dh, bool poll) {
   switch (mr) {
     case 1: return resident_kernel_1(dh, poll);
-    case 2: return poll ? nullptr : resident_kernel_2(dh);
-    case 4: return poll ? nullptr : resident_kernel_4(dh);
-    default: return poll ? nullptr : resident_kernel_8(dh);
+    case 2: return resident_kernel_2(dh, poll);
+    case 4: return resident_kernel_4(dh, poll);
+    default: return resident_kernel_8(dh, poll);
   }
 }
 

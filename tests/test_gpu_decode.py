@@ -151,14 +151,20 @@ def test_resident_loop_repeats_bit_identically():
         assert np.array_equal(lg, runs[0][1])
 
 
-def test_default_plan_runs_batch1_resident():
+def test_default_plan_runs_resident_up_to_two_sequences():
+    """The default plan: the resident loop with the polling exchange for 1 and
+    2 sequences, the fused graph from 3; with the barrier exchange asked for,
+    the resident loop for 1 sequence only."""
     g = configs.build_network(ra.Network(0), MID)
-    prompt = seeded.prompts(8, [17], MID.vocab)
-    g.generate(prompt, n_new=8)
-    assert g.last_timings()["decode_loop"] == "resident"
-    prompt2 = seeded.prompts(8, [17, 9], MID.vocab)
-    g.generate(prompt2, lens=[17, 9], n_new=8)
+    for lens, want in (([17], "resident"), ([17, 9], "resident"), ([17, 9, 4], "graph")):
+        prompt = seeded.prompts(8, lens, MID.vocab)
+        g.generate(prompt, lens=lens, n_new=8)
+        assert g.last_timings()["decode_loop"] == want, lens
+    g.resident_exchange(0)
+    prompt = seeded.prompts(8, [17, 9], MID.vocab)
+    g.generate(prompt, lens=[17, 9], n_new=8)
     assert g.last_timings()["decode_loop"] == "graph"
+    g.close()
 
 
 def test_graph_replay_fused_plan_is_deterministic():

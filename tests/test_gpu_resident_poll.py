@@ -80,6 +80,37 @@ def test_polled_and_barrier_loops_match_oracle(cfg, plen, n_new):
         o.close()
 
 
+@pytest.mark.parametrize("cfg,lens,n_new", [(C3S, [40, 23], 15), (C3S, [150, 7, 64, 33], 12),
+                                            (SMALL, [12, 30, 5, 17, 9, 26, 40, 3], 20), (LONG, [300, 120], 8)])
+def test_polled_and_barrier_loops_match_oracle_batched(cfg, lens, n_new):
+    """2-8 sequences of different lengths (plan 3): both exchanges against the
+    oracle, ids bit-exact and logits within REL_TOL, and equal to each other
+    bit for bit."""
+    g = configs.build_network(ra.Network(0), cfg)
+    o = configs.build_network(oracle.Network(), cfg)
+    prompt = seeded.prompts(500 + len(lens), lens, cfg.vocab)
+    io, lo = o.generate(prompt, lens=lens, n_new=n_new, want_logits=True)
+    try:
+        out = {}
+        for mode in (1, 0):
+            g.set_decode_plan(3)
+            g.resident_exchange(mode)
+            ids, lg = g.generate(prompt, lens=lens, n_new=n_new, want_logits=True)
+            loop, polled = g.last_timings()["decode_loop"], g.resident_exchange(-1)
+            err = max_rel_err(lg, lo)
+            log(f"{cfg.name} B={len(lens)} exchange {mode}: loop {loop}, polled {polled}, ids {np.array_equal(ids, io)}, "
+                f"logits {err:.2e}")
+            assert loop == "resident"
+            assert polled == (mode == 1)
+            assert np.array_equal(ids, io), f"exchange {mode}"
+            assert err < REL_TOL, f"exchange {mode}"
+            out[mode] = lg
+        assert np.array_equal(out[1], out[0])
+    finally:
+        g.close()
+        o.close()
+
+
 def test_polled_loop_repeats_on_one_network():
     """Three polled generates in a row on one network (the arena, barrier
     epochs and chunk counters carried between launches), with step counts of

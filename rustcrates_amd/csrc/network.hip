@@ -295,6 +295,7 @@ struct Spec {
   bool compress = false;             // apply the wavelet stages begin_call planned for this call
   double* hist_re = nullptr;         // Re-logits history [step][B][V] at hist_cnt[0] (token loop)
   const int* hist_cnt = nullptr;
+  int ctx_bound = 0;                 // keys a decode step of this call can reach (0: the layers' context)
 };
 
 struct Timing {
@@ -352,6 +353,7 @@ struct mitok_network {
   hipGraphExec_t graph = nullptr;
   uint32_t graph_B = 0, graph_nnew = 0;
   int graph_step = 0;
+  int graph_ctx = 0;  // the decode spec's ctx_bound the graph was captured for
   bool graph_logits = false;
   uint64_t ws_generation = 0, graph_generation = 0;
   int direct_launch = 0;
@@ -1056,7 +1058,9 @@ static int enqueue_decode_fused(Net* n, const Spec& sp) {
         a.ctx = A->max_ctx;
         a.kv_len = kv_len;
         a.T_add = 1;
-        a.T_max = A->max_ctx;
+        // the call's reach sizes the chunk split: at config 3 with 32 sequences
+        // (128 + 128 keys) 8 chunks, whose combine joins the row transform
+        a.T_max = sp.ctx_bound > 0 ? std::min<int>(sp.ctx_bound, (int)A->max_ctx) : (int)A->max_ctx;
         a.bias_re = A->bias_re.as<double>();
         a.mc = A->max_ctx;
         a.B = B;
@@ -2545,7 +2549,7 @@ static int run_prompt(Net* n, const uint32_t* prompt, const uint32_t* lens, uint
 static int ensure_step_graph(Net* n, const Spec& dec, bool want_logits, uint32_t hist_stride, int kind) {
   const uint32_t B = (uint32_t)dec.B;
   if (n->graph && n->graph_B == B && n->graph_nnew == hist_stride && n->graph_logits == want_logits &&
-      n->graph_step == kind && n->graph_generation == n->ws_generation)
+      n->graph_step == kind && n->graph_ctx == dec.ctx_bound && n->graph_generation == n->ws_generation)
     return OK;
   drop_graph(n);
   hipStream_t st = n->stream;
@@ -2566,6 +2570,7 @@ static int ensure_step_graph(Net* n, const Spec& dec, bool want_logits, uint32_t
   if (g) (void)hipGraphDestroy(g);
   if (out) return out;
   n->graph_B = B;
+  n->graph_ctx = dec.ctx_bound;
   n->graph_nnew = hist_stride;
   n->graph_logits = want_logits;
   n->graph_step = kind;
@@ -2587,6 +2592,7 @@ static int generate_impl(Net* n, const uint32_t* prompt, const uint32_t* lens, u
   // ---- decode steps ----
   Spec dec = decode_spec(n, B);
   bind_decode_inputs(n, dec);
+  dec.ctx_bound = (int)(S + n_new);  // every prompt fits S; n_new - 1 tokens follow
   bool used_graph = false, used_resident = false;
   if (n_new > 1 && n->timing.cls == 0) {
     Spec rs = dec;

@@ -1391,6 +1391,15 @@ static int resident_build(Net* n, const Spec& sp, int grid, ResBuilt* rb, ResAre
         a.dh = dh;
         a.scale = 1.0 / (1e-8 + sqrt((double)dh));  // masked_attention_head.rs:453-465
         a.err = err;
+        if (sp.ctx_bound > 0 && sp.ctx_bound < (int)A->max_ctx) {
+          // the split sized to the call's reach where that gives every chunk a
+          // block of its own (config 3, 2 sequences: 347 -> 323 us per step; at
+          // 1 sequence, with a block per chunk either way, 255 against 256)
+          Attn r = a;
+          r.T_max = sp.ctx_bound;
+          if ((long)attention_split_plan(a).nsplit * H * B > grid && (long)attention_split_plan(r).nsplit * H * B <= grid)
+            a.T_max = sp.ctx_bound;
+        }
         ROp at;
         at.kind = ROP_ATTN;
         at.M = B;

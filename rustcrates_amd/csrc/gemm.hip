@@ -203,11 +203,28 @@ __global__ __launch_bounds__(256) void k_gemv(RowOps ro, int M, const double2* _
         }
   }
 
+  // the epilogue, one output per lane of wave 0 rather than MR per column
+  // owner (a GELU is a chain of transcendentals: eight in one lane take eight
+  // times as long); the Re values come back to the owners for the argmax
   double re[MR];
-  if (owner && col_ok)
+  if (MR == 1) {
+    if (owner && col_ok) re[0] = apply_epi(ep, M, N, 0, n, acc[0]);
+  } else {
+    if (owner)
 #pragma unroll
-    for (int m = 0; m < MR; ++m)
-      if (m < M) re[m] = apply_epi(ep, M, N, m, n, acc[m]);
+      for (int m = 0; m < MR; ++m) red[0][m][lane] = acc[m];
+    __builtin_amdgcn_wave_barrier();
+    __shared__ double epi_re[MR][C];
+    if (wave == 0)
+      for (int i = lane; i < MR * C; i += 64) {
+        const int m = i / C, cc = i - (i / C) * C, nn = blockIdx.x * C + cc;
+        if (m < M && nn < N) epi_re[m][cc] = apply_epi(ep, M, N, m, nn, red[0][m][cc]);
+      }
+    __builtin_amdgcn_wave_barrier();
+    if (owner)
+#pragma unroll
+      for (int m = 0; m < MR; ++m) re[m] = epi_re[m][lane];
+  }
   if (!am.part_v || wave != 0) return;
 #pragma unroll
   for (int m = 0; m < MR; ++m)

@@ -374,6 +374,34 @@ __device__ __forceinline__ void prefetch_weights(const ROp& nx, double2 (&w)[RES
   }
 }
 
+// A product's epilogue for its column block, one output per lane of wave 0
+// rather than MR per column owner (a GELU is a chain of transcendentals: two
+// or more in one lane take that many times as long).  acc: the owners' sums;
+// re: the owners' Re values back (for the fused argmax).  red is free again.
+template <int MR, int C>
+__device__ __forceinline__ void epi_spread(const Epi& ep, int M, int N, int bx, int n, bool col_ok, bool owner,
+                                           const double2 (&acc)[MR], double2* red, double (&re)[MR]) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if constexpr (MR == 1) {
+    if (owner && col_ok) re[0] = apply_epi<AccRes>(ep, M, N, 0, n, acc[0]);
+  } else {
+    __shared__ double epi_re[MR * C];
+    if (owner)
+#pragma unroll
+      for (int m = 0; m < MR; ++m) red[m * C + lane] = acc[m];
+    __builtin_amdgcn_wave_barrier();
+    if (wave == 0)
+      for (int i = lane; i < MR * C; i += 64) {
+        const int m = i / C, cc = i - (i / C) * C, nn = bx * C + cc;
+        if (m < M && nn < N) epi_re[i] = apply_epi<AccRes>(ep, M, N, m, nn, red[i]);
+      }
+    __builtin_amdgcn_wave_barrier();
+    if (owner)
+#pragma unroll
+      for (int m = 0; m < MR; ++m) re[m] = epi_re[m * C + lane];
+  }
+}
+
 template <int MR, int C, bool POLL>
 __device__ __forceinline__ void r_gemv3(const ROp& op, int item, double2* lds2, double2* red, double2* st_mean,
                                         double2* st_sd, double2 (&w)[RES_NPF], bool have) {
@@ -445,10 +473,7 @@ __device__ __forceinline__ void r_gemv3(const ROp& op, int item, double2* lds2, 
         if (m < M) st_dev(ep.out + ((long)by * M + m) * N + n, acc[m]);
   } else {
     double re[MR];
-    if (owner && col_ok)
-#pragma unroll
-      for (int m = 0; m < MR; ++m)
-        if (m < M) re[m] = apply_epi<AccRes>(ep, M, N, m, n, acc[m]);
+    epi_spread<MR, C>(ep, M, N, bx, n, col_ok, owner, acc, red, re);
     const Argmax& am = op.am;
     if (am.part_v && wave == 0)
 #pragma unroll
@@ -603,10 +628,7 @@ __device__ __forceinline__ void r_gemv4(const ROp& op, int item, int prev, doubl
         if (m < M) st_dev(ep.out + ((long)by * M + m) * N + n, acc[m]);
   } else {
     double re[MR];
-    if (owner && col_ok)
-#pragma unroll
-      for (int m = 0; m < MR; ++m)
-        if (m < M) re[m] = apply_epi<AccRes>(ep, M, N, m, n, acc[m]);
+    epi_spread<MR, C>(ep, M, N, bx, n, col_ok, owner, acc, red, re);
     const Argmax& am = op.am;
     if (am.part_v && wave == 0)
 #pragma unroll

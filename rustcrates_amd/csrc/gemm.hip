@@ -70,12 +70,19 @@ __global__ __launch_bounds__(256) void k_argmax_finalize(Argmax am, int tiles) {
 // group of 64/C rows, so one wave instruction covers 64/C rows x C columns.
 // The first 16 weight loads per lane -- every row of the lane for the layer
 // products of config 3 -- are in flight while the prologue builds the block's
-// input rows in LDS; longer ranges keep two buffers of 8 loads in flight, each
-// refilled once consumed.  Every lane issues every load (rows past its range
-// read a zero constant), so each wait covers only the loads it needs.  Lanes of a column are summed by shuffles,
+// input rows in LDS; longer ranges then take 8 rows at a time.  Every lane
+// issues every load (rows past its range read a zero constant), so each wait
+// covers only the loads it needs.  Lanes of a column are summed by shuffles,
 // the 4 waves through LDS; blockIdx.y splits K (at most 8 ways, so few blocks
 // meet at each completion counter).
+// PRE: the input rows are plain (x[m][k] as stored, the decode products of 2-8
+// sequences), at most GEMV_PRE elements per thread.  They are requested before
+// the weights: a wave's loads return in order, so a prologue whose loads go
+// out after the weights' waits for the whole weight stream, and the
+// multiply-adds only start after it.  Requested first, the rows are in LDS
+// when the first weights arrive.
 // ===========================================================================
+constexpr int GEMV_PRE = 16;
 constexpr int GEMV_MAX_SPLIT = 8;
 __device__ const double2 gemv_zero2 = {0.0, 0.0};  // what a load past a lane's rows reads
 // w[u] <- rows u0 + u of the lane's column, u < 8 (zero past its nu rows)
@@ -97,7 +104,7 @@ __device__ __forceinline__ void gemv_fma(double2 (&acc)[MR], const double2* xw, 
 }
 constexpr int SKINNY_MAX_SPLIT = 8;
 
-template <int MR, int C, int NS>
+template <int MR, int C, bool PRE>
 __global__ __launch_bounds__(256) void k_gemv(RowOps ro, int M, const double2* __restrict__ W, long ldw, int N, int K,
                                               int kw, Epi ep, Argmax am, double2* __restrict__ ws,
                                               uint32_t* __restrict__ cnt) {
@@ -125,14 +132,27 @@ __global__ __launch_bounds__(256) void k_gemv(RowOps ro, int M, const double2* _
 
   const int nuc = col_ok ? nu : 0;  // rows this lane loads
   const int nu_max = (kw + RPW - 1) / RPW;  // the most rows of any lane (block-uniform)
-  static_assert(NS == 16 || NS == 24, "rows requested before the prologue");
-  double2 w0[8], w1[8], w2[8];
+  double2 xr[PRE ? GEMV_PRE : 1];
+  if constexpr (PRE) {  // element i = m * RL + (k - kb0) of the block's rows, before any weight
+#pragma unroll
+    for (int j = 0; j < GEMV_PRE; ++j) {
+      const int i = tid + 256 * j, m = i / RL, k = kb0 + (i - m * RL);
+      xr[j] = ld_glb((i < MR * RL && m < M && k < K) ? ro.x + (long)m * ro.ldx + k : &gemv_zero2);
+    }
+  }
+  double2 w0[8], w1[8];
   gemv_rows(w0, wp, wstep, 0, nuc);
   gemv_rows(w1, wp, wstep, 8, nuc);
-  if constexpr (NS == 24) gemv_rows(w2, wp, wstep, 16, nuc);
 
-  ro_prepare(ro, M, L);
-  ro_build<MR>(ro, M, K, ka, RL, kb0, min(K, kb0 + KB), lds2, L, st_mean, st_sd);
+  if constexpr (PRE) {
+#pragma unroll
+    for (int j = 0; j < GEMV_PRE; ++j)
+      if (tid + 256 * j < MR * RL) lds2[tid + 256 * j] = xr[j];
+    __syncthreads();
+  } else {
+    ro_prepare(ro, M, L);
+    ro_build<MR>(ro, M, K, ka, RL, kb0, min(K, kb0 + KB), lds2, L, st_mean, st_sd);
+  }
   if (blockIdx.x == 0 && blockIdx.y == 0 && tid < M) ro_check(ro, tid);
   const double2* xs = lds2 + (kb0 - ka);  // row m of the block's range at xs[m * RL]
   if (ro.save && blockIdx.x == 0)
@@ -151,9 +171,8 @@ __global__ __launch_bounds__(256) void k_gemv(RowOps ro, int M, const double2* _
     const double2* xw = xs + (nuc > 0 ? wave * kw + r : 0);
     gemv_fma<MR>(acc, xw, RL, RPW, 0, nuc, w0);
     gemv_fma<MR>(acc, xw, RL, RPW, 8, nuc, w1);
-    if constexpr (NS == 24) gemv_fma<MR>(acc, xw, RL, RPW, 16, nuc, w2);
-    // rows past the first NS (the wide vocab product), 8 at a time
-    for (int u0 = NS; u0 < nu_max; u0 += 8) {
+    // rows past the first 16 (the wide vocab product, config 5's products), 8 at a time
+    for (int u0 = 16; u0 < nu_max; u0 += 8) {
       gemv_rows(w0, wp, wstep, u0, nuc);
       gemv_fma<MR>(acc, xw, RL, RPW, u0, nuc, w0);
     }
@@ -1017,8 +1036,9 @@ static GemvPlan plan_gemv(int M, int N, int K, bool part, bool narrow = false) {
   p.ncb = cdiv_i(N, p.C);
   int P = std::min(GEMV_MAX_SPLIT, std::max(1, cdiv_i(256, p.ncb)));
   // a split product takes as many splits as keep every lane's range within
-  // the 24 weight rows k_gemv requests before its prologue (config 5's FFN
-  // Linear: 4 splits of 768 rows, not 3 of 1024)
+  // 24 weight rows, the 16 k_gemv requests before its prologue and one batch
+  // of 8 (config 5's FFN Linear: 4 splits of 768 rows, not 3 of 1024; 6
+  // splits of 512, 16 rows per lane, measured no faster)
   if (part && !wide) P = std::min(GEMV_MAX_SPLIT, std::max(P, cdiv_i(K, 4 * 24 * rpw)));
   // rows per block: a multiple of 4 waves x rpw, and its input rows fit 64 KB of LDS
   const int unit = 4 * rpw;
@@ -1179,13 +1199,12 @@ static void launch_gemv(hipStream_t st, const GemvPlan& p, const RowOps& ro, int
                         int K, const Epi& ep, const Argmax& am, const Sync& sy) {
   dim3 grid(p.ncb, p.P);
   const size_t shm = gemv_lds_bytes(p, ro, M, K);
-  // 24 rows per lane requested before the prologue where 16 would not cover
-  // the lane's range (both keep two blocks per CU within the registers)
-  if ((p.kw + 64 / C - 1) / (64 / C) > 16)
-    MITOK_LAUNCH((k_gemv<MR, C, 24>), grid, dim3(256), shm, st, ro, M, W, ldw, N, K, p.kw, ep, am, (double2*)sy.ws,
+  // plain rows that fit the staging registers are requested before the weights
+  if (ro.plain() && (long)MR * 4 * p.kw <= 256L * GEMV_PRE)
+    MITOK_LAUNCH((k_gemv<MR, C, true>), grid, dim3(256), shm, st, ro, M, W, ldw, N, K, p.kw, ep, am, (double2*)sy.ws,
                  sy.counters);
   else
-    MITOK_LAUNCH((k_gemv<MR, C, 16>), grid, dim3(256), shm, st, ro, M, W, ldw, N, K, p.kw, ep, am, (double2*)sy.ws,
+    MITOK_LAUNCH((k_gemv<MR, C, false>), grid, dim3(256), shm, st, ro, M, W, ldw, N, K, p.kw, ep, am, (double2*)sy.ws,
                  sy.counters);
 }
 template <int MR>

@@ -1035,6 +1035,13 @@ static GemvPlan plan_gemv(int M, int N, int K, bool part, bool narrow = false) {
   const int rpw = 64 / p.C;
   p.ncb = cdiv_i(N, p.C);
   int P = std::min(GEMV_MAX_SPLIT, std::max(1, cdiv_i(256, p.ncb)));
+  // the vocab product of 5-8 rows splits K in two: each lane's weight rows
+  // come 8 per memory round trip after the first 16, with eight rows of
+  // multiply-adds between, so halving them per lane pays for the completion.
+  // Decode per step at config 3 with 8 sequences 482 -> 449 us (4 splits:
+  // 460); with 4 rows the split measured slower (357 -> 369) and 16-column
+  // blocks slower for both (386, 500)
+  if (wide && M > 4) P = std::max(P, 2);
   // a split product takes as many splits as keep every lane's range within
   // 24 weight rows, the 16 k_gemv requests before its prologue and one batch
   // of 8 (config 5's FFN Linear: 4 splits of 768 rows, not 3 of 1024; 6

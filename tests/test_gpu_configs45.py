@@ -10,7 +10,8 @@ At the full configurations (12 layers, vocab 32000): config 4's batch of 64
 for all 256 new tokens with sequences 0, 63 and the longest prompt against
 the oracle (bit-exact ids; logits within the oracle's noise floor, as for
 config 3).  Config 5: its layer at the full 1920-token prompt
-against the oracle, and the full model's two decode plans against each other.
+against the oracle, the full model with four short prompts against the
+oracle, and the full model's two decode plans against each other.
 
 With the imaginary parts of the block weights scaled by 0.3 (no LayerNorm
 variance cancels), both full configurations against the oracle at REL_TOL
@@ -225,6 +226,39 @@ def test_config5_prompt1920_one_layer_vs_oracle():
         e, nw = max_rel_err(lg, lo), normwise_rel_err(lg, lo)
         log(f"prompt 1920, one layer, plan {plan}: elementwise {e:.3e}, normwise {nw:.3e}")
         assert e < REL_TOL
+
+
+def test_config5_full_depth_short_prompts_vs_oracle():
+    """Config 5 at full depth (12 layers, vocab 32000, seeded weights) with four
+    short prompts, decoded by the default plan for 4 sequences (the GEMV
+    products whose rows land before their weights), against the oracle: ids
+    bit-exact, logits within REL_TOL or the oracle's own spread.  The full
+    1920-token prompt is checked per layer and with the well-conditioned
+    variant above."""
+    cfg = configs.C5
+    lens = [96, 71, 88, 50]
+    n_new = 16
+    prompt = seeded.prompts(55, lens, cfg.vocab)
+    g = configs.build_network(ra.Network(0), cfg)
+    try:
+        ig, lg = g.generate(prompt, lens=lens, n_new=n_new, want_logits=True)
+        log(f"config 5 full depth, prompts {lens}: loop {g.last_timings()['decode_loop']}")
+    finally:
+        g.close()
+    o = configs.build_network(oracle.Network(), cfg)
+    try:
+        io, lo = o.generate(prompt, lens=lens, n_new=n_new, want_logits=True)
+        floor = oracle_floor_of(lambda: o.generate(prompt, lens=lens, n_new=n_new, want_logits=True)[1], lo)
+    finally:
+        o.close()
+    # twelve complex LayerNorm layers: single logits near zero move by more
+    # than their size between the oracle's own valid orders, so the bound is
+    # normwise (per step and sequence), against the oracle's normwise spread
+    nw = normwise_rel_err(lg, lo)
+    log(f"c5 full depth, four short prompts: ids match {np.array_equal(ig, io)}, normwise {nw:.3e} (the checker's own "
+        f"spread {floor[1]:.3e}), elementwise {max_rel_err(lg, lo):.3e} (spread {floor[0]:.3e})")
+    assert np.array_equal(ig, io)
+    assert nw <= NOISE_FACTOR * max(floor[1], REL_TOL)
 
 
 def test_config5_full_decode_plans_agree():

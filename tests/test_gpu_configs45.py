@@ -292,8 +292,8 @@ def test_config4_batch1_decoded_to_cache_end():
     """Full config 4 at batch 1 (the resident loop): a 64-token prompt decoded
     for 449 tokens, so the last step attends over all 512 cache rows
     (max_ctx).  Ids bit-exact against the oracle over every step; the logits
-    normwise error is logged beside the bound (the oracle's own summation
-    orders differ by about 1e-5 normwise on this model, see above)."""
+    normwise within NOISE_FACTOR x the oracle's own spread, measured here
+    against its k-descending summation order over the same 449 steps."""
     cfg = configs.C4
     lens = [64]
     n_new = cfg.max_ctx - lens[0] + 1
@@ -304,12 +304,19 @@ def test_config4_batch1_decoded_to_cache_end():
     ig, lg = g.generate(prompt, lens=lens, n_new=n_new, want_logits=True)
     assert g.last_timings()["decode_loop"] == "resident"
     io, lo = o.generate(prompt, lens=lens, n_new=n_new, want_logits=True)
+    oracle.set_gemm_order(1)
+    try:
+        _, alt = o.generate(prompt, lens=lens, n_new=n_new, want_logits=True)
+    finally:
+        oracle.set_gemm_order(0)
+        o.close()
+    floor = normwise_rel_err(alt, lo)
     first_diff = int(np.argmax(ig[0] != io[0])) if not np.array_equal(ig, io) else -1
     nw = normwise_rel_err(lg, lo)
-    log(f"  ids match {np.array_equal(ig, io)} (first difference {first_diff}); normwise {nw:.3e}; "
-        f"last step normwise {normwise_rel_err(lg[-1:], lo[-1:]):.3e}")
+    log(f"  ids match {np.array_equal(ig, io)} (first difference {first_diff}); normwise {nw:.3e} (the checker's own "
+        f"spread {floor:.3e}); last step normwise {normwise_rel_err(lg[-1:], lo[-1:]):.3e}")
     assert np.array_equal(ig, io)
-    assert nw < 1e-3
+    assert nw <= NOISE_FACTOR * max(floor, REL_TOL)
     g.close()
 
 

@@ -959,6 +959,12 @@ static bool fused_decode_ok(const Net* n, const Spec& sp) {
 // materialised (rowops_apply), and FFN Dense finishes its sums in-kernel
 // (GELU needs them); QKV and FFN Linear still leave partials for the
 // attention and the next row transform.
+// From this many sequences plan 1 materialises the rows its GEMV products read
+// (the transform before QKV, FFN Dense's GELU output), so every product takes
+// plain rows and requests them before its weights (k_gemv's PRE variant).
+// Measured on MI355X, decode per step at config 3: with 3 sequences 425 -> 354
+// us, with 2 370 -> 332 (the threshold was 4 before the rows-first GEMV)
+constexpr int FUSED_PLAIN_MIN_B = 2;
 static int enqueue_decode_fused(Net* n, const Spec& sp) {
   hipStream_t st = n->stream;
   uint32_t* err = n->err_d.as<uint32_t>();
@@ -1027,12 +1033,12 @@ static int enqueue_decode_fused(Net* n, const Spec& sp) {
         const int d = A->d_in, H = A->heads, dh = A->dh;
         if (pro.resid) materialize();           // its residual source is about to be overwritten
         double2* x1 = n->act0.as<double2>();  // the block input, kept for the residual
-        // from 4 sequences the row transform before QKV (split partials + bias
-        // + LayerNorm) is materialised once rather than redone by every QKV
-        // block: measured on MI355X, decode per step 763 -> 708 us at config 3
-        // with 8 sequences, 496 -> 489 with 4, 1943 -> 1911 at config 5 with 4;
-        // with one sequence (plan 1) 343 -> 375, so not below 4
-        if (mat || B >= 4) {
+        // from FUSED_PLAIN_MIN_B sequences the row transform before QKV (split
+        // partials + bias + LayerNorm) is materialised once rather than redone
+        // by every QKV block: measured on MI355X before the rows-first GEMV,
+        // decode per step 763 -> 708 us at config 3 with 8 sequences, 496 ->
+        // 489 with 4, 1943 -> 1911 at config 5 with 4
+        if (mat || B >= FUSED_PLAIN_MIN_B) {
           if (!pro.plain()) rowops_apply(st, B, d, pro, x1, d);
           else x1 = const_cast<double2*>(pro.x);  // a materialised row buffer (ld d), not reused before the combine
           pro = rows_of(x1, d);
@@ -1091,13 +1097,13 @@ static int enqueue_decode_fused(Net* n, const Spec& sp) {
       case K_FEED_FORWARD: {
         auto* F = (FeedForwardLayer*)L;
         RowOps h;
-        // Dense: + b1, GELU in the epilogue (layer.rs:132-166).  From 4
-        // sequences also for the GEMV: in FFN Linear's prologue every column
-        // block would evaluate GELU again over its K range (96 times over at
-        // config 5).  Measured on MI355X, decode per step 1791 -> 1643 us at
-        // config 5 with 4 sequences, 713 -> 707 at config 3 with 8, 494 -> 496
-        // with 4, 421 -> 428 with 2; ids unchanged
-        if (mat || B >= 4) {
+        // Dense: + b1, GELU in the epilogue (layer.rs:132-166).  From
+        // FUSED_PLAIN_MIN_B sequences also for the GEMV: in FFN Linear's
+        // prologue every column block would evaluate GELU again over its K
+        // range (96 times over at config 5).  Measured on MI355X, decode per
+        // step 1791 -> 1643 us at config 5 with 4 sequences, 713 -> 707 at
+        // config 3 with 8; ids unchanged
+        if (mat || B >= FUSED_PLAIN_MIN_B) {
           need_plain();
           Epi e1;
           e1.mode = EPI_GELU;

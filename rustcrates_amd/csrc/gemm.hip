@@ -720,8 +720,10 @@ __global__ __launch_bounds__(1024) void k_zgemm_rows16(const double2* __restrict
   }
 }
 
-// The same product for the planned shape of 8 k-steps (32 of K) per wave,
-// as straight-line code: the loads of all four 8-k batches go out first, an
+// The same product for the planned shapes of 8 or 12 k-steps (32 or 48 of K)
+// per wave, as straight-line code (12: config 4's FFN Dense, K 768 whole in
+// the block; 729 -> 725 ms of decode per call against k_zgemm_rows16): the
+// loads of all NB 8-k batches go out first, an
 // out-of-range operand lane reading a zero constant instead (no branch), so
 // the compiler waits for each batch's own loads (in-order vmcnt) and the
 // first batch's MFMAs run while the later batches are still in flight.  In
@@ -730,14 +732,15 @@ __global__ __launch_bounds__(1024) void k_zgemm_rows16(const double2* __restrict
 // in ascending order) is the same as there, so the results are identical.
 __device__ const double2 rows16s_zero = {0.0, 0.0};  // what an out-of-range operand lane reads
 
+template <int NB>  // batches of 2 k-steps: 4 (32 of K per wave, 512 per block) or 6 (48, 768)
 __global__ __launch_bounds__(1024) void k_zgemm_rows16s(const double2* __restrict__ X, long ldx, int M,
                                                       const double2* __restrict__ W, long ldw, int N, int K, Epi ep) {
-  constexpr int NB = 4, U = 2, NW = ROWS16_WAVES, LD = 16;  // 4 batches x 2 k-steps of 4 = 32 of K per wave
+  constexpr int U = 2, NW = ROWS16_WAVES, LD = 16;
   extern __shared__ double2 red16[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int i = lane & 15, kq = lane >> 4;
   const int n = blockIdx.x * 16 + i, m = blockIdx.y * 16 + i;
-  const int ka = (blockIdx.z * NW + wave) * 32;
+  const int ka = (blockIdx.z * NW + wave) * 8 * NB;
   const long nc = min(n, N - 1), mc = min(m, M - 1);
   const bool nok = n < N, mok = m < M;
   double2 a[NB][U], b[NB][U];
@@ -1230,7 +1233,8 @@ static void launch_skinny(hipStream_t st, const SkinnyPlan& p, const RowOps& ro,
   if (p.rows) {  // EPI_PART, or one K range per block (no argmax: not a vocab-wide output)
     const dim3 g3(p.ncb, p.rt, p.P);
     if (p.w16) {
-      if (p.nkw == 8) MITOK_LAUNCH(k_zgemm_rows16s, g3, dim3(64 * ROWS16_WAVES), ROWS16_LDS, st, ro.x, ro.ldx, M, W, ldw, N, K, ep);
+      if (p.nkw == 8) MITOK_LAUNCH(k_zgemm_rows16s<4>, g3, dim3(64 * ROWS16_WAVES), ROWS16_LDS, st, ro.x, ro.ldx, M, W, ldw, N, K, ep);
+      else if (p.nkw == 12) MITOK_LAUNCH(k_zgemm_rows16s<6>, g3, dim3(64 * ROWS16_WAVES), ROWS16_LDS, st, ro.x, ro.ldx, M, W, ldw, N, K, ep);
       else MITOK_LAUNCH(k_zgemm_rows16, g3, dim3(64 * ROWS16_WAVES), ROWS16_LDS, st, ro.x, ro.ldx, M, W, ldw, N, K, p.nkw, ep);
       return;
     }

@@ -1037,7 +1037,10 @@ static GemvPlan plan_gemv(int M, int N, int K, bool part, bool narrow = false) {
   p.C = wide ? 64 : (part || (narrow && cdiv_i(N, 8) >= 256) ? 8 : 16);
   const int rpw = 64 / p.C;
   p.ncb = cdiv_i(N, p.C);
-  int P = std::min(GEMV_MAX_SPLIT, std::max(1, cdiv_i(256, p.ncb)));
+  // K splits for a grid of about 256 blocks; with 5-8 rows about 192 (config 3
+  // with 8 sequences: QKV without a split, FFN Linear in 3, 447 -> 433 us per
+  // step; no change with 2-4 rows)
+  int P = std::min(GEMV_MAX_SPLIT, std::max(1, cdiv_i(M > 4 ? 192 : 256, p.ncb)));
   // the vocab product of 5-8 rows splits K in two: each lane's weight rows
   // come 8 per memory round trip after the first 16, with eight rows of
   // multiply-adds between, so halving them per lane pays for the completion.
